@@ -1,0 +1,832 @@
+// oz_oracle — CPU restatement of the reference ozTTgemm numerics. TEST INFRASTRUCTURE ONLY.
+// See oz_oracle.hpp for the rules of use and how each function is pinned.
+//
+// Build flags matter: -ffp-contract=off -fno-fast-math (the reference builds the same way,
+// Makefile:51-53), x86-64 SSE arithmetic for float/double, 80-bit long double, libquadmath.
+#include "oz_oracle.hpp"
+
+#include <quadmath.h>
+
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstring>
+#include <random>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// FP32 operation model of the reference's tile operations (experiments/src/checks/sfpu_tf_emu.hpp:66-88,
+// the model the reference compared with its hardware): each add/sub/mul is one binary32 RNE
+// operation, no FMA; denormal inputs and outputs become signed zero; a product with a zero factor
+// is +0; Rnd is (|v|+2^23)-2^23 with the sign of v, +0 for a zero result.
+// ---------------------------------------------------------------------------------------------
+inline float flush(float x) { return (x != 0.0f && std::fabs(x) < FLT_MIN) ? std::copysign(0.0f, x) : x; }
+inline float f_add(float a, float b) { return flush(flush(a) + flush(b)); }
+inline float f_sub(float a, float b) { return flush(flush(a) - flush(b)); }
+inline float f_mul(float a, float b) {
+    a = flush(a);
+    b = flush(b);
+    if (a == 0.0f || b == 0.0f) return 0.0f;
+    return flush(a * b);
+}
+inline float f_rnd(float v) {
+    v = flush(v);
+    const float a = std::fabs(v);
+    if (!(a < 8388608.0f)) return v;
+    const float t = (a + 8388608.0f) - 8388608.0f;
+    return t == 0.0f ? 0.0f : std::copysign(t, v);
+}
+inline float bits_f(uint32_t u) {
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+inline uint32_t f_bits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+
+// Error-free sums in the order of the reference procedures (sfpu_tf_proc.h:61-74).
+inline void two_sum(float x, float y, float& s, float& e) {
+    s = f_add(x, y);
+    float bb = f_sub(s, x);
+    float aa = f_sub(s, bb);
+    aa = f_sub(x, aa);
+    bb = f_sub(y, bb);
+    e = f_add(aa, bb);
+}
+inline void fast_two_sum(float a, float b, float& s, float& t) {
+    s = f_add(a, b);
+    const float w = f_sub(s, a);
+    t = f_sub(b, w);
+}
+
+// Triple-float times a power-of-two radix, renormalized (tfMulP2, sfpu_tf_proc.h:160-169).
+inline void tf_mul_pow2(float& hi, float& mid, float& lo, float r) {
+    hi = f_mul(hi, r);
+    mid = f_mul(mid, r);
+    lo = f_mul(lo, r);
+    float s3, e4, s5, e6;
+    two_sum(mid, lo, s3, e4);
+    two_sum(hi, s3, s5, e6);
+    hi = s5;
+    fast_two_sum(e6, e4, mid, lo);
+}
+
+// ModRound: d - Rnd(d*rinv)*m (sfpu_tf_proc.h:316-319).
+inline float mod_round(float d, float m, float rinv) {
+    float s = f_mul(d, rinv);
+    s = f_rnd(s);
+    s = f_mul(s, m);
+    return f_sub(d, s);
+}
+
+// split_f64 (f64_tf.h:141-172): FP64 x*2^d -> hi, braw, craw, s bit patterns, integer ops only.
+void split_words(uint32_t w1, uint32_t w0, int32_t d, uint32_t& hi, uint32_t& braw, uint32_t& craw, uint32_t& s) {
+    const uint32_t sgn = w1 & 0x80000000u;
+    const int32_t E = (int32_t)((w1 >> 20) & 0x7FFu);
+    if (E == 0) {
+        hi = 0u;
+        braw = 0x4B000000u;
+        craw = 0x4B000000u;
+        s = 0u;
+        return;
+    }
+    // 53-bit significand -> 23-bit head (rounded to nearest on the dropped 30 bits), signed 23-bit
+    // middle and 7-bit tail.
+    uint32_t a = 0x400000u | ((w1 & 0x000FFFFFu) << 2) | (w0 >> 30);
+    const uint32_t rem = w0 & 0x3FFFFFFFu;
+    int32_t r = (int32_t)rem;
+    if (rem >= 0x20000000u) {
+        a += 1u;
+        r = (int32_t)rem - 0x40000000;
+    }
+    const int32_t b = r >> 7;
+    const uint32_t c = (uint32_t)r & 0x7Fu;
+    const int32_t elsb = E - 1075 + d;
+    int32_t eh;
+    uint32_t mh;
+    if (a == 0x800000u) {
+        eh = elsb + 180;
+        mh = 0u;
+    } else {
+        eh = elsb + 179;
+        mh = (a << 1) & 0x7FFFFFu;
+    }
+    const int32_t es = elsb + 134;
+    hi = (eh > 0 && eh < 255) ? (sgn | ((uint32_t)eh << 23) | mh) : 0u;
+    s = (es > 0 && es < 255) ? (sgn | ((uint32_t)es << 23)) : 0u;
+    braw = 0x4B000000u | (((uint32_t)(b + 0x400000)) & 0x7FFFFFu);
+    craw = 0x4B000000u | c;
+}
+
+// tf_load_f64 (slice_tf_core.h:67-76): mid = (braw - 1.5*2^23)*s, lo = (craw - 2^23)*s*2^-7.
+void load_triple(double x, int32_t d, float& hi, float& mid, float& lo) {
+    uint64_t u;
+    std::memcpy(&u, &x, 8);
+    uint32_t h, br, cr, s;
+    split_words((uint32_t)(u >> 32), (uint32_t)u, d, h, br, cr, s);
+    const float sf = bits_f(s);
+    hi = bits_f(h);
+    mid = f_mul(f_add(bits_f(br), -12582912.0f), sf);
+    lo = f_mul(f_mul(f_add(bits_f(cr), -8388608.0f), sf), 0.0078125f);
+}
+
+// oz2_make_digits (digits.h:80-112): nd digits, top first.
+void make_digits(double x, int32_t d, int nd, float* dig) {
+    float hi, mid, lo;
+    load_triple(x, d, hi, mid, lo);
+    for (int i = 0; i < nd; ++i) {
+        if (i > 0) tf_mul_pow2(hi, mid, lo, 1048576.0f);
+        const float t = f_rnd(hi);
+        hi = f_sub(hi, t);
+        dig[i] = t;
+    }
+}
+
+// 2^e mod m for e >= 0 (moduli.hpp:688-692).
+float pow2mod(int e, long mod) {
+    long r = 1 % mod, base = 2 % mod;
+    for (int i = 0; i < e; ++i) r = (r * base) % mod;
+    return (float)r;
+}
+
+// oz2_residue (digits.h:165-179) on digits given top first (dig[0] = d_{nd-1}, ..., dig[nd-1] = d0).
+float residue(const float* dig, int nd, float m, float rinv, const float* c) {
+    const float d0 = dig[nd - 1], d1 = dig[nd - 2], d2 = dig[nd - 3];
+    float acc = d0;
+    float t = mod_round(d1, m, rinv);
+    acc = f_add(acc, f_mul(t, c[0]));
+    t = mod_round(d2, m, rinv);
+    acc = f_add(acc, f_mul(t, c[1]));
+    if (nd >= 4) {
+        acc = mod_round(acc, m, rinv);
+        if (nd >= 5) {
+            t = mod_round(dig[0], m, rinv);  // d4
+            acc = f_add(acc, f_mul(t, c[3]));
+            acc = mod_round(acc, m, rinv);
+        }
+        t = mod_round(dig[nd - 4], m, rinv);  // d3
+        acc = f_add(acc, f_mul(t, c[2]));
+    }
+    return mod_round(acc, m, rinv);
+}
+
+inline int32_t delta_of(const int32_t* delta, int mode, int r, int c) { return mode == 0 ? delta[r] : delta[c]; }
+
+// ---------------------------------------------------------------------------------------------
+// Reconstruction helpers of the reference (f64_tf.h:174-400)
+// ---------------------------------------------------------------------------------------------
+void dec32(uint32_t u, int32_t& e, int32_t& sig) {
+    const int32_t ee = (int32_t)((u >> 23) & 0xFFu);
+    if (ee == 0) {
+        e = 0;
+        sig = 0;
+        return;
+    }
+    e = ee;
+    const int32_t s = (int32_t)(0x800000u | (u & 0x7FFFFFu));
+    sig = (u & 0x80000000u) ? -s : s;
+}
+uint64_t pack_f64(uint64_t A, uint32_t Whi, uint32_t Wlo, int32_t total, uint64_t sgn) {
+    const unsigned __int128 p = (unsigned __int128)A * (((unsigned __int128)Whi << 32) | Wlo);
+    const uint64_t hi = (uint64_t)(p >> 64);
+    const int32_t n = (hi >> 63) ? 63 : 62;
+    int32_t exp2 = n + 64 + total;
+    uint64_t mant;
+    bool up;
+    if (n == 63) {
+        mant = hi >> 11;
+        up = (hi & 0x400ull) != 0;
+    } else {
+        mant = hi >> 10;
+        up = (hi & 0x200ull) != 0;
+    }
+    if (up) {
+        mant += 1ull;
+        if (mant >> 53) {
+            mant >>= 1;
+            exp2 += 1;
+        }
+    }
+    const int32_t ebias = exp2 + 1023;
+    if (ebias <= 0) return sgn;
+    if (ebias >= 2047) return sgn | 0x7FF0000000000000ull;
+    return sgn | ((uint64_t)ebias << 52) | (mant & 0x000FFFFFFFFFFFFFull);
+}
+struct A128 {
+    uint32_t w[4];
+};
+void a128_add(A128& a, int32_t k, uint32_t v) {
+    for (; k < 4 && v; ++k) {
+        const uint32_t o = a.w[k];
+        a.w[k] = o + v;
+        v = (a.w[k] < o);
+    }
+}
+void a128_sub(A128& a, int32_t k, uint32_t v) {
+    for (; k < 4 && v; ++k) {
+        const uint32_t o = a.w[k];
+        a.w[k] = o - v;
+        v = (o < v);
+    }
+}
+void a128_term(A128& a, int32_t sig, int32_t sh) {
+    if (!sig || sh <= -24) return;
+    const bool neg = sig < 0;
+    const uint64_t m = (uint64_t)(neg ? -(int64_t)sig : (int64_t)sig);
+    const uint64_t v = (sh < 0) ? (m >> (uint32_t)(-sh)) : (m << (sh & 31));
+    const int32_t w = (sh < 0) ? 0 : (sh >> 5);
+    if (!v) return;
+    if (neg) {
+        a128_sub(a, w, (uint32_t)v);
+        a128_sub(a, w + 1, (uint32_t)(v >> 32));
+    } else {
+        a128_add(a, w, (uint32_t)v);
+        a128_add(a, w + 1, (uint32_t)(v >> 32));
+    }
+}
+void a128_add_limbs(A128& a, const float* limb, int nl) {
+    for (int i = 0; i < nl; i++) {
+        int32_t e, sig;
+        dec32(f_bits(limb[i]), e, sig);
+        a128_term(a, sig, e - 26);
+    }
+}
+uint64_t a128_frac_to_f64(A128 a, int32_t g, uint32_t Whi, uint32_t Wlo, int32_t qw) {
+    const uint32_t top = a.w[3];
+    if (top + 0x08000000u >= 0x10000000u || top == 0xF8000000u) {
+        if ((int32_t)top >= 0x08000000)
+            a128_sub(a, 3, 0x10000000u);
+        else if ((int32_t)top < -0x08000000 || (a.w[0] | a.w[1] | a.w[2]) == 0u)
+            a128_add(a, 3, 0x10000000u);
+    }
+    const bool neg = (a.w[3] & 0x80000000u) != 0;
+    if (neg) {
+        for (int i = 0; i < 4; i++) a.w[i] = ~a.w[i];
+        a128_add(a, 0, 1u);
+    }
+    if (!(a.w[0] | a.w[1] | a.w[2] | a.w[3])) return 0ull;
+    int32_t wsh = 0;
+    while (a.w[3 - wsh] == 0) wsh++;
+    const int32_t lz = 32 * wsh + __builtin_clz(a.w[3 - wsh]);
+    uint64_t A;
+    if (lz <= 64) {
+        const int32_t k = (64 - lz) >> 5, off = (64 - lz) & 31;
+        A = (((uint64_t)a.w[k + 1] << 32) | a.w[k]) >> off;
+        if (off) A |= (uint64_t)a.w[k + 2] << (64 - off);
+    } else {
+        A = (((uint64_t)a.w[1] << 32) | a.w[0]) << (lz - 64);
+    }
+    return pack_f64(A, Whi, Wlo, qw + g - lz - 60, neg ? 0x8000000000000000ull : 0ull);
+}
+
+// Number of trailing reciprocal fragments added with the cheap step (moduli.hpp:772-800).
+uint32_t choose_small_tail(const float* rp, uint32_t nrp, const int* m, uint32_t s) {
+    if (nrp > 8) return 0;
+    float worst[8] = {0};
+    float vmax = 0.f;
+    for (uint32_t t = 0; t < nrp; t++) {
+        for (uint32_t i = 0; i < s; i++) {
+            const float v = std::fabs(rp[(size_t)i * nrp + t]) * (float)(m[i] / 2 + 1);
+            if (v > worst[t]) worst[t] = v;
+        }
+        if (worst[t] > vmax) vmax = worst[t];
+    }
+    const float scale = vmax < 1.f ? vmax : 1.f;
+    const float eps = (float)std::ldexp((double)scale, -30);
+    uint32_t n = 0;
+    for (uint32_t t = nrp; t-- > 0;) {
+        if (worst[t] <= eps)
+            n++;
+        else
+            break;
+    }
+    return n;
+}
+
+// Triple-float accumulator of the CRT pass (recon_crt.cpp kernel_main with recon_crt_proc.h).
+struct CrtAcc {
+    float hi = 0, mid = 0, lo = 0;
+    // tfAddS<3> (sfpu_tf_proc.h:184-198)
+    void add(float v) {
+        float s0, e0;
+        {
+            const float t0 = f_add(hi, v);
+            float t1 = f_sub(t0, hi);
+            float t2 = f_sub(t0, t1);
+            t2 = f_sub(hi, t2);
+            t1 = f_sub(v, t1);
+            e0 = f_add(t2, t1);
+            s0 = t0;
+        }
+        hi = s0;
+        const float t0 = f_add(mid, e0);
+        float t2 = f_sub(t0, mid);
+        float tm = f_sub(t0, t2);
+        tm = f_sub(mid, tm);
+        t2 = f_sub(e0, t2);
+        t2 = f_add(tm, t2);
+        mid = t0;
+        lo = f_add(lo, t2);
+    }
+    // tfAddSmall<3> (sfpu_tf_proc.h:237-258)
+    void add_small(float v) {
+        const float t0 = f_add(mid, v);
+        float t2 = f_sub(t0, mid);
+        float t1 = f_sub(t0, t2);
+        t1 = f_sub(mid, t1);
+        t2 = f_sub(v, t2);
+        t2 = f_add(t1, t2);
+        mid = t0;
+        lo = f_add(lo, t2);
+    }
+    // drop_integer (recon_crt_proc.h:56-60)
+    void drop_integer() { hi = f_sub(hi, f_rnd(hi)); }
+};
+
+// decode_signmag_residue (recon_crt.cpp:219-249) on the value of C_i.
+float decode_residue(int32_t C, float m, float rinv, float m16) {
+    const uint32_t mag = C < 0 ? (uint32_t)(-(int64_t)C) : (uint32_t)C;
+    const float sgn = C > 0 ? 1.0f : (C < 0 ? -1.0f : 0.0f);
+    float chi = f_mul((float)(int32_t)(mag & 0x7FFF0000u), 1.52587890625e-05f);
+    float keep = mod_round(chi, m, rinv);
+    keep = f_mul(keep, m16);
+    float t = mod_round((float)(int32_t)(mag & 0xFFFFu), m, rinv);
+    t = f_add(t, keep);
+    t = f_mul(t, sgn);
+    return mod_round(t, m, rinv);
+}
+
+// One pass of the reference CRT for one element: three limbs of frac.
+void crt_pass(const int32_t* C, size_t stride, size_t idx, const orc_crt_consts& k, const float* rp, int nrp,
+              uint32_t nsmall, float* limbs) {
+    CrtAcc acc;
+    for (int i = 0; i < k.S; i++) {
+        const float m = (float)k.m[i], rinv = k.rinv[i];
+        const float r = decode_residue(C[(size_t)i * stride + idx], m, rinv, k.m16[i]);
+        const float kk = mod_round(f_mul(r, (float)k.yi[i]), m, rinv);
+        for (int t = 0; t < nrp; t++) {
+            const float term = f_mul(kk, rp[i * nrp + t]);
+            if ((uint32_t)t >= (uint32_t)nrp - nsmall)
+                acc.add_small(term);
+            else
+                acc.add(term);
+        }
+        acc.drop_integer();
+    }
+    limbs[0] = acc.hi;
+    limbs[1] = acc.mid;
+    limbs[2] = acc.lo;
+}
+
+// ---------------------------------------------------------------------------------------------
+// 256-bit unsigned integers for the exact CRT
+// ---------------------------------------------------------------------------------------------
+struct U256 {
+    uint64_t w[4] = {0, 0, 0, 0};
+};
+void u256_mul_small(U256& x, uint64_t k) {
+    unsigned __int128 carry = 0;
+    for (int i = 0; i < 4; i++) {
+        const unsigned __int128 p = (unsigned __int128)x.w[i] * k + carry;
+        x.w[i] = (uint64_t)p;
+        carry = p >> 64;
+    }
+}
+void u256_add(U256& x, const U256& y) {
+    unsigned __int128 c = 0;
+    for (int i = 0; i < 4; i++) {
+        const unsigned __int128 s = (unsigned __int128)x.w[i] + y.w[i] + c;
+        x.w[i] = (uint64_t)s;
+        c = s >> 64;
+    }
+}
+void u256_sub(U256& x, const U256& y) {
+    uint64_t borrow = 0;
+    for (int i = 0; i < 4; i++) {
+        const unsigned __int128 d = (unsigned __int128)x.w[i] - y.w[i] - borrow;
+        x.w[i] = (uint64_t)d;
+        borrow = (uint64_t)(d >> 64) ? 1 : 0;
+    }
+}
+int u256_cmp(const U256& x, const U256& y) {
+    for (int i = 3; i >= 0; i--)
+        if (x.w[i] != y.w[i]) return x.w[i] < y.w[i] ? -1 : 1;
+    return 0;
+}
+// x / small (exact division assumed or floor)
+U256 u256_div_small(const U256& x, uint64_t d) {
+    U256 q;
+    unsigned __int128 r = 0;
+    for (int i = 3; i >= 0; i--) {
+        const unsigned __int128 cur = (r << 64) | x.w[i];
+        q.w[i] = (uint64_t)(cur / d);
+        r = cur % d;
+    }
+    return q;
+}
+
+// Signed 256-bit two's complement value times 2^e, rounded to FP64 nearest-even; below the
+// normal range -> signed zero.
+double u256_to_double(U256 v, int e) {
+    const bool neg = (v.w[3] >> 63) != 0;
+    if (neg) {
+        for (int i = 0; i < 4; i++) v.w[i] = ~v.w[i];
+        U256 one;
+        one.w[0] = 1;
+        u256_add(v, one);
+    }
+    int top = -1;
+    for (int i = 3; i >= 0; i--)
+        if (v.w[i]) {
+            top = 64 * i + 63 - __builtin_clzll(v.w[i]);
+            break;
+        }
+    if (top < 0) return neg ? -0.0 : 0.0;
+    // value = v * 2^e; leading bit at position top -> exponent top + e
+    auto bit = [&](int p) -> uint64_t { return p < 0 ? 0 : (v.w[p >> 6] >> (p & 63)) & 1ull; };
+    uint64_t mant = 0;
+    for (int p = top; p > top - 53; p--) mant = (mant << 1) | bit(p);
+    const int lowest = top - 52;  // position of the last kept bit
+    bool guard = lowest - 1 >= 0 ? bit(lowest - 1) : false;
+    bool sticky = false;
+    for (int p = lowest - 2; p >= 0; p--)
+        if (bit(p)) {
+            sticky = true;
+            break;
+        }
+    int exp2 = top + e;  // value = mant * 2^(exp2 - 52)
+    if (guard && (sticky || (mant & 1))) {
+        mant += 1;
+        if (mant >> 53) {
+            mant >>= 1;
+            exp2 += 1;
+        }
+    }
+    if (exp2 < -1022) return neg ? -0.0 : 0.0;
+    if (exp2 > 1023) return neg ? -HUGE_VAL : HUGE_VAL;
+    const double r = std::ldexp((double)mant, exp2 - 52);
+    return neg ? -r : r;
+}
+
+// Exact CRT of one element: C' = sum_i k_i (M/m_i) mod M with k_i = (r_i y_i) mod m_i, returned as
+// the symmetric representative in (-M/2, M/2] (two's complement).
+struct ExactCrt {
+    int S;
+    long m[24], y[24];
+    U256 Mv, Q[24];
+    ExactCrt(int S_, const int* mm) : S(S_) {
+        Mv.w[0] = 1;
+        for (int i = 0; i < S; i++) {
+            m[i] = mm[i];
+            u256_mul_small(Mv, (uint64_t)mm[i]);
+        }
+        for (int i = 0; i < S; i++) {
+            Q[i] = u256_div_small(Mv, (uint64_t)m[i]);
+            long P = 1;
+            for (int j = 0; j < S; j++)
+                if (j != i) P = (P * (m[j] % m[i])) % m[i];
+            y[i] = 0;
+            for (long t = 1; t < m[i]; t++)
+                if ((P * t) % m[i] == 1) {
+                    y[i] = t;
+                    break;
+                }
+        }
+    }
+    U256 value(const int32_t* r) const {
+        U256 acc;
+        for (int i = 0; i < S; i++) {
+            const long ri = ((long)r[i] % m[i] + m[i]) % m[i];
+            U256 t = Q[i];
+            u256_mul_small(t, (uint64_t)((ri * y[i]) % m[i]));
+            u256_add(acc, t);
+            while (u256_cmp(acc, Mv) >= 0) u256_sub(acc, Mv);
+        }
+        U256 twice = acc;
+        u256_add(twice, acc);
+        if (u256_cmp(twice, Mv) > 0) {
+            U256 mma = Mv;
+            u256_sub(mma, acc);
+            U256 neg;
+            u256_sub(neg, mma);
+            acc = neg;
+        }
+        return acc;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+uint64_t orc_hash_f64(const double* c, size_t n) {
+    uint64_t h = 1469598103934665603ull;
+    for (size_t z = 0; z < n; z++) {
+        uint64_t u;
+        std::memcpy(&u, &c[z], 8);
+        for (int b = 0; b < 64; b += 8) {
+            h ^= (u >> b) & 0xFFu;
+            h *= 1099511628211ull;
+        }
+    }
+    return h;
+}
+
+void orc_inputs(unsigned seed, double phi, size_t na, size_t nb, double* a, double* b) {
+    std::mt19937 rng(seed);
+    if (phi < 0) {
+        std::uniform_real_distribution<double> u(-1, 1);
+        for (size_t i = 0; i < na; i++) a[i] = u(rng);
+        for (size_t i = 0; i < nb; i++) b[i] = u(rng);
+        return;
+    }
+    std::uniform_real_distribution<double> u(0, 1);
+    std::normal_distribution<double> normal(0, 1);
+    auto value = [&] {
+        const double v = u(rng);
+        const double z = normal(rng);
+        return (v - 0.5) * std::exp(phi * z);
+    };
+    for (size_t i = 0; i < na; i++) a[i] = value();
+    for (size_t i = 0; i < nb; i++) b[i] = value();
+}
+
+void orc_scale(const double* X, int rows, int cols, int ld, int mode, int ceil_mode, int shift, int32_t* delta,
+               uint32_t* flags) {
+    const int nout = mode == 0 ? rows : cols;
+    uint32_t bad = 0;
+    for (int o = 0; o < nout; o++) {
+        uint64_t mx = 0;  // max of the magnitude bit patterns (sign cleared)
+        const int n = mode == 0 ? cols : rows;
+        for (int t = 0; t < n; t++) {
+            const double x = mode == 0 ? X[(size_t)o * ld + t] : X[(size_t)t * ld + o];
+            uint64_t u;
+            std::memcpy(&u, &x, 8);
+            u &= 0x7FFFFFFFFFFFFFFFull;
+            mx = std::max(mx, u);
+        }
+        const uint32_t h = (uint32_t)(mx >> 32), l = (uint32_t)mx;
+        // oz_absf64_to_bf16<CEIL> (scale_bits.h:34-45)
+        uint16_t v16;
+        const int32_t E = (int32_t)((h >> 20) & 0x7FFu);
+        if (E == 0x7FF)
+            v16 = 0xFFC0u;
+        else {
+            const int32_t e8 = E - 896;
+            if (e8 <= 0)
+                v16 = (h | l) ? 0xFF80u : 0u;
+            else if (e8 >= 255)
+                v16 = 0x7F80u;
+            else {
+                uint32_t v = ((uint32_t)e8 << 7) | ((h >> 13) & 0x7Fu);
+                if (ceil_mode == 1 && ((h & 0x1FFFu) || l)) v += 1u;
+                if (ceil_mode == 2 && ((h & 0x1FFFu) || l || !(v & 0x7Fu))) v += 1u;
+                v16 = (uint16_t)v;
+            }
+        }
+        // oz_bf16_scale_exp (scale_bits.h:56-62)
+        const uint32_t BE = (v16 >> 7) & 0xFFu, bm = v16 & 0x7Fu;
+        int32_t e;
+        if (BE == 0u)
+            e = 0;
+        else if (BE == 0xFFu) {
+            e = 0;
+            bad |= !(v16 & 0x8000u) ? 1u : bm ? 4u : 2u;
+        } else
+            e = (int32_t)BE - 127 + (bm ? 1 : 0);
+        delta[o] = shift - e;
+    }
+    *flags |= bad;
+}
+
+void orc_split_f64(uint32_t w1, uint32_t w0, int32_t d, uint32_t* out4) {
+    split_words(w1, w0, d, out4[0], out4[1], out4[2], out4[3]);
+}
+
+void orc_load_triple(double x, int32_t d, float* out3) { load_triple(x, d, out3[0], out3[1], out3[2]); }
+
+void orc_oz2_digits(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd,
+                    float* digits) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < cols; c++)
+            make_digits(X[(size_t)r * ld + c], delta_of(delta, mode, r, c), nd, digits + ((size_t)r * cols + c) * nd);
+}
+
+void orc_oz2_residues(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
+                      const int* m, int8_t* planes) {
+    std::vector<float> rinv(S), cw((size_t)S * 4);
+    for (int s = 0; s < S; s++) {
+        const __float128 q = (__float128)1 / (__float128)m[s];
+        rinv[s] = (float)(double)q;
+        for (int j = 0; j < 4; j++) cw[(size_t)s * 4 + j] = pow2mod(20 * (j + 1), m[s]);
+    }
+    const size_t plane = (size_t)rows * cols;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        float dig[5];
+        for (int c = 0; c < cols; c++) {
+            make_digits(X[(size_t)r * ld + c], delta_of(delta, mode, r, c), nd, dig);
+            for (int s = 0; s < S; s++) {
+                const float v = residue(dig, nd, (float)m[s], rinv[s], &cw[(size_t)s * 4]);
+                planes[(size_t)s * plane + (size_t)r * cols + c] = (int8_t)(int)v;
+            }
+        }
+    }
+}
+
+float orc_modround(float d, float m, float rinv) { return mod_round(d, m, rinv); }
+
+int64_t orc_gemm_i8(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K) {
+    int64_t mx = 0;
+#pragma omp parallel for schedule(static) reduction(max : mx)
+    for (int i = 0; i < M; i++) {
+        std::vector<int64_t> acc(N, 0);
+        for (int k = 0; k < K; k++) {
+            const int64_t a = A[(size_t)i * K + k];
+            if (!a) continue;
+            const int8_t* b = B + (size_t)k * N;
+            for (int j = 0; j < N; j++) acc[j] += a * b[j];
+        }
+        for (int j = 0; j < N; j++) {
+            mx = std::max(mx, acc[j] < 0 ? -acc[j] : acc[j]);
+            C[(size_t)i * N + j] = (int32_t)acc[j];
+        }
+    }
+    return mx;
+}
+
+void orc_crt_constants(int S, const int* m, int b, orc_crt_consts* k) {
+    std::memset(k, 0, sizeof(*k));
+    k->S = S;
+    k->b = b;
+    for (int i = 0; i < S; i++) k->m[i] = m[i];
+    // y_i = (prod_{j != i} m_j)^-1 mod m_i (extended Euclid), moduli.hpp:619-625
+    for (int i = 0; i < S; i++) {
+        long P = 1, mi = m[i];
+        for (int j = 0; j < S; j++)
+            if (j != i) P = (P * (m[j] % mi)) % mi;
+        long t = 0, nt = 1, r = mi, nr = P % mi;
+        while (nr != 0) {
+            const long q = r / nr;
+            long tmp = t - q * nt;
+            t = nt;
+            nt = tmp;
+            tmp = r - q * nr;
+            r = nr;
+            nr = tmp;
+        }
+        if (t < 0) t += mi;
+        k->yi[i] = (int)t;
+    }
+    // KM = M * 2^-2b in long double (moduli.hpp:628-631); W and qw by frexpl (bits.hpp:35-40)
+    long double Mld = 1.0L;
+    for (int i = 0; i < S; i++) Mld *= (long double)m[i];
+    const long double KMl = Mld * std::pow(2.0L, -2.0 * b);
+    k->KM = (double)KMl;
+    int e;
+    const long double f = frexpl(KMl, &e);
+    const unsigned long long W = (unsigned long long)ldexpl(f, 64);
+    k->Whi = (uint32_t)(W >> 32);
+    k->Wlo = (uint32_t)W;
+    k->qw = e - 64;
+    // 12-bit fragments of 1/m_i (moduli.hpp:654-686)
+    const float SPL = 4097.0f;
+    auto top12 = [&](__float128 v) {
+        const float p = (float)(double)v;
+        if (p == 0.0f) return 0.0f;
+        const float c = (float)((double)SPL * (double)p);
+        return (float)((double)c - (double)(float)((double)c - (double)p));
+    };
+    for (int i = 0; i < S; i++) {
+        const __float128 r = (__float128)1 / (__float128)m[i];
+        const __float128 gran = powq((__float128)2, -(__float128)64);
+        const __float128 Rg = roundq(r / gran) * gran;
+        __float128 v = Rg;
+        for (int t = 0; t < 5; ++t) {
+            k->rp1[i][t] = top12(v);
+            v -= (__float128)k->rp1[i][t];
+        }
+        const __float128 sum1 = Rg - v;
+        v = r - sum1;
+        for (int t = 0; t < 3; ++t) {
+            k->rp2[i][t] = (t + 1 < 3) ? top12(v) : (float)(double)v;
+            v -= (__float128)k->rp2[i][t];
+        }
+        v = r;
+        for (int t = 0; t < 5; ++t) {
+            k->rp0[i][t] = (t + 1 < 5) ? top12(v) : (float)(double)v;
+            v -= (__float128)k->rp0[i][t];
+        }
+        k->rinv[i] = (float)(double)r;
+        for (int j = 0; j < 4; j++) k->c[j][i] = pow2mod(20 * (j + 1), m[i]);
+        k->m16[i] = pow2mod(16, m[i]);
+    }
+    k->nsmall0 = choose_small_tail(&k->rp0[0][0], 5, k->m, (uint32_t)S);
+    k->nsmall1 = choose_small_tail(&k->rp1[0][0], 5, k->m, (uint32_t)S);
+    k->nsmall2 = choose_small_tail(&k->rp2[0][0], 3, k->m, (uint32_t)S);
+}
+
+void orc_oz2_crt_ref(const int32_t* C, int M, int N, int S, const int* m, int b, int nd, int two_pass,
+                     const int32_t* dA, const int32_t* dB, double* out) {
+    orc_crt_consts k;
+    orc_crt_constants(S, m, b, &k);
+    const int32_t shift = b - 20 * (nd - 1);
+    const int32_t sh2 = 2 * shift;
+    const size_t stride = (size_t)M * N;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            const size_t idx = (size_t)i * N + j;
+            const int32_t gg = sh2 - (dA[i] + dB[j]);
+            float limbs[3];
+            uint64_t u;
+            if (!two_pass) {
+                crt_pass(C, stride, idx, k, &k.rp0[0][0], 5, k.nsmall0, limbs);
+                A128 a{{0, 0, 0, 0}};
+                a128_add_limbs(a, limbs, 3);
+                u = a128_frac_to_f64(a, gg, k.Whi, k.Wlo, k.qw);
+            } else {
+                A128 a{{0, 0, 0, 0}};
+                crt_pass(C, stride, idx, k, &k.rp1[0][0], 5, k.nsmall1, limbs);
+                a128_add_limbs(a, limbs, 3);
+                crt_pass(C, stride, idx, k, &k.rp2[0][0], 3, k.nsmall2, limbs);
+                a128_add_limbs(a, limbs, 3);
+                u = a128_frac_to_f64(a, gg, k.Whi, k.Wlo, k.qw);
+            }
+            std::memcpy(&out[idx], &u, 8);
+        }
+    }
+}
+
+void orc_oz2_crt_exact_int(const int32_t* r, int S, const int* m, uint64_t* out4) {
+    ExactCrt x(S, m);
+    const U256 v = x.value(r);
+    for (int i = 0; i < 4; i++) out4[i] = v.w[i];
+}
+
+void orc_oz2_crt_exact(const int32_t* C, int M, int N, int S, const int* m, int b, int nd, const int32_t* dA,
+                       const int32_t* dB, double* out) {
+    const int32_t shift = b - 20 * (nd - 1);
+    const size_t stride = (size_t)M * N;
+    const ExactCrt x(S, m);
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++) {
+        int32_t r[24];
+        for (int j = 0; j < N; j++) {
+            const size_t idx = (size_t)i * N + j;
+            for (int s = 0; s < S; s++) r[s] = C[(size_t)s * stride + idx];
+            const U256 v = x.value(r);
+            const int g = 2 * shift - (dA[i] + dB[j]);  // eA + eB
+            out[idx] = u256_to_double(v, g - 2 * b);
+        }
+    }
+}
+
+void orc_gemm_quad_sample(const double* A, const double* B, int M, int N, int K, int nsample, const int* rows,
+                          const int* cols, double* out) {
+    (void)M;
+#pragma omp parallel for schedule(dynamic)
+    for (int t = 0; t < nsample; t++) {
+        __float128 s = 0;
+        const int i = rows[t], j = cols[t];
+        for (int k = 0; k < K; k++) s += (__float128)A[(size_t)i * K + k] * (__float128)B[(size_t)k * N + j];
+        out[t] = (double)s;
+    }
+}
+
+void orc_dot2_gemm(const double* A, const double* B, int M, int N, int K, int r0, int r1, double* Chi, double* Clo) {
+    (void)M;
+    const int IB = 8, JB = 512;
+    for (size_t z = (size_t)r0 * N; z < (size_t)r1 * N; z++) Chi[z] = Clo[z] = 0.0;
+#pragma omp parallel for schedule(static)
+    for (int ib = r0; ib < r1; ib += IB) {
+        const int i1 = std::min(ib + IB, r1);
+        for (int j0 = 0; j0 < N; j0 += JB) {
+            const int j1 = std::min(j0 + JB, N);
+            for (int k = 0; k < K; ++k) {
+                const double* Br = B + (size_t)k * N;
+                for (int i = ib; i < i1; ++i) {
+                    const double a = A[(size_t)i * K + k];
+                    double* chi = Chi + (size_t)i * N;
+                    double* clo = Clo + (size_t)i * N;
+                    for (int j = j0; j < j1; ++j) {
+                        const double bb = Br[j];
+                        const double p = a * bb, e = std::fma(a, bb, -p);
+                        const double c0 = chi[j];
+                        const double s = c0 + p, z = s - c0;
+                        clo[j] += (c0 - (s - z)) + (p - z) + e;
+                        chi[j] = s;
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // extern "C"
