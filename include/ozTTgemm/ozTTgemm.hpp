@@ -1,0 +1,105 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// ozTTgemm for AMD Instinct MI355X: FP64 matrix multiplication with the Ozaki schemes.
+//
+// Drop-in public interface of the reference library (reference include/ozTTgemm/ozTTgemm.hpp:21-123):
+// the same namespace, types, members and defaults, the same validation and exception contract.
+// Only the device changes: the low-precision products run on the CDNA4 matrix cores of one MI355X
+// through hand-written HIP kernels (include/oz_hip.h), and the splitting and reconstruction run on
+// the same GPU.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <span>
+#include <string>
+#include <vector>
+
+#define OZTTGEMM_VERSION_MAJOR 0
+#define OZTTGEMM_VERSION_MINOR 1
+#define OZTTGEMM_VERSION_PATCH 0
+
+namespace ozTTgemm {
+
+// Scheme I: slices and slice-pair products. Scheme II: residues modulo small coprime moduli and
+// the Chinese remainder theorem.
+enum class Scheme { I, II };
+
+// Format of the low-precision matrix products. The enumerators are those of the reference; a
+// format that this build does not implement reports is_available() == false and is rejected.
+enum class Format { BF16, FP16, TF32, BFP8, FP8, INT8, BFP4, BFP2 };
+
+// Scheme II reconstruction passes. Automatic: one pass when an error estimate from the input
+// statistics allows it, two otherwise.
+enum class Reconstruction { Automatic, OnePass, TwoPass };
+
+// Options of the scheme that is not selected must keep their defaults.
+struct Options {
+    Scheme scheme = Scheme::II;
+    Format format = Format::BFP8;
+    // Scheme I only: 0 chooses the number of slices from the input, 1..256 fixes it.
+    std::uint32_t slices = 0;
+    // Scheme II only: 0 leaves the number of moduli to the library, 1..24 limits it.
+    std::uint32_t max_moduli = 0;
+    // Scheme II only.
+    Reconstruction reconstruction = Reconstruction::Automatic;
+};
+
+struct DeviceOptions {
+    // HIP device ordinal.
+    int device_id = 0;
+    // Kept for interface compatibility: the HIP code objects are built into the library, so no
+    // kernel directory is needed. A non-empty value must name an existing directory.
+    std::string kernel_directory;
+};
+
+// What a call used.
+struct Info {
+    Scheme scheme;
+    Format format;
+    std::uint32_t slices = 0;                 // scheme I: slices
+    std::uint32_t moduli = 0;                 // scheme II: CRT moduli
+    std::uint32_t integer_bits = 0;           // scheme II: width b of the scaled operands
+    std::uint32_t reconstruction_passes = 0;  // scheme II: 1 or 2 (as planned)
+    // Dimensions after zero padding (m and n to multiples of 64, k to a multiple of 32).
+    std::size_t padded_m = 0, padded_n = 0, padded_k = 0;
+};
+
+// False for formats this build does not implement.
+bool is_available(Format format) noexcept;
+// "BF16", "FP16", "TF32", "BFP8", "FP8", "INT8", "BFP4" or "BFP2".
+const char* format_name(Format format) noexcept;
+
+// Owns one GPU, opened lazily by the first valid GEMM. Calls through all contexts of a process are
+// serialized.
+class Context {
+public:
+    // Throws std::invalid_argument for a negative device_id or a kernel_directory that does not exist.
+    explicit Context(DeviceOptions options = {});
+    ~Context();
+    Context(const Context&) = delete;
+    Context& operator=(const Context&) = delete;
+    Context(Context&&) = delete;
+    Context& operator=(Context&&) = delete;
+
+    // C = A*B for contiguous row-major FP64 matrices A[m,k], B[k,n], C[m,n]. Dimensions must be
+    // positive and the spans must hold exactly m*k, k*n and m*n elements. Inputs are consumed before
+    // C is written, so they may overlap C. Inputs must be finite and every nonzero row maximum of A
+    // and column maximum of B must lie in [2^-126, largest finite BF16].
+    // Throws std::invalid_argument for invalid input (before the device is used and before C is
+    // written), std::runtime_error for configurations that cannot be executed and for failures of
+    // the HIP runtime, and std::bad_alloc if host memory runs out. Never prints, never terminates.
+    Info gemm(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m, std::size_t n,
+              std::size_t k, const Options& options = {});
+
+    // Same as gemm(), returning C as a new vector.
+    std::vector<double> multiply(std::span<const double> a, std::span<const double> b, std::size_t m, std::size_t n,
+                                 std::size_t k, const Options& options = {});
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+}  // namespace ozTTgemm

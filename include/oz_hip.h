@@ -1,0 +1,120 @@
+/* oz_hip.h — C ABI of the MI355X (gfx950) device layer of ozTTgemm.
+ *
+ * The C++20 backends (oztt_amd/csrc/host/) call the device only through these functions; they
+ * replace the TT-Metalium program builders and enqueues of the reference (src/backend/ozaki{1,2}/stages.hpp,
+ * src/backend/common/scale.hpp, the EnqueueMeshWorkload calls of src/ozaki2.cpp). Each entry point
+ * cites the reference stage whose semantics it implements.
+ *
+ * Conventions
+ *   - Every function returns 0 (OZ_OK) on success or a negative oz_status; none throws. The message
+ *     of the last failure of a device handle is oz_last_error().
+ *   - All launches are ordered on the handle's own HIP stream (default priority); device pointers
+ *     are plain addresses from oz_dev_malloc (or any HIP allocation on the same device).
+ *   - Matrices are row-major. "Planes" are the per-modulus (Scheme II) or per-slice (Scheme I)
+ *     integer matrices; their layout is given with each function.
+ *   - Sizes are checked against what the kernels assume before anything is launched; a mismatch
+ *     returns OZ_ERR_ARG and launches nothing.
+ */
+#ifndef OZ_HIP_H
+#define OZ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum oz_status {
+    OZ_OK = 0,
+    OZ_ERR_ARG = -1,     /* invalid argument or shape the kernels do not support */
+    OZ_ERR_HIP = -2,     /* HIP runtime failure */
+    OZ_ERR_NOMEM = -3,   /* device allocation failed */
+    OZ_ERR_RANGE = -4    /* a value outside the exact range of a stage */
+};
+
+/* Largest number of moduli (reference digit_limits.h:19, OZ2_MAXS). */
+#define OZ2_MAXS 24
+
+typedef struct oz_dev oz_dev;
+
+/* ---- device handle (replaces MeshDevice::create_unit_mesh, context.cpp:155) ---------------- */
+int oz_dev_open(int device_id, oz_dev** out);
+void oz_dev_close(oz_dev* dev);
+const char* oz_last_error(const oz_dev* dev);
+int oz_device_count(int* count);
+int oz_dev_malloc(oz_dev* dev, size_t bytes, void** ptr);
+int oz_dev_free(oz_dev* dev, void* ptr);
+int oz_memcpy_h2d(oz_dev* dev, void* dst, const void* src, size_t bytes);
+int oz_memcpy_d2h(oz_dev* dev, void* dst, const void* src, size_t bytes);
+int oz_fill_u32(oz_dev* dev, void* dst, uint32_t value, size_t count);
+int oz_sync(oz_dev* dev);
+/* Stream-ordered timing (64 event slots per handle). */
+int oz_event_record(oz_dev* dev, int slot);
+int oz_event_elapsed_ms(oz_dev* dev, int slot_begin, int slot_end, float* ms);
+
+/* ---- A5: normalization (reference scale_f64_reader.cpp:129, expdelta.cpp:44, scale_bits.h) --
+ * Largest |x| of every row (mode 0, `rows` outputs) or column (mode 1, `cols` outputs) of X
+ * (rows x cols, leading dimension ld), compared on the FP64 bit patterns; converted to BF16
+ * rounding down (ceil_mode 0), up (1), or up and one more step at a power of two (2);
+ * e = ceil(log2(bf16)) (0 for a zero row/column); delta = shift - e.
+ * Out-of-range maxima OR bits into *flags (device word): 1 above the largest BF16, 2 nonzero and
+ * below 2^-126, 4 Inf/NaN; their delta uses e = 0. */
+int oz_scale_f64(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, int ceil_mode, int shift,
+                 int32_t* delta, uint32_t* flags);
+
+/* ---- A6-A8: Scheme II residues (reference modslice_int8.cpp:60, digits.h:80,165, f64_tf.h:141) -
+ * For every element x of X (rows x cols, ld) with exponent delta d (delta[row] for mode 0,
+ * delta[col] for mode 1): the triple-float of x*2^d, its nd radix-2^20 digits (nd = 3..5), and
+ * for each modulus s the residue r_s == A' (mod m_s), |r_s| <= 127, as int8 (two's complement).
+ * Output planes[s] has `prow` rows of `pld` bytes:
+ *   layout 0 ("row"):  planes[s][r][c] for r < rows, c < cols   (A operand: K contiguous)
+ *   layout 1 ("tran"): planes[s][c][r] for c < cols, r < rows   (B operand: K contiguous)
+ * Entries of the padded region (row index >= rows/cols, byte index >= cols/rows) are written 0.
+ * plane_stride is the byte distance between planes. */
+typedef struct oz2_moduli_dev {
+    int S;                 /* number of moduli, 1..OZ2_MAXS */
+    int nd;                /* radix-2^20 digits of A', 3..5 */
+    float m[OZ2_MAXS];     /* moduli (exact in FP32) */
+    float rinv[OZ2_MAXS];  /* FP32 nearest to 1/m (moduli.hpp:686) */
+    float c[4][OZ2_MAXS];  /* 2^(20(j+1)) mod m, j = 0..3 (moduli.hpp:694-699) */
+} oz2_moduli_dev;
+int oz2_split_int8(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
+                   const oz2_moduli_dev* mo, int8_t* planes, int layout, int prow, int pld, long long plane_stride);
+/* White-box view of A7: the nd digits (top first) of every element as FP32, digits[(r*cols+c)*nd+j]. */
+int oz2_digits_f32(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
+                   int nd, float* digits);
+
+/* ---- A9: exact integer products (reference bmm_int32_spill.cpp:265, ozaki2.cpp:333) ---------
+ * C[b] = A[b] * B[b]^T for b < batch: A[b] is M x K int8 (row stride lda bytes), Bt[b] is N x K
+ * int8 (row stride ldb bytes; i.e. B stored K-contiguous), C[b] is M x N int32 (row stride ldc).
+ * Exact: |C| <= K*127^2 must fit int32 (the planner guarantees it, moduli.hpp:217-231).
+ * Requirements: M % 256 == 0, N % 256 == 0, K % 128 == 0 (the planes are zero-padded to these),
+ * lda, ldb multiples of 16. */
+int oz_gemm_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K, int batch, int lda,
+               int ldb, int ldc, long long strideA, long long strideB, long long strideC);
+
+/* ---- A10-A11: CRT reconstruction to FP64 (reference recon_crt.cpp:293, recon_writer.cpp:70) --
+ * For each element (i < M, j < N): C' = the integer in (-Mprod/2, Mprod/2] congruent to C_s
+ * modulo m_s for every s (C_s read from C + s*strideC, row stride ldc), then
+ * out[i*ldo+j] = C' * 2^(eA_i + eB_j - 2b) rounded to nearest-even, where eA_i = shift - dA[i],
+ * eB_j = shift - dB[j]; results below 2^-1022 become signed zero (f64_tf.h:45-47).
+ * The reconstruction is exact, so it serves both of the reference's one- and two-pass modes. */
+typedef struct oz2_crt_dev {
+    int S;
+    int b;                          /* integer width */
+    int shift;                      /* b - 20*(nd-1) */
+    int nw;                         /* 32-bit words of the accumulator (host: bits of S*Mprod) */
+    uint32_t m[OZ2_MAXS];
+    uint32_t y[OZ2_MAXS];           /* (Mprod/m_s)^-1 mod m_s */
+    uint32_t Q[OZ2_MAXS][8];        /* Mprod/m_s, little-endian 32-bit words */
+    uint32_t Mw[8];                 /* Mprod */
+    double Mtop;                    /* Mprod as FP64 (quotient estimate) */
+} oz2_crt_dev;
+int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long strideC, const oz2_crt_dev* crt,
+                const int32_t* dA, const int32_t* dB, double* out, int ldo);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OZ_HIP_H */

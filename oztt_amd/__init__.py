@@ -1,0 +1,249 @@
+"""oztt_amd — ozTTgemm for AMD Instinct MI355X (gfx950).
+
+Python mirror of the reference's public C++ interface (reference include/ozTTgemm/ozTTgemm.hpp:21-123):
+the same enums, Options, Info and Context.gemm/multiply, with the same validation and error
+behaviour (ValueError for std::invalid_argument, RuntimeError for std::runtime_error, MemoryError
+for std::bad_alloc). The computation runs in the native libraries built in oztt_amd/lib/:
+
+  libozTTgemm.so  C++20 host library (planning, dispatch, drivers) — the drop-in C++ API
+  liboz_hip.so    HIP kernels for gfx950 behind the C ABI of include/oz_hip.h
+
+There is no CPU fallback: without the built libraries every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+LIB_DIR = Path(__file__).resolve().parent / "lib"
+
+__all__ = ["Scheme", "Format", "Reconstruction", "Options", "Info", "Context", "is_available", "format_name",
+           "hip", "host", "LIB_DIR"]
+
+
+class Scheme(enum.IntEnum):
+    I = 0
+    II = 1
+
+
+class Format(enum.IntEnum):
+    BF16 = 0
+    FP16 = 1
+    TF32 = 2
+    BFP8 = 3
+    FP8 = 4
+    INT8 = 5
+    BFP4 = 6
+    BFP2 = 7
+
+
+class Reconstruction(enum.IntEnum):
+    Automatic = 0
+    OnePass = 1
+    TwoPass = 2
+
+
+@dataclass
+class Options:
+    scheme: Scheme = Scheme.II
+    format: Format = Format.BFP8
+    slices: int = 0
+    max_moduli: int = 0
+    reconstruction: Reconstruction = Reconstruction.Automatic
+
+
+@dataclass
+class Info:
+    scheme: Scheme
+    format: Format
+    slices: int
+    moduli: int
+    integer_bits: int
+    reconstruction_passes: int
+    padded_m: int
+    padded_n: int
+    padded_k: int
+
+
+class _Info(ctypes.Structure):
+    _fields_ = [("scheme", ctypes.c_int), ("format", ctypes.c_int), ("slices", ctypes.c_uint),
+                ("moduli", ctypes.c_uint), ("integer_bits", ctypes.c_uint),
+                ("reconstruction_passes", ctypes.c_uint), ("padded_m", ctypes.c_ulonglong),
+                ("padded_n", ctypes.c_ulonglong), ("padded_k", ctypes.c_ulonglong)]
+
+
+class EvalStats(ctypes.Structure):
+    _fields_ = [("fixed_bits", ctypes.c_uint), ("warmup", ctypes.c_int), ("repeats", ctypes.c_int),
+                ("phase_ms", ctypes.c_double * 5), ("whole_ms", ctypes.c_double), ("whole_checked", ctypes.c_int),
+                ("partial_products", ctypes.c_uint), ("product_ops", ctypes.c_double),
+                ("gemm_launch_ms", ctypes.c_double), ("gemm_launches", ctypes.c_int)]
+
+
+class Plan2(ctypes.Structure):
+    _fields_ = [("ok", ctypes.c_int), ("b", ctypes.c_int), ("S", ctypes.c_int), ("nd", ctypes.c_int),
+                ("two_pass", ctypes.c_int), ("m_cap", ctypes.c_int), ("m", ctypes.c_int * 24),
+                ("log2M", ctypes.c_double), ("recon1_log2", ctypes.c_double), ("TA", ctypes.c_double),
+                ("TB", ctypes.c_double), ("nA", ctypes.c_double), ("nB", ctypes.c_double), ("nC", ctypes.c_double),
+                ("wA", ctypes.c_double), ("wB", ctypes.c_double), ("b_cap", ctypes.c_int)]
+
+
+_host = None
+_hip = None
+
+
+def _load(name: str) -> ctypes.CDLL:
+    path = LIB_DIR / name
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: build the native libraries first (python __graft_entry__.py build "
+                           f"or python -c 'import __graft_entry__ as g; g.build()')")
+    return ctypes.CDLL(str(path), mode=ctypes.RTLD_GLOBAL)
+
+
+def hip() -> ctypes.CDLL:
+    """The C ABI of include/oz_hip.h (liboz_hip.so)."""
+    global _hip
+    if _hip is None:
+        _hip = _load("liboz_hip.so")
+        _hip.oz_last_error.restype = ctypes.c_char_p
+    return _hip
+
+
+def host() -> ctypes.CDLL:
+    """The C entry points of libozTTgemm.so."""
+    global _host
+    if _host is None:
+        hip()
+        h = _load("libozTTgemm.so")
+        h.ozt_format_name.restype = ctypes.c_char_p
+        h.ozt_eval_hash.restype = ctypes.c_ulonglong
+        _host = h
+    return _host
+
+
+def is_available(fmt: Format) -> bool:
+    return bool(host().ozt_is_available(int(fmt)))
+
+
+def format_name(fmt: Format) -> str:
+    return host().ozt_format_name(int(fmt)).decode()
+
+
+_ERRORS = {1: ValueError, 2: RuntimeError, 3: MemoryError, 4: RuntimeError}
+
+
+def _raise(code: int, err: ctypes.Array) -> None:
+    if code:
+        raise _ERRORS.get(code, RuntimeError)(err.value.decode(errors="replace"))
+
+
+def _f64(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float64).reshape(-1)
+
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Context:
+    """Owns one GPU (opened lazily by the first valid GEMM), like ozTTgemm::Context."""
+
+    def __init__(self, device_id: int = 0, kernel_directory: str = ""):
+        self._ctx = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(1024)
+        kd = kernel_directory.encode() if kernel_directory else None
+        _raise(host().ozt_context_new(int(device_id), kd, ctypes.byref(self._ctx), err, ctypes.c_size_t(1024)), err)
+
+    def close(self) -> None:
+        if self._ctx:
+            host().ozt_context_free(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _call(self, a, b, c, m, n, k, options: Options, evaluation: EvalStats | None = None) -> Info:
+        err = ctypes.create_string_buffer(4096)
+        info = _Info()
+        o = options
+        args = [self._ctx, _ptr(a), ctypes.c_size_t(a.size), _ptr(b), ctypes.c_size_t(b.size), _ptr(c),
+                ctypes.c_size_t(c.size), ctypes.c_size_t(m), ctypes.c_size_t(n), ctypes.c_size_t(k), int(o.scheme),
+                int(o.format), ctypes.c_uint(o.slices), ctypes.c_uint(o.max_moduli), int(o.reconstruction),
+                ctypes.byref(info)]
+        if evaluation is None:
+            code = host().ozt_gemm(*args, err, ctypes.c_size_t(4096))
+        else:
+            code = host().ozt_eval_gemm(*args, ctypes.byref(evaluation), err, ctypes.c_size_t(4096))
+        _raise(code, err)
+        return Info(Scheme(info.scheme), Format(info.format), info.slices, info.moduli, info.integer_bits,
+                    info.reconstruction_passes, info.padded_m, info.padded_n, info.padded_k)
+
+    def gemm(self, a, b, c: np.ndarray, m: int, n: int, k: int, options: Options | None = None) -> Info:
+        """C = A*B into the float64 array c (m*n elements, contiguous); returns Info."""
+        if not (isinstance(c, np.ndarray) and c.dtype == np.float64 and c.flags.c_contiguous):
+            raise ValueError("c must be a contiguous float64 numpy array")
+        return self._call(_f64(a), _f64(b), c.reshape(-1), m, n, k, options or Options())
+
+    def multiply(self, a, b, m: int, n: int, k: int, options: Options | None = None) -> np.ndarray:
+        a, b = _f64(a), _f64(b)
+        if a.size != m * k or b.size != k * n:
+            raise ValueError("matrix span sizes do not match m, n, k")
+        c = np.empty(m * n, dtype=np.float64)
+        self.gemm(a, b, c, m, n, k, options)
+        return c
+
+    def evaluate(self, a, b, m: int, n: int, k: int, options: Options, fixed_bits: int = 0, warmup: int = 0,
+                 repeats: int = 0):
+        """GEMM under the evaluation hooks: returns (C, Info, EvalStats) with phase and whole-pass times."""
+        a, b = _f64(a), _f64(b)
+        c = np.empty(m * n, dtype=np.float64)
+        ev = EvalStats()
+        ev.fixed_bits, ev.warmup, ev.repeats = fixed_bits, warmup, repeats
+        info = self._call(a, b, c, m, n, k, options, ev)
+        return c, info, ev
+
+
+def plan2_int8(a, b, M: int, N: int, K: int, max_moduli: int = 0,
+               reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0) -> Plan2:
+    """Scheme II INT8 planner on padded row-major A (M x K) and B (K x N)."""
+    a, b = _f64(a), _f64(b)
+    out = Plan2()
+    err = ctypes.create_string_buffer(2048)
+    _raise(host().ozt_plan2_int8(_ptr(a), _ptr(b), M, N, K, max_moduli, int(reconstruction), fixed_bits,
+                                 ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
+    return out
+
+
+def choose_moduli_int8(K: int, num_moduli: int, b_cap: int) -> Plan2:
+    out = Plan2()
+    host().ozt_choose_moduli_int8(K, num_moduli, b_cap, ctypes.byref(out))
+    return out
+
+
+def eval_inputs(seed: int, phi: float, na: int, nb: int):
+    """Evaluator inputs (reference evaluation/numerics.hpp:19-38 with a seed): A then B, float64."""
+    a = np.empty(na, dtype=np.float64)
+    b = np.empty(nb, dtype=np.float64)
+    host().ozt_eval_inputs(ctypes.c_uint(seed), ctypes.c_double(phi), ctypes.c_size_t(na), ctypes.c_size_t(nb),
+                           _ptr(a), _ptr(b))
+    return a, b
+
+
+def eval_hash(c) -> int:
+    c = _f64(c)
+    return int(host().ozt_eval_hash(_ptr(c), ctypes.c_size_t(c.size)))
+
+
+def eval_quad_sample(a, b, M: int, N: int, K: int, rows, cols) -> np.ndarray:
+    a, b = _f64(a), _f64(b)
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    cols = np.ascontiguousarray(cols, dtype=np.int32)
+    out = np.empty(rows.size, dtype=np.float64)
+    host().ozt_eval_quad_sample(_ptr(a), _ptr(b), M, N, K, int(rows.size), _ptr(rows), _ptr(cols), _ptr(out))
+    return out

@@ -1,0 +1,72 @@
+// Interface between the public Context (context.cpp) and the backends (one per scheme and format),
+// and the device handle shared by them. Mirrors the reference's backend_interface.hpp:14-35: a
+// backend receives the validated, zero-padded problem and returns the padded result.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include <ozTTgemm/ozTTgemm.hpp>
+
+#include "oz_hip.h"
+
+namespace ozTTgemm::detail {
+
+// Throws std::runtime_error with the device layer's message when a C-ABI call fails.
+void device_check(oz_dev* dev, int status, const char* what);
+
+// Device allocations of one GPU kept by the Context between calls, grown on demand (the reference
+// rebuilds its buffers per call, README.md:81-85; reusing them avoids hipMalloc in repeated calls).
+class Workspace {
+public:
+    explicit Workspace(oz_dev* dev) : dev_(dev) {}
+    ~Workspace();
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+    // Buffer of at least `bytes` for role `slot` (contents undefined).
+    void* get(int slot, std::size_t bytes);
+    void release_all();
+
+private:
+    struct Buf {
+        void* p = nullptr;
+        std::size_t size = 0;
+    };
+    oz_dev* dev_;
+    std::vector<Buf> bufs_;
+};
+
+// The opened GPU (the reference's Device, backend_interface.hpp:14).
+struct Device {
+    oz_dev* dev = nullptr;
+    std::unique_ptr<Workspace> ws;
+};
+
+// One GEMM after validation and zero padding: A is m x k and B is k x n, row-major, with m and n
+// multiples of 64 and k a multiple of 32 (backend_interface.hpp:21-26).
+struct Problem {
+    std::uint32_t m, n, k;
+    const std::vector<double>& a;
+    const std::vector<double>& b;
+    const Options& options;
+};
+
+struct Output {
+    std::vector<double> values;  // padded m x n, row-major
+    Info info;
+};
+
+using Backend = Output (*)(Device&, const Problem&);
+
+// Throws std::invalid_argument for a (format, scheme) pair that this build does not implement.
+Backend backend_for(Format format, Scheme scheme);
+bool scheme_available(Format format, Scheme scheme) noexcept;
+
+// Backends.
+Output ozaki2_int8_run(Device& dev, const Problem& p);
+
+}  // namespace ozTTgemm::detail

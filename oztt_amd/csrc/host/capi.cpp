@@ -1,0 +1,197 @@
+// C entry points of libozTTgemm.so for callers without C++ (the Python mirror in oztt_amd/, the
+// tests and bench.py): the public Context API, the evaluation hooks and utilities, and a view of
+// the Scheme II planner. Each function returns 0 on success or one of the OZT_E* codes, mapping the
+// C++ exception types of the public API, and copies the exception's message into err.
+#include <cstring>
+#include <new>
+#include <optional>
+#include <stdexcept>
+
+#include <ozTTgemm/ozTTgemm.hpp>
+
+#include "evaluation.hpp"
+#include "plan2.hpp"
+
+namespace {
+enum { OZT_OK = 0, OZT_EINVAL = 1, OZT_ERUNTIME = 2, OZT_ENOMEM = 3, OZT_EOTHER = 4 };
+
+void put(char* err, std::size_t len, const char* msg) {
+    if (err && len) {
+        std::strncpy(err, msg, len - 1);
+        err[len - 1] = 0;
+    }
+}
+
+template <class F>
+int guarded(char* err, std::size_t len, F&& f) {
+    try {
+        f();
+        return OZT_OK;
+    } catch (const std::invalid_argument& e) {
+        put(err, len, e.what());
+        return OZT_EINVAL;
+    } catch (const std::bad_alloc& e) {
+        put(err, len, e.what());
+        return OZT_ENOMEM;
+    } catch (const std::runtime_error& e) {
+        put(err, len, e.what());
+        return OZT_ERUNTIME;
+    } catch (const std::exception& e) {
+        put(err, len, e.what());
+        return OZT_EOTHER;
+    }
+}
+
+ozTTgemm::Options make_options(int scheme, int format, unsigned slices, unsigned max_moduli, int recon) {
+    ozTTgemm::Options o;
+    o.scheme = static_cast<ozTTgemm::Scheme>(scheme);
+    o.format = static_cast<ozTTgemm::Format>(format);
+    o.slices = slices;
+    o.max_moduli = max_moduli;
+    o.reconstruction = static_cast<ozTTgemm::Reconstruction>(recon);
+    return o;
+}
+}  // namespace
+
+extern "C" {
+
+struct ozt_info {
+    int scheme, format;
+    unsigned slices, moduli, integer_bits, reconstruction_passes;
+    unsigned long long padded_m, padded_n, padded_k;
+};
+
+struct ozt_eval {
+    unsigned fixed_bits;
+    int warmup, repeats;
+    double phase_ms[5];
+    double whole_ms;
+    int whole_checked;
+    unsigned partial_products;
+    double product_ops;
+    double gemm_launch_ms;
+    int gemm_launches;
+};
+
+struct ozt_plan2 {
+    int ok, b, S, nd, two_pass, m_cap;
+    int m[24];
+    double log2M, recon1_log2;
+    double TA, TB, nA, nB, nC, wA, wB;
+    int b_cap;
+};
+
+int ozt_context_new(int device_id, const char* kernel_dir, void** out, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        ozTTgemm::DeviceOptions d;
+        d.device_id = device_id;
+        if (kernel_dir) d.kernel_directory = kernel_dir;
+        *out = new ozTTgemm::Context(d);
+    });
+}
+
+void ozt_context_free(void* ctx) { delete static_cast<ozTTgemm::Context*>(ctx); }
+
+static void fill_info(const ozTTgemm::Info& i, ozt_info* o) {
+    if (!o) return;
+    o->scheme = (int)i.scheme;
+    o->format = (int)i.format;
+    o->slices = i.slices;
+    o->moduli = i.moduli;
+    o->integer_bits = i.integer_bits;
+    o->reconstruction_passes = i.reconstruction_passes;
+    o->padded_m = i.padded_m;
+    o->padded_n = i.padded_n;
+    o->padded_k = i.padded_k;
+}
+
+int ozt_gemm(void* ctx, const double* a, std::size_t na, const double* b, std::size_t nb, double* c, std::size_t nc,
+             std::size_t m, std::size_t n, std::size_t k, int scheme, int format, unsigned slices, unsigned max_moduli,
+             int recon, ozt_info* info, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        auto* cx = static_cast<ozTTgemm::Context*>(ctx);
+        const auto i = cx->gemm({a, na}, {b, nb}, {c, nc}, m, n, k, make_options(scheme, format, slices, max_moduli, recon));
+        fill_info(i, info);
+    });
+}
+
+int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, std::size_t nb, double* c,
+                  std::size_t nc, std::size_t m, std::size_t n, std::size_t k, int scheme, int format, unsigned slices,
+                  unsigned max_moduli, int recon, ozt_info* info, ozt_eval* evo, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        ozTTgemm::evaluation::Settings s;
+        s.fixed_bits = evo->fixed_bits;
+        s.warmup = evo->warmup;
+        s.repeats = evo->repeats;
+        auto* cx = static_cast<ozTTgemm::Context*>(ctx);
+        ozTTgemm::Info i;
+        {
+            ozTTgemm::evaluation::Scope scope(s);
+            i = cx->gemm({a, na}, {b, nb}, {c, nc}, m, n, k, make_options(scheme, format, slices, max_moduli, recon));
+        }
+        fill_info(i, info);
+        for (int p = 0; p < 5; p++) evo->phase_ms[p] = s.phase_ms[p];
+        evo->whole_ms = s.whole_ms;
+        evo->whole_checked = s.whole_checked ? 1 : 0;
+        evo->partial_products = s.partial_products;
+        evo->product_ops = s.product_ops;
+        evo->gemm_launch_ms = s.gemm_launch_ms;
+        evo->gemm_launches = s.gemm_launches;
+    });
+}
+
+int ozt_is_available(int format) { return ozTTgemm::is_available(static_cast<ozTTgemm::Format>(format)) ? 1 : 0; }
+const char* ozt_format_name(int format) { return ozTTgemm::format_name(static_cast<ozTTgemm::Format>(format)); }
+
+// Scheme II INT8 planner on padded row-major A (M x K) and B (K x N).
+int ozt_plan2_int8(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned max_moduli,
+                   int recon, unsigned fixed_b, ozt_plan2* out, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        std::optional<unsigned> fb;
+        if (fixed_b) fb = fixed_b;
+        const auto p = ozTTgemm::detail::plan_scheme2_int8(A, B, M, N, K, max_moduli,
+                                                             static_cast<ozTTgemm::Reconstruction>(recon), fb);
+        std::memset(out, 0, sizeof(*out));
+        out->ok = p.mo.ok;
+        out->b = p.b;
+        out->S = p.S;
+        out->nd = p.nd;
+        out->two_pass = p.two_pass;
+        out->m_cap = p.mo.m_cap;
+        for (int s = 0; s < p.S && s < 24; s++) out->m[s] = p.mo.m[s];
+        out->log2M = p.mo.log2M;
+        out->recon1_log2 = p.recon1_log2;
+        out->TA = p.stats.TA;
+        out->TB = p.stats.TB;
+        out->nA = p.stats.nA;
+        out->nB = p.stats.nB;
+        out->nC = p.stats.nC;
+        out->wA = p.stats.wA;
+        out->wB = p.stats.wB;
+        out->b_cap = p.stats.measured ? ozTTgemm::detail::precision_cap(p.stats) : 0;
+    });
+}
+
+// Moduli selection alone (no input statistics).
+int ozt_choose_moduli_int8(unsigned K, int num_moduli, int b_cap, ozt_plan2* out) {
+    const auto mo = ozTTgemm::detail::choose_moduli_int8(K, num_moduli, b_cap);
+    std::memset(out, 0, sizeof(*out));
+    out->ok = mo.ok;
+    out->b = mo.b;
+    out->S = (int)mo.m.size();
+    out->m_cap = mo.m_cap;
+    for (int s = 0; s < out->S && s < 24; s++) out->m[s] = mo.m[s];
+    out->log2M = mo.log2M;
+    return 0;
+}
+
+void ozt_eval_inputs(unsigned seed, double phi, std::size_t na, std::size_t nb, double* a, double* b) {
+    ozTTgemm::evaluation::inputs(seed, phi, na, nb, a, b);
+}
+unsigned long long ozt_eval_hash(const double* c, std::size_t n) { return ozTTgemm::evaluation::output_hash(c, n); }
+void ozt_eval_quad_sample(const double* A, const double* B, int M, int N, int K, int nsample, const int* rows,
+                          const int* cols, double* out) {
+    ozTTgemm::evaluation::gemm_quad_sample(A, B, M, N, K, nsample, rows, cols, out);
+}
+
+}  // extern "C"

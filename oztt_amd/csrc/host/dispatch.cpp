@@ -1,0 +1,73 @@
+// (format, scheme) -> backend, format names, availability; the device workspace. Semantics of the
+// reference's dispatch.cpp:18-51: formats that are not built report is_available() == false.
+#include <stdexcept>
+
+#include "backend.hpp"
+
+namespace ozTTgemm::detail {
+
+void device_check(oz_dev* dev, int status, const char* what) {
+    if (status == OZ_OK) return;
+    throw std::runtime_error(std::string(what) + ": " + oz_last_error(dev));
+}
+
+Workspace::~Workspace() { release_all(); }
+
+void* Workspace::get(int slot, std::size_t bytes) {
+    if (slot < 0) throw std::logic_error("workspace slot");
+    if ((std::size_t)slot >= bufs_.size()) bufs_.resize(slot + 1);
+    Buf& b = bufs_[slot];
+    bytes = (bytes + 255) & ~std::size_t(255);
+    if (b.size < bytes) {
+        if (b.p) device_check(dev_, oz_dev_free(dev_, b.p), "hipFree");
+        b.p = nullptr;
+        b.size = 0;
+        void* p = nullptr;
+        device_check(dev_, oz_dev_malloc(dev_, bytes, &p), "device allocation");
+        b.p = p;
+        b.size = bytes;
+    }
+    return bufs_[slot].p;
+}
+
+void Workspace::release_all() {
+    for (auto& b : bufs_)
+        if (b.p) (void)oz_dev_free(dev_, b.p);
+    bufs_.clear();
+}
+
+bool scheme_available(Format format, Scheme scheme) noexcept {
+    switch (format) {
+    case Format::INT8: return scheme == Scheme::II;
+    default: return false;
+    }
+}
+
+Backend backend_for(Format format, Scheme scheme) {
+    if (format == Format::INT8 && scheme == Scheme::II) return ozaki2_int8_run;
+    throw std::invalid_argument("requested format was not built");
+}
+
+}  // namespace ozTTgemm::detail
+
+namespace ozTTgemm {
+
+bool is_available(Format format) noexcept {
+    return detail::scheme_available(format, Scheme::I) || detail::scheme_available(format, Scheme::II);
+}
+
+const char* format_name(Format format) noexcept {
+    switch (format) {
+    case Format::BF16: return "BF16";
+    case Format::FP16: return "FP16";
+    case Format::TF32: return "TF32";
+    case Format::BFP8: return "BFP8";
+    case Format::FP8: return "FP8";
+    case Format::INT8: return "INT8";
+    case Format::BFP4: return "BFP4";
+    case Format::BFP2: return "BFP2";
+    default: return "unknown";
+    }
+}
+
+}  // namespace ozTTgemm

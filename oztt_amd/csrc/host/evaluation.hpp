@@ -1,0 +1,60 @@
+// Evaluation hooks: per-phase timing and whole-pass timing of one GEMM call, and the evaluation
+// utilities (input generator, output hash, binary128 reference) of the paper evaluator.
+//
+// Counterpart of the reference's evaluation_hooks.hpp:29-219 and evaluation/numerics.hpp. While a
+// Scope is active on the calling thread, a backend
+//   - times each phase (scale, slice, gemm, compose, recon) with HIP events on its stream,
+//   - records every device step of the call and afterwards replays the whole pass `warmup` times
+//     untimed and `repeats` times between two events (inputs and intermediates resident in HBM,
+//     no host work inside), checks that the replayed output is bit-identical to the first pass,
+//     and reports the average whole-pass time.
+// Without a Scope the hooks cost nothing. The library itself never activates one.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <vector>
+
+namespace ozTTgemm::evaluation {
+
+enum Phase { Scale = 0, Slice, Gemm, Compose, Recon, PhaseCount };
+
+struct Settings {
+    // inputs
+    unsigned fixed_bits = 0;  // Scheme II: width b fixed by the caller (0: chosen from the input)
+    int warmup = 0;           // untimed whole-pass replays
+    int repeats = 0;          // timed whole-pass replays (0: no replay)
+    // outputs
+    double phase_ms[PhaseCount] = {};  // device time of each phase in the first pass
+    double whole_ms = 0;               // average time of one replayed whole pass
+    bool whole_checked = false;        // replayed output bit-identical to the first pass
+    unsigned partial_products = 0;     // low-precision matrix products per call (S or slice pairs)
+    double product_ops = 0;            // algorithmic operations of the product phase (2*M*N*K*products)
+    double gemm_launch_ms = 0;         // average duration of one product-kernel launch in the replays
+    int gemm_launches = 0;             // product-kernel launches per pass
+};
+
+// Activates `s` for the calling thread until destruction (not nestable).
+class Scope {
+public:
+    explicit Scope(Settings& s);
+    ~Scope();
+    Scope(const Scope&) = delete;
+    Scope& operator=(const Scope&) = delete;
+};
+
+Settings* active() noexcept;
+
+// ---- evaluation utilities (reference evaluation/numerics.hpp) ---------------------------------
+// Inputs of the paper evaluator with a seed (numerics.hpp:19-38): mt19937(seed); phi < 0 gives
+// uniform [-1,1); otherwise x = (u - 0.5) * exp(phi * z), u ~ U(0,1) drawn before z ~ N(0,1); all
+// of A (na elements) first, then B.
+void inputs(unsigned seed, double phi, std::size_t na, std::size_t nb, double* a, double* b);
+// FNV-style hash of the bit patterns (numerics.hpp:46-57).
+std::uint64_t output_hash(const double* c, std::size_t n);
+// Binary128 products for sampled output elements (rows[t], cols[t]).
+void gemm_quad_sample(const double* A, const double* B, int M, int N, int K, int nsample, const int* rows,
+                      const int* cols, double* out);
+
+}  // namespace ozTTgemm::evaluation

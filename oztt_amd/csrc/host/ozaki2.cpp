@@ -1,0 +1,162 @@
+// Ozaki scheme II driver (INT8 residues): one FP64 GEMM on the GPU.
+//
+// Pipeline of the reference's ozaki2.cpp:439-478: plan (moduli, width b, passes) -> upload the FP64
+// operands -> scale (row/column maxima, exponent deltas) -> slice (int8 residue planes per
+// modulus) -> products (one exact int32 GEMM per modulus) -> CRT reconstruction to FP64 -> read
+// back and check the range flags. The reference splits the output into row bands when its 32 GB
+// of DRAM is short (plan.hpp:386-444); at the sizes one MI355X (288 GB) serves, every buffer is
+// resident at once, so there are no bands.
+//
+// Device layout (all row-major, zero-padded so that every kernel runs unguarded full tiles):
+//   A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2];
+//   residue planes of A: S x Mg x Kg int8 (K contiguous), of B: S x Ng x Kg int8 (K contiguous,
+//   i.e. B transposed) with Mg, Ng multiples of 256 and Kg of 128;
+//   products: S x Mg x Ng int32; output: M x N f64.
+#include <chrono>
+#include <cstring>
+#include <functional>
+#include <stdexcept>
+
+#include "backend.hpp"
+#include "evaluation.hpp"
+#include "plan2.hpp"
+
+namespace ozTTgemm::detail {
+namespace {
+
+namespace ev = ::ozTTgemm::evaluation;
+
+enum Slot { kA = 0, kB, kDA, kDB, kFlags, kPlanesA, kPlanesB, kProducts, kOut };
+
+std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / q * q; }
+
+// A recorded device step: its phase and the launches it issues (stream-ordered, no host sync).
+struct Step {
+    ev::Phase phase;
+    std::function<void()> issue;
+};
+
+}  // namespace
+
+Output ozaki2_int8_run(Device& D, const Problem& p) {
+    oz_dev* dev = D.dev;
+    ev::Settings* es = ev::active();
+    std::optional<unsigned> fixed_b;
+    if (es && es->fixed_bits) fixed_b = es->fixed_bits;
+    const Plan2 plan = plan_scheme2_int8(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.max_moduli,
+                                         p.options.reconstruction, fixed_b);
+    const std::uint32_t M = p.m, N = p.n, K = p.k, S = (std::uint32_t)plan.S;
+    const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 128);
+    const oz2_moduli_dev mdesc = split_descriptor(plan);
+    const oz2_crt_dev cdesc = crt_descriptor(plan);
+
+    Workspace& ws = *D.ws;
+    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
+    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
+    auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
+    auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
+    auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
+    const long long strideA = (long long)Mg * Kg, strideB = (long long)Ng * Kg, strideC = (long long)Mg * Ng;
+    auto* planesA = static_cast<std::int8_t*>(ws.get(kPlanesA, (std::size_t)S * strideA));
+    auto* planesB = static_cast<std::int8_t*>(ws.get(kPlanesB, (std::size_t)S * strideB));
+    auto* prod = static_cast<std::int32_t*>(ws.get(kProducts, sizeof(std::int32_t) * (std::size_t)S * strideC));
+    auto* out = static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
+
+    device_check(dev, oz_memcpy_h2d(dev, dAf, p.a.data(), sizeof(double) * p.a.size()), "upload A");
+    device_check(dev, oz_memcpy_h2d(dev, dBf, p.b.data(), sizeof(double) * p.b.size()), "upload B");
+
+    const int shift = plan.shift();
+    std::vector<Step> steps;
+    steps.push_back({ev::Scale, [=] {
+                         device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
+                         // Scheme II rounds the BF16 of the maxima up (ozaki2.cpp:143-146)
+                         device_check(dev, oz_scale_f64(dev, dAf, (int)M, (int)K, (int)K, 0, 1, shift, dltA, flags),
+                                      "scale A");
+                         device_check(dev, oz_scale_f64(dev, dBf, (int)K, (int)N, (int)N, 1, 1, shift, dltB, flags + 1),
+                                      "scale B");
+                     }});
+    steps.push_back({ev::Slice, [=] {
+                         device_check(dev,
+                                      oz2_split_int8(dev, dAf, (int)M, (int)K, (int)K, 0, dltA, &mdesc, planesA, 0,
+                                                     (int)Mg, (int)Kg, strideA),
+                                      "slice A");
+                         device_check(dev,
+                                      oz2_split_int8(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, &mdesc, planesB, 1,
+                                                     (int)Ng, (int)Kg, strideB),
+                                      "slice B");
+                     }});
+    steps.push_back({ev::Gemm, [=] {
+                         device_check(dev,
+                                      oz_gemm_i8(dev, planesA, planesB, prod, (int)Mg, (int)Ng, (int)Kg, (int)S,
+                                                 (int)Kg, (int)Kg, (int)Ng, strideA, strideB, strideC),
+                                      "products");
+                     }});
+    steps.push_back({ev::Recon, [=] {
+                         device_check(dev,
+                                      oz2_crt_f64(dev, prod, (int)M, (int)N, (int)Ng, strideC, &cdesc, dltA, dltB, out,
+                                                  (int)N),
+                                      "reconstruction");
+                     }});
+
+    if (!es) {
+        for (auto& s : steps) s.issue();
+    } else {
+        // first pass: phase times with events on the stream (slots 2*phase, 2*phase+1)
+        for (auto& s : steps) {
+            device_check(dev, oz_event_record(dev, 2 * s.phase), "event");
+            s.issue();
+            device_check(dev, oz_event_record(dev, 2 * s.phase + 1), "event");
+        }
+        for (int ph = 0; ph < ev::PhaseCount; ph++) es->phase_ms[ph] = 0;
+        for (auto& s : steps) {
+            float ms = 0;
+            device_check(dev, oz_event_elapsed_ms(dev, 2 * s.phase, 2 * s.phase + 1, &ms), "event time");
+            es->phase_ms[s.phase] += ms;
+        }
+        es->partial_products = S;
+        es->product_ops = 2.0 * M * (double)N * K * S;
+        es->gemm_launches = 1;
+    }
+    std::vector<double> values((std::size_t)M * N);
+    device_check(dev, oz_memcpy_d2h(dev, values.data(), out, sizeof(double) * values.size()), "read C");
+    std::uint32_t fl[2];
+    device_check(dev, oz_memcpy_d2h(dev, fl, flags, sizeof fl), "read flags");
+
+    if (es && es->repeats > 0) {
+        // whole pass: warm up, then `repeats` replays between two events; then the product kernel
+        // alone, for its average launch time
+        for (int w = 0; w < es->warmup; w++)
+            for (auto& s : steps) s.issue();
+        device_check(dev, oz_event_record(dev, 20), "event");
+        for (int r = 0; r < es->repeats; r++)
+            for (auto& s : steps) s.issue();
+        device_check(dev, oz_event_record(dev, 21), "event");
+        float ms = 0;
+        device_check(dev, oz_event_elapsed_ms(dev, 20, 21, &ms), "event time");
+        es->whole_ms = ms / es->repeats;
+        std::vector<double> again(values.size());
+        device_check(dev, oz_memcpy_d2h(dev, again.data(), out, sizeof(double) * again.size()), "read C");
+        es->whole_checked = std::memcmp(again.data(), values.data(), sizeof(double) * values.size()) == 0;
+        device_check(dev, oz_event_record(dev, 22), "event");
+        for (int r = 0; r < es->repeats; r++) steps[2].issue();
+        device_check(dev, oz_event_record(dev, 23), "event");
+        device_check(dev, oz_event_elapsed_ms(dev, 22, 23, &ms), "event time");
+        es->gemm_launch_ms = ms / es->repeats;
+    }
+    // range flags of the scaling stage (scale.hpp:187-208); the host validation rejects these inputs
+    // first, so they only fire if the device disagrees with it
+    for (int t = 0; t < 2; t++)
+        if (fl[t]) {
+            const char* what = t == 0 ? "rows of A" : "columns of B";
+            if (fl[t] & 4u) throw std::runtime_error(std::string("the ") + what + " contain Inf or NaN");
+            if (fl[t] & 2u) throw std::runtime_error(std::string("a maximum of the ") + what + " is below 2^-126");
+            throw std::runtime_error(std::string("a maximum of the ") + what + " exceeds the BF16 range");
+        }
+    Info info{Scheme::II, Format::INT8};
+    info.moduli = S;
+    info.integer_bits = (std::uint32_t)plan.b;
+    info.reconstruction_passes = plan.two_pass ? 2 : 1;
+    return {std::move(values), info};
+}
+
+}  // namespace ozTTgemm::detail

@@ -1,0 +1,378 @@
+// Scheme II host planning; see plan2.hpp. Compiled with -ffp-contract=off: the floating-point
+// expressions below must round exactly like the reference's (its Makefile:51-53 sets the same).
+#include "plan2.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <limits>
+#include <numeric>
+#include <random>
+#include <stdexcept>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+namespace ozTTgemm::detail {
+namespace {
+
+static_assert(std::numeric_limits<long double>::digits == 64,
+              "the norm estimate accumulates in x86 extended precision, like the reference (bits.hpp:18-19)");
+
+// Candidate moduli of the INT8 path: pairwise coprime, descending (moduli.hpp:180-181).
+constexpr int kTableInt8[] = {255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217,
+                              211, 199, 197, 193, 191, 181, 179, 173, 167, 163, 157, 151};
+constexpr int kTableInt8Min = 151;
+constexpr int kInt8ModCap = 255;     // OZ2_ROUTE_INT8.mod_cap (split.hpp:73)
+constexpr double kWinEps = 1e-9;     // strict window comparison (moduli.hpp:48)
+constexpr double kTailTol = 0.25;    // OZ2_TAIL_EXCESS_TOL (moduli.hpp:54)
+constexpr double kRecon1EpsLog2 = -70.0, kRecon1Margin = 2.0;  // auto_precision.hpp:126-127
+
+// Power of two by which a matrix is divided before sums of squares (norm_estimate.hpp:21-30).
+double pow2_scale(const double* v, std::size_t n) {
+    double mx = 0;
+    for (std::size_t i = 0; i < n; i++) mx = std::max(mx, std::fabs(v[i]));
+    if (!(mx > 0) || !std::isfinite(mx)) return 1.0;
+    int e;
+    std::frexp(mx, &e);
+    e = std::min(std::max(e, -1000), 1000);
+    return std::ldexp(1.0, e);
+}
+
+// Largest |r| with K*r^2 <= 2^acc_bits - 1 (moduli.hpp:224-231).
+long int8_rmax(std::uint32_t K) {
+    const unsigned __int128 lim = ((unsigned __int128)1 << kAccBits) - 1;
+    long r = (long)std::floor(std::sqrt((double)lim / (double)K));
+    while (r > 0 && (unsigned __int128)K * r * r > lim) --r;
+    while ((unsigned __int128)K * (r + 1) * (r + 1) <= lim) ++r;
+    return r;
+}
+
+bool int8_fits(std::uint32_t K, int m) {
+    const unsigned __int128 r = (unsigned)(m / 2);
+    return (unsigned __int128)K * r * r <= (((unsigned __int128)1 << kAccBits) - 1);
+}
+
+bool coprime_to_all(int v, const std::vector<int>& set) {
+    for (int x : set)
+        if (std::gcd(x, v) != 1) return false;
+    return true;
+}
+
+// Replace the last two moduli by one modulus or a coprime pair that covers the window with the
+// least excess (moduli.hpp:365-451); for INT8 every modulus is one product, so the preference is
+// (fewer moduli, excess within tolerance, smaller product).
+void reselect_tail(std::vector<int>& m, double& logM, double need, int m_cap) {
+    if (!(m.size() >= 2 && logM > need)) return;
+    const std::vector<int> head(m.begin(), m.end() - 2);
+    double base = 0.0;
+    for (int x : head) base += std::log2((double)x);
+    double best = logM;
+    int bp = m[m.size() - 2], bq = m.back(), bcost = 2;
+    auto over = [&](double l) { return (l - need) > kTailTol ? 1 : 0; };
+    auto better = [&](int c, double l) {
+        if (c != bcost) return c < bcost;
+        if (over(l) != over(best)) return over(l) < over(best);
+        return l < best;
+    };
+    bool head_even = false;
+    for (int x : head) head_even = head_even || (x % 2 == 0);
+    const int step = head_even ? 2 : 1;
+    for (int p = 3; p <= m_cap; p += step) {
+        if (!coprime_to_all(p, head)) continue;
+        const double lp = base + std::log2((double)p);
+        if (lp >= need && better(1, lp)) {
+            best = lp;
+            bp = p;
+            bq = 0;
+            bcost = 1;
+        }
+        for (int q = p + step; q <= m_cap; q += step) {
+            if (std::gcd(p, q) != 1 || !coprime_to_all(q, head)) continue;
+            const double lq = lp + std::log2((double)q);
+            if (lq >= need && better(2, lq)) {
+                best = lq;
+                bp = p;
+                bq = q;
+                bcost = 2;
+            }
+        }
+    }
+    m = head;
+    m.push_back(bp);
+    if (bq) m.push_back(bq);
+    logM = best;
+}
+
+}  // namespace
+
+OperandStats measure_stats(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K) {
+    OperandStats st;
+    const double rgA = 1.0 / pow2_scale(A, (std::size_t)M * K), rgB = 1.0 / pow2_scale(B, (std::size_t)K * N);
+    // Row statistics of A and column statistics of B (auto_precision.hpp:24-56). Per-row and per-column
+    // values are computed in parallel with the reference's inner order; the sums over rows/columns
+    // run sequentially in the reference's order.
+    std::vector<double> tA(M), sA(M), tB(N), sB(N), wA(M, 0.0), wB(N, 0.0);
+#pragma omp parallel for schedule(static)
+    for (std::int64_t r = 0; r < (std::int64_t)M; r++) {
+        double mx = 0, s2 = 0;
+        for (std::uint32_t c = 0; c < K; c++) {
+            const double v = A[(std::size_t)r * K + c] * rgA;
+            mx = std::max(mx, std::fabs(v));
+            s2 += v * v;
+        }
+        double t2 = 0;
+        if (mx > 0) {
+            const double t = std::exp2(std::ceil(std::log2(mx)));
+            t2 = t * t;
+            wA[r] = std::sqrt(s2) / t;
+        }
+        tA[r] = t2;
+        sA[r] = s2;
+    }
+    constexpr std::uint32_t CB = 64;  // column block: row-major sweep, per-column order kept
+#pragma omp parallel for schedule(static)
+    for (std::int64_t cb = 0; cb < (std::int64_t)((N + CB - 1) / CB); cb++) {
+        const std::uint32_t c0 = (std::uint32_t)cb * CB, c1 = std::min<std::uint32_t>(N, c0 + CB);
+        double mx[CB] = {}, s2[CB] = {};
+        for (std::uint32_t r = 0; r < K; r++)
+            for (std::uint32_t c = c0; c < c1; c++) {
+                const double v = B[(std::size_t)r * N + c] * rgB;
+                mx[c - c0] = std::max(mx[c - c0], std::fabs(v));
+                s2[c - c0] += v * v;
+            }
+        for (std::uint32_t c = c0; c < c1; c++) {
+            double t2 = 0;
+            if (mx[c - c0] > 0) {
+                const double t = std::exp2(std::ceil(std::log2(mx[c - c0])));
+                t2 = t * t;
+                wB[c] = std::sqrt(s2[c - c0]) / t;
+            }
+            tB[c] = t2;
+            sB[c] = s2[c - c0];
+        }
+    }
+    for (std::uint32_t r = 0; r < M; r++) {
+        st.TA += tA[r];
+        st.nA += sA[r];
+        st.wA = std::max(st.wA, wA[r]);
+    }
+    for (std::uint32_t c = 0; c < N; c++) {
+        st.TB += tB[c];
+        st.nB += sB[c];
+        st.wB = std::max(st.wB, wB[c]);
+    }
+    // Hutchinson estimate of ||C||_F^2 with L = 8 Gaussian vectors, drop the largest sample, divide by
+    // 1 + 2 sqrt(2/L) (norm_estimate.hpp:49-73).
+    const std::uint32_t L = 8;
+    std::mt19937 rg(12345);
+    std::normal_distribution<double> nd(0.0, 1.0);
+    std::vector<double> g(N), y(K), q_i(M);
+    double cs2 = 0, cmax = 0;
+    for (std::uint32_t l = 0; l < L; l++) {
+        for (std::uint32_t j = 0; j < N; j++) g[j] = nd(rg);
+#pragma omp parallel for schedule(static)
+        for (std::int64_t k = 0; k < (std::int64_t)K; k++) {
+            long double s = 0;
+            const double* row = B + (std::size_t)k * N;
+            for (std::uint32_t j = 0; j < N; j++) s += (long double)(row[j] * rgB) * g[j];
+            y[k] = (double)s;
+        }
+#pragma omp parallel for schedule(static)
+        for (std::int64_t i = 0; i < (std::int64_t)M; i++) {
+            long double s = 0;
+            const double* row = A + (std::size_t)i * K;
+            for (std::uint32_t k = 0; k < K; k++) s += (long double)(row[k] * rgA) * y[k];
+            q_i[i] = (double)s;
+        }
+        double q = 0;
+        for (std::uint32_t i = 0; i < M; i++) q += q_i[i] * q_i[i];
+        cs2 += q;
+        cmax = std::max(cmax, q);
+    }
+    st.nC = (cs2 - cmax) / (L - 1) / (1.0 + 2.0 * std::sqrt(2.0 / (double)L));
+    st.measured = true;
+    return st;
+}
+
+int precision_cap(const OperandStats& st) {
+    const double k2 = std::min(std::sqrt((st.TA * st.nB + st.TB * st.nA) / std::max(12.0 * st.nC, 1e-300)), 1e18);
+    return std::min(kMaxDigits * kDigitBits, kTargetBits + (int)std::ceil(std::log2(std::max(k2, 1.0))));
+}
+
+ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap) {
+    ModuliSet o;
+    const double W = std::log2((double)K);
+    const int m_cap = (int)std::min<long>(kInt8ModCap, 2 * int8_rmax(K) + 1);
+    double logM = 0.0;
+    for (int mm : kTableInt8) {
+        if ((int)o.m.size() >= num_moduli) break;
+        if (mm > m_cap) continue;
+        o.m.push_back(mm);
+        logM += std::log2((double)mm);
+    }
+    // extension below the table when K lowers the cap (moduli.hpp:310-327)
+    const int want = std::min(num_moduli, kMaxModuli);
+    for (int mm = std::min(m_cap, kTableInt8Min - 1); mm >= 3 && (int)o.m.size() < want; --mm) {
+        if (!coprime_to_all(mm, o.m)) continue;
+        o.m.push_back(mm);
+        logM += std::log2((double)mm);
+    }
+    o.m_cap = m_cap;
+    o.ncand = (int)o.m.size();
+    // width from the window |C'| <= K 2^(2b) < M/2 (moduli.hpp:338-344)
+    const double room = logM - 1.0 - W - kWinEps;
+    o.b = std::min(std::min((int)std::floor(room / 2.0), kMaxDigits * kDigitBits), b_cap);
+    const double need = 2.0 * o.b + 1.0 + W + kWinEps;
+    // drop surplus moduli from the end (moduli.hpp:347-355), then reselect the last two
+    while (o.m.size() > 2) {
+        const double l2 = std::log2((double)o.m.back());
+        if (logM - l2 < need) break;
+        o.m.pop_back();
+        logM -= l2;
+    }
+    reselect_tail(o.m, logM, need, m_cap);
+    o.log2M = logM;
+    const int s = (int)o.m.size();
+    o.ok = (logM >= need) && s > 0 && s <= kMaxModuli && s <= num_moduli && o.b > 0;
+    for (int i = 0; i < s; ++i)
+        for (int j = i + 1; j < s; ++j)
+            if (std::gcd(o.m[i], o.m[j]) != 1) o.ok = false;
+    for (int mm : o.m)
+        if (!int8_fits(K, mm)) {
+            if (o.acc_fail.empty())
+                o.acc_fail = "the product bound K*floor(m/2)^2 of modulus " + std::to_string(mm) +
+                             " exceeds the exact int32 range 2^31-1";
+            o.ok = o.acc_ok = false;
+        }
+    return o;
+}
+
+double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st) {
+    if (!(st.nC > 0) || !(st.TA > 0) || !(st.TB > 0)) return -INFINITY;
+    double l2m = 0;
+    for (int m : mo.m) l2m += std::log2((double)m);
+    return kRecon1EpsLog2 + l2m - 2.0 * b + 0.5 * (std::log2(st.TA) + std::log2(st.TB) - std::log2(st.nC));
+}
+
+Plan2 plan_scheme2_int8(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K,
+                        std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b) {
+    Plan2 p;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    int b_cap = kDefaultBits;
+    const bool b_fixed = fixed_b.has_value();
+    if (b_fixed)
+        b_cap = (int)*fixed_b;
+    else {
+        p.stats = measure_stats(A, B, M, N, K);
+        b_cap = precision_cap(p.stats);
+    }
+    // limit on the number of moduli (plan.hpp:281): the caller's, else 16 with a fixed width, else 24
+    p.S_req = max_moduli ? max_moduli : (b_fixed ? 16u : (std::uint32_t)kMaxModuli);
+    if (b_fixed && passes == Reconstruction::Automatic) p.stats = measure_stats(A, B, M, N, K);
+    p.mo = choose_moduli_int8(K, (int)p.S_req, b_cap);
+    if (!p.mo.ok) {
+        if (!p.mo.acc_ok)
+            throw std::runtime_error("Ozaki II: the padded inner dimension K=" + std::to_string(K) +
+                                     " is too large for this format: " + p.mo.acc_fail +
+                                     ". Use a smaller K or a different format; Options::max_moduli does not change "
+                                     "this limit.");
+        std::string cause;
+        if ((std::uint32_t)p.mo.ncand < std::min<std::uint32_t>(p.S_req, kMaxModuli))
+            cause = "Every candidate modulus is in use, so a larger Options::max_moduli does not help.";
+        else if (p.S_req < (std::uint32_t)kMaxModuli)
+            cause = "The limit of " + std::to_string(p.S_req) + " moduli is too small; raise Options::max_moduli.";
+        else
+            cause = "The maximum of 24 moduli is not enough; use a smaller K or a different format.";
+        throw std::runtime_error("Ozaki II: the available moduli do not cover the CRT window for the padded inner "
+                                 "dimension K=" +
+                                 std::to_string(K) + ". " + cause);
+    }
+    if (!b_fixed && p.mo.b < kTargetBits)
+        throw std::runtime_error("Ozaki II: for the padded inner dimension K=" + std::to_string(K) + " the " +
+                                 std::to_string(p.mo.m.size()) + " selected moduli cover a width of only " +
+                                 std::to_string(p.mo.b) + " bits, below the 53 bits of FP64-equivalent accuracy; "
+                                 "raise Options::max_moduli or use a smaller K.");
+    p.b = p.mo.b;
+    p.S = (int)p.mo.m.size();
+    // passes (plan.hpp:245-252)
+    p.recon1_log2 = p.stats.measured ? recon1_log2(p.mo, p.b, p.stats) : -INFINITY;
+    if (passes != Reconstruction::Automatic)
+        p.two_pass = passes == Reconstruction::TwoPass;
+    else
+        p.two_pass = !(p.recon1_log2 <= -(kTargetBits + kRecon1Margin));
+    p.nd = (p.b > 4 * kDigitBits) ? 5 : ((p.b > 3 * kDigitBits) ? 4 : 3);
+    return p;
+}
+
+oz2_moduli_dev split_descriptor(const Plan2& p) {
+    oz2_moduli_dev d{};
+    d.S = p.S;
+    d.nd = p.nd;
+    for (int s = 0; s < p.S; s++) {
+        const int m = p.mo.m[s];
+        d.m[s] = (float)m;
+        d.rinv[s] = (float)(1.0 / (double)m);  // correctly rounded binary64 then binary32 (see below)
+        for (int j = 0; j < 4; j++) {
+            long r = 1 % m;
+            for (int e = 0; e < kDigitBits * (j + 1); e++) r = (r * 2) % m;
+            d.c[j][s] = (float)r;
+        }
+    }
+    return d;
+}
+
+oz2_crt_dev crt_descriptor(const Plan2& p) {
+    oz2_crt_dev d{};
+    d.S = p.S;
+    d.b = p.b;
+    d.shift = p.shift();
+    // Mprod and Q_s = Mprod / m_s as little-endian 32-bit words (at most 24 * 8 = 192 bits)
+    auto mul_small = [](std::vector<std::uint32_t>& w, std::uint32_t k) {
+        std::uint64_t c = 0;
+        for (auto& x : w) {
+            const std::uint64_t t = (std::uint64_t)x * k + c;
+            x = (std::uint32_t)t;
+            c = t >> 32;
+        }
+        if (c) w.push_back((std::uint32_t)c);
+    };
+    std::vector<std::uint32_t> Mw{1};
+    for (int m : p.mo.m) mul_small(Mw, (std::uint32_t)m);
+    // accumulator width: (S+1)*M plus a sign bit
+    std::vector<std::uint32_t> bound = Mw;
+    mul_small(bound, (std::uint32_t)(p.S + 1));
+    int bits = 32 * ((int)bound.size() - 1) + (32 - __builtin_clz(bound.back())) + 1;
+    d.nw = std::max(3, (bits + 31) / 32);
+    if (d.nw > 8) throw std::runtime_error("Ozaki II: the CRT modulus exceeds the 256-bit reconstruction width");
+    for (std::size_t w = 0; w < Mw.size() && w < 8; w++) d.Mw[w] = Mw[w];
+    double mt = 0;
+    for (int w = 7; w >= 0; w--) mt = mt * 4294967296.0 + (double)d.Mw[w];
+    d.Mtop = mt;
+    for (int s = 0; s < p.S; s++) {
+        const std::uint32_t m = (std::uint32_t)p.mo.m[s];
+        d.m[s] = m;
+        // Q = M / m (exact), long division from the top word
+        std::uint64_t r = 0;
+        for (int w = 7; w >= 0; w--) {
+            const std::uint64_t cur = (r << 32) | d.Mw[w];
+            d.Q[s][w] = (std::uint32_t)(cur / m);
+            r = cur % m;
+        }
+        // y = (Q mod m)^-1 mod m
+        std::uint64_t qm = 0;
+        for (int w = 7; w >= 0; w--) qm = ((qm << 32) | d.Q[s][w]) % m;
+        std::uint32_t y = 0;
+        for (std::uint32_t t = 1; t < m; t++)
+            if ((qm * t) % m == 1) {
+                y = t;
+                break;
+            }
+        d.y[s] = y;
+    }
+    return d;
+}
+
+}  // namespace ozTTgemm::detail

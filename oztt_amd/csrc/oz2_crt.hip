@@ -1,0 +1,226 @@
+// A10-A11: CRT reconstruction of Scheme II to FP64.
+//
+// Semantics (reference recon_crt.cpp:293 + recon_writer.cpp:70, f64_tf.h:327-400): from the S exact
+// products C_s (C' = C_s mod m_s) recover C' in (-M/2, M/2), M = prod m_s, and return
+// C' * 2^(eA_i + eB_j - 2b) as FP64, with results below the normal range flushed to signed zero.
+// The reference approximates C'/M as a triple-float fraction (one pass, absolute accuracy about
+// 2^-67) or two passes (granularity 2^-124) and rounds ties away from zero. This kernel computes C'
+// exactly and rounds once to nearest-even, so it is at least as accurate as either reference mode
+// and serves both.
+//
+// Per element, with k_s = (C_s mod m_s) * y_s mod m_s and Q_s = M/m_s (host constants):
+//   acc = sum_s k_s * Q_s   (nw 32-bit words, < S*M), C' = acc mod M, then the symmetric
+//   representative; the residues use exact integer division by the small moduli.
+// MI355X design: one thread per output element; the S planes are read coalesced (plane-major),
+// the constants are kernel arguments (uniform, held in scalar registers), the multiword
+// arithmetic is 32-bit multiply-add with carries.
+#include "oz_internal.hpp"
+
+namespace {
+
+// x mod m for 0 <= x < 2^32 (m <= 255): q = mulhi(x, floor(2^32/m)) is floor(x/m) or one less.
+__device__ __forceinline__ uint32_t mod_small(uint32_t x, uint32_t m, uint32_t magic) {
+    const uint32_t q = __umulhi(x, magic);
+    uint32_t r = x - q * m;
+    if (r >= m) r -= m;
+    return r;
+}
+
+template <int NW>
+__device__ __forceinline__ double to_double_scaled(const uint32_t* w, int e2) {
+    // w: two's complement NW-word integer; returns w * 2^e2 rounded to nearest-even (subnormal -> 0)
+    uint32_t v[NW];
+    const bool neg = (w[NW - 1] >> 31) != 0;
+    if (neg) {
+        uint32_t c = 1;
+#pragma unroll
+        for (int i = 0; i < NW; i++) {
+            const uint64_t t = (uint64_t)(~w[i]) + c;
+            v[i] = (uint32_t)t;
+            c = (uint32_t)(t >> 32);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NW; i++) v[i] = w[i];
+    }
+    int top = -1;  // index of the highest nonzero word
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+        if (v[i]) top = i;
+    if (top < 0) return neg ? -0.0 : 0.0;
+    // gather the 96 bits below and including the leading bit: hi word, next, next
+    const uint32_t w2 = v[top];
+    const uint32_t w1 = top >= 1 ? v[top - 1] : 0u;
+    const uint32_t w0 = top >= 2 ? v[top - 2] : 0u;
+    bool sticky_low = false;
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+        if (i < top - 2 && v[i]) sticky_low = true;
+    const int lz = __clz(w2);
+    // normalize the 96-bit window so that the leading bit is bit 95
+    uint64_t hi64 = ((uint64_t)w2 << 32) | w1;  // bits 95..32 of the window
+    uint32_t lo32 = w0;
+    if (lz) {
+        hi64 = (hi64 << lz) | (lo32 >> (32 - lz));
+        lo32 <<= lz;
+    }
+    // hi64 holds the leading 64 bits; keep 53, round on the remaining 11 bits + lo32 + lower words
+    uint64_t mant = hi64 >> 11;
+    const uint64_t rest = hi64 & 0x7FFull;
+    const bool guard = (rest >> 10) & 1ull;
+    const bool sticky = (rest & 0x3FFull) || lo32 || sticky_low;
+    // value = mant * 2^(position of mant LSB) with the leading bit at 32*top + 31 - lz
+    int exp_lead = 32 * top + 31 - lz + e2;  // exponent of the leading bit
+    if (guard && (sticky || (mant & 1ull))) {
+        mant += 1ull;
+        if (mant >> 53) {
+            mant >>= 1;
+            exp_lead += 1;
+        }
+    }
+    if (exp_lead < -1022) return neg ? -0.0 : 0.0;
+    if (exp_lead > 1023) return neg ? -__builtin_huge_val() : __builtin_huge_val();
+    const uint64_t bits = ((uint64_t)(exp_lead + 1023) << 52) | (mant & 0x000FFFFFFFFFFFFFull);
+    const double r = __longlong_as_double((long long)bits);
+    return neg ? -r : r;
+}
+
+struct CrtArgs {
+    oz2_crt_dev k;
+    uint32_t magic[OZ2_MAXS];  // floor(2^32/m)
+    uint32_t Mhalf[8];         // floor(M/2)
+};
+
+template <int NW>
+__global__ void __launch_bounds__(256) crt_kernel(const int32_t* __restrict__ C, int M, int N, int ldc, long long sC,
+                                                  CrtArgs a, const int32_t* __restrict__ dA,
+                                                  const int32_t* __restrict__ dB, double* __restrict__ out, int ldo) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.y;
+    if (j >= N) return;
+    const int32_t* c = C + (long long)i * ldc + j;
+    uint32_t acc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; w++) acc[w] = 0;
+    for (int s = 0; s < a.k.S; s++) {
+        const int32_t v = c[(long long)s * sC];
+        const uint32_t m = a.k.m[s], mg = a.magic[s];
+        uint32_t r = mod_small(v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v, m, mg);
+        if (v < 0 && r) r = m - r;
+        const uint32_t k = mod_small(r * a.k.y[s], m, mg);
+        uint32_t carry = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const uint64_t p = (uint64_t)k * a.k.Q[s][w] + acc[w] + carry;
+            acc[w] = (uint32_t)p;
+            carry = (uint32_t)(p >> 32);
+        }
+    }
+    // q = floor(acc / M) from FP64 approximations (|error| <= 1), then acc -= q*M with one correction
+    double ahi = 0.0;
+#pragma unroll
+    for (int w = NW - 1; w >= 0; w--) ahi = ahi * 4294967296.0 + (double)acc[w];
+    uint32_t q = (uint32_t)__builtin_floor(ahi / a.k.Mtop);
+    {
+        uint32_t carry = 0, borrow = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const uint64_t p = (uint64_t)q * a.k.Mw[w] + carry;
+            carry = (uint32_t)(p >> 32);
+            const uint64_t d = (uint64_t)acc[w] - (uint32_t)p - borrow;
+            acc[w] = (uint32_t)d;
+            borrow = (uint32_t)(d >> 63);
+        }
+        if (borrow || carry) {  // q was one too large: add M back
+            uint32_t c2 = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const uint64_t t = (uint64_t)acc[w] + a.k.Mw[w] + c2;
+                acc[w] = (uint32_t)t;
+                c2 = (uint32_t)(t >> 32);
+            }
+        }
+    }
+    // q was one too small: subtract M once more when acc >= M (compare from the top word)
+    {
+        int cmp = 0;
+#pragma unroll
+        for (int w = NW - 1; w >= 0; w--)
+            if (cmp == 0 && acc[w] != a.k.Mw[w]) cmp = acc[w] > a.k.Mw[w] ? 1 : -1;
+        if (cmp >= 0) {
+            uint32_t borrow = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const uint64_t d = (uint64_t)acc[w] - a.k.Mw[w] - borrow;
+                acc[w] = (uint32_t)d;
+                borrow = (uint32_t)(d >> 63);
+            }
+        }
+    }
+    // symmetric representative: acc > floor(M/2) -> acc - M
+    {
+        int cmp = 0;
+#pragma unroll
+        for (int w = NW - 1; w >= 0; w--)
+            if (cmp == 0 && acc[w] != a.Mhalf[w]) cmp = acc[w] > a.Mhalf[w] ? 1 : -1;
+        if (cmp > 0) {
+            uint32_t borrow = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const uint64_t d = (uint64_t)acc[w] - a.k.Mw[w] - borrow;
+                acc[w] = (uint32_t)d;
+                borrow = (uint32_t)(d >> 63);
+            }
+        }
+    }
+    const int g = 2 * a.k.shift - (dA[i] + dB[j]);  // eA + eB
+    out[(long long)i * ldo + j] = to_double_scaled<NW>(acc, g - 2 * a.k.b);
+}
+
+template <int NW>
+int launch_crt(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long sC, const CrtArgs& a,
+               const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    hipLaunchKernelGGL(crt_kernel<NW>, dim3(oz::ceil_div(N, 256), M), dim3(256), 0, dev->stream, C, M, N, ldc, sC, a, dA,
+                       dB, out, ldo);
+    return oz::launch_check(dev, "crt_kernel");
+}
+
+}  // namespace
+
+extern "C" int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long strideC,
+                           const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    if (int st = oz::use(dev)) return st;
+    if (!C || !crt || !dA || !dB || !out || M <= 0 || N <= 0 || ldc < N || ldo < N || crt->S < 1 ||
+        crt->S > OZ2_MAXS || crt->nw < 3 || crt->nw > 8 || crt->Mtop <= 0.0)
+        return oz::fail(dev, OZ_ERR_ARG, "oz2_crt_f64: invalid arguments");
+    CrtArgs a{};
+    a.k = *crt;
+    for (int s = 0; s < crt->S; s++) {
+        if (crt->m[s] < 2 || crt->m[s] > 255) return oz::fail(dev, OZ_ERR_ARG, "oz2_crt_f64: modulus out of range");
+        a.magic[s] = (uint32_t)(0x100000000ull / crt->m[s]);
+    }
+    // floor(M/2)
+    uint32_t r = 0;
+    for (int w = 7; w >= 0; w--) {
+        const uint64_t cur = ((uint64_t)r << 32) | crt->Mw[w];
+        a.Mhalf[w] = (uint32_t)(cur >> 1);
+        r = (uint32_t)(cur & 1u);
+    }
+    // the grid puts rows on y (at most 65535 per launch): launch in row chunks
+    for (int i0 = 0; i0 < M; i0 += 65535) {
+        const int rows = std::min(65535, M - i0);
+        const int32_t* Ci = C + (long long)i0 * ldc;
+        double* oi = out + (long long)i0 * ldo;
+        int st;
+        switch (crt->nw) {
+        case 3: st = launch_crt<3>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 4: st = launch_crt<4>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 5: st = launch_crt<5>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 6: st = launch_crt<6>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 7: st = launch_crt<7>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        default: st = launch_crt<8>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        }
+        if (st) return st;
+    }
+    return OZ_OK;
+}

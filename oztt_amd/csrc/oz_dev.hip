@@ -1,0 +1,116 @@
+// Device handle, memory and timing entry points of the C ABI (include/oz_hip.h).
+// One handle owns one HIP stream on one GPU; the C++ context (host/context.cpp) opens it lazily on
+// the first valid GEMM, as the reference opens its device (context.cpp:152-161).
+#include "oz_internal.hpp"
+
+#include <new>
+
+namespace {
+__global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t v, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = v;
+}
+}  // namespace
+
+extern "C" {
+
+int oz_device_count(int* count) {
+    if (!count) return OZ_ERR_ARG;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return OZ_OK;
+}
+
+int oz_dev_open(int device_id, oz_dev** out) {
+    if (!out || device_id < 0) return OZ_ERR_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device_id >= n) return OZ_ERR_HIP;
+    oz_dev* d = new (std::nothrow) oz_dev;
+    if (!d) return OZ_ERR_NOMEM;
+    d->device = device_id;
+    if (hipSetDevice(device_id) != hipSuccess || hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete d;
+        return OZ_ERR_HIP;
+    }
+    for (auto& e : d->events) {
+        if (hipEventCreate(&e) != hipSuccess) {
+            oz_dev_close(d);
+            return OZ_ERR_HIP;
+        }
+    }
+    *out = d;
+    return OZ_OK;
+}
+
+void oz_dev_close(oz_dev* dev) {
+    if (!dev) return;
+    (void)hipSetDevice(dev->device);
+    if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+    for (auto& e : dev->events)
+        if (e) (void)hipEventDestroy(e);
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
+    delete dev;
+}
+
+const char* oz_last_error(const oz_dev* dev) { return dev ? dev->error.c_str() : "no device handle"; }
+
+int oz_dev_malloc(oz_dev* dev, size_t bytes, void** ptr) {
+    if (int st = oz::use(dev)) return st;
+    if (!ptr) return oz::fail(dev, OZ_ERR_ARG, "oz_dev_malloc: null output pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return OZ_OK;
+    return oz::hip_check(dev, hipMalloc(ptr, bytes), "hipMalloc");
+}
+
+int oz_dev_free(oz_dev* dev, void* ptr) {
+    if (int st = oz::use(dev)) return st;
+    if (!ptr) return OZ_OK;
+    return oz::hip_check(dev, hipFree(ptr), "hipFree");
+}
+
+int oz_memcpy_h2d(oz_dev* dev, void* dst, const void* src, size_t bytes) {
+    if (int st = oz::use(dev)) return st;
+    if (!bytes) return OZ_OK;
+    if (int st = oz::hip_check(dev, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream), "hipMemcpyAsync H2D"))
+        return st;
+    return oz::hip_check(dev, hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+int oz_memcpy_d2h(oz_dev* dev, void* dst, const void* src, size_t bytes) {
+    if (int st = oz::use(dev)) return st;
+    if (!bytes) return OZ_OK;
+    if (int st = oz::hip_check(dev, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream), "hipMemcpyAsync D2H"))
+        return st;
+    return oz::hip_check(dev, hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+int oz_fill_u32(oz_dev* dev, void* dst, uint32_t value, size_t count) {
+    if (int st = oz::use(dev)) return st;
+    if (!count) return OZ_OK;
+    if (!dst) return oz::fail(dev, OZ_ERR_ARG, "oz_fill_u32: null pointer");
+    const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks), dim3(256), 0, dev->stream, (uint32_t*)dst, value, count);
+    return oz::launch_check(dev, "fill_u32_kernel");
+}
+
+int oz_sync(oz_dev* dev) {
+    if (int st = oz::use(dev)) return st;
+    return oz::hip_check(dev, hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+int oz_event_record(oz_dev* dev, int slot) {
+    if (int st = oz::use(dev)) return st;
+    if (slot < 0 || slot >= 64) return oz::fail(dev, OZ_ERR_ARG, "event slot %d out of range", slot);
+    return oz::hip_check(dev, hipEventRecord(dev->events[slot], dev->stream), "hipEventRecord");
+}
+
+int oz_event_elapsed_ms(oz_dev* dev, int a, int b, float* ms) {
+    if (int st = oz::use(dev)) return st;
+    if (a < 0 || a >= 64 || b < 0 || b >= 64 || !ms) return oz::fail(dev, OZ_ERR_ARG, "bad event slots");
+    if (int st = oz::hip_check(dev, hipEventSynchronize(dev->events[b]), "hipEventSynchronize")) return st;
+    return oz::hip_check(dev, hipEventElapsedTime(ms, dev->events[a], dev->events[b]), "hipEventElapsedTime");
+}
+
+}  // extern "C"

@@ -1,0 +1,51 @@
+// Internal helpers of the device layer (liboz_hip.so): the device handle, error reporting and
+// launch checks shared by the kernel sources.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "oz_hip.h"
+
+struct oz_dev {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t events[64] = {};
+    std::string error;
+};
+
+namespace oz {
+
+// Records a message on the handle and returns the status (printf-style).
+inline int fail(oz_dev* dev, int status, const char* fmt, ...) {
+    if (dev) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        std::vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        dev->error = buf;
+    }
+    return status;
+}
+
+// Checks a HIP call; on failure records "what: hip error" and returns OZ_ERR_HIP.
+inline int hip_check(oz_dev* dev, hipError_t e, const char* what) {
+    if (e == hipSuccess) return OZ_OK;
+    return fail(dev, e == hipErrorOutOfMemory ? OZ_ERR_NOMEM : OZ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Checks the launch that was just issued (configuration errors surface here).
+inline int launch_check(oz_dev* dev, const char* kernel) { return hip_check(dev, hipGetLastError(), kernel); }
+
+// Sets the handle's device current for the calling thread.
+inline int use(oz_dev* dev) {
+    if (!dev) return OZ_ERR_ARG;
+    return hip_check(dev, hipSetDevice(dev->device), "hipSetDevice");
+}
+
+inline unsigned ceil_div(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace oz

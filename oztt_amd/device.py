@@ -1,0 +1,144 @@
+"""Thin Python access to the C ABI of include/oz_hip.h (liboz_hip.so): a device handle, device
+buffers and the stage entry points, for tests and the evaluator. Every call checks the status and
+raises RuntimeError with the device layer's message."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import hip
+
+OZ2_MAXS = 24
+
+
+class ModuliDesc(ctypes.Structure):
+    _fields_ = [("S", ctypes.c_int), ("nd", ctypes.c_int), ("m", ctypes.c_float * OZ2_MAXS),
+                ("rinv", ctypes.c_float * OZ2_MAXS), ("c", (ctypes.c_float * OZ2_MAXS) * 4)]
+
+
+class CrtDesc(ctypes.Structure):
+    _fields_ = [("S", ctypes.c_int), ("b", ctypes.c_int), ("shift", ctypes.c_int), ("nw", ctypes.c_int),
+                ("m", ctypes.c_uint32 * OZ2_MAXS), ("y", ctypes.c_uint32 * OZ2_MAXS),
+                ("Q", (ctypes.c_uint32 * 8) * OZ2_MAXS), ("Mw", ctypes.c_uint32 * 8), ("Mtop", ctypes.c_double)]
+
+
+def moduli_desc(moduli, nd: int) -> ModuliDesc:
+    d = ModuliDesc()
+    d.S, d.nd = len(moduli), nd
+    for s, m in enumerate(moduli):
+        d.m[s] = float(m)
+        d.rinv[s] = float(np.float32(1.0 / m))
+        for j in range(4):
+            d.c[j][s] = float(pow(2, 20 * (j + 1), m))
+    return d
+
+
+def crt_desc(moduli, b: int, nd: int) -> CrtDesc:
+    d = CrtDesc()
+    S = len(moduli)
+    M = 1
+    for m in moduli:
+        M *= m
+    d.S, d.b, d.shift = S, b, b - 20 * (nd - 1)
+    bits = ((S + 1) * M).bit_length() + 1
+    d.nw = max(3, (bits + 31) // 32)
+    for w in range(8):
+        d.Mw[w] = (M >> (32 * w)) & 0xFFFFFFFF
+    d.Mtop = float(M)
+    for s, m in enumerate(moduli):
+        d.m[s] = m
+        Q = M // m
+        for w in range(8):
+            d.Q[s][w] = (Q >> (32 * w)) & 0xFFFFFFFF
+        d.y[s] = pow(Q % m, -1, m)
+    return d
+
+
+class Buffer:
+    def __init__(self, dev: "Device", nbytes: int):
+        self.dev, self.nbytes = dev, int(nbytes)
+        self.ptr = ctypes.c_void_p()
+        dev._check(hip().oz_dev_malloc(dev.h, ctypes.c_size_t(max(self.nbytes, 1)), ctypes.byref(self.ptr)),
+                   "oz_dev_malloc")
+
+    def free(self):
+        if self.ptr:
+            hip().oz_dev_free(self.dev.h, self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def offset(self, nbytes: int) -> ctypes.c_void_p:
+        return ctypes.c_void_p(self.ptr.value + int(nbytes))
+
+
+class Device:
+    def __init__(self, device_id: int = 0):
+        self.h = ctypes.c_void_p()
+        st = hip().oz_dev_open(device_id, ctypes.byref(self.h))
+        if st != 0:
+            raise RuntimeError(f"oz_dev_open({device_id}) failed with status {st}")
+        self.bufs: list[Buffer] = []
+
+    def _check(self, st: int, what: str):
+        if st != 0:
+            raise RuntimeError(f"{what}: status {st}: {hip().oz_last_error(self.h).decode(errors='replace')}")
+
+    def close(self):
+        for b in self.bufs:
+            b.free()
+        self.bufs.clear()
+        if self.h:
+            hip().oz_dev_close(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def alloc(self, nbytes: int) -> Buffer:
+        b = Buffer(self, nbytes)
+        self.bufs.append(b)
+        return b
+
+    def upload(self, arr: np.ndarray) -> Buffer:
+        arr = np.ascontiguousarray(arr)
+        b = self.alloc(arr.nbytes)
+        self._check(hip().oz_memcpy_h2d(self.h, b.ptr, arr.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(arr.nbytes)),
+                    "oz_memcpy_h2d")
+        return b
+
+    def download(self, buf: Buffer, dtype, count: int, offset_bytes: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        src = buf.offset(offset_bytes)
+        self._check(hip().oz_memcpy_d2h(self.h, out.ctypes.data_as(ctypes.c_void_p), src, ctypes.c_size_t(out.nbytes)),
+                    "oz_memcpy_d2h")
+        return out
+
+    def fill_u32(self, buf: Buffer, value: int, count: int):
+        self._check(hip().oz_fill_u32(self.h, buf.ptr, ctypes.c_uint32(value), ctypes.c_size_t(count)), "oz_fill_u32")
+
+    def sync(self):
+        self._check(hip().oz_sync(self.h), "oz_sync")
+
+    # ---- stages --------------------------------------------------------------------------------
+    def scale(self, X: Buffer, rows, cols, ld, mode, ceil_mode, shift, delta: Buffer, flags: Buffer, flag_index=0):
+        self._check(hip().oz_scale_f64(self.h, X.ptr, rows, cols, ld, mode, ceil_mode, shift, delta.ptr,
+                                       flags.offset(4 * flag_index)), "oz_scale_f64")
+
+    def split_int8(self, X: Buffer, rows, cols, ld, mode, delta: Buffer, desc: ModuliDesc, planes: Buffer, layout, prow,
+                   pld, pstride):
+        self._check(hip().oz2_split_int8(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, ctypes.byref(desc), planes.ptr,
+                                         layout, prow, pld, ctypes.c_longlong(pstride)), "oz2_split_int8")
+
+    def digits(self, X: Buffer, rows, cols, ld, mode, delta: Buffer, nd, out: Buffer):
+        self._check(hip().oz2_digits_f32(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, nd, out.ptr), "oz2_digits_f32")
+
+    def gemm_i8(self, A: Buffer, Bt: Buffer, C: Buffer, M, N, K, batch, lda, ldb, ldc, sA, sB, sC):
+        self._check(hip().oz_gemm_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, batch, lda, ldb, ldc, ctypes.c_longlong(sA),
+                                     ctypes.c_longlong(sB), ctypes.c_longlong(sC)), "oz_gemm_i8")
+
+    def crt(self, C: Buffer, M, N, ldc, sC, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
+        self._check(hip().oz2_crt_f64(self.h, C.ptr, M, N, ldc, ctypes.c_longlong(sC), ctypes.byref(desc), dA.ptr,
+                                      dB.ptr, out.ptr, ldo), "oz2_crt_f64")

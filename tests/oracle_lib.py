@@ -1,0 +1,127 @@
+"""ctypes access to the CPU oracle (oracle/build/liboz_oracle.so). Tests only: the oracle is the
+checker, never part of the product path."""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+ORACLE_SO = ROOT / "oracle" / "build" / "liboz_oracle.so"
+
+_lib = None
+
+
+def P(a: np.ndarray) -> ctypes.c_void_p:
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Oracle:
+    def __init__(self, lib: ctypes.CDLL):
+        self.lib = lib
+        lib.orc_hash_f64.restype = ctypes.c_uint64
+        lib.orc_gemm_i8.restype = ctypes.c_int64
+        lib.orc_modround.restype = ctypes.c_float
+        lib.orc_modround.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_float]
+
+    def inputs(self, seed, phi, na, nb):
+        a = np.empty(na)
+        b = np.empty(nb)
+        self.lib.orc_inputs(ctypes.c_uint(seed), ctypes.c_double(phi), ctypes.c_size_t(na), ctypes.c_size_t(nb), P(a), P(b))
+        return a, b
+
+    def hash(self, c) -> int:
+        c = np.ascontiguousarray(c, dtype=np.float64).reshape(-1)
+        return int(self.lib.orc_hash_f64(P(c), ctypes.c_size_t(c.size)))
+
+    def scale(self, X, rows, cols, mode, ceil_mode, shift):
+        X = np.ascontiguousarray(X, dtype=np.float64)
+        n = rows if mode == 0 else cols
+        d = np.empty(n, dtype=np.int32)
+        fl = np.zeros(1, dtype=np.uint32)
+        self.lib.orc_scale(P(X), rows, cols, cols, mode, ceil_mode, shift, P(d), P(fl))
+        return d, int(fl[0])
+
+    def split_f64(self, x: float, d: int):
+        u = np.frombuffer(np.float64(x).tobytes(), dtype=np.uint64)[0]
+        out = np.zeros(4, dtype=np.uint32)
+        self.lib.orc_split_f64(ctypes.c_uint32(int(u >> np.uint64(32))), ctypes.c_uint32(int(u & np.uint64(0xFFFFFFFF))),
+                               ctypes.c_int32(d), P(out))
+        return out
+
+    def load_triple(self, x: float, d: int):
+        out = np.zeros(3, dtype=np.float32)
+        self.lib.orc_load_triple(ctypes.c_double(x), ctypes.c_int32(d), P(out))
+        return out
+
+    def digits(self, X, rows, cols, mode, delta, nd):
+        X = np.ascontiguousarray(X, dtype=np.float64)
+        out = np.empty(rows * cols * nd, dtype=np.float32)
+        self.lib.orc_oz2_digits(P(X), rows, cols, cols, mode, P(np.ascontiguousarray(delta, np.int32)), nd, P(out))
+        return out.reshape(rows, cols, nd)
+
+    def residues(self, X, rows, cols, mode, delta, nd, moduli):
+        X = np.ascontiguousarray(X, dtype=np.float64)
+        m = np.array(moduli, dtype=np.int32)
+        out = np.empty((len(moduli), rows, cols), dtype=np.int8)
+        self.lib.orc_oz2_residues(P(X), rows, cols, cols, mode, P(np.ascontiguousarray(delta, np.int32)), nd, len(moduli),
+                                  P(m), P(out))
+        return out
+
+    def modround(self, d, m, rinv) -> float:
+        return float(self.lib.orc_modround(d, m, rinv))
+
+    def gemm_i8(self, A, B):
+        M, K = A.shape
+        K2, N = B.shape
+        assert K == K2
+        C = np.empty((M, N), dtype=np.int32)
+        mx = self.lib.orc_gemm_i8(P(np.ascontiguousarray(A)), P(np.ascontiguousarray(B)), P(C), M, N, K)
+        return C, int(mx)
+
+    def crt_ref(self, C, M, N, moduli, b, nd, two_pass, dA, dB):
+        m = np.array(moduli, dtype=np.int32)
+        out = np.empty(M * N)
+        self.lib.orc_oz2_crt_ref(P(np.ascontiguousarray(C, np.int32)), M, N, len(moduli), P(m), b, nd, int(two_pass),
+                                 P(np.ascontiguousarray(dA, np.int32)), P(np.ascontiguousarray(dB, np.int32)), P(out))
+        return out
+
+    def crt_exact(self, C, M, N, moduli, b, nd, dA, dB):
+        m = np.array(moduli, dtype=np.int32)
+        out = np.empty(M * N)
+        self.lib.orc_oz2_crt_exact(P(np.ascontiguousarray(C, np.int32)), M, N, len(moduli), P(m), b, nd,
+                                   P(np.ascontiguousarray(dA, np.int32)), P(np.ascontiguousarray(dB, np.int32)), P(out))
+        return out
+
+    def crt_exact_int(self, r, moduli) -> int:
+        r = np.ascontiguousarray(r, np.int32)
+        m = np.array(moduli, dtype=np.int32)
+        out = np.zeros(4, dtype=np.uint64)
+        self.lib.orc_oz2_crt_exact_int(P(r), len(moduli), P(m), P(out))
+        v = sum(int(out[i]) << (64 * i) for i in range(4))
+        return v - (1 << 256) if v >> 255 else v
+
+    def quad_sample(self, A, B, M, N, K, rows, cols):
+        rows = np.ascontiguousarray(rows, np.int32)
+        cols = np.ascontiguousarray(cols, np.int32)
+        out = np.empty(rows.size)
+        self.lib.orc_gemm_quad_sample(P(np.ascontiguousarray(A)), P(np.ascontiguousarray(B)), M, N, K, rows.size, P(rows),
+                                      P(cols), P(out))
+        return out
+
+    def dot2(self, A, B, M, N, K, r0, r1):
+        hi = np.empty(M * N)
+        lo = np.empty(M * N)
+        self.lib.orc_dot2_gemm(P(np.ascontiguousarray(A)), P(np.ascontiguousarray(B)), M, N, K, r0, r1, P(hi), P(lo))
+        return hi, lo
+
+
+def load_oracle() -> Oracle:
+    global _lib
+    if _lib is None:
+        if not ORACLE_SO.exists():
+            subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+        _lib = Oracle(ctypes.CDLL(str(ORACLE_SO)))
+    return _lib

@@ -1,0 +1,212 @@
+"""GPU parity of each Scheme II stage against the CPU oracle, through the C ABI (include/oz_hip.h).
+
+Bar: bit-exact (delta and flags of the scale stage, FP32 digits, int8 residues, int32 products, FP64
+reconstruction). Inputs are seeded and cover the edge cases of each stage."""
+import math
+
+import numpy as np
+import pytest
+
+from oztt_amd.device import Device, crt_desc, moduli_desc
+
+pytestmark = pytest.mark.gpu
+
+INT8_16 = [255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199, 47, 79]  # K=8192, b=54
+
+
+def edge_matrix(rows, cols, rng):
+    """Rows exercising the maxima rules: zero row, exact powers of two, dropped significand bits,
+    the BF16 extremes, subnormal-only, huge, NaN, Inf; the rest random over 60 binades."""
+    X = rng.uniform(-1, 1, (rows, cols)) * np.exp2(rng.integers(-30, 30, (rows, 1)))
+    X[0] = 0.0
+    X[1, :] = 0.5
+    X[1, 3] = -1.0                       # exact power of two maximum
+    X[2, 5] = 1.0 + 2.0 ** -40           # dropped bits below the BF16 significand
+    X[3, 7] = float.fromhex("0x1.fep127")  # largest BF16
+    X[4, :] = 0.0
+    X[4, 2] = 2.0 ** -130                # nonzero maximum below 2^-126
+    X[5, 1] = float.fromhex("0x1.ff8p127")  # above the largest BF16
+    X[6, 9] = np.nan
+    X[7, 4] = -np.inf
+    X[8, :] = 2.0 ** -126                # smallest admissible maximum
+    X[9, 0] = float.fromhex("0x1.fe00000000001p127")  # rounds up past the BF16 range
+    return X
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("ceil_mode", [0, 1, 2])
+def test_scale_matches_oracle(dev, oracle, mode, ceil_mode):
+    rng = np.random.default_rng(100 + 3 * mode + ceil_mode)
+    rows, cols = (70, 300) if mode == 0 else (300, 70)
+    X = edge_matrix(rows, cols, rng) if mode == 0 else edge_matrix(cols, rows, rng).T.copy()
+    shift = 14
+    want_d, want_f = oracle.scale(X, rows, cols, mode, ceil_mode, shift)
+    bx = dev.upload(X)
+    n = rows if mode == 0 else cols
+    bd = dev.alloc(4 * n)
+    bf = dev.alloc(8)
+    dev.fill_u32(bf, 0, 2)
+    dev.scale(bx, rows, cols, cols, mode, ceil_mode, shift, bd, bf)
+    got_d = dev.download(bd, np.int32, n)
+    got_f = int(dev.download(bf, np.uint32, 1)[0])
+    np.testing.assert_array_equal(got_d, want_d)
+    assert got_f == want_f
+    assert want_f == (6 if ceil_mode == 0 else 7)  # rounding down keeps 0x1.ff8p127 inside the BF16 range
+
+
+def test_scale_large_column_reduction(dev, oracle):
+    # many row chunks per column strip (atomic combination across workgroups)
+    rng = np.random.default_rng(7)
+    rows, cols = 4096, 192
+    X = rng.standard_normal((rows, cols)) * np.exp2(rng.integers(-20, 20, (rows, cols)))
+    want_d, want_f = oracle.scale(X, rows, cols, 1, 1, 14)
+    bx = dev.upload(X)
+    bd = dev.alloc(4 * cols)
+    bf = dev.alloc(8)
+    dev.fill_u32(bf, 0, 2)
+    dev.scale(bx, rows, cols, cols, 1, 1, 14, bd, bf)
+    np.testing.assert_array_equal(dev.download(bd, np.int32, cols), want_d)
+    assert int(dev.download(bf, np.uint32, 1)[0]) == want_f == 0
+
+
+def split_inputs(rows, cols, rng, phi):
+    """Random operand with wide exponent spread plus crafted rounding-boundary elements."""
+    X = (rng.uniform(0, 1, (rows, cols)) - 0.5) * np.exp(phi * rng.standard_normal((rows, cols)))
+    X[0, :] = 0.0
+    X[1, 0] = 1.0
+    X[1, 1] = 2.0 ** -55 + 2.0 ** -80   # digits.h:44: with b = 54 and row maximum 1, A' = 0
+    X[1, 2] = 2.0 ** -55                # exact half: ties to even
+    X[1, 3] = 3 * 2.0 ** -55            # exact 1.5 ulp of A'
+    X[1, 4] = -(2.0 ** -54) * 5 - 2.0 ** -55
+    X[2, :] = rng.uniform(-1, 1, cols) * 2.0 ** -70   # far below the row maximum
+    X[2, 0] = 1.0
+    X[3, :] = np.ldexp(rng.integers(-2 ** 52, 2 ** 52, cols).astype(np.float64), -52)  # full significands
+    return X
+
+
+@pytest.mark.parametrize("nd,b", [(3, 54), (3, 60), (4, 72), (5, 96)])
+def test_digits_match_oracle(dev, oracle, nd, b):
+    rng = np.random.default_rng(nd * 100 + b)
+    rows, cols = 37, 129
+    X = split_inputs(rows, cols, rng, 2.0)
+    shift = b - 20 * (nd - 1)
+    delta, _ = oracle.scale(X, rows, cols, 0, 1, shift)
+    want = oracle.digits(X, rows, cols, 0, delta, nd)
+    bx, bd = dev.upload(X), dev.upload(delta)
+    bo = dev.alloc(4 * rows * cols * nd)
+    dev.digits(bx, rows, cols, cols, 0, bd, nd, bo)
+    got = dev.download(bo, np.float32, rows * cols * nd).reshape(rows, cols, nd)
+    np.testing.assert_array_equal(got, want)  # values (a zero's sign may differ, it carries no value)
+    if nd == 3 and b == 54:
+        A1 = sum(float(want[1, 1, j]) * 2.0 ** (20 * (nd - 1 - j)) for j in range(nd))
+        assert A1 == 0.0  # the documented example of the reference
+
+
+def moduli_for(b, nd, K):
+    from oztt_amd import choose_moduli_int8
+    p = choose_moduli_int8(K, 24, b)
+    return [p.m[i] for i in range(p.S)]
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("nd,b,phi", [(3, 54, 0.5), (3, 56, 2.0), (4, 70, 4.0), (5, 90, 1.0)])
+def test_residues_match_oracle(dev, oracle, layout, nd, b, phi):
+    rng = np.random.default_rng(1000 + 10 * nd + layout)
+    rows, cols = (96, 200) if layout == 0 else (200, 96)
+    X = split_inputs(rows, cols, rng, phi) if layout == 0 else split_inputs(cols, rows, rng, phi).T.copy()
+    mode = 0 if layout == 0 else 1
+    shift = b - 20 * (nd - 1)
+    moduli = moduli_for(b, nd, 4096)
+    if 254 not in moduli:
+        moduli = moduli + [254] if len(moduli) < 24 else moduli[:-1] + [254]
+    delta, _ = oracle.scale(X, rows, cols, mode, 1, shift)
+    want = oracle.residues(X, rows, cols, mode, delta, nd, moduli)  # [S][rows][cols]
+    S = len(moduli)
+    prow = (rows if layout == 0 else cols)
+    prow = (prow + 63) // 64 * 64 + 64
+    pld = ((cols if layout == 0 else rows) + 63) // 64 * 64 + 64
+    pstride = prow * pld + 128
+    bx, bd = dev.upload(X), dev.upload(delta)
+    bp = dev.alloc(S * pstride)
+    dev.split_int8(bx, rows, cols, cols, mode, bd, moduli_desc(moduli, nd), bp, layout, prow, pld, pstride)
+    got = dev.download(bp, np.int8, S * pstride).reshape(S, pstride)[:, :prow * pld].reshape(S, prow, pld)
+    if layout == 0:
+        np.testing.assert_array_equal(got[:, :rows, :cols], want)
+        assert not got[:, rows:, :].any() and not got[:, :, cols:].any()
+    else:
+        np.testing.assert_array_equal(got[:, :cols, :rows], want.transpose(0, 2, 1))
+        assert not got[:, cols:, :].any() and not got[:, :, rows:].any()
+    assert np.abs(want.astype(np.int32)).max() <= 127
+
+
+@pytest.mark.parametrize("M,N,K,batch", [(256, 256, 128, 3), (512, 768, 384, 2), (256, 512, 1024, 1)])
+def test_gemm_i8_exact(dev, M, N, K, batch):
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-127, 128, (batch, M, K), dtype=np.int8)
+    Bt = rng.integers(-127, 128, (batch, N, K), dtype=np.int8)
+    A[0, 0, :] = 127
+    Bt[0, 0, :] = 127       # largest positive sum
+    A[0, 1, :] = -127       # largest negative sum
+    bA, bB = dev.upload(A), dev.upload(Bt)
+    bC = dev.alloc(4 * batch * M * N)
+    dev.gemm_i8(bA, bB, bC, M, N, K, batch, K, K, N, M * K, N * K, M * N)
+    C = dev.download(bC, np.int32, batch * M * N).reshape(batch, M, N)
+    for t in range(batch):
+        want = A[t].astype(np.int64) @ Bt[t].astype(np.int64).T
+        np.testing.assert_array_equal(C[t].astype(np.int64), want)
+
+
+def test_gemm_i8_rejects_bad_shapes(dev):
+    bA = dev.alloc(256 * 128)
+    bC = dev.alloc(4 * 256 * 256)
+    with pytest.raises(RuntimeError):
+        dev.gemm_i8(bA, bA, bC, 256, 256, 96, 1, 96, 96, 256, 0, 0, 0)  # K not a multiple of 128
+    with pytest.raises(RuntimeError):
+        dev.gemm_i8(bA, bA, bC, 200, 256, 128, 1, 128, 128, 256, 0, 0, 0)  # M not a multiple of 256
+
+
+def exact_double(cprime: int, e: int) -> float:
+    """cprime * 2^e rounded to nearest-even, below 2^-1022 -> signed zero (the documented contract)."""
+    if cprime == 0:
+        return 0.0
+    f = math.ldexp(float(cprime), e) if abs(cprime).bit_length() < 1020 else float(cprime) * 2.0 ** e
+    if abs(f) < 2.0 ** -1022:
+        return math.copysign(0.0, cprime)
+    return f
+
+
+@pytest.mark.parametrize("moduli,b,nd", [(INT8_16, 54, 3), ([255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223,
+                                                              217, 211, 199, 197, 193, 191, 181, 179], 70, 4),
+                                         ([251, 241, 239], 10, 3)])
+def test_crt_exact(dev, oracle, moduli, b, nd):
+    rng = np.random.default_rng(len(moduli) * 31 + b)
+    Mprod = 1
+    for m in moduli:
+        Mprod *= m
+    M, N = 3, 517
+    n = M * N
+    import random
+    pyr = random.Random(int(b) * 7919 + len(moduli))
+    half = (Mprod - 1) // 2
+    vals = [pyr.randint(-half, half) >> pyr.randint(0, Mprod.bit_length() - 1) for _ in range(n)]
+    vals[:8] = [0, 1, -1, half, -half, half - 1, -(half - 1), Mprod // 3]
+    S = len(moduli)
+    C = np.empty((S, M, N), dtype=np.int32)
+    for idx, v in enumerate(vals):
+        i, j = divmod(idx, N)
+        for s, m in enumerate(moduli):
+            r = v % m
+            k = int(rng.integers(-(2 ** 31 - 1) // m + 1, (2 ** 31 - 1) // m - 1))
+            C[s, i, j] = r + k * m  # any representative within int32
+    dA = rng.integers(-5, 30, M).astype(np.int32)
+    dB = rng.integers(-5, 30, N).astype(np.int32)
+    shift = b - 20 * (nd - 1)
+    bC, bdA, bdB = dev.upload(C), dev.upload(dA), dev.upload(dB)
+    bo = dev.alloc(8 * n)
+    dev.crt(bC, M, N, N, M * N, crt_desc(moduli, b, nd), bdA, bdB, bo, N)
+    got = dev.download(bo, np.float64, n)
+    want = np.array([exact_double(vals[idx], 2 * shift - int(dA[idx // N]) - int(dB[idx % N]) - 2 * b)
+                     for idx in range(n)])
+    np.testing.assert_array_equal(got.view(np.uint64), want.view(np.uint64))
+    np.testing.assert_array_equal(got.view(np.uint64),
+                                  oracle.crt_exact(C, M, N, moduli, b, nd, dA, dB).view(np.uint64))

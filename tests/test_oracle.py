@@ -1,0 +1,163 @@
+"""The CPU oracle pinned against what the reference itself holds and against closed forms.
+
+- inputs: the reference's recorded input hashes ahash/bhash (dgemm_ref.log:6,12);
+- end to end: the reference's published output hash of II INT8 at 128^3 (tools/validated/quick.csv:13);
+- ModRound: the reference's worked examples (sfpu_tf_proc.h:271, :303, :312);
+- digits: the reference's example x = 2^-55 + 2^-80 -> A' = 0 (digits.h:44) and |A' - X| <= 1;
+- split_f64: exactness hi + mid + lo == x*2^d (checked in exact rational arithmetic);
+- residues: r == A' (mod m) and |r| <= floor(m/2), A' recomposed from the digits;
+- exact CRT: against Python integers; Dot2 and binary128 references against exact rationals.
+"""
+import math
+import random
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from tests.oracle_lib import load_oracle
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return load_oracle()
+
+
+@pytest.mark.parametrize("phi,ahash,bhash", [(0.0, 0x1d42484422793a1f, 0xd122911129734494),
+                                             (0.5, 0xef34b292fe872ee4, 0xdf4dbd7b81b31c40)])
+def test_inputs_match_reference_hashes(orc, phi, ahash, bhash):
+    n = 4096
+    a, b = orc.inputs(7, phi, n * n, n * n)
+    assert orc.hash(a) == ahash and orc.hash(b) == bhash
+
+
+INT8_K128 = [255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 83, 139]  # moduli at K=128, b=54
+
+
+def test_end_to_end_reference_hash_quick_int8(orc):
+    n, b, nd = 128, 54, 3
+    a, bb = orc.inputs(7, -1.0, n * n, n * n)
+    A, B = a.reshape(n, n), bb.reshape(n, n)
+    shift = b - 40
+    dA, fa = orc.scale(A, n, n, 0, 1, shift)
+    dB, fb = orc.scale(B, n, n, 1, 1, shift)
+    assert fa == fb == 0
+    pa = orc.residues(A, n, n, 0, dA, nd, INT8_K128)
+    pb = orc.residues(B, n, n, 1, dB, nd, INT8_K128)
+    C = np.stack([orc.gemm_i8(pa[s], pb[s])[0] for s in range(len(INT8_K128))])
+    out = orc.crt_ref(C, n, n, INT8_K128, b, nd, False, dA, dB)
+    assert orc.hash(out) == 0xfe063f5214e93e2e
+    # the exact reconstruction is at least as accurate (long-double reference)
+    R = A.astype(np.longdouble) @ B.astype(np.longdouble)
+    ex = orc.crt_exact(C, n, n, INT8_K128, b, nd, dA, dB)
+    e_ref = float(np.sqrt(np.sum((out.reshape(n, n) - R) ** 2) / np.sum(R ** 2)))
+    e_ex = float(np.sqrt(np.sum((ex.reshape(n, n) - R) ** 2) / np.sum(R ** 2)))
+    assert e_ex <= e_ref < 8 * np.finfo(float).eps
+
+
+def f32(x):
+    return float(np.float32(x))
+
+
+@pytest.mark.parametrize("d,m,expect", [(2.0 ** 24, 29, -8), (-16425964.0, 2005, -1004)])
+def test_modround_reference_examples(orc, d, m, expect):
+    assert orc.modround(d, float(m), f32(1.0 / m)) == expect
+
+
+def test_modround_crt_example(orc):
+    # sfpu_tf_proc.h:303: m = 3475, r = 1737, y = 3474 gives k = 1738 (one beyond floor(m/2))
+    m = 3475
+    assert orc.modround(f32(1737 * 3474), float(m), f32(1.0 / m)) == 1738
+
+
+def test_modround_symmetric_below_2_22(orc):
+    rng = np.random.default_rng(5)
+    for m in [255, 254, 253, 199, 47, 3]:
+        ri = f32(1.0 / m)
+        for d in rng.integers(-(2 ** 22) + 1, 2 ** 22, 2000):
+            r = orc.modround(float(d), float(m), ri)
+            assert (int(d) - int(r)) % m == 0 and abs(r) <= m // 2
+
+
+def test_split_f64_exact(orc):
+    rng = random.Random(11)
+    xs = [1.0, -1.0, 0.5, 2.0 ** -30, 1.0 + 2.0 ** -52, -(1.0 + 2.0 ** -23 + 2.0 ** -52)]
+    xs += [rng.uniform(-1, 1) * 2.0 ** rng.randint(-60, 0) for _ in range(3000)]
+    # tails around the rounding point of the 23-bit head: low 30 bits = 2^29 exactly and 2^29 + c
+    for _ in range(200):
+        x = rng.uniform(0.5, 1.0)
+        u = np.frombuffer(np.float64(x).tobytes(), np.uint64)[0]
+        for low in (0x20000000, 0x20000000 + rng.randint(1, 127), 0x1FFFFFFF):
+            v = (int(u) & ~0x3FFFFFFF) | low
+            xs.append(float(np.frombuffer(np.uint64(v).tobytes(), np.float64)[0]))
+    for x in xs:
+        d = rng.randint(-5, 20)
+        hi, mid, lo = (float(v) for v in orc.load_triple(x, d))
+        if abs(x) * 2.0 ** d >= 2.0 ** -72:
+            assert Fraction(hi) + Fraction(mid) + Fraction(lo) == Fraction(x) * Fraction(2) ** d, (x, d)
+
+
+def digits_to_int(dig):
+    nd = len(dig)
+    return sum(int(dig[j]) * (1 << (20 * (nd - 1 - j))) for j in range(nd))
+
+
+def test_digits_reference_example_and_bound(orc):
+    b, nd = 54, 3
+    shift = b - 20 * (nd - 1)
+    rng = np.random.default_rng(3)
+    X = rng.uniform(-1, 1, (4, 300)) * np.exp2(rng.integers(-40, 0, (4, 300)))
+    X[:, 0] = 1.0
+    X[0, 1] = 2.0 ** -55 + 2.0 ** -80
+    delta, _ = orc.scale(X, 4, 300, 0, 1, shift)
+    dig = orc.digits(X, 4, 300, 0, delta, nd)
+    assert digits_to_int(dig[0, 1]) == 0  # digits.h:44
+    for r in range(4):
+        e = shift - int(delta[r])
+        for c in range(300):
+            Xv = Fraction(float(X[r, c])) / Fraction(2) ** e * Fraction(2) ** b
+            assert abs(digits_to_int(dig[r, c]) - Xv) <= 1
+            assert abs(dig[r, c, 0]) <= 2 ** (b - 40) and all(abs(dig[r, c, j]) <= 2 ** 19 + 2 ** 16 + 1 for j in (1, 2))
+
+
+@pytest.mark.parametrize("b,nd", [(54, 3), (72, 4), (96, 5)])
+def test_residue_classes(orc, b, nd):
+    rng = np.random.default_rng(b)
+    X = (rng.uniform(0, 1, (8, 200)) - 0.5) * np.exp(3.0 * rng.standard_normal((8, 200)))
+    shift = b - 20 * (nd - 1)
+    delta, _ = orc.scale(X, 8, 200, 0, 1, shift)
+    moduli = [255, 254, 253, 251, 247, 241, 199, 173, 151, 47, 3]
+    dig = orc.digits(X, 8, 200, 0, delta, nd)
+    res = orc.residues(X, 8, 200, 0, delta, nd, moduli)
+    for r in range(8):
+        for c in range(200):
+            Ap = digits_to_int(dig[r, c])
+            for s, m in enumerate(moduli):
+                v = int(res[s, r, c])
+                assert (Ap - v) % m == 0 and abs(v) <= m // 2
+
+
+def test_exact_crt_against_python_integers(orc):
+    moduli = [255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199, 47, 79]
+    M = math.prod(moduli)
+    rng = random.Random(9)
+    for _ in range(300):
+        v = rng.randint(-(M - 1) // 2, (M - 1) // 2) >> rng.randint(0, 120)
+        r = [v % m - m * rng.randint(-1000, 1000) for m in moduli]
+        assert orc.crt_exact_int(np.array(r, np.int32), moduli) == v
+
+
+def test_quad_and_dot2_references(orc):
+    rng = np.random.default_rng(2)
+    M, N, K = 7, 9, 300
+    A = rng.standard_normal((M, K)) * np.exp2(rng.integers(-20, 20, (M, K)))
+    B = rng.standard_normal((K, N))
+    rows, cols = np.repeat(np.arange(M), N), np.tile(np.arange(N), M)
+    q = orc.quad_sample(A, B, M, N, K, rows, cols)
+    hi, lo = orc.dot2(A, B, M, N, K, 0, M)
+    for t in range(M * N):
+        exact = sum(Fraction(float(A[rows[t], k])) * Fraction(float(B[k, cols[t]])) for k in range(K))
+        assert q[t] == float(exact)
+        absab = sum(abs(Fraction(float(A[rows[t], k])) * Fraction(float(B[k, cols[t]]))) for k in range(K))
+        # Dot2: hi + lo carries the sum to about twice the working precision (gamma_K^2 sum|ab|)
+        assert abs(Fraction(float(hi[t])) + Fraction(float(lo[t])) - exact) <= absab * Fraction(2) ** -85

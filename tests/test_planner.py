@@ -1,0 +1,121 @@
+"""The Scheme II planner (product host code) against the reference's recorded decisions.
+
+- moduli sets at b = 54, 16 moduli requested (measure_logs/cool_oz2int8_{3520,7040,14080}.log:22)
+  and the 15-modulus set at 128^3 (tools/validated/quick.csv:13);
+- automatic width b, number of moduli and the one-pass error estimate at 4096^3, seed 7, for
+  phi = 0 ... 16 (accuracy_logs/phi_sweep.log:122,266,410,554,698,842 and phi_sweep_05.log:122);
+- closed-form invariants of every selection (coprimality, window inequality, int32 exactness).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oztt_amd as oz
+
+HEAD = [255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199]
+
+
+@pytest.mark.parametrize("K,tail", [(3520, [37, 43]), (7040, [53, 61]), (14080, [37, 173])])
+def test_moduli_records(K, tail):
+    p = oz.choose_moduli_int8(K, 16, 54)
+    assert p.ok and p.b == 54 and [p.m[i] for i in range(p.S)] == HEAD + tail
+
+
+def test_moduli_quick_128():
+    p = oz.choose_moduli_int8(128, 16, 54)
+    assert p.ok and p.S == 15 and p.b == 54
+
+
+@pytest.mark.parametrize("K", [32, 64, 1024, 4096, 8192, 16384, 65536, 133120])
+@pytest.mark.parametrize("b_cap", [54, 60, 84, 100])
+def test_selection_invariants(K, b_cap):
+    p = oz.choose_moduli_int8(K, 24, b_cap)
+    ms = [p.m[i] for i in range(p.S)]
+    for i in range(len(ms)):
+        for j in range(i + 1, len(ms)):
+            assert math.gcd(ms[i], ms[j]) == 1
+    if p.ok:
+        M = math.prod(ms)
+        assert M > 2 * K * 2 ** (2 * p.b)                    # the CRT window covers |C'| <= K 2^(2b)
+        assert all(K * (m // 2) ** 2 <= 2 ** 31 - 1 for m in ms)  # int32-exact products
+        assert p.b <= b_cap
+
+
+PHI_RECORDS = [  # phi, auto b, moduli, recon1_pred of the research planner (two-pass forced), reference logs
+    (0.0, 53, 15, -62.44), (0.5, 56, 16, -60.51), (1.0, 57, 16, -59.59), (2.0, 59, 16, -58.24),
+    (4.0, 61, 17, -54.44), (8.0, 69, 19, -47.71), (16.0, 84, 23, -32.95)]
+TABLE = [255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199, 197, 193, 191, 181, 179, 173, 167, 163,
+         157, 151]
+
+
+def research_int8_set(K, b_cap, wlog2):
+    """The INT8 selection of the research planner that wrote the phi-sweep logs: the library's rules
+    (moduli.hpp:719-769) with the CRT window log2 K replaced by a window measured from the input
+    (experiments/src/ozaki2/ozaki2_autop.hpp:104-108). Test-side restatement; the library keeps log2 K."""
+    ms, logM = [], 0.0
+    for m in TABLE:
+        ms.append(m)
+        logM += math.log2(m)
+    b = min(math.floor((logM - 1.0 - wlog2 - 1e-9) / 2.0), 100, b_cap)
+    need = 2.0 * b + 1.0 + wlog2 + 1e-9
+    while len(ms) > 2 and logM - math.log2(ms[-1]) >= need:
+        logM -= math.log2(ms.pop())
+    head = ms[:-2]
+    base = sum(math.log2(x) for x in head)
+    best, bp, bq, bcost = logM, ms[-2], ms[-1], 2
+    over = lambda l: 1 if l - need > 0.25 else 0
+    def better(c, l):
+        if c != bcost:
+            return c < bcost
+        if over(l) != over(best):
+            return over(l) < over(best)
+        return l < best
+    if logM > need:
+        step = 2 if any(x % 2 == 0 for x in head) else 1
+        cop = lambda v: all(math.gcd(v, x) == 1 for x in head)
+        for p in range(3, 256, step):
+            if not cop(p):
+                continue
+            lp = base + math.log2(p)
+            if lp >= need and better(1, lp):
+                best, bp, bq, bcost = lp, p, 0, 1
+            for q in range(p + step, 256, step):
+                if math.gcd(p, q) == 1 and cop(q):
+                    lq = lp + math.log2(q)
+                    if lq >= need and better(2, lq):
+                        best, bp, bq, bcost = lq, p, q, 2
+        ms = head + [bp] + ([bq] if bq else [])
+    return ms, b
+
+
+@pytest.mark.parametrize("phi,b,S,pred", [PHI_RECORDS[i] for i in (0, 1, 4, 6)])
+def test_auto_precision_records(phi, b, S, pred):
+    n = 4096
+    a, bb = oz.eval_inputs(7, phi, n * n, n * n)
+    p = oz.plan2_int8(a, bb, n, n, n, reconstruction=oz.Reconstruction.TwoPass)
+    assert p.b == b and p.two_pass == 1 and p.nd == (5 if b > 80 else 4 if b > 60 else 3)
+    # the library's window (log2 K) needs at least as many moduli as the research set
+    lib = oz.choose_moduli_int8(n, 24, b)
+    assert p.S == lib.S and p.S >= S
+    # the statistics behind b reproduce the research planner's one-pass estimate to 0.01 bit
+    r = math.sqrt(n)
+    f = (1 + r / math.ldexp(p.wA, b)) * (1 + r / math.ldexp(p.wB, b))
+    wlog2 = math.log2(p.wA * p.wB * max(f, 1.001))
+    ms, b_r = research_int8_set(n, b, wlog2)
+    assert b_r == b and len(ms) == S
+    est = -70.0 + sum(math.log2(m) for m in ms) - 2.0 * b + 0.5 * (math.log2(p.TA) + math.log2(p.TB) - math.log2(p.nC))
+    assert round(est, 2) == pred
+
+
+def test_fixed_width_uses_sixteen_moduli():
+    n = 4096
+    a, bb = oz.eval_inputs(7, 0.0, 64 * n, n * 64)
+    p = oz.plan2_int8(a, bb, 64, 64, n, reconstruction=oz.Reconstruction.OnePass, fixed_bits=54)
+    assert p.b == 54 and p.S == 16 and p.two_pass == 0
+
+
+def test_eval_inputs_match_reference_hashes():
+    n = 4096
+    a, b = oz.eval_inputs(7, 1.0, n * n, n * n)
+    assert oz.eval_hash(a) == 0x108dbf997fae1816 and oz.eval_hash(b) == 0x292d509b232b2c21  # dgemm_ref.log:18
