@@ -67,11 +67,18 @@ int oz_scale_f64(oz_dev* dev, const double* X, int rows, int cols, int ld, int m
  * For every element x of X (rows x cols, ld) with exponent delta d (delta[row] for mode 0,
  * delta[col] for mode 1): the triple-float of x*2^d, its nd radix-2^20 digits (nd = 3..5), and
  * for each modulus s the residue r_s == A' (mod m_s), |r_s| <= 127, as int8 (two's complement).
- * Output planes[s] has `prow` rows of `pld` bytes:
- *   layout 0 ("row"):  planes[s][r][c] for r < rows, c < cols   (A operand: K contiguous)
- *   layout 1 ("tran"): planes[s][c][r] for c < cols, r < rows   (B operand: K contiguous)
- * Entries of the padded region (row index >= rows/cols, byte index >= cols/rows) are written 0.
- * plane_stride is the byte distance between planes. */
+ * A plane is a matrix of `prow` rows and `pld` columns (entries outside the operand are 0):
+ *   layout 0 (row):        plane[r][c] = residue of X[r][c], row-major, row stride pld bytes
+ *   layout 1 (tran):       plane[c][r] = residue of X[r][c], row-major, row stride pld bytes
+ *   layout 2 (block):      as layout 0, stored in OZ_BLOCK tiles (below)
+ *   layout 3 (block tran): as layout 1, stored in OZ_BLOCK tiles
+ * OZ_BLOCK tiles: 1024-byte blocks of 16 plane rows x 64 plane columns, block (i, j) at byte
+ * (i*(pld/64) + j)*1024; inside, plane element (r, c) of the block (r < 16, c < 64) is at byte
+ * 64*r + 16*((c/16) ^ oz_block_swizzle(r)) + c%16 with oz_block_swizzle(r) = ((r>>1) ^ (r>>2)) & 3.
+ * This is the operand layout of oz_gemm_i8: one 1 KB block is one contiguous direct-to-LDS copy,
+ * and the swizzle spreads the rows of each LDS fragment read over all banks.
+ * prow and pld must be multiples of 64 (blocked: of 16 and 64); plane_stride is the byte distance
+ * between planes (multiple of 1024 for the blocked layouts). */
 typedef struct oz2_moduli_dev {
     int S;                 /* number of moduli, 1..OZ2_MAXS */
     int nd;                /* radix-2^20 digits of A', 3..5 */
@@ -86,13 +93,14 @@ int oz2_digits_f32(oz_dev* dev, const double* X, int rows, int cols, int ld, int
                    int nd, float* digits);
 
 /* ---- A9: exact integer products (reference bmm_int32_spill.cpp:265, ozaki2.cpp:333) ---------
- * C[b] = A[b] * B[b]^T for b < batch: A[b] is M x K int8 (row stride lda bytes), Bt[b] is N x K
- * int8 (row stride ldb bytes; i.e. B stored K-contiguous), C[b] is M x N int32 (row stride ldc).
+ * C[b] = A[b] * B[b]^T for b < batch: A[b] is an M x K int8 plane and Bt[b] an N x K int8 plane,
+ * both in OZ_BLOCK tiles (layout 2 / 3 of oz2_split_int8: 1 KB blocks of 16 rows x 64 K-bytes,
+ * K/64 blocks per 16 rows); C[b] is M x N int32, row stride ldc. strideA/strideB/strideC are the
+ * distances between batches in bytes (A, B) and elements (C).
  * Exact: |C| <= K*127^2 must fit int32 (the planner guarantees it, moduli.hpp:217-231).
- * Requirements: M % 256 == 0, N % 256 == 0, K % 128 == 0 (the planes are zero-padded to these),
- * lda, ldb multiples of 16. */
-int oz_gemm_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K, int batch, int lda,
-               int ldb, int ldc, long long strideA, long long strideB, long long strideC);
+ * Requirements: M % 256 == 0, N % 256 == 0, K % 64 == 0, strideA and strideB multiples of 1024. */
+int oz_gemm_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K, int batch, int ldc,
+               long long strideA, long long strideB, long long strideC);
 
 /* ---- A10-A11: CRT reconstruction to FP64 (reference recon_crt.cpp:293, recon_writer.cpp:70) --
  * For each element (i < M, j < N): C' = the integer in (-Mprod/2, Mprod/2] congruent to C_s

@@ -9,8 +9,9 @@
 //
 // Device layout (all row-major, zero-padded so that every kernel runs unguarded full tiles):
 //   A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2];
-//   residue planes of A: S x Mg x Kg int8 (K contiguous), of B: S x Ng x Kg int8 (K contiguous,
-//   i.e. B transposed) with Mg, Ng multiples of 256 and Kg of 128;
+//   residue planes of A: S x Mg x Kg int8, of B: S x Ng x Kg int8 (B transposed), both K-major in
+//   the GEMM's OZ_BLOCK tiles (1 KB blocks of 16 rows x 64 K-bytes), Mg, Ng multiples of 256 and
+//   Kg of 64;
 //   products: S x Mg x Ng int32; output: M x N f64.
 #include <chrono>
 #include <cstring>
@@ -46,7 +47,7 @@ Output ozaki2_int8_run(Device& D, const Problem& p) {
     const Plan2 plan = plan_scheme2_int8(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.max_moduli,
                                          p.options.reconstruction, fixed_b);
     const std::uint32_t M = p.m, N = p.n, K = p.k, S = (std::uint32_t)plan.S;
-    const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 128);
+    const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
     const oz2_moduli_dev mdesc = split_descriptor(plan);
     const oz2_crt_dev cdesc = crt_descriptor(plan);
 
@@ -77,18 +78,18 @@ Output ozaki2_int8_run(Device& D, const Problem& p) {
                      }});
     steps.push_back({ev::Slice, [=] {
                          device_check(dev,
-                                      oz2_split_int8(dev, dAf, (int)M, (int)K, (int)K, 0, dltA, &mdesc, planesA, 0,
+                                      oz2_split_int8(dev, dAf, (int)M, (int)K, (int)K, 0, dltA, &mdesc, planesA, 2,
                                                      (int)Mg, (int)Kg, strideA),
                                       "slice A");
                          device_check(dev,
-                                      oz2_split_int8(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, &mdesc, planesB, 1,
+                                      oz2_split_int8(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, &mdesc, planesB, 3,
                                                      (int)Ng, (int)Kg, strideB),
                                       "slice B");
                      }});
     steps.push_back({ev::Gemm, [=] {
                          device_check(dev,
                                       oz_gemm_i8(dev, planesA, planesB, prod, (int)Mg, (int)Ng, (int)Kg, (int)S,
-                                                 (int)Kg, (int)Kg, (int)Ng, strideA, strideB, strideC),
+                                                 (int)Ng, strideA, strideB, strideC),
                                       "products");
                      }});
     steps.push_back({ev::Recon, [=] {

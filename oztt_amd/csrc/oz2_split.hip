@@ -200,6 +200,47 @@ __global__ void __launch_bounds__(256) split_tran_kernel(const double* __restric
     }
 }
 
+// Layouts 2/3 (OZ_BLOCK tiles): one wave per 1 KB block of 16 plane rows x 64 plane columns.
+// Lane l owns plane row l/4 of the block and the 16 plane columns 16*(l%4)..+15; for each modulus it
+// stores those 16 residues as one 16-byte chunk at its swizzled position, so a wave writes each
+// block with one contiguous 1 KB store. TRAN: plane row = column of X (layout 3).
+__device__ __forceinline__ int block_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+template <int ND, bool TRAN>
+__global__ void __launch_bounds__(256) split_block_kernel(const double* __restrict__ X, int rows, int cols, int ld,
+                                                          int mode, const int32_t* __restrict__ delta, SplitConsts k,
+                                                          int S, uint4* __restrict__ planes, int kblocks,
+                                                          long long nblocks, long long pstride_chunks) {
+    const long long blk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);  // block index within a plane
+    if (blk >= nblocks) return;
+    const int lane = threadIdx.x & 63;
+    const int br = (int)(blk / kblocks), bk = (int)(blk % kblocks);
+    const int pr = br * 16 + (lane >> 2);          // plane row
+    const int pc0 = bk * 64 + 16 * (lane & 3);     // first of this lane's 16 plane columns
+    float dig[16][ND];
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const int xr = TRAN ? pc0 + e : pr, xc = TRAN ? pr : pc0 + e;
+        if (xr < rows && xc < cols) {
+            const int32_t d = mode == 0 ? delta[xr] : delta[xc];
+            make_digits<ND>(X[(size_t)xr * ld + xc], d, dig[e]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < ND; j++) dig[e][j] = 0.0f;
+        }
+    }
+    const int rr = lane >> 2;
+    uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
+    for (int s = 0; s < S; s++) {
+        uint4 v;
+        v.x = pack4(residue<ND>(dig[0], k, s), residue<ND>(dig[1], k, s), residue<ND>(dig[2], k, s), residue<ND>(dig[3], k, s));
+        v.y = pack4(residue<ND>(dig[4], k, s), residue<ND>(dig[5], k, s), residue<ND>(dig[6], k, s), residue<ND>(dig[7], k, s));
+        v.z = pack4(residue<ND>(dig[8], k, s), residue<ND>(dig[9], k, s), residue<ND>(dig[10], k, s), residue<ND>(dig[11], k, s));
+        v.w = pack4(residue<ND>(dig[12], k, s), residue<ND>(dig[13], k, s), residue<ND>(dig[14], k, s), residue<ND>(dig[15], k, s));
+        out[(long long)s * pstride_chunks] = v;
+    }
+}
+
 template <int ND>
 __global__ void digits_kernel(const double* __restrict__ X, int rows, int cols, int ld, int mode,
                               const int32_t* __restrict__ delta, float* __restrict__ out) {
@@ -231,6 +272,18 @@ int launch_split(oz_dev* dev, const double* X, int rows, int cols, int ld, int m
                            cols, ld, mode, delta, k, S, reinterpret_cast<uint32_t*>(planes), prow, pq, pstride / 4);
         return oz::launch_check(dev, "split_row_kernel");
     }
+    if (layout >= 2) {
+        const int kblocks = pld / 64;
+        const long long nblocks = (long long)(prow / 16) * kblocks;
+        const unsigned grid = oz::ceil_div(nblocks, 4);
+        if (layout == 2)
+            hipLaunchKernelGGL((split_block_kernel<ND, false>), dim3(grid), dim3(256), 0, dev->stream, X, rows, cols, ld,
+                               mode, delta, k, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks, pstride / 16);
+        else
+            hipLaunchKernelGGL((split_block_kernel<ND, true>), dim3(grid), dim3(256), 0, dev->stream, X, rows, cols, ld,
+                               mode, delta, k, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks, pstride / 16);
+        return oz::launch_check(dev, "split_block_kernel");
+    }
     // transposed: plane rows = columns of X (prow of them, multiple of 64); plane bytes = rows of X
     hipLaunchKernelGGL(split_tran_kernel<ND>, dim3(prow / 64, pld / 64), dim3(256), 0, dev->stream, X, rows, cols, ld,
                        mode, delta, k, S, reinterpret_cast<uint32_t*>(planes), pld / 4, pstride / 4);
@@ -244,13 +297,16 @@ extern "C" int oz2_split_int8(oz_dev* dev, const double* X, int rows, int cols, 
                               int pld, long long plane_stride) {
     if (int st = oz::use(dev)) return st;
     if (int st = check_moduli(dev, mo)) return st;
-    if (!X || !delta || !planes || rows <= 0 || cols <= 0 || ld < cols || (mode != 0 && mode != 1) ||
-        (layout != 0 && layout != 1))
+    if (!X || !delta || !planes || rows <= 0 || cols <= 0 || ld < cols || (mode != 0 && mode != 1) || layout < 0 ||
+        layout > 3)
         return oz::fail(dev, OZ_ERR_ARG, "oz2_split_int8: invalid arguments");
-    // The plane must hold the operand: layout 0 rows x cols, layout 1 cols x rows.
-    const int need_rows = layout == 0 ? rows : cols, need_ld = layout == 0 ? cols : rows;
+    // The plane must hold the operand: layouts 0/2 rows x cols, layouts 1/3 cols x rows.
+    const bool tran = layout == 1 || layout == 3;
+    const int need_rows = tran ? cols : rows, need_ld = tran ? rows : cols;
+    const bool blocked = layout >= 2;
     if (prow < need_rows || pld < need_ld || pld % 64 != 0 || (layout == 1 && prow % 64 != 0) ||
-        plane_stride < (long long)prow * pld || plane_stride % 16 != 0 || ((uintptr_t)planes & 15u))
+        (blocked && (prow % 16 != 0 || plane_stride % 1024 != 0)) || plane_stride < (long long)prow * pld ||
+        plane_stride % 16 != 0 || ((uintptr_t)planes & 15u))
         return oz::fail(dev, OZ_ERR_ARG, "oz2_split_int8: plane geometry %dx%d (stride %lld) does not fit", prow, pld,
                         plane_stride);
     SplitConsts k{};

@@ -2,149 +2,195 @@
 //
 // Semantics (reference bmm_int32_spill.cpp:265 as driven by ozaki2.cpp:333-350): for every modulus,
 // C_s = A_s * B_s with exact int32 accumulation (the planner bounds |C_s| <= K*127^2 < 2^31,
-// moduli.hpp:217-231). Integer MFMA accumulation is exact, so the result is independent of the
+// moduli.hpp:217-231). Integer MFMA accumulation is exact, so the result does not depend on the
 // summation order.
 //
-// MI355X design: both operands are K-contiguous int8 planes (A: M x K, Bt: N x K), zero-padded to
-// the tile grid, so every global load is a 16-byte vector and every LDS fragment read feeds one
-// v_mfma_i32_16x16x64_i8 directly (lane l holds row l%16, bytes 16*(l/16)..+15 of a 64-byte K
-// slice for both operands; output lane l holds column l%16, rows 4*(l/16)..+3). A workgroup of 4
-// waves computes a BM x BN tile; K advances in BK-byte steps through double-buffered LDS with the
-// next step's global loads in flight during the current step's MFMAs. Workgroups are ordered
-// moduli-major with the N tiles of one row band adjacent, so concurrently running workgroups
-// share A rows in L2.
+// MI355X design
+//   - Operands are int8 planes in OZ_BLOCK tiles (written so by the splitter): 1 KB blocks of 16
+//     rows x 64 K-bytes, the K/64 blocks of each 16-row band consecutive, zero-padded to the tile
+//     grid, so no load is guarded. Inside a block, 16-byte chunk c of row r sits at chunk position
+//     c ^ f(r), f(r) = ((r >> 1) ^ (r >> 2)) & 3.
+//   - A workgroup of 4 waves (one per SIMD) computes a 256 x 256 tile; each wave owns 128 x 128
+//     (4 x 4 blocks of v_mfma_i32_32x32x32_i8, 256 accumulator registers). A single wave keeps the
+//     32x32x32 MFMA pipe close to full, unlike the 16x16x64 form (measured on MI355X). Lane l holds
+//     row l%32 and the 16 K-bytes 16*(l/32).. of a 32-byte K slice of both operands; output register
+//     q of lane l is row 8*(q/4) + 4*(l/32) + q%4, column l%32.
+//   - K advances in 64-byte steps through a ring of NS LDS stages filled by direct global->LDS
+//     loads (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS base + 16*l),
+//     NS-1 stages ahead of the MFMAs, with no register staging. One wave instruction copies one
+//     whole 1 KB block, contiguous in HBM and in LDS, so a stage's 256 rows are 16 blocks per
+//     operand and the swizzle comes with the data: the 64 lanes of each fragment read
+//     (ds_read_b128, rows r..r+31, two chunk columns) spread evenly over the LDS banks.
+//   - Workgroups are mapped to tiles XCD-aware (tile_of below).
 #include "oz_internal.hpp"
 
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-template <int BM, int BN, int BK, int WGM, int WGN>
-struct GemmCfg {
-    static constexpr int THREADS = 64 * WGM * WGN;
-    static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
-    static constexpr int FM = WM / 16, FN = WN / 16;    // 16x16 fragments per wave
-    static constexpr int LDSROW = BK + 16;              // bytes per LDS row (padded)
-    static constexpr int A_CHUNKS = BM * BK / 16;       // 16-byte chunks per stage
-    static constexpr int B_CHUNKS = BN * BK / 16;
-    static constexpr int A_PER_T = A_CHUNKS / THREADS;
-    static constexpr int B_PER_T = B_CHUNKS / THREADS;
-    static_assert(A_CHUNKS % THREADS == 0 && B_CHUNKS % THREADS == 0, "tile loads must divide evenly");
-    static_assert(BK % 64 == 0, "K step is a multiple of the MFMA K (64)");
-    static constexpr int LDS_BYTES = 2 * (BM + BN) * LDSROW;
-};
-
-template <int BM, int BN, int BK, int WGM, int WGN>
-__global__ void __launch_bounds__(64 * WGM * WGN) gemm_i8_kernel(const int8_t* __restrict__ A,
-                                                                  const int8_t* __restrict__ Bt,
-                                                                  int32_t* __restrict__ C, int M, int N, int K, int lda,
-                                                                  int ldb, int ldc, long long sA, long long sB,
-                                                                  long long sC, int tiles_n, int tiles_per_batch) {
-    using G = GemmCfg<BM, BN, BK, WGM, WGN>;
-    __shared__ __attribute__((aligned(16))) int8_t lds[G::LDS_BYTES];
-    constexpr int STAGE = (BM + BN) * G::LDSROW;  // bytes of one stage: A rows, then B rows
-
-    const int tid = threadIdx.x;
-    const int batch = blockIdx.x / tiles_per_batch;
-    const int tile = blockIdx.x % tiles_per_batch;
-    const int tm = tile / tiles_n, tn = tile % tiles_n;
-    const int8_t* Ab = A + batch * sA + (long long)tm * BM * lda;
-    const int8_t* Bb = Bt + batch * sB + (long long)tn * BN * ldb;
-
-    const int wave = tid >> 6, lane = tid & 63;
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int frow = lane & 15, fk = (lane >> 4) * 16;
-
-    v4i acc[G::FM][G::FN];
-#pragma unroll
-    for (int i = 0; i < G::FM; i++)
-#pragma unroll
-        for (int j = 0; j < G::FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
-
-    uint4 ra[G::A_PER_T], rb[G::B_PER_T];
-    constexpr int CPR = BK / 16;  // 16-byte chunks per row of a stage
-#define OZ_GEMM_GLOAD(k0)                                                                                   \
-    do {                                                                                                    \
-        _Pragma("unroll") for (int i = 0; i < G::A_PER_T; i++) {                                            \
-            const int c = tid + i * G::THREADS;                                                             \
-            ra[i] = *reinterpret_cast<const uint4*>(Ab + (long long)(c / CPR) * lda + (k0) + (c % CPR) * 16); \
-        }                                                                                                   \
-        _Pragma("unroll") for (int i = 0; i < G::B_PER_T; i++) {                                            \
-            const int c = tid + i * G::THREADS;                                                             \
-            rb[i] = *reinterpret_cast<const uint4*>(Bb + (long long)(c / CPR) * ldb + (k0) + (c % CPR) * 16); \
-        }                                                                                                   \
-    } while (0)
-#define OZ_GEMM_LSTORE(buf)                                                                              \
-    do {                                                                                                 \
-        int8_t* sa = lds + (buf) * STAGE;                                                                \
-        int8_t* sb = sa + BM * G::LDSROW;                                                                \
-        _Pragma("unroll") for (int i = 0; i < G::A_PER_T; i++) {                                         \
-            const int c = tid + i * G::THREADS;                                                          \
-            *reinterpret_cast<uint4*>(sa + (c / CPR) * G::LDSROW + (c % CPR) * 16) = ra[i];              \
-        }                                                                                                \
-        _Pragma("unroll") for (int i = 0; i < G::B_PER_T; i++) {                                         \
-            const int c = tid + i * G::THREADS;                                                          \
-            *reinterpret_cast<uint4*>(sb + (c / CPR) * G::LDSROW + (c % CPR) * 16) = rb[i];              \
-        }                                                                                                \
-    } while (0)
-
-    const int nk = K / BK;
-#define OZ_GEMM_COMPUTE(cur)                                                                                  \
-    do {                                                                                                      \
-        const int8_t* la = lds + (cur) * STAGE + (wm * G::WM + frow) * G::LDSROW + fk;                        \
-        const int8_t* lb = lds + (cur) * STAGE + BM * G::LDSROW + (wn * G::WN + frow) * G::LDSROW + fk;       \
-        _Pragma("unroll") for (int ks = 0; ks < BK; ks += 64) {                                               \
-            v4i fa[G::FM], fb[G::FN];                                                                         \
-            _Pragma("unroll") for (int i = 0; i < G::FM; i++) fa[i] =                                         \
-                *reinterpret_cast<const v4i*>(la + i * 16 * G::LDSROW + ks);                                  \
-            _Pragma("unroll") for (int j = 0; j < G::FN; j++) fb[j] =                                         \
-                *reinterpret_cast<const v4i*>(lb + j * 16 * G::LDSROW + ks);                                  \
-            _Pragma("unroll") for (int i = 0; i < G::FM; i++) _Pragma("unroll") for (int j = 0; j < G::FN; j++) \
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);          \
-        }                                                                                                     \
-    } while (0)
-    OZ_GEMM_GLOAD(0);
-    OZ_GEMM_LSTORE(0);
-    __syncthreads();
-    for (int kt = 0; kt + 1 < nk; kt++) {
-        OZ_GEMM_GLOAD((kt + 1) * BK);
-        OZ_GEMM_COMPUTE(kt & 1);
-        OZ_GEMM_LSTORE((kt + 1) & 1);
-        __syncthreads();
-    }
-    OZ_GEMM_COMPUTE((nk - 1) & 1);
-#undef OZ_GEMM_COMPUTE
-#undef OZ_GEMM_GLOAD
-#undef OZ_GEMM_LSTORE
-
-    int32_t* Cb = C + batch * sC + (long long)(tm * BM + wm * G::WM) * ldc + tn * BN + wn * G::WN;
-#pragma unroll
-    for (int i = 0; i < G::FM; i++)
-#pragma unroll
-        for (int j = 0; j < G::FN; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                Cb[(long long)(i * 16 + (lane >> 4) * 4 + r) * ldc + j * 16 + (lane & 15)] = acc[i][j][r];
+// Workgroup -> (batch, tile row, tile column). Workgroups are dispatched round-robin over the 8
+// XCDs (workgroup w runs on XCD w % 8), and each XCD has its own L2. The map gives every XCD one
+// contiguous range of the logical tile sequence, and orders that sequence batch-major, then in
+// groups of GROUP_M tile rows walked column by column, so the ~32 workgroups an XCD runs at a time
+// cover a compact block of tiles and share their A rows and B columns in that L2. It is a
+// bijection for any workgroup count.
+constexpr int XCDS = 8, GROUP_M = 4;
+__device__ __forceinline__ void tile_of(int w, int tiles_m, int tiles_n, int nbatch, int& batch, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n * nbatch;
+    const int q = total / XCDS, r = total % XCDS;
+    const int x = w % XCDS, j = w / XCDS;
+    const int t = x * q + min(x, r) + j;  // logical index
+    const int per_batch = tiles_m * tiles_n;
+    batch = t / per_batch;
+    const int u = t % per_batch;
+    const int group = u / (GROUP_M * tiles_n);
+    const int first_m = group * GROUP_M;
+    const int gm = min(tiles_m - first_m, GROUP_M);
+    const int v = u % (GROUP_M * tiles_n);
+    tm = first_m + v % gm;
+    tn = v / gm;
 }
 
-using Cfg128 = GemmCfg<128, 128, 128, 2, 2>;
+// Workgroup barrier without the memory fences of __syncthreads(): those would wait for every
+// outstanding load, including the direct-to-LDS loads of the stages still in flight. Each wave
+// first waits (vmcnt) for its own loads of the stage about to be read, so after the barrier the
+// whole stage is in LDS; the empty asm statements keep the compiler from moving LDS accesses
+// across the barrier.
+__device__ __forceinline__ void stage_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding of simm16).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+constexpr int BM = 256, BN = 256, BK = 64, NS = 4, THREADS = 256;
+constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;  // bytes
+constexpr int LOADS_A = STAGE_A / 16 / THREADS, LOADS_B = STAGE_B / 16 / THREADS;  // per thread per stage
+static_assert(LOADS_A == 4 && LOADS_B == 4, "each thread moves 4+4 chunks of 16 bytes per stage");
+
+__global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ Bt,
+                                                          int32_t* __restrict__ C, int K, int ldc, long long sA,
+                                                          long long sB, long long sC, int tiles_m, int tiles_n,
+                                                          int nbatch) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[NS * STAGE];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    int batch, tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, nbatch, batch, tm, tn);
+    const int nk = K / BK;  // blocks per 16-row band
+    const long long band = (long long)nk * 1024;  // bytes of one 16-row band
+    // Lane l copies bytes 16l..16l+15 of each block; the tile's first band is 16*tm (A), 16*tn (B).
+    const int8_t* Ab = A + batch * sA + (long long)tm * (BM / 16) * band + 16 * lane;
+    const int8_t* Bb = Bt + batch * sB + (long long)tn * (BN / 16) * band + 16 * lane;
+
+    // Loader: wave instruction j (= 4*i + wave) copies block (band j of the tile, K step kstep) to
+    // bytes 1024j.. of the stage, i.e. rows 16j..16j+15 of the 256 x 64 stage, swizzle included.
+#define OZ_GEMM_ISSUE(kstep, buf)                                                                                 \
+    do {                                                                                                          \
+        const long long koff = (long long)(kstep) * 1024;                                                         \
+        int8_t* sa = lds + (buf) * STAGE;                                                                         \
+        _Pragma("unroll") for (int i = 0; i < LOADS_A; i++)                                                       \
+            __builtin_amdgcn_global_load_lds(Ab + (4 * i + wave) * band + koff, (lds_void*)(sa + 1024 * (4 * i + wave)), \
+                                             16, 0, 0);                                                           \
+        _Pragma("unroll") for (int i = 0; i < LOADS_B; i++)                                                       \
+            __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + koff,                                   \
+                                             (lds_void*)(sa + STAGE_A + 1024 * (4 * i + wave)), 16, 0, 0);        \
+    } while (0)
+
+    const int wm = wave >> 1, wn = wave & 1;
+    // fragment addresses: row r = lane%32 of each 32-row block, logical chunk c = 2*ks + lane/32,
+    // stored at chunk position c ^ f(r) (f sees bits 1..3 of r only, so r%16 or r gives the same)
+    const int frow = lane & 31;
+    int offA[2], offB[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const int pos = 16 * ((2 * ks + (lane >> 5)) ^ (((frow >> 1) ^ (frow >> 2)) & 3));
+        offA[ks] = (wm * 128 + frow) * BK + pos;
+        offB[ks] = STAGE_A + (wn * 128 + frow) * BK + pos;
+    }
+
+    v16i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc[i][j][q] = 0;
+
+    // Pipeline. Loads run NS stages ahead: at step kt the stages kt+1 .. kt+NS are in flight or
+    // landed. The fragments of stage kt are already in registers (read during step kt-1); step kt
+    // waits for stage kt+1, refills the buffer of stage kt (nobody reads it any more) with stage
+    // kt+NS, and reads the fragments of stage kt+1 while its MFMAs run on those of stage kt. The
+    // tail re-loads the last valid step (clamped), so every step has the same number of loads in
+    // flight and the same wait count.
+#pragma unroll
+    for (int s = 0; s < NS; s++) OZ_GEMM_ISSUE(min(s, nk - 1), s);
+    v4i fa[2][4], fb[2][4], ga[2][4], gb[2][4];  // [k substep][block]
+    wait_vmcnt<(LOADS_A + LOADS_B) * (NS - 1)>();  // stage 0
+    stage_barrier();
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            fa[ks][i] = *reinterpret_cast<const v4i*>(lds + offA[ks] + i * 32 * BK);
+            fb[ks][i] = *reinterpret_cast<const v4i*>(lds + offB[ks] + i * 32 * BK);
+        }
+#define OZ_GEMM_STEP(kt, F_A, F_B, G_A, G_B)                                                                     \
+    do {                                                                                                         \
+        wait_vmcnt<(LOADS_A + LOADS_B) * (NS - 2)>(); /* stage kt+1 landed (this thread) */                       \
+        stage_barrier();                              /* ... everyone's; stage kt fully read */                  \
+        OZ_GEMM_ISSUE(min((kt) + NS, nk - 1), (kt) % NS);                                                        \
+        const int8_t* nx = lds + (((kt) + 1) % NS) * STAGE;                                                      \
+        _Pragma("unroll") for (int ks = 0; ks < 2; ks++) {                                                       \
+            _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                      \
+                G_A[ks][i] = *reinterpret_cast<const v4i*>(nx + offA[ks] + i * 32 * BK);                         \
+                G_B[ks][i] = *reinterpret_cast<const v4i*>(nx + offB[ks] + i * 32 * BK);                         \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) acc[i][j] =                                        \
+                    __builtin_amdgcn_mfma_i32_32x32x32_i8(F_A[ks][i], F_B[ks][j], acc[i][j], 0, 0, 0);           \
+            }                                                                                                    \
+        }                                                                                                        \
+    } while (0)
+    int kt = 0;
+    for (; kt + 2 <= nk; kt += 2) {
+        OZ_GEMM_STEP(kt, fa, fb, ga, gb);
+        OZ_GEMM_STEP(kt + 1, ga, gb, fa, fb);
+    }
+    if (kt < nk) OZ_GEMM_STEP(kt, fa, fb, ga, gb);  // (the prefetch of the clamped stage is unused)
+#undef OZ_GEMM_STEP
+#undef OZ_GEMM_ISSUE
+    wait_vmcnt<0>();  // drain the clamped tail loads before the workgroup ends
+
+    int32_t* Cb = C + batch * sC + (long long)(tm * BM + wm * 128) * ldc + tn * BN + wn * 128;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int q = 0; q < 16; q++)
+                Cb[(long long)(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * ldc + 32 * j + (lane & 31)] =
+                    acc[i][j][q];
+}
 
 }  // namespace
 
 extern "C" int oz_gemm_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K, int batch,
-                          int lda, int ldb, int ldc, long long strideA, long long strideB, long long strideC) {
+                          int ldc, long long strideA, long long strideB, long long strideC) {
     if (int st = oz::use(dev)) return st;
-    constexpr int BM = 128, BN = 128, BK = 128;
-    if (!A || !Bt || !C || M <= 0 || N <= 0 || K <= 0 || batch <= 0 || M % 256 || N % 256 || K % 128 || lda < K ||
-        ldb < K || ldc < N || lda % 16 || ldb % 16 || ((uintptr_t)A & 15) || ((uintptr_t)Bt & 15))
-        return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: unsupported shape M=%d N=%d K=%d lda=%d ldb=%d", M, N, K, lda, ldb);
-    if (K % BK)
-        return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: K=%d must be a multiple of %d", K, BK);
-    const int tiles_n = N / BN, tiles_m = M / BM;
+    if (!A || !Bt || !C || M <= 0 || N <= 0 || K <= 0 || batch <= 0 || M % BM || N % BN || K % BK || ldc < N ||
+        ((uintptr_t)A & 15) || ((uintptr_t)Bt & 15) || strideA % 1024 || strideB % 1024 ||
+        (batch > 1 && (strideA < (long long)M * K || strideB < (long long)N * K || strideC < (long long)M * ldc)))
+        return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: unsupported shape M=%d N=%d K=%d batch=%d", M, N, K, batch);
+    const int tiles_m = M / BM, tiles_n = N / BN;
     const long long grid = (long long)tiles_m * tiles_n * batch;
     if (grid > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: grid too large");
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, 2, 2>), dim3((unsigned)grid), dim3(Cfg128::THREADS), 0,
-                       dev->stream, A, Bt, C, M, N, K, lda, ldb, ldc, strideA, strideB, strideC,
-                       tiles_n, tiles_m * tiles_n);
+    hipLaunchKernelGGL(gemm_i8_kernel, dim3((unsigned)grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc, strideA,
+                       strideB, strideC, tiles_m, tiles_n, batch);
     return oz::launch_check(dev, "gemm_i8_kernel");
 }

@@ -135,10 +135,44 @@ class Device:
     def digits(self, X: Buffer, rows, cols, ld, mode, delta: Buffer, nd, out: Buffer):
         self._check(hip().oz2_digits_f32(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, nd, out.ptr), "oz2_digits_f32")
 
-    def gemm_i8(self, A: Buffer, Bt: Buffer, C: Buffer, M, N, K, batch, lda, ldb, ldc, sA, sB, sC):
-        self._check(hip().oz_gemm_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, batch, lda, ldb, ldc, ctypes.c_longlong(sA),
+    def gemm_i8(self, A: Buffer, Bt: Buffer, C: Buffer, M, N, K, batch, ldc, sA, sB, sC):
+        """C[b] = A[b] Bt[b]^T with A, Bt in OZ_BLOCK tiles (see to_blocks)."""
+        self._check(hip().oz_gemm_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, batch, ldc, ctypes.c_longlong(sA),
                                      ctypes.c_longlong(sB), ctypes.c_longlong(sC)), "oz_gemm_i8")
 
     def crt(self, C: Buffer, M, N, ldc, sC, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
         self._check(hip().oz2_crt_f64(self.h, C.ptr, M, N, ldc, ctypes.c_longlong(sC), ctypes.byref(desc), dA.ptr,
                                       dB.ptr, out.ptr, ldo), "oz2_crt_f64")
+
+
+
+def block_swizzle(r):
+    """Chunk swizzle of the OZ_BLOCK tiles: ((r >> 1) ^ (r >> 2)) & 3."""
+    return ((r >> 1) ^ (r >> 2)) & 3
+
+
+def block_offsets(R: int, C: int) -> np.ndarray:
+    """Byte offset, in OZ_BLOCK tiles, of every element of a row-major R x C plane (R % 16 == 0,
+    C % 64 == 0): block (i, j) of 16 rows x 64 columns at (i*(C/64) + j)*1024, element (r, c) of a
+    block at 64*r + 16*((c/16) ^ block_swizzle(r)) + c%16."""
+    if R % 16 or C % 64:
+        raise ValueError("OZ_BLOCK planes need R % 16 == 0 and C % 64 == 0")
+    r = np.arange(R, dtype=np.int64)[:, None]
+    c = np.arange(C, dtype=np.int64)[None, :]
+    rb, cb = r % 16, c % 64
+    return ((r // 16) * (C // 64) + c // 64) * 1024 + 64 * rb + 16 * ((cb // 16) ^ block_swizzle(rb)) + cb % 16
+
+
+def to_blocks(plane: np.ndarray) -> np.ndarray:
+    """Row-major planes (..., R, C) -> the same bytes in OZ_BLOCK tiles, flat per plane (..., R*C)."""
+    *lead, R, C = plane.shape
+    src = plane.reshape(-1, R * C)
+    out = np.empty_like(src)
+    out[:, block_offsets(R, C).ravel()] = src
+    return out.reshape(*lead, R * C)
+
+
+def from_blocks(blocks: np.ndarray, R: int, C: int) -> np.ndarray:
+    """Inverse of to_blocks: planes in OZ_BLOCK tiles (..., R*C) -> row-major (..., R, C)."""
+    src = blocks.reshape(-1, R * C)
+    return src[:, block_offsets(R, C).ravel()].reshape(*blocks.shape[:-1], R, C)

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oztt_amd as oz
-from oztt_amd.device import crt_desc, moduli_desc
+from oztt_amd.device import crt_desc, from_blocks, moduli_desc
 
 pytestmark = pytest.mark.gpu
 
@@ -103,7 +103,7 @@ def test_too_few_moduli_rejected_and_c_untouched(ctx):
 def run_stages(dev, A, B, M, N, K, moduli, b, nd):
     """scale -> split -> products -> CRT on the GPU through the C ABI; returns host copies."""
     S = len(moduli)
-    Mg, Ng, Kg = -(-M // 256) * 256, -(-N // 256) * 256, -(-K // 128) * 128
+    Mg, Ng, Kg = -(-M // 256) * 256, -(-N // 256) * 256, -(-K // 64) * 64
     shift = b - 20 * (nd - 1)
     bA, bB = dev.upload(A), dev.upload(B)
     bdA, bdB = dev.alloc(4 * M), dev.alloc(4 * N)
@@ -113,16 +113,16 @@ def run_stages(dev, A, B, M, N, K, moduli, b, nd):
     dev.scale(bB, K, N, N, 1, 1, shift, bdB, bfl, 1)
     md = moduli_desc(moduli, nd)
     pA, pB = dev.alloc(S * Mg * Kg), dev.alloc(S * Ng * Kg)
-    dev.split_int8(bA, M, K, K, 0, bdA, md, pA, 0, Mg, Kg, Mg * Kg)
-    dev.split_int8(bB, K, N, N, 1, bdB, md, pB, 1, Ng, Kg, Ng * Kg)
+    dev.split_int8(bA, M, K, K, 0, bdA, md, pA, 2, Mg, Kg, Mg * Kg)  # OZ_BLOCK tiles
+    dev.split_int8(bB, K, N, N, 1, bdB, md, pB, 3, Ng, Kg, Ng * Kg)
     bC = dev.alloc(4 * S * Mg * Ng)
-    dev.gemm_i8(pA, pB, bC, Mg, Ng, Kg, S, Kg, Kg, Ng, Mg * Kg, Ng * Kg, Mg * Ng)
+    dev.gemm_i8(pA, pB, bC, Mg, Ng, Kg, S, Ng, Mg * Kg, Ng * Kg, Mg * Ng)
     bo = dev.alloc(8 * M * N)
     dev.crt(bC, M, N, Ng, Mg * Ng, crt_desc(moduli, b, nd), bdA, bdB, bo, N)
     r = dict(dA=dev.download(bdA, np.int32, M), dB=dev.download(bdB, np.int32, N),
              flags=dev.download(bfl, np.uint32, 2),
-             planesA=dev.download(pA, np.int8, S * Mg * Kg).reshape(S, Mg, Kg)[:, :M, :K],
-             planesB=dev.download(pB, np.int8, S * Ng * Kg).reshape(S, Ng, Kg)[:, :N, :K],
+             planesA=from_blocks(dev.download(pA, np.int8, S * Mg * Kg).reshape(S, -1), Mg, Kg)[:, :M, :K],
+             planesB=from_blocks(dev.download(pB, np.int8, S * Ng * Kg).reshape(S, -1), Ng, Kg)[:, :N, :K],
              C=dev.download(bC, np.int32, S * Mg * Ng).reshape(S, Mg, Ng)[:, :M, :N],
              out=dev.download(bo, np.float64, M * N))
     for buf in (bA, bB, bdA, bdB, bfl, pA, pB, bC, bo):

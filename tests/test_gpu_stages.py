@@ -7,7 +7,7 @@ import math
 import numpy as np
 import pytest
 
-from oztt_amd.device import Device, crt_desc, moduli_desc
+from oztt_amd.device import Device, crt_desc, from_blocks, moduli_desc, to_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -108,13 +108,16 @@ def moduli_for(b, nd, K):
     return [p.m[i] for i in range(p.S)]
 
 
-@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("layout", [0, 1, 2, 3])
 @pytest.mark.parametrize("nd,b,phi", [(3, 54, 0.5), (3, 56, 2.0), (4, 70, 4.0), (5, 90, 1.0)])
 def test_residues_match_oracle(dev, oracle, layout, nd, b, phi):
+    """Layouts 0/2: A operand (rows of X = plane rows); 1/3: B operand (plane rows = columns of X).
+    Layouts 2/3 are the OZ_BLOCK tiles of the GEMM, decoded on the host."""
     rng = np.random.default_rng(1000 + 10 * nd + layout)
-    rows, cols = (96, 200) if layout == 0 else (200, 96)
-    X = split_inputs(rows, cols, rng, phi) if layout == 0 else split_inputs(cols, rows, rng, phi).T.copy()
-    mode = 0 if layout == 0 else 1
+    tran = layout in (1, 3)
+    rows, cols = (200, 96) if tran else (96, 200)
+    X = split_inputs(cols, rows, rng, phi).T.copy() if tran else split_inputs(rows, cols, rng, phi)
+    mode = 1 if tran else 0
     shift = b - 20 * (nd - 1)
     moduli = moduli_for(b, nd, 4096)
     if 254 not in moduli:
@@ -122,15 +125,16 @@ def test_residues_match_oracle(dev, oracle, layout, nd, b, phi):
     delta, _ = oracle.scale(X, rows, cols, mode, 1, shift)
     want = oracle.residues(X, rows, cols, mode, delta, nd, moduli)  # [S][rows][cols]
     S = len(moduli)
-    prow = (rows if layout == 0 else cols)
+    prow = (cols if tran else rows)
     prow = (prow + 63) // 64 * 64 + 64
-    pld = ((cols if layout == 0 else rows) + 63) // 64 * 64 + 64
-    pstride = prow * pld + 128
+    pld = ((rows if tran else cols) + 63) // 64 * 64 + 64
+    pstride = prow * pld + 1024
     bx, bd = dev.upload(X), dev.upload(delta)
     bp = dev.alloc(S * pstride)
     dev.split_int8(bx, rows, cols, cols, mode, bd, moduli_desc(moduli, nd), bp, layout, prow, pld, pstride)
-    got = dev.download(bp, np.int8, S * pstride).reshape(S, pstride)[:, :prow * pld].reshape(S, prow, pld)
-    if layout == 0:
+    got = dev.download(bp, np.int8, S * pstride).reshape(S, pstride)[:, :prow * pld]
+    got = from_blocks(got, prow, pld) if layout >= 2 else got.reshape(S, prow, pld)
+    if not tran:
         np.testing.assert_array_equal(got[:, :rows, :cols], want)
         assert not got[:, rows:, :].any() and not got[:, :, cols:].any()
     else:
@@ -139,17 +143,19 @@ def test_residues_match_oracle(dev, oracle, layout, nd, b, phi):
     assert np.abs(want.astype(np.int32)).max() <= 127
 
 
-@pytest.mark.parametrize("M,N,K,batch", [(256, 256, 128, 3), (512, 768, 384, 2), (256, 512, 1024, 1)])
+@pytest.mark.parametrize("M,N,K,batch", [(256, 256, 128, 3), (512, 768, 384, 2), (256, 512, 1024, 1),
+                                         (256, 256, 64, 2), (512, 256, 320, 1)])
 def test_gemm_i8_exact(dev, M, N, K, batch):
+    """Operands in OZ_BLOCK tiles; K/64 odd and K = 64 exercise the pipeline's tail."""
     rng = np.random.default_rng(M + N + K)
     A = rng.integers(-127, 128, (batch, M, K), dtype=np.int8)
     Bt = rng.integers(-127, 128, (batch, N, K), dtype=np.int8)
     A[0, 0, :] = 127
     Bt[0, 0, :] = 127       # largest positive sum
     A[0, 1, :] = -127       # largest negative sum
-    bA, bB = dev.upload(A), dev.upload(Bt)
+    bA, bB = dev.upload(to_blocks(A)), dev.upload(to_blocks(Bt))
     bC = dev.alloc(4 * batch * M * N)
-    dev.gemm_i8(bA, bB, bC, M, N, K, batch, K, K, N, M * K, N * K, M * N)
+    dev.gemm_i8(bA, bB, bC, M, N, K, batch, N, M * K, N * K, M * N)
     C = dev.download(bC, np.int32, batch * M * N).reshape(batch, M, N)
     for t in range(batch):
         want = A[t].astype(np.int64) @ Bt[t].astype(np.int64).T
@@ -160,9 +166,11 @@ def test_gemm_i8_rejects_bad_shapes(dev):
     bA = dev.alloc(256 * 128)
     bC = dev.alloc(4 * 256 * 256)
     with pytest.raises(RuntimeError):
-        dev.gemm_i8(bA, bA, bC, 256, 256, 96, 1, 96, 96, 256, 0, 0, 0)  # K not a multiple of 128
+        dev.gemm_i8(bA, bA, bC, 256, 256, 96, 1, 256, 0, 0, 0)  # K not a multiple of 64
     with pytest.raises(RuntimeError):
-        dev.gemm_i8(bA, bA, bC, 200, 256, 128, 1, 128, 128, 256, 0, 0, 0)  # M not a multiple of 256
+        dev.gemm_i8(bA, bA, bC, 200, 256, 128, 1, 256, 0, 0, 0)  # M not a multiple of 256
+    with pytest.raises(RuntimeError):
+        dev.gemm_i8(bA, bA, bC, 256, 256, 128, 2, 256, 512, 512, 65536)  # batch stride not a multiple of 1 KB
 
 
 def exact_double(cprime: int, e: int) -> float:
