@@ -64,11 +64,18 @@ __device__ __forceinline__ void stage_barrier() {
     __asm__ volatile("" ::: "memory");
 }
 
-// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding of simm16).
+// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding of simm16: vmcnt
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// vmcnt = N and lgkmcnt = 0 (this wave's LDS reads complete).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
 constexpr int BM = 256, BN = 256, BK = 64, NS = 4, THREADS = 256;
@@ -124,46 +131,59 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
 #pragma unroll
             for (int q = 0; q < 16; q++) acc[i][j][q] = 0;
 
-    // Pipeline. Loads run NS stages ahead: at step kt the stages kt+1 .. kt+NS are in flight or
-    // landed. The fragments of stage kt are already in registers (read during step kt-1); step kt
-    // waits for stage kt+1, refills the buffer of stage kt (nobody reads it any more) with stage
-    // kt+NS, and reads the fragments of stage kt+1 while its MFMAs run on those of stage kt. The
-    // tail re-loads the last valid step (clamped), so every step has the same number of loads in
-    // flight and the same wait count.
+    // Pipeline. Loads run NS stages ahead: while stage kt is consumed, stages kt+1 .. kt+NS-1 are in
+    // flight or landed. Fragments are double-buffered per 32-byte K substep (F, G: 8 fragments of
+    // 4 registers each): substep (kt, 0) reads G = substep (kt, 1) while its MFMAs run on F;
+    // substep (kt, 1) waits for stage kt+1, makes sure every wave has finished reading stage kt
+    // (own LDS reads complete, then the barrier), refills that buffer with stage kt+NS, and reads
+    // F = substep (kt+1, 0) while its MFMAs run on G. The tail re-loads the last valid stage
+    // (clamped), so every step has the same number of loads in flight and the same wait count.
 #pragma unroll
     for (int s = 0; s < NS; s++) OZ_GEMM_ISSUE(min(s, nk - 1), s);
-    v4i fa[2][4], fb[2][4], ga[2][4], gb[2][4];  // [k substep][block]
+    v4i fa[4], fb[4], ga[4], gb[4];
     wait_vmcnt<(LOADS_A + LOADS_B) * (NS - 1)>();  // stage 0
     stage_barrier();
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            fa[ks][i] = *reinterpret_cast<const v4i*>(lds + offA[ks] + i * 32 * BK);
-            fb[ks][i] = *reinterpret_cast<const v4i*>(lds + offB[ks] + i * 32 * BK);
-        }
-#define OZ_GEMM_STEP(kt, F_A, F_B, G_A, G_B)                                                                     \
-    do {                                                                                                         \
-        wait_vmcnt<(LOADS_A + LOADS_B) * (NS - 2)>(); /* stage kt+1 landed (this thread) */                       \
-        stage_barrier();                              /* ... everyone's; stage kt fully read */                  \
-        OZ_GEMM_ISSUE(min((kt) + NS, nk - 1), (kt) % NS);                                                        \
-        const int8_t* nx = lds + (((kt) + 1) % NS) * STAGE;                                                      \
-        _Pragma("unroll") for (int ks = 0; ks < 2; ks++) {                                                       \
-            _Pragma("unroll") for (int i = 0; i < 4; i++) {                                                      \
-                G_A[ks][i] = *reinterpret_cast<const v4i*>(nx + offA[ks] + i * 32 * BK);                         \
-                G_B[ks][i] = *reinterpret_cast<const v4i*>(nx + offB[ks] + i * 32 * BK);                         \
-                _Pragma("unroll") for (int j = 0; j < 4; j++) acc[i][j] =                                        \
-                    __builtin_amdgcn_mfma_i32_32x32x32_i8(F_A[ks][i], F_B[ks][j], acc[i][j], 0, 0, 0);           \
-            }                                                                                                    \
-        }                                                                                                        \
-    } while (0)
-    int kt = 0;
-    for (; kt + 2 <= nk; kt += 2) {
-        OZ_GEMM_STEP(kt, fa, fb, ga, gb);
-        OZ_GEMM_STEP(kt + 1, ga, gb, fa, fb);
+    for (int i = 0; i < 4; i++) {
+        fa[i] = *reinterpret_cast<const v4i*>(lds + offA[0] + i * 32 * BK);
+        fb[i] = *reinterpret_cast<const v4i*>(lds + offB[0] + i * 32 * BK);
     }
-    if (kt < nk) OZ_GEMM_STEP(kt, fa, fb, ga, gb);  // (the prefetch of the clamped stage is unused)
-#undef OZ_GEMM_STEP
+    // The issue order inside a step is fixed with sched_barrier fences (left alone, the compiler
+    // sinks every fragment read to just before its first use, which stalls the MFMAs on LDS
+    // latency): the 8 fragment reads of the other buffer, and after the barrier the 8 global->LDS
+    // loads, go one per MFMA over the first 8 of the 16 MFMAs of each substep.
+    for (int kt = 0; kt < nk; kt++) {
+        const int8_t* cur = lds + (kt % NS) * STAGE;
+        const int8_t* nxt = lds + ((kt + 1) % NS) * STAGE;
+        // substep (kt, 0): MFMAs on F, reads of G = substep (kt, 1)
+#pragma unroll
+        for (int g = 0; g < 16; g++) {
+            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[g >> 2], fb[g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            if (g < 4) ga[g] = *reinterpret_cast<const v4i*>(cur + offA[1] + g * 32 * BK);
+            else if (g < 8) gb[g - 4] = *reinterpret_cast<const v4i*>(cur + offB[1] + (g - 4) * 32 * BK);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        wait_vmcnt_lgkm0<(LOADS_A + LOADS_B) * (NS - 2)>();  // stage kt+1 landed; own reads of stage kt done
+        stage_barrier();                                      // ... for every wave
+        // substep (kt, 1): MFMAs on G, refill of stage kt's buffer, reads of F = substep (kt+1, 0)
+        const long long koff = (long long)min(kt + NS, nk - 1) * 1024;
+        int8_t* sa = lds + (kt % NS) * STAGE;
+#pragma unroll
+        for (int g = 0; g < 16; g++) {
+            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ga[g >> 2], gb[g & 3], acc[g >> 2][g & 3], 0, 0, 0);
+            if (g < 4) {
+                __builtin_amdgcn_global_load_lds(Ab + (4 * g + wave) * band + koff, (lds_void*)(sa + 1024 * (4 * g + wave)),
+                                                 16, 0, 0);
+                fa[g] = *reinterpret_cast<const v4i*>(nxt + offA[0] + g * 32 * BK);
+            } else if (g < 8) {
+                const int i = g - 4;
+                __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + koff,
+                                                 (lds_void*)(sa + STAGE_A + 1024 * (4 * i + wave)), 16, 0, 0);
+                fb[i] = *reinterpret_cast<const v4i*>(nxt + offB[0] + i * 32 * BK);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
 #undef OZ_GEMM_ISSUE
     wait_vmcnt<0>();  // drain the clamped tail loads before the workgroup ends
 
