@@ -122,6 +122,20 @@ typedef struct oz2_crt_dev {
 int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long strideC, const oz2_crt_dev* crt,
                 const int32_t* dA, const int32_t* dB, double* out, int ldo);
 
+/* ---- A9 + A10 fused: products reduced to CRT digits (reference ozaki2.cpp:333-350 followed by
+ * the residue step of recon_crt.cpp:293) -------------------------------------------------------
+ * The products of oz_gemm_i8 for the S moduli of crt (batch = S), each reduced in the GEMM's
+ * epilogue to its CRT digit k_s = (C_s mod m_s) * y_s mod m_s in [0, m_s), stored as uint8:
+ * D[s] is M x N bytes, row stride ldd, plane stride strideD bytes. Same operand rules as
+ * oz_gemm_i8. Writing one byte instead of four per product is what makes this the production path. */
+int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, int M, int N, int K, int S, int ldd,
+                    long long strideA, long long strideB, long long strideD, const oz2_crt_dev* crt);
+
+/* CRT reconstruction from the digits of oz2_gemm_digits: same result as oz2_crt_f64 on the
+ * products. ldd and strideD (bytes) multiples of 4, D 4-byte aligned. */
+int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long strideD,
+                       const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,7 +12,7 @@
 //   residue planes of A: S x Mg x Kg int8, of B: S x Ng x Kg int8 (B transposed), both K-major in
 //   the GEMM's OZ_BLOCK tiles (1 KB blocks of 16 rows x 64 K-bytes), Mg, Ng multiples of 256 and
 //   Kg of 64;
-//   products: S x Mg x Ng int32; output: M x N f64.
+//   CRT digits of the products: S x Mg x Ng uint8; output: M x N f64.
 #include <chrono>
 #include <cstring>
 #include <functional>
@@ -60,7 +60,7 @@ Output ozaki2_int8_run(Device& D, const Problem& p) {
     const long long strideA = (long long)Mg * Kg, strideB = (long long)Ng * Kg, strideC = (long long)Mg * Ng;
     auto* planesA = static_cast<std::int8_t*>(ws.get(kPlanesA, (std::size_t)S * strideA));
     auto* planesB = static_cast<std::int8_t*>(ws.get(kPlanesB, (std::size_t)S * strideB));
-    auto* prod = static_cast<std::int32_t*>(ws.get(kProducts, sizeof(std::int32_t) * (std::size_t)S * strideC));
+    auto* prod = static_cast<std::uint8_t*>(ws.get(kProducts, (std::size_t)S * strideC));
     auto* out = static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
 
     device_check(dev, oz_memcpy_h2d(dev, dAf, p.a.data(), sizeof(double) * p.a.size()), "upload A");
@@ -88,14 +88,14 @@ Output ozaki2_int8_run(Device& D, const Problem& p) {
                      }});
     steps.push_back({ev::Gemm, [=] {
                          device_check(dev,
-                                      oz_gemm_i8(dev, planesA, planesB, prod, (int)Mg, (int)Ng, (int)Kg, (int)S,
-                                                 (int)Ng, strideA, strideB, strideC),
+                                      oz2_gemm_digits(dev, planesA, planesB, prod, (int)Mg, (int)Ng, (int)Kg, (int)S,
+                                                      (int)Ng, strideA, strideB, strideC, &cdesc),
                                       "products");
                      }});
     steps.push_back({ev::Recon, [=] {
                          device_check(dev,
-                                      oz2_crt_f64(dev, prod, (int)M, (int)N, (int)Ng, strideC, &cdesc, dltA, dltB, out,
-                                                  (int)N),
+                                      oz2_crt_digits_f64(dev, prod, (int)M, (int)N, (int)Ng, strideC, &cdesc, dltA,
+                                                         dltB, out, (int)N),
                                       "reconstruction");
                      }});
 

@@ -14,17 +14,12 @@
 // MI355X design: one thread per output element; the S planes are read coalesced (plane-major),
 // the constants are kernel arguments (uniform, held in scalar registers), the multiword
 // arithmetic is 32-bit multiply-add with carries.
+#include "oz2_modular.hpp"
 #include "oz_internal.hpp"
 
 namespace {
 
-// x mod m for 0 <= x < 2^32 (m <= 255): q = mulhi(x, floor(2^32/m)) is floor(x/m) or one less.
-__device__ __forceinline__ uint32_t mod_small(uint32_t x, uint32_t m, uint32_t magic) {
-    const uint32_t q = __umulhi(x, magic);
-    uint32_t r = x - q * m;
-    if (r >= m) r -= m;
-    return r;
-}
+using oz2::mod_small;
 
 template <int NW>
 __device__ __forceinline__ double to_double_scaled(const uint32_t* w, int e2) {
@@ -91,31 +86,9 @@ struct CrtArgs {
     uint32_t Mhalf[8];         // floor(M/2)
 };
 
+// acc = sum_s k_s Q_s (< S*M) -> the symmetric representative of acc mod M, scaled by 2^e2, as FP64.
 template <int NW>
-__global__ void __launch_bounds__(256) crt_kernel(const int32_t* __restrict__ C, int M, int N, int ldc, long long sC,
-                                                  CrtArgs a, const int32_t* __restrict__ dA,
-                                                  const int32_t* __restrict__ dB, double* __restrict__ out, int ldo) {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    const int i = blockIdx.y;
-    if (j >= N) return;
-    const int32_t* c = C + (long long)i * ldc + j;
-    uint32_t acc[NW];
-#pragma unroll
-    for (int w = 0; w < NW; w++) acc[w] = 0;
-    for (int s = 0; s < a.k.S; s++) {
-        const int32_t v = c[(long long)s * sC];
-        const uint32_t m = a.k.m[s], mg = a.magic[s];
-        uint32_t r = mod_small(v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v, m, mg);
-        if (v < 0 && r) r = m - r;
-        const uint32_t k = mod_small(r * a.k.y[s], m, mg);
-        uint32_t carry = 0;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const uint64_t p = (uint64_t)k * a.k.Q[s][w] + acc[w] + carry;
-            acc[w] = (uint32_t)p;
-            carry = (uint32_t)(p >> 32);
-        }
-    }
+__device__ __forceinline__ double crt_finish(uint32_t* acc, const CrtArgs& a, int e2) {
     // q = floor(acc / M) from FP64 approximations (|error| <= 1), then acc -= q*M with one correction
     double ahi = 0.0;
 #pragma unroll
@@ -173,30 +146,92 @@ __global__ void __launch_bounds__(256) crt_kernel(const int32_t* __restrict__ C,
             }
         }
     }
+    return to_double_scaled<NW>(acc, e2);
+}
+
+// acc += k * Q_s (NW words)
+template <int NW>
+__device__ __forceinline__ void crt_add(uint32_t* acc, uint32_t k, const uint32_t* Q) {
+    uint32_t carry = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        const uint64_t p = (uint64_t)k * Q[w] + acc[w] + carry;
+        acc[w] = (uint32_t)p;
+        carry = (uint32_t)(p >> 32);
+    }
+}
+
+// From the exact products C_s (int32): one thread per output element.
+template <int NW>
+__global__ void __launch_bounds__(256) crt_kernel(const int32_t* __restrict__ C, int M, int N, int ldc, long long sC,
+                                                  CrtArgs a, const int32_t* __restrict__ dA,
+                                                  const int32_t* __restrict__ dB, double* __restrict__ out, int ldo) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.y;
+    if (j >= N) return;
+    const int32_t* c = C + (long long)i * ldc + j;
+    uint32_t acc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; w++) acc[w] = 0;
+    for (int s = 0; s < a.k.S; s++)
+        crt_add<NW>(acc, oz2::crt_digit(c[(long long)s * sC], a.k.m[s], a.k.y[s], a.magic[s]), a.k.Q[s]);
     const int g = 2 * a.k.shift - (dA[i] + dB[j]);  // eA + eB
-    out[(long long)i * ldo + j] = to_double_scaled<NW>(acc, g - 2 * a.k.b);
+    out[(long long)i * ldo + j] = crt_finish<NW>(acc, a, g - 2 * a.k.b);
+}
+
+// From the CRT digits k_s (uint8, written by the product kernel): one thread per 4 consecutive
+// output elements of a row, so that each plane read is one 32-bit word per thread.
+template <int NW>
+__global__ void __launch_bounds__(256) crt_digits_kernel(const uint8_t* __restrict__ D, int M, int N, int ldd,
+                                                         long long sD, CrtArgs a, const int32_t* __restrict__ dA,
+                                                         const int32_t* __restrict__ dB, double* __restrict__ out,
+                                                         int ldo) {
+    const int j0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+    const int i = blockIdx.y;
+    if (j0 >= N) return;
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(D + (long long)i * ldd + j0);
+    const long long sw = sD / 4;
+    uint32_t acc[4][NW];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int w = 0; w < NW; w++) acc[e][w] = 0;
+    for (int s = 0; s < a.k.S; s++) {
+        const uint32_t v = d[(long long)s * sw];
+#pragma unroll
+        for (int e = 0; e < 4; e++) crt_add<NW>(acc[e], (v >> (8 * e)) & 0xFFu, a.k.Q[s]);
+    }
+    const int gi = 2 * a.k.shift - dA[i] - 2 * a.k.b;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (j0 + e < N) out[(long long)i * ldo + j0 + e] = crt_finish<NW>(acc[e], a, gi - dB[j0 + e]);
 }
 
 template <int NW>
-int launch_crt(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long sC, const CrtArgs& a,
+int launch_crt(oz_dev* dev, const void* C, bool digits, int M, int N, int ldc, long long sC, const CrtArgs& a,
                const int32_t* dA, const int32_t* dB, double* out, int ldo) {
-    hipLaunchKernelGGL(crt_kernel<NW>, dim3(oz::ceil_div(N, 256), M), dim3(256), 0, dev->stream, C, M, N, ldc, sC, a, dA,
-                       dB, out, ldo);
+    if (digits) {
+        hipLaunchKernelGGL(crt_digits_kernel<NW>, dim3(oz::ceil_div(N, 1024), M), dim3(256), 0, dev->stream,
+                           static_cast<const uint8_t*>(C), M, N, ldc, sC, a, dA, dB, out, ldo);
+        return oz::launch_check(dev, "crt_digits_kernel");
+    }
+    hipLaunchKernelGGL(crt_kernel<NW>, dim3(oz::ceil_div(N, 256), M), dim3(256), 0, dev->stream,
+                       static_cast<const int32_t*>(C), M, N, ldc, sC, a, dA, dB, out, ldo);
     return oz::launch_check(dev, "crt_kernel");
 }
 
-}  // namespace
-
-extern "C" int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long strideC,
-                           const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+// Both entry points: C is int32 products (element strides) or uint8 digits (byte strides).
+int crt_f64(oz_dev* dev, const char* name, const void* C, bool digits, int M, int N, int ldc, long long strideC,
+            const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
     if (int st = oz::use(dev)) return st;
     if (!C || !crt || !dA || !dB || !out || M <= 0 || N <= 0 || ldc < N || ldo < N || crt->S < 1 ||
-        crt->S > OZ2_MAXS || crt->nw < 3 || crt->nw > 8 || crt->Mtop <= 0.0)
-        return oz::fail(dev, OZ_ERR_ARG, "oz2_crt_f64: invalid arguments");
+        crt->S > OZ2_MAXS || crt->nw < 3 || crt->nw > 8 || crt->Mtop <= 0.0 ||
+        (digits && (ldc % 4 || strideC % 4 || ((uintptr_t)C & 3))))
+        return oz::fail(dev, OZ_ERR_ARG, "%s: invalid arguments", name);
     CrtArgs a{};
     a.k = *crt;
     for (int s = 0; s < crt->S; s++) {
-        if (crt->m[s] < 2 || crt->m[s] > 255) return oz::fail(dev, OZ_ERR_ARG, "oz2_crt_f64: modulus out of range");
+        if (crt->m[s] < 2 || crt->m[s] > 255) return oz::fail(dev, OZ_ERR_ARG, "%s: modulus out of range", name);
         a.magic[s] = (uint32_t)(0x100000000ull / crt->m[s]);
     }
     // floor(M/2)
@@ -206,21 +241,34 @@ extern "C" int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc,
         a.Mhalf[w] = (uint32_t)(cur >> 1);
         r = (uint32_t)(cur & 1u);
     }
+    const size_t esz = digits ? 1 : 4;
     // the grid puts rows on y (at most 65535 per launch): launch in row chunks
     for (int i0 = 0; i0 < M; i0 += 65535) {
         const int rows = std::min(65535, M - i0);
-        const int32_t* Ci = C + (long long)i0 * ldc;
+        const void* Ci = static_cast<const char*>(C) + (size_t)i0 * ldc * esz;
         double* oi = out + (long long)i0 * ldo;
         int st;
         switch (crt->nw) {
-        case 3: st = launch_crt<3>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
-        case 4: st = launch_crt<4>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
-        case 5: st = launch_crt<5>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
-        case 6: st = launch_crt<6>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
-        case 7: st = launch_crt<7>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
-        default: st = launch_crt<8>(dev, Ci, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 3: st = launch_crt<3>(dev, Ci, digits, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 4: st = launch_crt<4>(dev, Ci, digits, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 5: st = launch_crt<5>(dev, Ci, digits, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 6: st = launch_crt<6>(dev, Ci, digits, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        case 7: st = launch_crt<7>(dev, Ci, digits, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
+        default: st = launch_crt<8>(dev, Ci, digits, rows, N, ldc, strideC, a, dA + i0, dB, oi, ldo); break;
         }
         if (st) return st;
     }
     return OZ_OK;
+}
+
+}  // namespace
+
+extern "C" int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long strideC,
+                           const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    return crt_f64(dev, "oz2_crt_f64", C, false, M, N, ldc, strideC, crt, dA, dB, out, ldo);
+}
+
+extern "C" int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long strideD,
+                                  const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    return crt_f64(dev, "oz2_crt_digits_f64", D, true, M, N, ldd, strideD, crt, dA, dB, out, ldo);
 }

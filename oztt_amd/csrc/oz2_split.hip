@@ -200,10 +200,16 @@ __global__ void __launch_bounds__(256) split_tran_kernel(const double* __restric
     }
 }
 
-// Layouts 2/3 (OZ_BLOCK tiles): one wave per 1 KB block of 16 plane rows x 64 plane columns.
-// Lane l owns plane row l/4 of the block and the 16 plane columns 16*(l%4)..+15; for each modulus it
-// stores those 16 residues as one 16-byte chunk at its swizzled position, so a wave writes each
-// block with one contiguous 1 KB store. TRAN: plane row = column of X (layout 3).
+// Layouts 2/3 (OZ_BLOCK tiles): one wave per 1 KB block of 16 plane rows x 64 plane columns; the
+// wave writes each plane's block with one contiguous 1 KB store (16 bytes per lane, lane l -> block
+// bytes 16l..16l+15).
+//   Layout 3 (TRAN, plane row = column of X): lane l computes plane row l/4, plane columns
+//   16*(l%4)..+15 (= 16 consecutive rows of X in one column; a load instruction reads 4 runs of 16
+//   consecutive doubles) and packs its 16 residues into its own stored chunk.
+//   Layout 2: lane l computes plane column l of the 16 rows (each load instruction reads one
+//   contiguous 512-byte row segment of X); the residues of a plane are transposed through a 1 KB
+//   LDS image of the block (byte writes, then one 16-byte read per lane). The image is private to
+//   the wave, whose LDS operations execute in order, so no barrier is needed.
 __device__ __forceinline__ int block_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
 template <int ND, bool TRAN>
@@ -215,29 +221,55 @@ __global__ void __launch_bounds__(256) split_block_kernel(const double* __restri
     if (blk >= nblocks) return;
     const int lane = threadIdx.x & 63;
     const int br = (int)(blk / kblocks), bk = (int)(blk % kblocks);
-    const int pr = br * 16 + (lane >> 2);          // plane row
-    const int pc0 = bk * 64 + 16 * (lane & 3);     // first of this lane's 16 plane columns
     float dig[16][ND];
+    if constexpr (TRAN) {
+        const int pr = br * 16 + (lane >> 2);       // plane row = column of X
+        const int pc0 = bk * 64 + 16 * (lane & 3);  // first of this lane's 16 plane columns = rows of X
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-        const int xr = TRAN ? pc0 + e : pr, xc = TRAN ? pr : pc0 + e;
-        if (xr < rows && xc < cols) {
-            const int32_t d = mode == 0 ? delta[xr] : delta[xc];
-            make_digits<ND>(X[(size_t)xr * ld + xc], d, dig[e]);
-        } else {
+        for (int e = 0; e < 16; e++) {
+            const int xr = pc0 + e, xc = pr;
+            if (xr < rows && xc < cols) {
+                const int32_t d = mode == 0 ? delta[xr] : delta[xc];
+                make_digits<ND>(X[(size_t)xr * ld + xc], d, dig[e]);
+            } else {
 #pragma unroll
-            for (int j = 0; j < ND; j++) dig[e][j] = 0.0f;
+                for (int j = 0; j < ND; j++) dig[e][j] = 0.0f;
+            }
         }
-    }
-    const int rr = lane >> 2;
-    uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
-    for (int s = 0; s < S; s++) {
-        uint4 v;
-        v.x = pack4(residue<ND>(dig[0], k, s), residue<ND>(dig[1], k, s), residue<ND>(dig[2], k, s), residue<ND>(dig[3], k, s));
-        v.y = pack4(residue<ND>(dig[4], k, s), residue<ND>(dig[5], k, s), residue<ND>(dig[6], k, s), residue<ND>(dig[7], k, s));
-        v.z = pack4(residue<ND>(dig[8], k, s), residue<ND>(dig[9], k, s), residue<ND>(dig[10], k, s), residue<ND>(dig[11], k, s));
-        v.w = pack4(residue<ND>(dig[12], k, s), residue<ND>(dig[13], k, s), residue<ND>(dig[14], k, s), residue<ND>(dig[15], k, s));
-        out[(long long)s * pstride_chunks] = v;
+        const int rr = lane >> 2;
+        uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
+        for (int s = 0; s < S; s++) {
+            uint4 v;
+            v.x = pack4(residue<ND>(dig[0], k, s), residue<ND>(dig[1], k, s), residue<ND>(dig[2], k, s), residue<ND>(dig[3], k, s));
+            v.y = pack4(residue<ND>(dig[4], k, s), residue<ND>(dig[5], k, s), residue<ND>(dig[6], k, s), residue<ND>(dig[7], k, s));
+            v.z = pack4(residue<ND>(dig[8], k, s), residue<ND>(dig[9], k, s), residue<ND>(dig[10], k, s), residue<ND>(dig[11], k, s));
+            v.w = pack4(residue<ND>(dig[12], k, s), residue<ND>(dig[13], k, s), residue<ND>(dig[14], k, s), residue<ND>(dig[15], k, s));
+            out[(long long)s * pstride_chunks] = v;
+        }
+    } else {
+        __shared__ __attribute__((aligned(16))) uint8_t image[4][1024];
+        uint8_t* img = image[threadIdx.x >> 6];
+        const int xc = bk * 64 + lane;  // plane column = column of X
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int xr = br * 16 + e;
+            if (xr < rows && xc < cols) {
+                const int32_t d = mode == 0 ? delta[xr] : delta[xc];
+                make_digits<ND>(X[(size_t)xr * ld + xc], d, dig[e]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < ND; j++) dig[e][j] = 0.0f;
+            }
+        }
+        // byte of (row e, column lane) inside the block image
+        const int colpart = 16 * (lane >> 4), colbyte = lane & 15;
+        uint4* out = planes + blk * 64 + lane;
+        for (int s = 0; s < S; s++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)residue<ND>(dig[e], k, s);
+            out[(long long)s * pstride_chunks] = *reinterpret_cast<const uint4*>(img + 16 * lane);
+        }
     }
 }
 

@@ -22,6 +22,7 @@
 //     operand and the swizzle comes with the data: the 64 lanes of each fragment read
 //     (ds_read_b128, rows r..r+31, two chunk columns) spread evenly over the LDS banks.
 //   - Workgroups are mapped to tiles XCD-aware (tile_of below).
+#include "oz2_modular.hpp"
 #include "oz_internal.hpp"
 
 namespace {
@@ -83,10 +84,13 @@ constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;  
 constexpr int LOADS_A = STAGE_A / 16 / THREADS, LOADS_B = STAGE_B / 16 / THREADS;  // per thread per stage
 static_assert(LOADS_A == 4 && LOADS_B == 4, "each thread moves 4+4 chunks of 16 bytes per stage");
 
+// DIGITS = false: C is int32 (the exact products). DIGITS = true: C is uint8 and receives the CRT
+// digit of each product for modulus `batch` (oz2::crt_digit with dc.m/y/magic[batch]).
+template <bool DIGITS>
 __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ Bt,
-                                                          int32_t* __restrict__ C, int K, int ldc, long long sA,
+                                                          void* __restrict__ C, int K, int ldc, long long sA,
                                                           long long sB, long long sC, int tiles_m, int tiles_n,
-                                                          int nbatch) {
+                                                          int nbatch, oz2::DigitConsts dc) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * STAGE];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     int batch, tm, tn;
@@ -187,15 +191,50 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
 #undef OZ_GEMM_ISSUE
     wait_vmcnt<0>();  // drain the clamped tail loads before the workgroup ends
 
-    int32_t* Cb = C + batch * sC + (long long)(tm * BM + wm * 128) * ldc + tn * BN + wn * 128;
+    const long long c0 = batch * sC + (long long)(tm * BM + wm * 128) * ldc + tn * BN + wn * 128;
+    if constexpr (DIGITS) {
+        uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
+        const uint32_t m = dc.m[batch], y = dc.y[batch], mg = dc.magic[batch];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int q = 0; q < 16; q++)
-                Cb[(long long)(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * ldc + 32 * j + (lane & 31)] =
-                    acc[i][j][q];
+                for (int q = 0; q < 16; q++)
+                    Cb[(long long)(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * ldc + 32 * j + (lane & 31)] =
+                        (uint8_t)oz2::crt_digit(acc[i][j][q], m, y, mg);
+    } else {
+        int32_t* Cb = static_cast<int32_t*>(C) + c0;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    Cb[(long long)(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * ldc + 32 * j + (lane & 31)] =
+                        acc[i][j][q];
+    }
+}
+
+// Shape rules shared by both entry points; returns a message or nullptr.
+const char* check_gemm(const int8_t* A, const int8_t* Bt, const void* C, int M, int N, int K, int batch, int ldc,
+                       long long strideA, long long strideB, long long strideC) {
+    if (!A || !Bt || !C || M <= 0 || N <= 0 || K <= 0 || batch <= 0 || M % BM || N % BN || K % BK || ldc < N ||
+        ((uintptr_t)A & 15) || ((uintptr_t)Bt & 15) || strideA % 1024 || strideB % 1024 ||
+        (batch > 1 && (strideA < (long long)M * K || strideB < (long long)N * K || strideC < (long long)M * ldc)))
+        return "unsupported shape";
+    if ((long long)(M / BM) * (N / BN) * batch > 0x7FFFFFFFll) return "grid too large";
+    return nullptr;
+}
+
+template <bool DIGITS>
+int launch_gemm(oz_dev* dev, const int8_t* A, const int8_t* Bt, void* C, int M, int N, int K, int batch, int ldc,
+                long long strideA, long long strideB, long long strideC, const oz2::DigitConsts& dc) {
+    const int tiles_m = M / BM, tiles_n = N / BN;
+    const unsigned grid = (unsigned)((long long)tiles_m * tiles_n * batch);
+    hipLaunchKernelGGL(gemm_i8_kernel<DIGITS>, dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc, strideA,
+                       strideB, strideC, tiles_m, tiles_n, batch, dc);
+    return oz::launch_check(dev, "gemm_i8_kernel");
 }
 
 }  // namespace
@@ -203,14 +242,25 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
 extern "C" int oz_gemm_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K, int batch,
                           int ldc, long long strideA, long long strideB, long long strideC) {
     if (int st = oz::use(dev)) return st;
-    if (!A || !Bt || !C || M <= 0 || N <= 0 || K <= 0 || batch <= 0 || M % BM || N % BN || K % BK || ldc < N ||
-        ((uintptr_t)A & 15) || ((uintptr_t)Bt & 15) || strideA % 1024 || strideB % 1024 ||
-        (batch > 1 && (strideA < (long long)M * K || strideB < (long long)N * K || strideC < (long long)M * ldc)))
-        return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: unsupported shape M=%d N=%d K=%d batch=%d", M, N, K, batch);
-    const int tiles_m = M / BM, tiles_n = N / BN;
-    const long long grid = (long long)tiles_m * tiles_n * batch;
-    if (grid > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: grid too large");
-    hipLaunchKernelGGL(gemm_i8_kernel, dim3((unsigned)grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc, strideA,
-                       strideB, strideC, tiles_m, tiles_n, batch);
-    return oz::launch_check(dev, "gemm_i8_kernel");
+    if (const char* e = check_gemm(A, Bt, C, M, N, K, batch, ldc, strideA, strideB, strideC))
+        return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: %s (M=%d N=%d K=%d batch=%d)", e, M, N, K, batch);
+    return launch_gemm<false>(dev, A, Bt, C, M, N, K, batch, ldc, strideA, strideB, strideC, oz2::DigitConsts{});
+}
+
+extern "C" int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, int M, int N, int K, int S,
+                               int ldd, long long strideA, long long strideB, long long strideD,
+                               const oz2_crt_dev* crt) {
+    if (int st = oz::use(dev)) return st;
+    if (const char* e = check_gemm(A, Bt, D, M, N, K, S, ldd, strideA, strideB, strideD))
+        return oz::fail(dev, OZ_ERR_ARG, "oz2_gemm_digits: %s (M=%d N=%d K=%d S=%d)", e, M, N, K, S);
+    if (!crt || crt->S != S || S > OZ2_MAXS) return oz::fail(dev, OZ_ERR_ARG, "oz2_gemm_digits: S does not match crt");
+    oz2::DigitConsts dc{};
+    for (int s = 0; s < S; s++) {
+        const uint32_t m = crt->m[s];
+        if (m < 2 || m > 255 || crt->y[s] >= m) return oz::fail(dev, OZ_ERR_ARG, "oz2_gemm_digits: bad modulus %u", m);
+        dc.m[s] = m;
+        dc.y[s] = crt->y[s];
+        dc.magic[s] = (uint32_t)(0x100000000ull / m);
+    }
+    return launch_gemm<true>(dev, A, Bt, D, M, N, K, S, ldd, strideA, strideB, strideD, dc);
 }

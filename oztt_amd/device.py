@@ -140,6 +140,16 @@ class Device:
         self._check(hip().oz_gemm_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, batch, ldc, ctypes.c_longlong(sA),
                                      ctypes.c_longlong(sB), ctypes.c_longlong(sC)), "oz_gemm_i8")
 
+    def gemm_digits(self, A: Buffer, Bt: Buffer, D: Buffer, M, N, K, S, ldd, sA, sB, sD, desc: CrtDesc):
+        """D[s] = CRT digits ((A_s Bt_s^T) mod m_s) * y_s mod m_s as uint8 (operands as gemm_i8)."""
+        self._check(hip().oz2_gemm_digits(self.h, A.ptr, Bt.ptr, D.ptr, M, N, K, S, ldd, ctypes.c_longlong(sA),
+                                          ctypes.c_longlong(sB), ctypes.c_longlong(sD), ctypes.byref(desc)),
+                    "oz2_gemm_digits")
+
+    def crt_digits(self, D: Buffer, M, N, ldd, sD, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
+        self._check(hip().oz2_crt_digits_f64(self.h, D.ptr, M, N, ldd, ctypes.c_longlong(sD), ctypes.byref(desc),
+                                             dA.ptr, dB.ptr, out.ptr, ldo), "oz2_crt_digits_f64")
+
     def crt(self, C: Buffer, M, N, ldc, sC, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
         self._check(hip().oz2_crt_f64(self.h, C.ptr, M, N, ldc, ctypes.c_longlong(sC), ctypes.byref(desc), dA.ptr,
                                       dB.ptr, out.ptr, ldo), "oz2_crt_f64")

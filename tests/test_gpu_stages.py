@@ -218,3 +218,35 @@ def test_crt_exact(dev, oracle, moduli, b, nd):
     np.testing.assert_array_equal(got.view(np.uint64), want.view(np.uint64))
     np.testing.assert_array_equal(got.view(np.uint64),
                                   oracle.crt_exact(C, M, N, moduli, b, nd, dA, dB).view(np.uint64))
+    # the same from CRT digits k_s = (C_s mod m_s) y_s mod m_s (uint8 planes, row stride a multiple of 4)
+    desc = crt_desc(moduli, b, nd)
+    ldd = (N + 3) // 4 * 4 + 4
+    D = np.zeros((S, M, ldd), dtype=np.uint8)
+    for s, m in enumerate(moduli):
+        D[s, :, :N] = (C[s].astype(np.int64) % m * int(desc.y[s]) % m).astype(np.uint8)
+    bD = dev.upload(D)
+    bo2 = dev.alloc(8 * n)
+    dev.crt_digits(bD, M, N, ldd, M * ldd, desc, bdA, bdB, bo2, N)
+    np.testing.assert_array_equal(dev.download(bo2, np.float64, n).view(np.uint64), want.view(np.uint64))
+
+
+@pytest.mark.parametrize("M,N,K,S", [(256, 512, 320, 17), (512, 256, 8192, 5)])
+def test_gemm_digits_exact(dev, M, N, K, S):
+    """oz2_gemm_digits: the products of oz_gemm_i8 reduced to CRT digits in the epilogue, bit-exact;
+    K = 8192 with all-127 rows reaches the largest products the planner admits (K*127^2 < 2^31)."""
+    moduli = INT8_16[:S] if S <= 16 else INT8_16 + [193]
+    rng = np.random.default_rng(M * 3 + K)
+    A = rng.integers(-127, 128, (S, M, K), dtype=np.int8)
+    Bt = rng.integers(-127, 128, (S, N, K), dtype=np.int8)
+    A[:, 0, :] = 127
+    Bt[:, 0, :] = 127
+    A[:, 1, :] = -127
+    desc = crt_desc(moduli, 54, 3)
+    bA, bB = dev.upload(to_blocks(A)), dev.upload(to_blocks(Bt))
+    bD = dev.alloc(S * M * N)
+    dev.gemm_digits(bA, bB, bD, M, N, K, S, N, M * K, N * K, M * N, desc)
+    D = dev.download(bD, np.uint8, S * M * N).reshape(S, M, N)
+    for s, m in enumerate(moduli):
+        prod = (A[s].astype(np.float64) @ Bt[s].astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
+        want = (prod % m) * int(desc.y[s]) % m
+        np.testing.assert_array_equal(D[s].astype(np.int64), want)
