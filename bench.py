@@ -35,6 +35,10 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "effective FP64 TFLOP/s (2mnk/t) + max rel err vs binary128, Ozaki-II INT8 8192³"
 INT8_PEAK_TOPS = 5000.0  # MI355X dense INT8 MFMA, 5.0 POP/s
+# HBM bytes per launch of the product kernel at n = 8192 (17 moduli), from the rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes over this script scaled by the counters' readings for a plain 1 GiB copy
+# (factors 2.000 and 1.000): profiles/scheme2_int8_c3_8192_traffic.md.
+C3_GEMM_TRAFFIC_BYTES = 15.00e9
 
 
 def log(msg: str) -> None:
@@ -54,6 +58,19 @@ def cpu_baseline(a, b, n: int, rows: int) -> dict:
                                      f"0..{rows - 1} of C (full N={n}, K={n}), {dt:.2f} s; value = 2*rows*N*K/t"}
 
 
+def copy_probe(nbytes: int) -> int:
+    """Reference transfer for the traffic counters: copy16_kernel reads and writes nbytes once each."""
+    from oztt_amd.device import Device
+    dev = Device(0)
+    src, dst = dev.alloc(nbytes), dev.alloc(nbytes)
+    dev.fill_u32(src, 0x01020304, nbytes // 4)
+    for _ in range(3):
+        dev.copy(dst, src, nbytes)
+    dev.sync()
+    print(json.dumps({"copy_probe_bytes": nbytes, "launches": 3}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -61,10 +78,14 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--n", type=int, default=8192)
     ap.add_argument("--cpu-rows", type=int, default=1024, help="rows of the CPU baseline slab (0: skip)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only copy BYTES device-to-device with the plain copy kernel (calibrates HBM counters)")
     args = ap.parse_args()
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              f"(the path shards by output blocks without collectives, see DESIGN.md)", file=sys.stderr)
+              f"(the path would shard by 2-D output blocks with no exchange between GPUs)", file=sys.stderr)
         return 2
     import oztt_amd as oz
 
@@ -82,6 +103,14 @@ def main() -> int:
         raise SystemExit("whole-pass replay output differs from the first pass")
     ms = ev.whole_ms
     value = 2.0 * n * n * n / (ms * 1e-3) / 1e12
+    # one plain Context.gemm from host buffers: planning + PCIe transfers + the pass (not the metric)
+    c2 = np.empty(n * n)
+    t0 = time.perf_counter()
+    ctx.gemm(a, b, c2, n, n, n, opts)
+    call_ms = (time.perf_counter() - t0) * 1e3
+    if not np.array_equal(c2.view(np.uint64), c.view(np.uint64)):
+        raise SystemExit("Context.gemm output differs from the evaluated pass")
+    del c2
 
     # accuracy on a 64 x 64 sample at full K against binary128, next to a native FP64 dot product
     log("accuracy sample (binary128)")
@@ -121,9 +150,12 @@ def main() -> int:
         "fp64_max_rel_err_vs_binary128": float(rel64.max()),
         "max_err_over_fp64_bound": float((rel / bound).max()),
         "phases_ms": {k: round(ev.phase_ms[i], 4) for i, k in enumerate(["scale", "slice", "gemm", "compose", "recon"])},
+        "host_call_ms": round(call_ms, 2),
+        "host_call_tflops": round(2.0 * n * n * n / (call_ms * 1e-3) / 1e12, 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
-                     "kernel": "gemm_i8_kernel", "launch_ms": round(gemm_ms, 4),
+                     "frac": round(achieved / INT8_PEAK_TOPS, 4),
+                     "traffic": C3_GEMM_TRAFFIC_BYTES if (n == 8192 and info.moduli == 17) else None,
+                     "kernel": "gemm_i8_kernel<true> (oz2_gemm_digits)", "launch_ms": round(gemm_ms, 4),
                      "ops_per_launch": ev.product_ops},
     }
     if args.cpu_rows > 0:

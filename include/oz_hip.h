@@ -48,6 +48,9 @@ int oz_dev_free(oz_dev* dev, void* ptr);
 int oz_memcpy_h2d(oz_dev* dev, void* dst, const void* src, size_t bytes);
 int oz_memcpy_d2h(oz_dev* dev, void* dst, const void* src, size_t bytes);
 int oz_fill_u32(oz_dev* dev, void* dst, uint32_t value, size_t count);
+/* Device-to-device copy by a plain streaming kernel (16-byte aligned pointers and size); also the
+ * reference transfer for calibrating HBM traffic counters. */
+int oz_memcpy_d2d(oz_dev* dev, void* dst, const void* src, size_t bytes);
 int oz_sync(oz_dev* dev);
 /* Stream-ordered timing (64 event slots per handle). */
 int oz_event_record(oz_dev* dev, int slot);
@@ -126,8 +129,8 @@ int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long 
  * the residue step of recon_crt.cpp:293) -------------------------------------------------------
  * The products of oz_gemm_i8 for the S moduli of crt (batch = S), each reduced in the GEMM's
  * epilogue to its CRT digit k_s = (C_s mod m_s) * y_s mod m_s in [0, m_s), stored as uint8:
- * D[s] is M x N bytes, row stride ldd, plane stride strideD bytes. Same operand rules as
- * oz_gemm_i8. Writing one byte instead of four per product is what makes this the production path. */
+ * D[s] is M x N bytes, row stride ldd, plane stride strideD bytes (D, ldd and strideD 16-byte
+ * aligned). Same operand rules as oz_gemm_i8. Writing one byte instead of four per product is what makes this the production path. */
 int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, int M, int N, int K, int S, int ldd,
                     long long strideA, long long strideB, long long strideD, const oz2_crt_dev* crt);
 

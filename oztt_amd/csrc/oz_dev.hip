@@ -10,6 +10,12 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t v, size_t n
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = v;
 }
+
+// n16 chunks of 16 bytes; every byte is read once and written once (the HBM reference transfer).
+__global__ void copy16_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src, size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
 }  // namespace
 
 extern "C" {
@@ -93,6 +99,17 @@ int oz_fill_u32(oz_dev* dev, void* dst, uint32_t value, size_t count) {
     const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
     hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks), dim3(256), 0, dev->stream, (uint32_t*)dst, value, count);
     return oz::launch_check(dev, "fill_u32_kernel");
+}
+
+int oz_memcpy_d2d(oz_dev* dev, void* dst, const void* src, size_t bytes) {
+    if (int st = oz::use(dev)) return st;
+    if (!bytes) return OZ_OK;
+    if (!dst || !src || bytes % 16 || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15))
+        return oz::fail(dev, OZ_ERR_ARG, "oz_memcpy_d2d: pointers and size must be 16-byte aligned");
+    const size_t n16 = bytes / 16;
+    const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 8192);
+    hipLaunchKernelGGL(copy16_kernel, dim3(blocks), dim3(256), 0, dev->stream, (uint4*)dst, (const uint4*)src, n16);
+    return oz::launch_check(dev, "copy16_kernel");
 }
 
 int oz_sync(oz_dev* dev) {

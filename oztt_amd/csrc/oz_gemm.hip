@@ -193,7 +193,14 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
 
     const long long c0 = batch * sC + (long long)(tm * BM + wm * 128) * ldc + tn * BN + wn * 128;
     if constexpr (DIGITS) {
-        uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
+        // Digits go through LDS (the stages are free once every wave has left the main loop) so
+        // that each lane stores 16 contiguous bytes: the wave's 128 x 128 byte tile is written
+        // with row stride 144 (rows r and r+4, written by the two lane halves, then fall on
+        // different banks) and read back as 16-byte chunks, 8 per row.
+        constexpr int TS = 144;
+        static_assert(4 * 128 * TS <= NS * STAGE, "epilogue tiles fit in the stage ring");
+        __syncthreads();
+        uint8_t* tile = reinterpret_cast<uint8_t*>(lds) + wave * (128 * TS);
         const uint32_t m = dc.m[batch], y = dc.y[batch], mg = dc.magic[batch];
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -201,8 +208,14 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int q = 0; q < 16; q++)
-                    Cb[(long long)(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * ldc + 32 * j + (lane & 31)] =
+                    tile[(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * TS + 32 * j + (lane & 31)] =
                         (uint8_t)oz2::crt_digit(acc[i][j][q], m, y, mg);
+        uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const int c = 64 * t + lane, r = c >> 3, x = 16 * (c & 7);
+            *reinterpret_cast<uint4*>(Cb + (long long)r * ldc + x) = *reinterpret_cast<const uint4*>(tile + r * TS + x);
+        }
     } else {
         int32_t* Cb = static_cast<int32_t*>(C) + c0;
 #pragma unroll
@@ -254,6 +267,8 @@ extern "C" int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, u
     if (const char* e = check_gemm(A, Bt, D, M, N, K, S, ldd, strideA, strideB, strideD))
         return oz::fail(dev, OZ_ERR_ARG, "oz2_gemm_digits: %s (M=%d N=%d K=%d S=%d)", e, M, N, K, S);
     if (!crt || crt->S != S || S > OZ2_MAXS) return oz::fail(dev, OZ_ERR_ARG, "oz2_gemm_digits: S does not match crt");
+    if (ldd % 16 || strideD % 16 || ((uintptr_t)D & 15))
+        return oz::fail(dev, OZ_ERR_ARG, "oz2_gemm_digits: D, ldd and strideD must be 16-byte aligned");
     oz2::DigitConsts dc{};
     for (int s = 0; s < S; s++) {
         const uint32_t m = crt->m[s];

@@ -119,6 +119,9 @@ class Device:
     def fill_u32(self, buf: Buffer, value: int, count: int):
         self._check(hip().oz_fill_u32(self.h, buf.ptr, ctypes.c_uint32(value), ctypes.c_size_t(count)), "oz_fill_u32")
 
+    def copy(self, dst: Buffer, src: Buffer, nbytes: int):
+        self._check(hip().oz_memcpy_d2d(self.h, dst.ptr, src.ptr, ctypes.c_size_t(nbytes)), "oz_memcpy_d2d")
+
     def sync(self):
         self._check(hip().oz_sync(self.h), "oz_sync")
 

@@ -250,3 +250,13 @@ def test_gemm_digits_exact(dev, M, N, K, S):
         prod = (A[s].astype(np.float64) @ Bt[s].astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
         want = (prod % m) * int(desc.y[s]) % m
         np.testing.assert_array_equal(D[s].astype(np.int64), want)
+
+
+def test_device_copy(dev):
+    rng = np.random.default_rng(5)
+    x = rng.integers(0, 2 ** 32, 4096 + 64, dtype=np.uint64).astype(np.uint32)
+    src, dst = dev.upload(x), dev.alloc(4 * x.size)
+    dev.copy(dst, src, 4 * x.size)
+    np.testing.assert_array_equal(dev.download(dst, np.uint32, x.size), x)
+    with pytest.raises(RuntimeError):
+        dev.copy(dst, src, 20)  # not a multiple of 16
