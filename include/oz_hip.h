@@ -139,6 +139,43 @@ int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, 
 int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long strideD,
                        const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo);
 
+/* ==== Scheme I (reference src/ozaki1.cpp run(): scale, slice, diagonal products, Horner) ==== */
+
+/* ---- A15: slicing (reference ozaki1/kernels/slice_tf_body.h:86-131, slice_tf_sm8.cpp) --------
+ * For every element x of X (as oz2_split_int8: mode 0 delta per row, 1 per column) the p digits of
+ * x*2^delta in radix `radix` with digit bound dmax: t = triple-float(x*2^delta); per digit
+ * t *= radix (tfMulR, or tfMulP2 for a power of two), d = clamp(round(t_hi), +-dmax), t_hi -= d.
+ * Plane i holds digit i (weight radix^-(i+1)) as int8, in OZ_BLOCK tiles: layout 2 (planes of
+ * rows x cols) or layout 3 (transposed, cols x rows); geometry rules as oz2_split_int8's blocked
+ * layouts. radix <= 254, dmax <= 127, p <= 64. */
+int oz1_split_int8(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int p,
+                   int radix, int dmax, int8_t* planes, int layout, int prow, int pld, long long plane_stride);
+
+/* ---- A16: diagonal partial products (reference ozaki1/gemm.hpp:315, stages.hpp:157) ----------
+ * C[d] = sum_{i=0..d} A[i] * Bt[d-i]^T for d < ndiag, exact int32 (the d+1 pairs concatenated along
+ * K in one accumulation; requires ndiag*K*127^2 < 2^31, the reference's single-K-block INT8 plan).
+ * A[i]: M x K, Bt[i]: N x K int8 in OZ_BLOCK tiles; operand rules as oz_gemm_i8. */
+int oz1_gemm_diag_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K, int ndiag,
+                     int ldc, long long strideA, long long strideB, long long strideC);
+
+/* ---- A17: reconstruction (reference recon_tf_i32in.cpp:116-157, recon_f64_writer.cpp:148-160) -
+ * out[i][j] = S * radix^-(L+2) * 2^-(dA[i]+dB[j]) with S = sum_d radix^(L-d) P_d (L = ndiag-1)
+ * evaluated by Horner in triple-float exactly as the reference does, then assembled to FP64 with
+ * the 64-bit significand W = Whi:Wlo of radix^-(L+2) = W * 2^qw. P[d] is read from
+ * P + d*strideP (row stride ldp). signmag = 1: P_d enters as sign * (|P_d| & ~0xFF) and
+ * sign * (|P_d| & 0xFF) (INT8 products); 0: as (P_d & ~0xFF) and (P_d & 0xFF), except the first
+ * nsingle diagonals, which enter whole (their |P_d| <= 2^24). */
+typedef struct oz1_recon_dev {
+    int ndiag;      /* L + 1 */
+    int radix;      /* 2..254 */
+    int signmag;    /* 1: split of the INT8 products; 0: two's-complement split */
+    int nsingle;    /* leading diagonals read whole (signmag = 0 only) */
+    uint32_t Whi, Wlo;
+    int32_t qw;
+} oz1_recon_dev;
+int oz1_recon_f64(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long strideP, const oz1_recon_dev* r,
+                  const int32_t* dA, const int32_t* dB, double* out, int ldo);
+
 #ifdef __cplusplus
 }
 #endif

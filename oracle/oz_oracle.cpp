@@ -522,6 +522,114 @@ struct ExactCrt {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------------------------
+// Scheme I (ozaki1/kernels/slice_tf_body.h:86-131, recon_tf_i32in.cpp:116-157, f64_tf.h:253-300)
+// ---------------------------------------------------------------------------------------------
+// tfMulR: triple-float times a general radix with Dekker splitting by 4097 (sfpu_tf_proc.h:108-141);
+// the register names follow the procedure so that the operation order can be checked line by line.
+void tf_mul_r(float& hi, float& mid, float& lo, float r) {
+    float acc_hi = hi, acc_mid = mid, acc_lo = lo, term, tmp0, tmp1, tmp2, keep;
+    acc_lo = f_mul(acc_lo, r);
+    tmp1 = f_mul(acc_mid, 4097.0f);
+    tmp2 = f_sub(tmp1, acc_mid);
+    tmp1 = f_sub(tmp1, tmp2);
+    tmp2 = f_sub(acc_mid, tmp1);
+    tmp1 = f_mul(tmp1, r);
+    tmp2 = f_mul(tmp2, r);
+    term = f_add(tmp1, tmp2);
+    keep = f_sub(term, tmp1);
+    tmp0 = f_sub(tmp2, keep);
+    tmp1 = f_mul(acc_hi, 4097.0f);
+    tmp2 = f_sub(tmp1, acc_hi);
+    tmp1 = f_sub(tmp1, tmp2);
+    tmp2 = f_sub(acc_hi, tmp1);
+    tmp1 = f_mul(tmp1, r);
+    tmp2 = f_mul(tmp2, r);
+    acc_mid = f_add(tmp1, tmp2);
+    keep = f_sub(acc_mid, tmp1);
+    acc_hi = f_sub(tmp2, keep);
+    tmp0 = f_add(tmp0, acc_lo);
+    two_sum(term, tmp0, tmp1, tmp2);
+    two_sum(acc_hi, tmp1, term, tmp0);
+    two_sum(acc_mid, term, acc_hi, tmp1);
+    tmp2 = f_add(tmp2, tmp0);
+    fast_two_sum(tmp1, tmp2, acc_mid, acc_lo);
+    hi = acc_hi;
+    mid = acc_mid;
+    lo = acc_lo;
+}
+// tfMulRadix: the power-of-two form when the radix has no significand bits (sfpu_tf.h:131-134).
+inline void tf_mul_radix(float& hi, float& mid, float& lo, float r) {
+    if ((f_bits(r) & 0x7FFFFFu) == 0u)
+        tf_mul_pow2(hi, mid, lo, r);
+    else
+        tf_mul_r(hi, mid, lo, r);
+}
+// tfAddS<3> (sfpu_tf_proc.h:184-198) on a plain triple.
+void tf_add_s(float& hi, float& mid, float& lo, float v) {
+    float tmp0 = f_add(hi, v);
+    float tmp1 = f_sub(tmp0, hi);
+    float tmp2 = f_sub(tmp0, tmp1);
+    tmp2 = f_sub(hi, tmp2);
+    tmp1 = f_sub(v, tmp1);
+    tmp1 = f_add(tmp2, tmp1);
+    hi = tmp0;
+    tmp0 = f_add(mid, tmp1);
+    tmp2 = f_sub(tmp0, mid);
+    float term = f_sub(tmp0, tmp2);
+    term = f_sub(mid, term);
+    tmp2 = f_sub(tmp1, tmp2);
+    tmp2 = f_add(term, tmp2);
+    mid = tmp0;
+    lo = f_add(lo, tmp2);
+}
+// acc64_term and assemble_tf_f64 (f64_tf.h:214-300): three limbs -> FP64 times W 2^qw 2^g.
+int64_t acc64_term(int32_t sig, int32_t sh) {
+    if (!sig) return 0;
+    if (sh >= 0) return (int64_t)((uint64_t)(int64_t)sig << sh);
+    if (sh <= -32) return 0;
+    const uint32_t n = (uint32_t)(-sh);
+    const int32_t m = sig < 0 ? -sig : sig;
+    const int64_t q = (int64_t)(m >> n);
+    return sig < 0 ? -q : q;
+}
+uint64_t assemble_tf_f64(uint32_t hb, uint32_t mb, uint32_t lb, int32_t g, uint32_t Whi, uint32_t Wlo, int32_t qw) {
+    int32_t eh, em, el, gh, gm, gl;
+    dec32(hb, eh, gh);
+    dec32(mb, em, gm);
+    dec32(lb, el, gl);
+    if (gh == 0 && gm == 0 && gl == 0) return 0ull;
+    int32_t ebase = std::max(eh, std::max(em, el));
+    const int64_t ch = acc64_term(gh, eh - ebase + 37), cm = acc64_term(gm, em - ebase + 37),
+                  cl = acc64_term(gl, el - ebase + 37);
+    int64_t acc = ch + cm + cl;
+    if (acc == 0) {
+        if (ch) eh = gh = 0;
+        if (cm) em = gm = 0;
+        if (cl) el = gl = 0;
+        if (gh == 0 && gm == 0 && gl == 0) return 0ull;
+        ebase = std::max(eh, std::max(em, el));
+        acc = acc64_term(gh, eh - ebase + 37) + acc64_term(gm, em - ebase + 37) + acc64_term(gl, el - ebase + 37);
+    }
+    if (acc == 0) return 0ull;
+    const uint64_t sgn = acc < 0 ? 0x8000000000000000ull : 0ull;
+    uint64_t A = acc < 0 ? (uint64_t)(-acc) : (uint64_t)acc;
+    const int32_t shA = __builtin_clzll(A);
+    A <<= shA;
+    return pack_f64(A, Whi, Wlo, qw + g + (ebase - 187) - shA, sgn);
+}
+// radix^-(L+2) as a 64-bit significand and exponent (ozaki1/plan.hpp:446-460, bits.hpp:35-40).
+void oz1_scale_w(int radix, int L, uint32_t& Whi, uint32_t& Wlo, int32_t& qw) {
+    long double w = 1.0L;
+    for (int i = 0; i < L + 2; i++) w /= (long double)radix;
+    int e;
+    const long double f = frexpl(w, &e);
+    const unsigned long long W = (unsigned long long)ldexpl(f, 64);
+    Whi = (uint32_t)(W >> 32);
+    Wlo = (uint32_t)W;
+    qw = e - 64;
+}
+
 extern "C" {
 
 uint64_t orc_hash_f64(const double* c, size_t n) {
@@ -827,6 +935,119 @@ void orc_dot2_gemm(const double* A, const double* B, int M, int N, int K, int r0
             }
         }
     }
+}
+
+// Scheme I slicer (slice_tf_body.h:86-131 with the step of sfpu_tf_emu.hpp:193-198): p digits of
+// x*2^delta in radix `radix`, digit bound dmax, planes[i][r][c] as int8.
+void orc_oz1_slices(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int p, int radix,
+                    int dmax, int8_t* planes) {
+    const float r = (float)radix, dm = (float)dmax;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < rows; i++)
+        for (int j = 0; j < cols; j++) {
+            float hi, mid, lo;
+            load_triple(X[(size_t)i * ld + j], delta_of(delta, mode, i, j), hi, mid, lo);
+            for (int t = 0; t < p; t++) {
+                tf_mul_radix(hi, mid, lo, r);
+                float d = f_rnd(hi);
+                if (d < -dm)
+                    d = -dm;
+                else if (d >= dm)
+                    d = dm;
+                hi = f_sub(hi, d);
+                planes[((size_t)t * rows + i) * cols + j] = (int8_t)(int)d;
+            }
+        }
+}
+
+// Diagonal partial products P_d = sum_{i<=d} A_i B_{d-i} (ozaki1/gemm.hpp:315, stages.hpp:157), exact in
+// int64; A: p planes M x K, B: p planes K x N (row-major); P: ndiag planes M x N as int32. Returns the
+// largest |P| seen.
+int64_t orc_oz1_gemm_diag(const int8_t* A, const int8_t* B, int32_t* P, int M, int N, int K, int p, int ndiag) {
+    int64_t big = 0;
+#pragma omp parallel for schedule(static) reduction(max : big)
+    for (int i = 0; i < M; i++) {
+        std::vector<int64_t> row((size_t)N);
+        for (int d = 0; d < ndiag; d++) {
+            std::fill(row.begin(), row.end(), 0);
+            for (int a = 0; a <= d && a < p; a++) {
+                const int b = d - a;
+                if (b >= p) continue;
+                const int8_t* Ar = A + ((size_t)a * M + i) * K;
+                const int8_t* Bp = B + (size_t)b * K * N;
+                for (int k = 0; k < K; k++) {
+                    const int64_t av = Ar[k];
+                    if (!av) continue;
+                    const int8_t* Br = Bp + (size_t)k * N;
+                    for (int j = 0; j < N; j++) row[j] += av * Br[j];
+                }
+            }
+            for (int j = 0; j < N; j++) {
+                big = std::max<int64_t>(big, row[j] < 0 ? -row[j] : row[j]);
+                P[((size_t)d * M + i) * N + j] = (int32_t)row[j];
+            }
+        }
+    }
+    return big;
+}
+
+// Horner reconstruction and FP64 assembly of scheme I (recon_tf_i32in.cpp:116-157 with decode :87-113,
+// recon_f64_writer.cpp:148-160, assemble_tf_f64). P: ndiag int32 planes M x N. signmag = 1: the INT8
+// partial products (magnitude split at bit 8, sign multiplied back); 0: two's-complement split
+// (v & ~0xFF) + (v & 0xFF). The first nsingle diagonals are read with one conversion (two's complement
+// only). out = (hi+mid+lo) * radix^-(L+2) * 2^-(dA+dB).
+void orc_oz1_recon(const int32_t* P, int M, int N, int ndiag, int radix, int signmag, int nsingle, const int32_t* dA,
+                   const int32_t* dB, double* out) {
+    uint32_t Whi, Wlo;
+    int32_t qw;
+    oz1_scale_w(radix, ndiag - 1, Whi, Wlo, qw);
+    const float r = (float)radix;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float hi = 0.0f, mid = 0.0f, lo = 0.0f;
+            for (int d = 0; d < ndiag; d++) {
+                if (d > 0) tf_mul_radix(hi, mid, lo, r);
+                const int32_t v = P[((size_t)d * M + i) * N + j];
+                if (d < nsingle) {
+                    tf_add_s(hi, mid, lo, (float)v);
+                    continue;
+                }
+                float vh, vl;
+                if (signmag) {
+                    const uint32_t mag = v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
+                    const float sg = v > 0 ? 1.0f : (v < 0 ? -1.0f : 0.0f);
+                    vh = f_mul((float)(int32_t)(mag & 0x7FFFFF00u), sg);
+                    vl = f_mul((float)(int32_t)(mag & 0xFFu), sg);
+                } else {
+                    vh = (float)(int32_t)((uint32_t)v & 0xFFFFFF00u);
+                    vl = (float)(int32_t)((uint32_t)v & 0xFFu);
+                }
+                tf_add_s(hi, mid, lo, vh);
+                tf_add_s(hi, mid, lo, vl);
+            }
+            const uint64_t u = assemble_tf_f64(f_bits(hi), f_bits(mid), f_bits(lo), -(dA[i] + dB[j]), Whi, Wlo, qw);
+            std::memcpy(&out[(size_t)i * N + j], &u, 8);
+        }
+}
+
+void orc_oz1_scale_w(int radix, int L, uint32_t* Whi, uint32_t* Wlo, int32_t* qw) { oz1_scale_w(radix, L, *Whi, *Wlo, *qw); }
+
+// Scheme I INT8 end to end (ozaki1.cpp run(): scale with nshift -1 and rounding up, p slices of
+// radix 254, diagonal products, Horner reconstruction). A: M x K, B: K x N row-major, dimensions
+// already padded. Returns the largest |P_d|.
+int64_t orc_oz1_int8_gemm(const double* A, const double* B, int M, int N, int K, int p, double* out) {
+    std::vector<int32_t> dA(M), dB(N);
+    uint32_t fl = 0;
+    orc_scale(A, M, K, K, 0, 1, -1, dA.data(), &fl);
+    orc_scale(B, K, N, N, 1, 1, -1, dB.data(), &fl);
+    std::vector<int8_t> sa((size_t)p * M * K), sb((size_t)p * K * N);
+    orc_oz1_slices(A, M, K, K, 0, dA.data(), p, 254, 127, sa.data());
+    orc_oz1_slices(B, K, N, N, 1, dB.data(), p, 254, 127, sb.data());
+    std::vector<int32_t> P((size_t)p * M * N);
+    const int64_t big = orc_oz1_gemm_diag(sa.data(), sb.data(), P.data(), M, N, K, p, p);
+    orc_oz1_recon(P.data(), M, N, p, 254, 1, 0, dA.data(), dB.data(), out);
+    return big;
 }
 
 }  // extern "C"

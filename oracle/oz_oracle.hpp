@@ -14,6 +14,9 @@
 //   orc_oz2_crt_ref               reference output hashes (tools/validated/quick.csv:13,
 //                                 phi_sweep.log:116,122)
 //   orc_oz2_crt_exact             exact integer arithmetic; cross-checked against a binary128 GEMM
+//   orc_oz1_slices/gemm_diag/     reference output hashes of scheme I INT8 (tools/validated/quick.csv:12,
+//   recon/int8_gemm               phi_sweep.log chash of I-INT8 4096^3), the slice exactness
+//                                 invariant sum_i d_i radix^-(i+1) + residual == x*2^delta, brute force
 #pragma once
 #include <cstddef>
 #include <cstdint>
@@ -79,4 +82,19 @@ void orc_gemm_quad_sample(const double* A, const double* B, int M, int N, int K,
 // Dot2 compensated FP64 GEMM as the reference evaluator runs it (evaluation/numerics.hpp:58-93),
 // OpenMP over row blocks; returns hi and lo parts. rows [r0, r1) only.
 void orc_dot2_gemm(const double* A, const double* B, int M, int N, int K, int r0, int r1, double* Chi, double* Clo);
+
+// ---- Scheme I ----
+// Slicer (slice_tf_body.h:86-131): p digits of x*2^delta, radix `radix` (tfMulR, or tfMulP2 for a power
+// of two), digits clamp(Rnd(t0), +-dmax); planes[i][r][c].
+void orc_oz1_slices(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int p, int radix,
+                    int dmax, int8_t* planes);
+// Diagonal partial products P_d = sum_{i<=d} A_i B_{d-i} (ozaki1/gemm.hpp:315), exact; returns max |P|.
+int64_t orc_oz1_gemm_diag(const int8_t* A, const int8_t* B, int32_t* P, int M, int N, int K, int p, int ndiag);
+// Horner reconstruction + FP64 assembly (recon_tf_i32in.cpp:116-157, recon_f64_writer.cpp:148-160).
+void orc_oz1_recon(const int32_t* P, int M, int N, int ndiag, int radix, int signmag, int nsingle, const int32_t* dA,
+                   const int32_t* dB, double* out);
+// radix^-(L+2) as W = Whi:Wlo (64-bit significand) and 2^qw (ozaki1/plan.hpp:446-460).
+void orc_oz1_scale_w(int radix, int L, uint32_t* Whi, uint32_t* Wlo, int32_t* qw);
+// Scheme I INT8 end to end with p slices on padded row-major A, B; returns max |P_d|.
+int64_t orc_oz1_int8_gemm(const double* A, const double* B, int M, int N, int K, int p, double* out);
 }

@@ -91,6 +91,13 @@ class Plan2(ctypes.Structure):
                 ("wA", ctypes.c_double), ("wB", ctypes.c_double), ("b_cap", ctypes.c_int)]
 
 
+class Plan1(ctypes.Structure):
+    _fields_ = [("p", ctypes.c_int), ("pmax", ctypes.c_int), ("nsmall", ctypes.c_int), ("Kc", ctypes.c_uint),
+                ("nkb", ctypes.c_uint), ("pairloop", ctypes.c_int), ("pairwise", ctypes.c_int), ("fuse", ctypes.c_int),
+                ("defer", ctypes.c_int), ("Whi", ctypes.c_uint), ("Wlo", ctypes.c_uint), ("qw", ctypes.c_int),
+                ("bits_indep", ctypes.c_double), ("bits_sampled", ctypes.c_double)]
+
+
 _host = None
 _hip = None
 
@@ -217,6 +224,16 @@ def plan2_int8(a, b, M: int, N: int, K: int, max_moduli: int = 0,
     err = ctypes.create_string_buffer(2048)
     _raise(host().ozt_plan2_int8(_ptr(a), _ptr(b), M, N, K, max_moduli, int(reconstruction), fixed_bits,
                                  ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
+    return out
+
+
+def plan1(a, b, M: int, N: int, K: int, slices: int = 0, fmt: Format = Format.INT8) -> Plan1:
+    """Scheme I planner (slices, issue, reconstruction constants) on padded row-major A (M x K), B (K x N)."""
+    a, b = _f64(a), _f64(b)
+    out = Plan1()
+    err = ctypes.create_string_buffer(2048)
+    _raise(host().ozt_plan1(_ptr(a), _ptr(b), M, N, K, slices, int(fmt), ctypes.byref(out), err,
+                            ctypes.c_size_t(2048)), err)
     return out
 
 

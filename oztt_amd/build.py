@@ -38,10 +38,13 @@ HIP_SOURCES = {
     "oz2_split.hip": ["-fgpu-flush-denormals-to-zero"],
     "oz_gemm.hip": [],
     "oz2_crt.hip": [],
+    "oz1_slice.hip": ["-fgpu-flush-denormals-to-zero"],
+    "oz1_recon.hip": ["-fgpu-flush-denormals-to-zero"],
 }
 HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
               "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{CSRC / 'host'}"]
-HOST_SOURCES = ["context.cpp", "dispatch.cpp", "plan2.cpp", "ozaki2.cpp", "evaluation.cpp", "capi.cpp"]
+HOST_SOURCES = ["context.cpp", "dispatch.cpp", "norm.cpp", "pipeline.cpp", "plan1.cpp", "plan2.cpp", "ozaki1.cpp",
+                "ozaki2.cpp", "evaluation.cpp", "capi.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -10,6 +10,7 @@
 #include <ozTTgemm/ozTTgemm.hpp>
 
 #include "evaluation.hpp"
+#include "plan1.hpp"
 #include "plan2.hpp"
 
 namespace {
@@ -183,6 +184,38 @@ int ozt_choose_moduli_int8(unsigned K, int num_moduli, int b_cap, ozt_plan2* out
     for (int s = 0; s < out->S && s < 24; s++) out->m[s] = mo.m[s];
     out->log2M = mo.log2M;
     return 0;
+}
+
+// Scheme I planner on padded row-major A (M x K) and B (K x N); format 5 = INT8, 0 = BF16 constants.
+struct ozt_plan1 {
+    int p, pmax, nsmall;
+    unsigned Kc, nkb;
+    int pairloop, pairwise, fuse, defer;
+    unsigned Whi, Wlo;
+    int qw;
+    double bits_indep, bits_sampled;
+};
+int ozt_plan1(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned slices, int format,
+              ozt_plan1* out, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        const auto& f = format == 0 ? ozTTgemm::detail::kOz1Bf16 : ozTTgemm::detail::kOz1Int8;
+        const auto pl = ozTTgemm::detail::plan_scheme1(A, B, M, N, K, slices, f);
+        std::memset(out, 0, sizeof(*out));
+        out->p = pl.p;
+        out->pmax = pl.autop.pmax;
+        out->nsmall = pl.nsmall;
+        out->Kc = pl.issue.Kc;
+        out->nkb = pl.issue.nkb;
+        out->pairloop = pl.issue.pairloop;
+        out->pairwise = pl.issue.pairwise;
+        out->fuse = pl.issue.fuse;
+        out->defer = pl.issue.defer;
+        out->Whi = pl.Whi;
+        out->Wlo = pl.Wlo;
+        out->qw = pl.qw;
+        out->bits_indep = pl.autop.bits_indep;
+        out->bits_sampled = pl.autop.bits_sampled;
+    });
 }
 
 void ozt_eval_inputs(unsigned seed, double phi, std::size_t na, std::size_t nb, double* a, double* b) {

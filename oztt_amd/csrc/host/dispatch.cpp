@@ -38,13 +38,13 @@ void Workspace::release_all() {
 
 bool scheme_available(Format format, Scheme scheme) noexcept {
     switch (format) {
-    case Format::INT8: return scheme == Scheme::II;
+    case Format::INT8: return true;
     default: return false;
     }
 }
 
 Backend backend_for(Format format, Scheme scheme) {
-    if (format == Format::INT8 && scheme == Scheme::II) return ozaki2_int8_run;
+    if (format == Format::INT8) return scheme == Scheme::II ? ozaki2_int8_run : ozaki1_int8_run;
     throw std::invalid_argument("requested format was not built");
 }
 

@@ -1,0 +1,99 @@
+// Ozaki scheme I driver (INT8 slices): one FP64 GEMM on the GPU.
+//
+// Pipeline of the reference's src/ozaki1.cpp run(): number of slices p (given, or chosen from the
+// input, auto_precision.hpp:506) and the issue plan (plan.hpp:223) -> upload the FP64 operands ->
+// scale (row/column maxima rounded up to BF16, deltas nshift - e with nshift = -1) -> p slices of
+// radix 254 per operand -> the diagonal partial products P_d = sum_{i<=d} A_i B_{d-i}, each one
+// exact int32 accumulation over the d+1 pairs concatenated along K -> Horner reconstruction in
+// triple-float and FP64 assembly. INT8 admits a single K block only (plan.hpp:187-195), so the
+// reference's panels and row bands reduce to one launch per stage on one MI355X.
+//
+// Device layout: A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2]; slices of A: p planes of
+// Mg x Kg int8, of B: p planes of Ng x Kg (B transposed), both in the GEMM's OZ_BLOCK tiles (Mg, Ng
+// multiples of 256, Kg of 64); partial sums: p planes of Mg x Ng int32; output: M x N f64.
+#include <stdexcept>
+
+#include "backend.hpp"
+#include "evaluation.hpp"
+#include "pipeline.hpp"
+#include "plan1.hpp"
+
+namespace ozTTgemm::detail {
+namespace {
+
+namespace ev = ::ozTTgemm::evaluation;
+
+enum Slot { kA = 0, kB, kDA, kDB, kFlags, kSlicesA, kSlicesB, kPartial, kOut };
+
+std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / q * q; }
+
+}  // namespace
+
+Output ozaki1_int8_run(Device& D, const Problem& p) {
+    oz_dev* dev = D.dev;
+    const Oz1Format& f = kOz1Int8;
+    const Plan1 plan = plan_scheme1(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.slices, f);
+    const std::uint32_t M = p.m, N = p.n, K = p.k, P = (std::uint32_t)plan.p;
+    const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
+    if ((std::uint64_t)P * Kg * 127 * 127 > 0x7FFFFFFFull)
+        throw std::logic_error("scheme I plan: padded K breaks the single-block exactness");
+    const oz1_recon_dev rdesc{(int)P, f.radix, 1, 0, plan.Whi, plan.Wlo, plan.qw};
+
+    Workspace& ws = *D.ws;
+    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
+    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
+    auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
+    auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
+    auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
+    const long long strideA = (long long)Mg * Kg, strideB = (long long)Ng * Kg, strideP = (long long)Mg * Ng;
+    auto* slA = static_cast<std::int8_t*>(ws.get(kSlicesA, (std::size_t)P * strideA));
+    auto* slB = static_cast<std::int8_t*>(ws.get(kSlicesB, (std::size_t)P * strideB));
+    auto* part = static_cast<std::int32_t*>(ws.get(kPartial, sizeof(std::int32_t) * (std::size_t)P * strideP));
+    auto* out = static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
+
+    device_check(dev, oz_memcpy_h2d(dev, dAf, p.a.data(), sizeof(double) * p.a.size()), "upload A");
+    device_check(dev, oz_memcpy_h2d(dev, dBf, p.b.data(), sizeof(double) * p.b.size()), "upload B");
+
+    std::vector<Step> steps;
+    steps.push_back({ev::Scale, [=] {
+                         device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
+                         // INT8 rounds the BF16 of the maxima up; target 1/2 (format.hpp:76-101)
+                         device_check(dev, oz_scale_f64(dev, dAf, (int)M, (int)K, (int)K, 0, (int)f.ceil, f.nshift,
+                                                        dltA, flags),
+                                      "scale A");
+                         device_check(dev, oz_scale_f64(dev, dBf, (int)K, (int)N, (int)N, 1, (int)f.ceil, f.nshift,
+                                                        dltB, flags + 1),
+                                      "scale B");
+                     }});
+    steps.push_back({ev::Slice, [=] {
+                         device_check(dev,
+                                      oz1_split_int8(dev, dAf, (int)M, (int)K, (int)K, 0, dltA, (int)P, f.radix, f.dmax,
+                                                     slA, 2, (int)Mg, (int)Kg, strideA),
+                                      "slice A");
+                         device_check(dev,
+                                      oz1_split_int8(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, (int)P, f.radix, f.dmax,
+                                                     slB, 3, (int)Ng, (int)Kg, strideB),
+                                      "slice B");
+                     }});
+    steps.push_back({ev::Gemm, [=] {
+                         device_check(dev,
+                                      oz1_gemm_diag_i8(dev, slA, slB, part, (int)Mg, (int)Ng, (int)Kg, (int)P, (int)Ng,
+                                                       strideA, strideB, strideP),
+                                      "diagonal products");
+                     }});
+    steps.push_back({ev::Recon, [=] {
+                         device_check(dev,
+                                      oz1_recon_f64(dev, part, (int)M, (int)N, (int)Ng, strideP, &rdesc, dltA, dltB, out,
+                                                    (int)N),
+                                      "reconstruction");
+                     }});
+    // P(P+1)/2 slice-pair products of 2*M*N*K operations each
+    const unsigned pairs = P * (P + 1) / 2;
+    std::vector<double> values =
+        run_pipeline(dev, steps, 2, out, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
+    Info info{Scheme::I, Format::INT8};
+    info.slices = P;
+    return {std::move(values), info};
+}
+
+}  // namespace ozTTgemm::detail

@@ -20,6 +20,7 @@
 
 #include "backend.hpp"
 #include "evaluation.hpp"
+#include "pipeline.hpp"
 #include "plan2.hpp"
 
 namespace ozTTgemm::detail {
@@ -30,12 +31,6 @@ namespace ev = ::ozTTgemm::evaluation;
 enum Slot { kA = 0, kB, kDA, kDB, kFlags, kPlanesA, kPlanesB, kProducts, kOut };
 
 std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / q * q; }
-
-// A recorded device step: its phase and the launches it issues (stream-ordered, no host sync).
-struct Step {
-    ev::Phase phase;
-    std::function<void()> issue;
-};
 
 }  // namespace
 
@@ -99,60 +94,8 @@ Output ozaki2_int8_run(Device& D, const Problem& p) {
                                       "reconstruction");
                      }});
 
-    if (!es) {
-        for (auto& s : steps) s.issue();
-    } else {
-        // first pass: phase times with events on the stream (slots 2*phase, 2*phase+1)
-        for (auto& s : steps) {
-            device_check(dev, oz_event_record(dev, 2 * s.phase), "event");
-            s.issue();
-            device_check(dev, oz_event_record(dev, 2 * s.phase + 1), "event");
-        }
-        for (int ph = 0; ph < ev::PhaseCount; ph++) es->phase_ms[ph] = 0;
-        for (auto& s : steps) {
-            float ms = 0;
-            device_check(dev, oz_event_elapsed_ms(dev, 2 * s.phase, 2 * s.phase + 1, &ms), "event time");
-            es->phase_ms[s.phase] += ms;
-        }
-        es->partial_products = S;
-        es->product_ops = 2.0 * M * (double)N * K * S;
-        es->gemm_launches = 1;
-    }
-    std::vector<double> values((std::size_t)M * N);
-    device_check(dev, oz_memcpy_d2h(dev, values.data(), out, sizeof(double) * values.size()), "read C");
-    std::uint32_t fl[2];
-    device_check(dev, oz_memcpy_d2h(dev, fl, flags, sizeof fl), "read flags");
-
-    if (es && es->repeats > 0) {
-        // whole pass: warm up, then `repeats` replays between two events; then the product kernel
-        // alone, for its average launch time
-        for (int w = 0; w < es->warmup; w++)
-            for (auto& s : steps) s.issue();
-        device_check(dev, oz_event_record(dev, 20), "event");
-        for (int r = 0; r < es->repeats; r++)
-            for (auto& s : steps) s.issue();
-        device_check(dev, oz_event_record(dev, 21), "event");
-        float ms = 0;
-        device_check(dev, oz_event_elapsed_ms(dev, 20, 21, &ms), "event time");
-        es->whole_ms = ms / es->repeats;
-        std::vector<double> again(values.size());
-        device_check(dev, oz_memcpy_d2h(dev, again.data(), out, sizeof(double) * again.size()), "read C");
-        es->whole_checked = std::memcmp(again.data(), values.data(), sizeof(double) * values.size()) == 0;
-        device_check(dev, oz_event_record(dev, 22), "event");
-        for (int r = 0; r < es->repeats; r++) steps[2].issue();
-        device_check(dev, oz_event_record(dev, 23), "event");
-        device_check(dev, oz_event_elapsed_ms(dev, 22, 23, &ms), "event time");
-        es->gemm_launch_ms = ms / es->repeats;
-    }
-    // range flags of the scaling stage (scale.hpp:187-208); the host validation rejects these inputs
-    // first, so they only fire if the device disagrees with it
-    for (int t = 0; t < 2; t++)
-        if (fl[t]) {
-            const char* what = t == 0 ? "rows of A" : "columns of B";
-            if (fl[t] & 4u) throw std::runtime_error(std::string("the ") + what + " contain Inf or NaN");
-            if (fl[t] & 2u) throw std::runtime_error(std::string("a maximum of the ") + what + " is below 2^-126");
-            throw std::runtime_error(std::string("a maximum of the ") + what + " exceeds the BF16 range");
-        }
+    std::vector<double> values = run_pipeline(dev, steps, 2, out, (std::size_t)M * N, flags,
+                                              2.0 * M * (double)N * K * S, S);
     Info info{Scheme::II, Format::INT8};
     info.moduli = S;
     info.integer_bits = (std::uint32_t)plan.b;

@@ -2,6 +2,8 @@
 // expressions below must round exactly like the reference's (its Makefile:51-53 sets the same).
 #include "plan2.hpp"
 
+#include "norm.hpp"
+
 #include <algorithm>
 #include <cmath>
 #include <limits>
@@ -16,9 +18,6 @@
 namespace ozTTgemm::detail {
 namespace {
 
-static_assert(std::numeric_limits<long double>::digits == 64,
-              "the norm estimate accumulates in x86 extended precision, like the reference (bits.hpp:18-19)");
-
 // Candidate moduli of the INT8 path: pairwise coprime, descending (moduli.hpp:180-181).
 constexpr int kTableInt8[] = {255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217,
                               211, 199, 197, 193, 191, 181, 179, 173, 167, 163, 157, 151};
@@ -27,17 +26,6 @@ constexpr int kInt8ModCap = 255;     // OZ2_ROUTE_INT8.mod_cap (split.hpp:73)
 constexpr double kWinEps = 1e-9;     // strict window comparison (moduli.hpp:48)
 constexpr double kTailTol = 0.25;    // OZ2_TAIL_EXCESS_TOL (moduli.hpp:54)
 constexpr double kRecon1EpsLog2 = -70.0, kRecon1Margin = 2.0;  // auto_precision.hpp:126-127
-
-// Power of two by which a matrix is divided before sums of squares (norm_estimate.hpp:21-30).
-double pow2_scale(const double* v, std::size_t n) {
-    double mx = 0;
-    for (std::size_t i = 0; i < n; i++) mx = std::max(mx, std::fabs(v[i]));
-    if (!(mx > 0) || !std::isfinite(mx)) return 1.0;
-    int e;
-    std::frexp(mx, &e);
-    e = std::min(std::max(e, -1000), 1000);
-    return std::ldexp(1.0, e);
-}
 
 // Largest |r| with K*r^2 <= 2^acc_bits - 1 (moduli.hpp:224-231).
 long int8_rmax(std::uint32_t K) {
@@ -162,35 +150,7 @@ OperandStats measure_stats(const double* A, const double* B, std::uint32_t M, st
         st.nB += sB[c];
         st.wB = std::max(st.wB, wB[c]);
     }
-    // Hutchinson estimate of ||C||_F^2 with L = 8 Gaussian vectors, drop the largest sample, divide by
-    // 1 + 2 sqrt(2/L) (norm_estimate.hpp:49-73).
-    const std::uint32_t L = 8;
-    std::mt19937 rg(12345);
-    std::normal_distribution<double> nd(0.0, 1.0);
-    std::vector<double> g(N), y(K), q_i(M);
-    double cs2 = 0, cmax = 0;
-    for (std::uint32_t l = 0; l < L; l++) {
-        for (std::uint32_t j = 0; j < N; j++) g[j] = nd(rg);
-#pragma omp parallel for schedule(static)
-        for (std::int64_t k = 0; k < (std::int64_t)K; k++) {
-            long double s = 0;
-            const double* row = B + (std::size_t)k * N;
-            for (std::uint32_t j = 0; j < N; j++) s += (long double)(row[j] * rgB) * g[j];
-            y[k] = (double)s;
-        }
-#pragma omp parallel for schedule(static)
-        for (std::int64_t i = 0; i < (std::int64_t)M; i++) {
-            long double s = 0;
-            const double* row = A + (std::size_t)i * K;
-            for (std::uint32_t k = 0; k < K; k++) s += (long double)(row[k] * rgA) * y[k];
-            q_i[i] = (double)s;
-        }
-        double q = 0;
-        for (std::uint32_t i = 0; i < M; i++) q += q_i[i] * q_i[i];
-        cs2 += q;
-        cmax = std::max(cmax, q);
-    }
-    st.nC = (cs2 - cmax) / (L - 1) / (1.0 + 2.0 * std::sqrt(2.0 / (double)L));
+    st.nC = estimate_product_norm(A, B, M, N, K, rgA, rgB);
     st.measured = true;
     return st;
 }

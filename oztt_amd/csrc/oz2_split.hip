@@ -18,13 +18,14 @@
 //      MR(v) = v - rint(v*rinv)*m. Every product and sum there is an exact integer below 2^24
 //      except the rounded v*rinv, so writing MR as rint + fma gives the same value.
 //
-// MI355X design: one thread per 4 elements along the contiguous dimension of the output plane, so
-// every plane store is a 32-bit word and a wave writes 256 contiguous bytes. The B operand (layout
-// 1) is transposed through LDS so that its planes are K-contiguous for the MFMA GEMM. The kernel
-// is bound by its VALU work (about 12 operations per element and modulus), not by HBM.
-#include "oz_internal.hpp"
-
+// MI355X design. Layouts 2/3 (the GEMM's OZ_BLOCK tiles, the production path) run the blocked
+// splitter of oz_tf32.hpp: one wave per 1 KB block, one contiguous 1 KB store per plane. Layouts 0/1
+// (plain row-major planes): one thread per 4 elements along the contiguous dimension of the plane,
+// so every store is a 32-bit word; layout 1 is transposed through LDS. The kernels are bound by
+// their VALU work (about 12 operations per element and modulus), not by HBM.
 #pragma clang fp contract(off)
+
+#include "oz_tf32.hpp"
 
 namespace {
 
@@ -34,51 +35,6 @@ struct SplitConsts {
     float c[4][OZ2_MAXS];
 };
 
-// Step 1 (split_f64 + tf_load_f64).
-__device__ __forceinline__ void load_triple(double x, int32_t d, float& hi, float& mid, float& lo) {
-    const unsigned long long u = (unsigned long long)__double_as_longlong(x);
-    const uint32_t w1 = (uint32_t)(u >> 32), w0 = (uint32_t)u;
-    const uint32_t sgn = w1 & 0x80000000u;
-    const int32_t E = (int32_t)((w1 >> 20) & 0x7FFu);
-    if (E == 0) {  // zero and subnormals
-        hi = 0.0f;
-        mid = 0.0f;
-        lo = 0.0f;
-        return;
-    }
-    uint32_t a = 0x400000u | ((w1 & 0x000FFFFFu) << 2) | (w0 >> 30);
-    const uint32_t rem = w0 & 0x3FFFFFFFu;
-    int32_t r = (int32_t)rem;
-    if (rem >= 0x20000000u) {
-        a += 1u;
-        r = (int32_t)rem - 0x40000000;
-    }
-    const int32_t b = r >> 7;
-    const uint32_t c = (uint32_t)r & 0x7Fu;
-    const int32_t elsb = E - 1075 + d;
-    const bool carry = (a == 0x800000u);
-    const int32_t eh = carry ? elsb + 180 : elsb + 179;
-    const uint32_t mh = carry ? 0u : ((a << 1) & 0x7FFFFFu);
-    const int32_t es = elsb + 134;
-    const uint32_t hb = (eh > 0 && eh < 255) ? (sgn | ((uint32_t)eh << 23) | mh) : 0u;
-    const uint32_t sb = (es > 0 && es < 255) ? (sgn | ((uint32_t)es << 23)) : 0u;
-    const uint32_t braw = 0x4B000000u | (((uint32_t)(b + 0x400000)) & 0x7FFFFFu);
-    const uint32_t craw = 0x4B000000u | c;
-    const float s = __uint_as_float(sb);
-    hi = __uint_as_float(hb);
-    mid = (__uint_as_float(braw) - 12582912.0f) * s;
-    lo = ((__uint_as_float(craw) - 8388608.0f) * s) * 0.0078125f;
-}
-
-__device__ __forceinline__ void two_sum(float x, float y, float& s, float& e) {
-    s = x + y;
-    float bb = s - x;
-    float aa = s - bb;
-    aa = x - aa;
-    bb = y - bb;
-    e = aa + bb;
-}
-
 // Step 2: nd digits, top first.
 template <int ND>
 __device__ __forceinline__ void make_digits(double x, int32_t d, float* dig) {
@@ -86,17 +42,7 @@ __device__ __forceinline__ void make_digits(double x, int32_t d, float* dig) {
     load_triple(x, d, hi, mid, lo);
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
-        if (i > 0) {
-            hi = hi * 1048576.0f;
-            mid = mid * 1048576.0f;
-            lo = lo * 1048576.0f;
-            float s3, e4, s5, e6;
-            two_sum(mid, lo, s3, e4);
-            two_sum(hi, s3, s5, e6);
-            hi = s5;
-            mid = e6 + e4;  // FastTwoSum(e6, e4) -> (mid, lo)
-            lo = e4 - (mid - e6);
-        }
+        if (i > 0) tf_mul_pow2(hi, mid, lo, 1048576.0f);  // tfMulP2 by 2^20
         const float t = __builtin_rintf(hi);
         hi = hi - t;
         dig[i] = t;
@@ -126,9 +72,6 @@ __device__ __forceinline__ int residue(const float* dig, const SplitConsts& k, i
     return (int)mod_round(acc, m, ri);
 }
 
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
-}
 
 // Layout 0: planes[s][r][c], thread = 4 consecutive c of one row r; grid covers prow x pld.
 template <int ND>
@@ -200,78 +143,17 @@ __global__ void __launch_bounds__(256) split_tran_kernel(const double* __restric
     }
 }
 
-// Layouts 2/3 (OZ_BLOCK tiles): one wave per 1 KB block of 16 plane rows x 64 plane columns; the
-// wave writes each plane's block with one contiguous 1 KB store (16 bytes per lane, lane l -> block
-// bytes 16l..16l+15).
-//   Layout 3 (TRAN, plane row = column of X): lane l computes plane row l/4, plane columns
-//   16*(l%4)..+15 (= 16 consecutive rows of X in one column; a load instruction reads 4 runs of 16
-//   consecutive doubles) and packs its 16 residues into its own stored chunk.
-//   Layout 2: lane l computes plane column l of the 16 rows (each load instruction reads one
-//   contiguous 512-byte row segment of X); the residues of a plane are transposed through a 1 KB
-//   LDS image of the block (byte writes, then one 16-byte read per lane). The image is private to
-//   the wave, whose LDS operations execute in order, so no barrier is needed.
-__device__ __forceinline__ int block_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
-
-template <int ND, bool TRAN>
-__global__ void __launch_bounds__(256) split_block_kernel(const double* __restrict__ X, int rows, int cols, int ld,
-                                                          int mode, const int32_t* __restrict__ delta, SplitConsts k,
-                                                          int S, uint4* __restrict__ planes, int kblocks,
-                                                          long long nblocks, long long pstride_chunks) {
-    const long long blk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);  // block index within a plane
-    if (blk >= nblocks) return;
-    const int lane = threadIdx.x & 63;
-    const int br = (int)(blk / kblocks), bk = (int)(blk % kblocks);
-    float dig[16][ND];
-    if constexpr (TRAN) {
-        const int pr = br * 16 + (lane >> 2);       // plane row = column of X
-        const int pc0 = bk * 64 + 16 * (lane & 3);  // first of this lane's 16 plane columns = rows of X
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int xr = pc0 + e, xc = pr;
-            if (xr < rows && xc < cols) {
-                const int32_t d = mode == 0 ? delta[xr] : delta[xc];
-                make_digits<ND>(X[(size_t)xr * ld + xc], d, dig[e]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < ND; j++) dig[e][j] = 0.0f;
-            }
-        }
-        const int rr = lane >> 2;
-        uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
-        for (int s = 0; s < S; s++) {
-            uint4 v;
-            v.x = pack4(residue<ND>(dig[0], k, s), residue<ND>(dig[1], k, s), residue<ND>(dig[2], k, s), residue<ND>(dig[3], k, s));
-            v.y = pack4(residue<ND>(dig[4], k, s), residue<ND>(dig[5], k, s), residue<ND>(dig[6], k, s), residue<ND>(dig[7], k, s));
-            v.z = pack4(residue<ND>(dig[8], k, s), residue<ND>(dig[9], k, s), residue<ND>(dig[10], k, s), residue<ND>(dig[11], k, s));
-            v.w = pack4(residue<ND>(dig[12], k, s), residue<ND>(dig[13], k, s), residue<ND>(dig[14], k, s), residue<ND>(dig[15], k, s));
-            out[(long long)s * pstride_chunks] = v;
-        }
-    } else {
-        __shared__ __attribute__((aligned(16))) uint8_t image[4][1024];
-        uint8_t* img = image[threadIdx.x >> 6];
-        const int xc = bk * 64 + lane;  // plane column = column of X
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int xr = br * 16 + e;
-            if (xr < rows && xc < cols) {
-                const int32_t d = mode == 0 ? delta[xr] : delta[xc];
-                make_digits<ND>(X[(size_t)xr * ld + xc], d, dig[e]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < ND; j++) dig[e][j] = 0.0f;
-            }
-        }
-        // byte of (row e, column lane) inside the block image
-        const int colpart = 16 * (lane >> 4), colbyte = lane & 15;
-        uint4* out = planes + blk * 64 + lane;
-        for (int s = 0; s < S; s++) {
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-                img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)residue<ND>(dig[e], k, s);
-            out[(long long)s * pstride_chunks] = *reinterpret_cast<const uint4*>(img + 16 * lane);
-        }
-    }
-}
+// Layouts 2/3 (OZ_BLOCK tiles): split_block_kernel of oz_tf32.hpp with this generator: the
+// state of an element is its nd digits, plane s is its residue modulo m_s.
+template <int ND>
+struct ResidueGen {
+    SplitConsts k;
+    struct State {
+        float dig[ND];
+    };
+    __device__ __forceinline__ void load(State& st, double x, int32_t d) const { make_digits<ND>(x, d, st.dig); }
+    __device__ __forceinline__ int plane(State& st, int s) const { return residue<ND>(st.dig, k, s); }
+};
 
 template <int ND>
 __global__ void digits_kernel(const double* __restrict__ X, int rows, int cols, int ld, int mode,
@@ -308,12 +190,15 @@ int launch_split(oz_dev* dev, const double* X, int rows, int cols, int ld, int m
         const int kblocks = pld / 64;
         const long long nblocks = (long long)(prow / 16) * kblocks;
         const unsigned grid = oz::ceil_div(nblocks, 4);
+        const ResidueGen<ND> gen{k};
         if (layout == 2)
-            hipLaunchKernelGGL((split_block_kernel<ND, false>), dim3(grid), dim3(256), 0, dev->stream, X, rows, cols, ld,
-                               mode, delta, k, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks, pstride / 16);
+            hipLaunchKernelGGL((split_block_kernel<ResidueGen<ND>, false>), dim3(grid), dim3(256), 0, dev->stream, X,
+                               rows, cols, ld, mode, delta, gen, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks,
+                               pstride / 16);
         else
-            hipLaunchKernelGGL((split_block_kernel<ND, true>), dim3(grid), dim3(256), 0, dev->stream, X, rows, cols, ld,
-                               mode, delta, k, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks, pstride / 16);
+            hipLaunchKernelGGL((split_block_kernel<ResidueGen<ND>, true>), dim3(grid), dim3(256), 0, dev->stream, X,
+                               rows, cols, ld, mode, delta, gen, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks,
+                               pstride / 16);
         return oz::launch_check(dev, "split_block_kernel");
     }
     // transposed: plane rows = columns of X (prow of them, multiple of 64); plane bytes = rows of X

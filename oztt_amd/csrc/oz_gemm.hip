@@ -84,9 +84,13 @@ constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;  
 constexpr int LOADS_A = STAGE_A / 16 / THREADS, LOADS_B = STAGE_B / 16 / THREADS;  // per thread per stage
 static_assert(LOADS_A == 4 && LOADS_B == 4, "each thread moves 4+4 chunks of 16 bytes per stage");
 
-// DIGITS = false: C is int32 (the exact products). DIGITS = true: C is uint8 and receives the CRT
-// digit of each product for modulus `batch` (oz2::crt_digit with dc.m/y/magic[batch]).
-template <bool DIGITS>
+// Output modes. PRODUCTS: C[b] = A[b] Bt[b]^T as int32. DIGITS: the same products reduced in the
+// epilogue to the CRT digit for modulus b (oz2::crt_digit with dc.m/y/magic[b]), C as uint8. DIAG
+// (scheme I): C[d] = sum_{i <= d} A[i] Bt[d-i]^T as int32 for the diagonals d < nbatch, the d+1
+// slice pairs concatenated along K in one accumulation.
+enum GemmMode { PRODUCTS = 0, DIGITS = 1, DIAG = 2 };
+
+template <int MODE>
 __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ Bt,
                                                           void* __restrict__ C, int K, int ldc, long long sA,
                                                           long long sB, long long sC, int tiles_m, int tiles_n,
@@ -94,24 +98,46 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * STAGE];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     int batch, tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, nbatch, batch, tm, tn);
+    if constexpr (MODE == DIAG) {
+        // Diagonal d has d+1 pairs: the heaviest go first (workgroups start in index order), and
+        // within a diagonal the XCD-aware order applies.
+        const int per = tiles_m * tiles_n, b = blockIdx.x / per;
+        int unused;
+        tile_of(blockIdx.x - b * per, tiles_m, tiles_n, 1, unused, tm, tn);
+        batch = nbatch - 1 - b;
+    } else {
+        tile_of(blockIdx.x, tiles_m, tiles_n, nbatch, batch, tm, tn);
+    }
     const int nk = K / BK;  // blocks per 16-row band
+    const int nsteps = MODE == DIAG ? (batch + 1) * nk : nk;  // K steps of this tile
     const long long band = (long long)nk * 1024;  // bytes of one 16-row band
     // Lane l copies bytes 16l..16l+15 of each block; the tile's first band is 16*tm (A), 16*tn (B).
-    const int8_t* Ab = A + batch * sA + (long long)tm * (BM / 16) * band + 16 * lane;
-    const int8_t* Bb = Bt + batch * sB + (long long)tn * (BN / 16) * band + 16 * lane;
+    const int8_t* Ab = A + (MODE == DIAG ? 0 : batch * sA) + (long long)tm * (BM / 16) * band + 16 * lane;
+    const int8_t* Bb = Bt + (MODE == DIAG ? 0 : batch * sB) + (long long)tn * (BN / 16) * band + 16 * lane;
+    // Byte offsets of K step u: block u of the bands, or for DIAG block u%nk of pair i = u/nk
+    // (A plane i, B plane batch-i).
+    auto step_off = [&](int u, long long& oa, long long& ob) {
+        if constexpr (MODE == DIAG) {
+            const int i = u / nk, kt = u - i * nk;
+            oa = i * sA + (long long)kt * 1024;
+            ob = (batch - i) * sB + (long long)kt * 1024;
+        } else {
+            oa = ob = (long long)u * 1024;
+        }
+    };
 
     // Loader: wave instruction j (= 4*i + wave) copies block (band j of the tile, K step kstep) to
     // bytes 1024j.. of the stage, i.e. rows 16j..16j+15 of the 256 x 64 stage, swizzle included.
 #define OZ_GEMM_ISSUE(kstep, buf)                                                                                 \
     do {                                                                                                          \
-        const long long koff = (long long)(kstep) * 1024;                                                         \
+        long long oa, ob;                                                                                         \
+        step_off(kstep, oa, ob);                                                                                  \
         int8_t* sa = lds + (buf) * STAGE;                                                                         \
         _Pragma("unroll") for (int i = 0; i < LOADS_A; i++)                                                       \
-            __builtin_amdgcn_global_load_lds(Ab + (4 * i + wave) * band + koff, (lds_void*)(sa + 1024 * (4 * i + wave)), \
+            __builtin_amdgcn_global_load_lds(Ab + (4 * i + wave) * band + oa, (lds_void*)(sa + 1024 * (4 * i + wave)), \
                                              16, 0, 0);                                                           \
         _Pragma("unroll") for (int i = 0; i < LOADS_B; i++)                                                       \
-            __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + koff,                                   \
+            __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + ob,                                     \
                                              (lds_void*)(sa + STAGE_A + 1024 * (4 * i + wave)), 16, 0, 0);        \
     } while (0)
 
@@ -143,7 +169,7 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
     // F = substep (kt+1, 0) while its MFMAs run on G. The tail re-loads the last valid stage
     // (clamped), so every step has the same number of loads in flight and the same wait count.
 #pragma unroll
-    for (int s = 0; s < NS; s++) OZ_GEMM_ISSUE(min(s, nk - 1), s);
+    for (int s = 0; s < NS; s++) OZ_GEMM_ISSUE(min(s, nsteps - 1), s);
     v4i fa[4], fb[4], ga[4], gb[4];
     wait_vmcnt<(LOADS_A + LOADS_B) * (NS - 1)>();  // stage 0
     stage_barrier();
@@ -156,7 +182,7 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
     // sinks every fragment read to just before its first use, which stalls the MFMAs on LDS
     // latency): the 8 fragment reads of the other buffer, and after the barrier the 8 global->LDS
     // loads, go one per MFMA over the first 8 of the 16 MFMAs of each substep.
-    for (int kt = 0; kt < nk; kt++) {
+    for (int kt = 0; kt < nsteps; kt++) {
         const int8_t* cur = lds + (kt % NS) * STAGE;
         const int8_t* nxt = lds + ((kt + 1) % NS) * STAGE;
         // substep (kt, 0): MFMAs on F, reads of G = substep (kt, 1)
@@ -170,18 +196,19 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
         wait_vmcnt_lgkm0<(LOADS_A + LOADS_B) * (NS - 2)>();  // stage kt+1 landed; own reads of stage kt done
         stage_barrier();                                      // ... for every wave
         // substep (kt, 1): MFMAs on G, refill of stage kt's buffer, reads of F = substep (kt+1, 0)
-        const long long koff = (long long)min(kt + NS, nk - 1) * 1024;
+        long long oa, ob;
+        step_off(min(kt + NS, nsteps - 1), oa, ob);
         int8_t* sa = lds + (kt % NS) * STAGE;
 #pragma unroll
         for (int g = 0; g < 16; g++) {
             acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ga[g >> 2], gb[g & 3], acc[g >> 2][g & 3], 0, 0, 0);
             if (g < 4) {
-                __builtin_amdgcn_global_load_lds(Ab + (4 * g + wave) * band + koff, (lds_void*)(sa + 1024 * (4 * g + wave)),
+                __builtin_amdgcn_global_load_lds(Ab + (4 * g + wave) * band + oa, (lds_void*)(sa + 1024 * (4 * g + wave)),
                                                  16, 0, 0);
                 fa[g] = *reinterpret_cast<const v4i*>(nxt + offA[0] + g * 32 * BK);
             } else if (g < 8) {
                 const int i = g - 4;
-                __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + koff,
+                __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + ob,
                                                  (lds_void*)(sa + STAGE_A + 1024 * (4 * i + wave)), 16, 0, 0);
                 fb[i] = *reinterpret_cast<const v4i*>(nxt + offB[0] + i * 32 * BK);
             }
@@ -192,7 +219,7 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
     wait_vmcnt<0>();  // drain the clamped tail loads before the workgroup ends
 
     const long long c0 = batch * sC + (long long)(tm * BM + wm * 128) * ldc + tn * BN + wn * 128;
-    if constexpr (DIGITS) {
+    if constexpr (MODE == DIGITS) {
         // Digits go through LDS (the stages are free once every wave has left the main loop) so
         // that each lane stores 16 contiguous bytes: the wave's 128 x 128 byte tile is written
         // with row stride 144 (rows r and r+4, written by the two lane halves, then fall on
@@ -240,12 +267,12 @@ const char* check_gemm(const int8_t* A, const int8_t* Bt, const void* C, int M, 
     return nullptr;
 }
 
-template <bool DIGITS>
+template <int MODE>
 int launch_gemm(oz_dev* dev, const int8_t* A, const int8_t* Bt, void* C, int M, int N, int K, int batch, int ldc,
                 long long strideA, long long strideB, long long strideC, const oz2::DigitConsts& dc) {
     const int tiles_m = M / BM, tiles_n = N / BN;
     const unsigned grid = (unsigned)((long long)tiles_m * tiles_n * batch);
-    hipLaunchKernelGGL(gemm_i8_kernel<DIGITS>, dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc, strideA,
+    hipLaunchKernelGGL(gemm_i8_kernel<MODE>, dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc, strideA,
                        strideB, strideC, tiles_m, tiles_n, batch, dc);
     return oz::launch_check(dev, "gemm_i8_kernel");
 }
@@ -257,7 +284,7 @@ extern "C" int oz_gemm_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_
     if (int st = oz::use(dev)) return st;
     if (const char* e = check_gemm(A, Bt, C, M, N, K, batch, ldc, strideA, strideB, strideC))
         return oz::fail(dev, OZ_ERR_ARG, "oz_gemm_i8: %s (M=%d N=%d K=%d batch=%d)", e, M, N, K, batch);
-    return launch_gemm<false>(dev, A, Bt, C, M, N, K, batch, ldc, strideA, strideB, strideC, oz2::DigitConsts{});
+    return launch_gemm<PRODUCTS>(dev, A, Bt, C, M, N, K, batch, ldc, strideA, strideB, strideC, oz2::DigitConsts{});
 }
 
 extern "C" int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, int M, int N, int K, int S,
@@ -277,5 +304,16 @@ extern "C" int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, u
         dc.y[s] = crt->y[s];
         dc.magic[s] = (uint32_t)(0x100000000ull / m);
     }
-    return launch_gemm<true>(dev, A, Bt, D, M, N, K, S, ldd, strideA, strideB, strideD, dc);
+    return launch_gemm<DIGITS>(dev, A, Bt, D, M, N, K, S, ldd, strideA, strideB, strideD, dc);
+}
+
+extern "C" int oz1_gemm_diag_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K,
+                                int ndiag, int ldc, long long strideA, long long strideB, long long strideC) {
+    if (int st = oz::use(dev)) return st;
+    if (const char* e = check_gemm(A, Bt, C, M, N, K, ndiag, ldc, strideA, strideB, strideC))
+        return oz::fail(dev, OZ_ERR_ARG, "oz1_gemm_diag_i8: %s (M=%d N=%d K=%d ndiag=%d)", e, M, N, K, ndiag);
+    // one accumulation covers ndiag*K products of at most 127^2: it must stay exact in int32
+    if ((long long)ndiag * K * 127 * 127 > 0x7FFFFFFFll)
+        return oz::fail(dev, OZ_ERR_ARG, "oz1_gemm_diag_i8: %d pairs of K=%d can overflow int32", ndiag, K);
+    return launch_gemm<DIAG>(dev, A, Bt, C, M, N, K, ndiag, ldc, strideA, strideB, strideC, oz2::DigitConsts{});
 }

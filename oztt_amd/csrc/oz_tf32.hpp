@@ -1,0 +1,210 @@
+// Triple-float FP32 procedures of the splitters and the scheme I reconstruction, and the blocked
+// splitter kernel shared by both schemes.
+//
+// The reference defines its slices, digits and residues through binary32 operations with
+// round-to-nearest-even, no fused multiply-add, and denormal inputs and outputs flushed to zero
+// (its FP32 model, experiments/src/checks/sfpu_tf_emu.hpp:66-156). Every file that includes this
+// header is compiled with -ffp-contract=off and -fgpu-flush-denormals-to-zero, and sets
+// `#pragma clang fp contract(off)` before the include, so each operation below is one such binary32
+// operation. Zero signs can differ from the model (its products with a zero factor are +0); a zero's
+// sign never changes a digit, residue or reconstructed value.
+#pragma once
+#include "oz_internal.hpp"
+
+namespace {
+
+// split_f64 + tf_load_f64 (reference f64_tf.h:141-172, slice_tf_core.h:67-76): x*2^d as the
+// triple-float (hi, mid, lo), built with integer operations on the FP64 words.
+__device__ __forceinline__ void load_triple(double x, int32_t d, float& hi, float& mid, float& lo) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(x);
+    const uint32_t w1 = (uint32_t)(u >> 32), w0 = (uint32_t)u;
+    const uint32_t sgn = w1 & 0x80000000u;
+    const int32_t E = (int32_t)((w1 >> 20) & 0x7FFu);
+    if (E == 0) {  // zero and subnormals
+        hi = 0.0f;
+        mid = 0.0f;
+        lo = 0.0f;
+        return;
+    }
+    uint32_t a = 0x400000u | ((w1 & 0x000FFFFFu) << 2) | (w0 >> 30);
+    const uint32_t rem = w0 & 0x3FFFFFFFu;
+    int32_t r = (int32_t)rem;
+    if (rem >= 0x20000000u) {
+        a += 1u;
+        r = (int32_t)rem - 0x40000000;
+    }
+    const int32_t b = r >> 7;
+    const uint32_t c = (uint32_t)r & 0x7Fu;
+    const int32_t elsb = E - 1075 + d;
+    const bool carry = (a == 0x800000u);
+    const int32_t eh = carry ? elsb + 180 : elsb + 179;
+    const uint32_t mh = carry ? 0u : ((a << 1) & 0x7FFFFFu);
+    const int32_t es = elsb + 134;
+    const uint32_t hb = (eh > 0 && eh < 255) ? (sgn | ((uint32_t)eh << 23) | mh) : 0u;
+    const uint32_t sb = (es > 0 && es < 255) ? (sgn | ((uint32_t)es << 23)) : 0u;
+    const uint32_t braw = 0x4B000000u | (((uint32_t)(b + 0x400000)) & 0x7FFFFFu);
+    const uint32_t craw = 0x4B000000u | c;
+    const float s = __uint_as_float(sb);
+    hi = __uint_as_float(hb);
+    mid = (__uint_as_float(braw) - 12582912.0f) * s;
+    lo = ((__uint_as_float(craw) - 8388608.0f) * s) * 0.0078125f;
+}
+
+// TwoSum (Knuth) and FastTwoSum (Dekker) in the reference's operation order (sfpu_tf_proc.h:61-74).
+__device__ __forceinline__ void two_sum(float x, float y, float& s, float& e) {
+    s = x + y;
+    float bb = s - x;
+    float aa = s - bb;
+    aa = x - aa;
+    bb = y - bb;
+    e = aa + bb;
+}
+__device__ __forceinline__ void fast_two_sum(float a, float b, float& s, float& t) {
+    s = a + b;
+    const float w = s - a;
+    t = b - w;
+}
+
+// tfMulP2: the triple times a power of two r, renormalized (sfpu_tf_proc.h:160-169).
+__device__ __forceinline__ void tf_mul_pow2(float& hi, float& mid, float& lo, float r) {
+    hi = hi * r;
+    mid = mid * r;
+    lo = lo * r;
+    float s3, e4, s5, e6;
+    two_sum(mid, lo, s3, e4);
+    two_sum(hi, s3, s5, e6);
+    hi = s5;
+    fast_two_sum(e6, e4, mid, lo);
+}
+
+// tfMulR: the triple times a general radix r <= 254, each limb split by Dekker's 4097 so that the
+// limb products are exact, then renormalized (sfpu_tf_proc.h:108-141; names of the procedure).
+__device__ __forceinline__ void tf_mul_r(float& hi, float& mid, float& lo, float r) {
+    const float acc_lo = lo * r;
+    float t1 = mid * 4097.0f;
+    float t2 = t1 - mid;
+    t1 = t1 - t2;                    // upper half of mid
+    t2 = mid - t1;                   // lower half of mid
+    t1 = t1 * r;
+    t2 = t2 * r;
+    const float P1 = t1 + t2;        // term
+    float keep = P1 - t1;
+    float tmp0 = t2 - keep;          // F1
+    t1 = hi * 4097.0f;
+    t2 = t1 - hi;
+    t1 = t1 - t2;                    // upper half of hi
+    t2 = hi - t1;                    // lower half of hi
+    t1 = t1 * r;
+    t2 = t2 * r;
+    const float P0 = t1 + t2;        // acc_mid
+    keep = P0 - t1;
+    const float F0 = t2 - keep;      // acc_hi
+    tmp0 = tmp0 + acc_lo;            // G1
+    float sa, ea, sb, eb, r0, ec;
+    two_sum(P1, tmp0, sa, ea);
+    two_sum(F0, sa, sb, eb);
+    two_sum(P0, sb, r0, ec);
+    const float G = ea + eb;
+    hi = r0;
+    fast_two_sum(ec, G, mid, lo);
+}
+
+// tfMulRadix (sfpu_tf.h:131-134): tfMulP2 for a power-of-two radix, tfMulR otherwise.
+template <bool POW2>
+__device__ __forceinline__ void tf_mul_radix(float& hi, float& mid, float& lo, float r) {
+    if constexpr (POW2)
+        tf_mul_pow2(hi, mid, lo, r);
+    else
+        tf_mul_r(hi, mid, lo, r);
+}
+
+// tfAddS<3>: the triple plus v (sfpu_tf_proc.h:184-198).
+__device__ __forceinline__ void tf_add_s(float& hi, float& mid, float& lo, float v) {
+    float tmp0 = hi + v;
+    float tmp1 = tmp0 - hi;
+    float tmp2 = tmp0 - tmp1;
+    tmp2 = hi - tmp2;
+    tmp1 = v - tmp1;
+    tmp1 = tmp2 + tmp1;
+    hi = tmp0;
+    tmp0 = mid + tmp1;
+    tmp2 = tmp0 - mid;
+    float term = tmp0 - tmp2;
+    term = mid - term;
+    tmp2 = tmp1 - tmp2;
+    tmp2 = term + tmp2;
+    mid = tmp0;
+    lo = lo + tmp2;
+}
+
+// ---- Blocked splitter ----------------------------------------------------------------------
+// OZ_BLOCK tiles (include/oz_hip.h): 1 KB blocks of 16 plane rows x 64 plane columns, chunk c of
+// row r at chunk position c ^ block_swizzle(r).
+__device__ __forceinline__ int block_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+// One wave per block; the wave writes each plane's block with one contiguous 1 KB store (lane l ->
+// block bytes 16l..16l+15). GEN supplies the per-element state and, called with s = 0, 1, ... in
+// order, the int8 value of plane s (GEN::State, GEN::load, GEN::plane).
+//   TRAN (plane row = column of X): lane l computes plane row l/4, plane columns 16*(l%4)..+15
+//   (16 consecutive rows of X in one column; a load instruction reads 4 runs of 16 consecutive
+//   doubles) and packs its 16 values into its own stored chunk.
+//   !TRAN: lane l computes plane column l of the 16 rows (each load instruction reads one
+//   contiguous 512-byte row segment of X); each plane is transposed through a 1 KB LDS image of the
+//   block (byte writes, then one 16-byte read per lane). The image is private to the wave, whose
+//   LDS operations execute in order, so no barrier is needed.
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
+}
+
+template <class GEN, bool TRAN>
+__global__ void __launch_bounds__(256) split_block_kernel(const double* __restrict__ X, int rows, int cols, int ld,
+                                                          int mode, const int32_t* __restrict__ delta, GEN gen,
+                                                          int nplanes, uint4* __restrict__ planes, int kblocks,
+                                                          long long nblocks, long long pstride_chunks) {
+    const long long blk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);  // block index within a plane
+    if (blk >= nblocks) return;
+    const int lane = threadIdx.x & 63;
+    const int br = (int)(blk / kblocks), bk = (int)(blk % kblocks);
+    typename GEN::State st[16];
+    if constexpr (TRAN) {
+        const int pr = br * 16 + (lane >> 2);       // plane row = column of X
+        const int pc0 = bk * 64 + 16 * (lane & 3);  // first of this lane's 16 plane columns = rows of X
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int xr = pc0 + e, xc = pr;
+            const bool in = xr < rows && xc < cols;
+            gen.load(st[e], in ? X[(size_t)xr * ld + xc] : 0.0, in ? (mode == 0 ? delta[xr] : delta[xc]) : 0);
+        }
+        const int rr = lane >> 2;
+        uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
+        for (int s = 0; s < nplanes; s++) {
+            int v[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) v[e] = gen.plane(st[e], s);
+            out[(long long)s * pstride_chunks] = make_uint4(pack4(v[0], v[1], v[2], v[3]), pack4(v[4], v[5], v[6], v[7]),
+                                                            pack4(v[8], v[9], v[10], v[11]),
+                                                            pack4(v[12], v[13], v[14], v[15]));
+        }
+    } else {
+        __shared__ __attribute__((aligned(16))) uint8_t image[4][1024];
+        uint8_t* img = image[threadIdx.x >> 6];
+        const int xc = bk * 64 + lane;  // plane column = column of X
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int xr = br * 16 + e;
+            const bool in = xr < rows && xc < cols;
+            gen.load(st[e], in ? X[(size_t)xr * ld + xc] : 0.0, in ? (mode == 0 ? delta[xr] : delta[xc]) : 0);
+        }
+        // byte of (row e, column lane) inside the block image
+        const int colpart = 16 * (lane >> 4), colbyte = lane & 15;
+        uint4* out = planes + blk * 64 + lane;
+        for (int s = 0; s < nplanes; s++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)gen.plane(st[e], s);
+            out[(long long)s * pstride_chunks] = *reinterpret_cast<const uint4*>(img + 16 * lane);
+        }
+    }
+}
+
+}  // namespace

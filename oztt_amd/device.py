@@ -17,6 +17,11 @@ class ModuliDesc(ctypes.Structure):
                 ("rinv", ctypes.c_float * OZ2_MAXS), ("c", (ctypes.c_float * OZ2_MAXS) * 4)]
 
 
+class Oz1ReconDesc(ctypes.Structure):
+    _fields_ = [("ndiag", ctypes.c_int), ("radix", ctypes.c_int), ("signmag", ctypes.c_int), ("nsingle", ctypes.c_int),
+                ("Whi", ctypes.c_uint32), ("Wlo", ctypes.c_uint32), ("qw", ctypes.c_int32)]
+
+
 class CrtDesc(ctypes.Structure):
     _fields_ = [("S", ctypes.c_int), ("b", ctypes.c_int), ("shift", ctypes.c_int), ("nw", ctypes.c_int),
                 ("m", ctypes.c_uint32 * OZ2_MAXS), ("y", ctypes.c_uint32 * OZ2_MAXS),
@@ -152,6 +157,20 @@ class Device:
     def crt_digits(self, D: Buffer, M, N, ldd, sD, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
         self._check(hip().oz2_crt_digits_f64(self.h, D.ptr, M, N, ldd, ctypes.c_longlong(sD), ctypes.byref(desc),
                                              dA.ptr, dB.ptr, out.ptr, ldo), "oz2_crt_digits_f64")
+
+    # ---- scheme I ----
+    def oz1_split(self, X: Buffer, rows, cols, ld, mode, delta: Buffer, p, radix, dmax, planes: Buffer, layout, prow,
+                  pld, pstride):
+        self._check(hip().oz1_split_int8(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, p, radix, dmax, planes.ptr,
+                                         layout, prow, pld, ctypes.c_longlong(pstride)), "oz1_split_int8")
+
+    def oz1_gemm_diag(self, A: Buffer, Bt: Buffer, C: Buffer, M, N, K, ndiag, ldc, sA, sB, sC):
+        self._check(hip().oz1_gemm_diag_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, ndiag, ldc, ctypes.c_longlong(sA),
+                                           ctypes.c_longlong(sB), ctypes.c_longlong(sC)), "oz1_gemm_diag_i8")
+
+    def oz1_recon(self, P: Buffer, M, N, ldp, sP, desc: "Oz1ReconDesc", dA: Buffer, dB: Buffer, out: Buffer, ldo):
+        self._check(hip().oz1_recon_f64(self.h, P.ptr, M, N, ldp, ctypes.c_longlong(sP), ctypes.byref(desc), dA.ptr,
+                                        dB.ptr, out.ptr, ldo), "oz1_recon_f64")
 
     def crt(self, C: Buffer, M, N, ldc, sC, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
         self._check(hip().oz2_crt_f64(self.h, C.ptr, M, N, ldc, ctypes.c_longlong(sC), ctypes.byref(desc), dA.ptr,

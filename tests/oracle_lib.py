@@ -25,6 +25,8 @@ class Oracle:
         lib.orc_gemm_i8.restype = ctypes.c_int64
         lib.orc_modround.restype = ctypes.c_float
         lib.orc_modround.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        lib.orc_oz1_gemm_diag.restype = ctypes.c_int64
+        lib.orc_oz1_int8_gemm.restype = ctypes.c_int64
 
     def inputs(self, seed, phi, na, nb):
         a = np.empty(na)
@@ -116,6 +118,56 @@ class Oracle:
         lo = np.empty(M * N)
         self.lib.orc_dot2_gemm(P(np.ascontiguousarray(A)), P(np.ascontiguousarray(B)), M, N, K, r0, r1, P(hi), P(lo))
         return hi, lo
+
+
+def _oz1_slices(self, X, rows, cols, mode, delta, p, radix, dmax):
+    """Scheme I digit planes [p][rows][cols] (int8)."""
+    X = np.ascontiguousarray(X, dtype=np.float64)
+    out = np.empty((p, rows, cols), dtype=np.int8)
+    self.lib.orc_oz1_slices(P(X), rows, cols, cols, mode, P(np.ascontiguousarray(delta, dtype=np.int32)), p, radix,
+                            dmax, P(out))
+    return out
+
+
+def _oz1_gemm_diag(self, A, B, ndiag):
+    """A: [p][M][K] int8, B: [p][K][N] int8 -> P_d [ndiag][M][N] int32 (and the largest |P|)."""
+    A = np.ascontiguousarray(A, dtype=np.int8)
+    B = np.ascontiguousarray(B, dtype=np.int8)
+    p, M, K = A.shape
+    N = B.shape[2]
+    out = np.empty((ndiag, M, N), dtype=np.int32)
+    big = self.lib.orc_oz1_gemm_diag(P(A), P(B), P(out), M, N, K, p, ndiag)
+    return out, int(big)
+
+
+def _oz1_recon(self, Pd, radix, signmag, nsingle, dA, dB):
+    Pd = np.ascontiguousarray(Pd, dtype=np.int32)
+    ndiag, M, N = Pd.shape
+    out = np.empty(M * N)
+    self.lib.orc_oz1_recon(P(Pd), M, N, ndiag, radix, signmag, nsingle, P(np.ascontiguousarray(dA, dtype=np.int32)),
+                           P(np.ascontiguousarray(dB, dtype=np.int32)), P(out))
+    return out
+
+
+def _oz1_scale_w(self, radix, L):
+    whi, wlo, qw = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_int32()
+    self.lib.orc_oz1_scale_w(radix, L, ctypes.byref(whi), ctypes.byref(wlo), ctypes.byref(qw))
+    return whi.value, wlo.value, qw.value
+
+
+def _oz1_int8_gemm(self, A, B, M, N, K, p):
+    A = np.ascontiguousarray(A, dtype=np.float64)
+    B = np.ascontiguousarray(B, dtype=np.float64)
+    out = np.empty(M * N)
+    big = self.lib.orc_oz1_int8_gemm(P(A), P(B), M, N, K, p, P(out))
+    return out, int(big)
+
+
+Oracle.oz1_slices = _oz1_slices
+Oracle.oz1_gemm_diag = _oz1_gemm_diag
+Oracle.oz1_recon = _oz1_recon
+Oracle.oz1_scale_w = _oz1_scale_w
+Oracle.oz1_int8_gemm = _oz1_int8_gemm
 
 
 def load_oracle() -> Oracle:

@@ -1,0 +1,188 @@
+"""Scheme I INT8 on the GPU, through the C ABI and the public API.
+
+1. Stages against the oracle, bit-exact: digit planes (radix 254 and 64, OZ_BLOCK layouts 2 and 3),
+   the int32 diagonal products, and the Horner reconstruction (both input encodings).
+2. The whole call reproduces the reference's published outputs bit for bit: the I-INT8 128^3 hash
+   (tools/validated/quick.csv:12) and the 4096^3 output hashes of the phi sweep
+   (experiments/paper_logs/accuracy_logs/phi_sweep.log, CONFIG chash, seed 7), with the slice
+   count given and chosen automatically.
+3. C2 itself (4096^3, seed 2, phi 1, automatic p): slices and int32 diagonal products bit-exact
+   against the oracle, C within the error model against binary128.
+"""
+import numpy as np
+import pytest
+
+import oztt_amd as oz
+from oztt_amd.device import Oz1ReconDesc, from_blocks, to_blocks
+
+pytestmark = pytest.mark.gpu
+
+I_INT8 = oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = oz.Context()
+    yield c
+    c.close()
+
+
+def edge_rows(rows, cols, rng):
+    X = rng.uniform(-1, 1, (rows, cols)) * np.exp2(rng.integers(-40, 40, (rows, 1)))
+    X[0] = 0.0
+    X[1, :] = 0.25
+    X[1, 3] = -0.5                                   # exact power-of-two maximum
+    X[2, 5] = 1.0 + 2.0 ** -40                        # dropped bits below the BF16 significand
+    X[3, :] = rng.uniform(-1, 1, cols) * 2.0 ** -60   # wide range inside one row
+    X[3, 0] = 1.0
+    X[4, 1] = 1e-300                                  # an element far below its row maximum
+    return X
+
+
+@pytest.mark.parametrize("layout", [2, 3])
+@pytest.mark.parametrize("radix,dmax,ceil,p", [(254, 127, 1, 8), (254, 127, 1, 13), (64, 32, 0, 10)])
+def test_slices_match_oracle(dev, oracle, layout, radix, dmax, ceil, p):
+    rng = np.random.default_rng(radix + p + layout)
+    tran = layout == 3
+    rows, cols = (200, 96) if tran else (96, 200)
+    X = edge_rows(cols, rows, rng).T.copy() if tran else edge_rows(rows, cols, rng)
+    mode = 1 if tran else 0
+    delta, fl = oracle.scale(X, rows, cols, mode, ceil, -1)
+    want = oracle.oz1_slices(X, rows, cols, mode, delta, p, radix, dmax)  # [p][rows][cols]
+    prow = ((cols if tran else rows) + 15) // 16 * 16 + 16
+    pld = ((rows if tran else cols) + 63) // 64 * 64 + 64
+    pstride = prow * pld + 1024
+    bx, bd = dev.upload(X), dev.upload(delta)
+    bp = dev.alloc(p * pstride)
+    dev.oz1_split(bx, rows, cols, cols, mode, bd, p, radix, dmax, bp, layout, prow, pld, pstride)
+    got = from_blocks(dev.download(bp, np.int8, p * pstride).reshape(p, pstride)[:, :prow * pld], prow, pld)
+    if tran:
+        np.testing.assert_array_equal(got[:, :cols, :rows], want.transpose(0, 2, 1))
+        assert not got[:, cols:, :].any() and not got[:, :, rows:].any()
+    else:
+        np.testing.assert_array_equal(got[:, :rows, :cols], want)
+        assert not got[:, rows:, :].any() and not got[:, :, cols:].any()
+
+
+@pytest.mark.parametrize("M,N,K,p", [(256, 512, 192, 8), (512, 256, 1024, 13), (256, 256, 64, 1)])
+def test_diagonal_products_exact(dev, M, N, K, p):
+    """P_d = sum_{i<=d} A_i B_{d-i}^T with all d+1 pairs in one exact int32 accumulation; the all-127 rows
+    reach the largest sums of the last diagonal."""
+    rng = np.random.default_rng(M + K + p)
+    A = rng.integers(-127, 128, (p, M, K), dtype=np.int8)
+    Bt = rng.integers(-127, 128, (p, N, K), dtype=np.int8)
+    A[:, 0, :] = 127
+    Bt[:, 0, :] = 127
+    A[:, 1, :] = -127
+    bA, bB = dev.upload(to_blocks(A)), dev.upload(to_blocks(Bt))
+    bC = dev.alloc(4 * p * M * N)
+    dev.oz1_gemm_diag(bA, bB, bC, M, N, K, p, N, M * K, N * K, M * N)
+    C = dev.download(bC, np.int32, p * M * N).reshape(p, M, N)
+    Af, Bf = A.astype(np.float64), Bt.astype(np.float64)
+    for d in range(p):
+        want = sum(Af[i] @ Bf[d - i].T for i in range(d + 1))  # exact: |sum| < 2^53
+        np.testing.assert_array_equal(C[d].astype(np.int64), want.astype(np.int64))
+
+
+def test_diagonal_products_reject_overflow(dev):
+    b = dev.alloc(1 << 20)
+    with pytest.raises(RuntimeError):
+        dev.oz1_gemm_diag(b, b, b, 256, 256, 16384, 9, 256, 256 * 16384, 256 * 16384, 256 * 256)  # 9*K*127^2 > 2^31
+
+
+@pytest.mark.parametrize("radix,signmag,nsingle,ndiag", [(254, 1, 0, 8), (254, 1, 0, 13), (64, 0, 0, 8),
+                                                         (64, 0, 5, 10)])
+def test_recon_matches_oracle(dev, oracle, radix, signmag, nsingle, ndiag):
+    """Partial sums up to the largest magnitude the planner admits: |S| < 2^116 (the FP32 exponent budget of
+    the Horner evaluation, format.hpp:160-171), i.e. |P_d| < 2^(116 - (ndiag-1) log2 radix), and int32."""
+    rng = np.random.default_rng(radix * ndiag + nsingle)
+    M, N = 5, 777
+    top = min(2 ** 31 - 1, int(2.0 ** (116 - (ndiag - 1) * np.log2(radix) - 1)))
+    Pd = rng.integers(-top, top, (ndiag, M, N)).astype(np.int32)
+    Pd[:nsingle] = rng.integers(-(2 ** 24), 2 ** 24, (nsingle, M, N))
+    Pd[nsingle:, 0, :5] = [0, 1, -1, top, -top]
+    Pd[:, 1, :] = 0
+    Pd[1:, 2, :] = 0                                   # only the leading diagonal
+    dA = rng.integers(-10, 40, M).astype(np.int32)
+    dB = rng.integers(-10, 40, N).astype(np.int32)
+    whi, wlo, qw = oracle.oz1_scale_w(radix, ndiag - 1)
+    desc = Oz1ReconDesc(ndiag, radix, signmag, nsingle, whi, wlo, qw)
+    ldp = N + 3
+    Pp = np.zeros((ndiag, M, ldp), dtype=np.int32)
+    Pp[:, :, :N] = Pd
+    bP, bA, bB = dev.upload(Pp), dev.upload(dA), dev.upload(dB)
+    bo = dev.alloc(8 * M * N)
+    dev.oz1_recon(bP, M, N, ldp, M * ldp, desc, bA, bB, bo, N)
+    got = dev.download(bo, np.float64, M * N)
+    want = oracle.oz1_recon(Pd, radix, signmag, nsingle, dA, dB)
+    np.testing.assert_array_equal(got.view(np.uint64), want.view(np.uint64))
+
+
+def test_reference_hash_int8_128(ctx):
+    """quick.csv:12: I INT8 128^3, uniform seed 7, p = 8 -> 6c9693442bfc11b0, from the GPU directly."""
+    n = 128
+    a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
+    c = np.empty(n * n)
+    info = ctx.gemm(a, b, c, n, n, n, oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8, slices=8))
+    assert (info.scheme, info.slices) == (oz.Scheme.I, 8)
+    assert oz.eval_hash(c) == 0x6C9693442BFC11B0
+
+
+# phi_sweep.log CONFIG lines of I-INT8 at 4096^3, seed 7: (phi, slices option, p used, chash)
+PHI_HASHES = [(0.0, 8, 8, 0x2D5687AE78334480), (0.0, 0, 7, 0x16D398E7A7E7AB7E), (16.0, 0, 11, 0x53768BF42D24E8DE),
+              (2.0, 8, 8, 0xB94DEA61BA62020B)]
+
+
+@pytest.mark.parametrize("phi,slices,p,h", PHI_HASHES)
+def test_reference_hashes_4096(ctx, phi, slices, p, h):
+    n = 4096
+    a, b = oz.eval_inputs(7, phi, n * n, n * n)
+    c = np.empty(n * n)
+    info = ctx.gemm(a, b, c, n, n, n, oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8, slices=slices))
+    assert info.slices == p
+    assert oz.eval_hash(c) == h
+
+
+def test_c2_bit_exact_chain(ctx, dev, oracle):
+    """BASELINE C2: 4096^3, seed 2, phi 1, automatic p. The slice planes of both operands and the int32
+    diagonal products on a 64-row slab equal the oracle's; C is within the error model (binary128 sample)."""
+    n = 4096
+    a, b = oz.eval_inputs(2, 1.0, n * n, n * n)
+    A, B = a.reshape(n, n), b.reshape(n, n)
+    pl = oz.plan1(a, b, n, n, n)
+    p = pl.p
+    c = np.empty(n * n)
+    info = ctx.gemm(a, b, c, n, n, n, I_INT8)
+    assert info.slices == p
+    # stages through the C ABI with the same p
+    dA, _ = oracle.scale(A, n, n, 0, 1, -1)
+    dB, _ = oracle.scale(B, n, n, 1, 1, -1)
+    sa = oracle.oz1_slices(A, n, n, 0, dA, p, 254, 127)
+    sb = oracle.oz1_slices(B, n, n, 1, dB, p, 254, 127)
+    bA, bB, bdA, bdB = dev.upload(A), dev.upload(B), dev.upload(dA), dev.upload(dB)
+    pA, pB = dev.alloc(p * n * n), dev.alloc(p * n * n)
+    dev.oz1_split(bA, n, n, n, 0, bdA, p, 254, 127, pA, 2, n, n, n * n)
+    dev.oz1_split(bB, n, n, n, 1, bdB, p, 254, 127, pB, 3, n, n, n * n)
+    gA = from_blocks(dev.download(pA, np.int8, p * n * n).reshape(p, -1), n, n)
+    np.testing.assert_array_equal(gA, sa)
+    gB = from_blocks(dev.download(pB, np.int8, p * n * n).reshape(p, -1), n, n)
+    np.testing.assert_array_equal(gB, sb.transpose(0, 2, 1))
+    del gA, gB
+    bP = dev.alloc(4 * p * n * n)
+    dev.oz1_gemm_diag(pA, pB, bP, n, n, n, p, n, n * n, n * n, n * n)
+    P = dev.download(bP, np.int32, p * n * n).reshape(p, n, n)
+    rows = slice(1000, 1064)
+    for d in range(p):
+        want = sum(sa[i, rows].astype(np.float64) @ sb[d - i].astype(np.float64) for i in range(d + 1))
+        np.testing.assert_array_equal(P[d, rows].astype(np.int64), want.astype(np.int64))
+    for buf in (bA, bB, bdA, bdB, pA, pB, bP):
+        buf.free()
+    dev.bufs.clear()
+    # accuracy on a sample against binary128, next to the FP64 error bound gamma_K |A||B|
+    rng = np.random.default_rng(0)
+    rs, cs = rng.choice(n, 48, replace=False), rng.choice(n, 48, replace=False)
+    r_, c_ = np.repeat(rs, 48).astype(np.int32), np.tile(cs, 48).astype(np.int32)
+    q = oz.eval_quad_sample(a, b, n, n, n, r_, c_)
+    got = c.reshape(n, n)[r_, c_]
+    absab = np.einsum("ij,ij->i", np.abs(A[r_]), np.abs(B[:, c_].T))
+    assert np.all(np.abs(got - q) <= n * 2.0 ** -53 * absab)

@@ -161,3 +161,88 @@ def test_quad_and_dot2_references(orc):
         absab = sum(abs(Fraction(float(A[rows[t], k])) * Fraction(float(B[k, cols[t]]))) for k in range(K))
         # Dot2: hi + lo carries the sum to about twice the working precision (gamma_K^2 sum|ab|)
         assert abs(Fraction(float(hi[t])) + Fraction(float(lo[t])) - exact) <= absab * Fraction(2) ** -85
+
+
+# ---- Scheme I ----------------------------------------------------------------------------------
+
+def test_scheme1_int8_reference_hash(orc):
+    """tools/validated/quick.csv:12: I INT8 128^3, uniform seed 7, p = 8 -> hash 6c9693442bfc11b0. The
+    oracle's slicer (tfMulR, radix 254), exact diagonal products, triple-float Horner and FP64
+    assembly reproduce the reference's output bit for bit."""
+    n = 128
+    a, b = orc.inputs(7, -1.0, n * n, n * n)
+    out, big = orc.oz1_int8_gemm(a, b, n, n, n, 8)
+    assert orc.hash(out) == 0x6C9693442BFC11B0
+    assert 0 < big < 2 ** 31
+
+
+def test_scheme1_bf16_reference_hash(orc):
+    """quick.csv:2 (and :4, :6, :8): I BF16 128^3, uniform seed 7, p = 10 -> be6558fa9f435fa0. Radix 64
+    (tfMulP2), digits +-32, maxima truncated to BF16, all ten diagonals read whole (nsmall = 10)."""
+    n, p = 128, 10
+    a, b = orc.inputs(7, -1.0, n * n, n * n)
+    A, B = a.reshape(n, n), b.reshape(n, n)
+    dA, _ = orc.scale(A, n, n, 0, 0, -1)
+    dB, _ = orc.scale(B, n, n, 1, 0, -1)
+    sa = orc.oz1_slices(A, n, n, 0, dA, p, 64, 32)
+    sb = orc.oz1_slices(B, n, n, 1, dB, p, 64, 32)
+    Pd, _ = orc.oz1_gemm_diag(sa, sb, p)
+    out = orc.oz1_recon(Pd, 64, 0, 10, dA, dB)
+    assert orc.hash(out) == 0xBE6558FA9F435FA0
+
+
+@pytest.mark.parametrize("radix,dmax", [(254, 127), (64, 32)])
+def test_scheme1_slices_expand_the_element(orc, radix, dmax):
+    """The digits are a balanced radix expansion of x*2^delta: |digit| <= dmax and, with R = dmax/(radix-1),
+    |x*2^delta - sum_i d_i radix^-(i+1)| <= R radix^-p (slice_tf_body.h:60-75), checked in exact
+    rational arithmetic; rows cover zeros, exact powers of two, tiny and full-range values."""
+    rng = np.random.default_rng(radix)
+    rows, cols, p = 6, 40, 9
+    X = rng.uniform(-1, 1, (rows, cols)) * np.exp2(rng.integers(-40, 40, (rows, 1)))
+    X[0] = 0.0
+    X[1, :] = 0.25
+    X[1, 3] = -0.5
+    X[2, 5] = 1.0
+    X[2, 6] = 1e-30
+    X[3, 7] = -np.nextafter(1.0, 0.0)
+    ceil = 1 if radix == 254 else 0
+    dA, fl = orc.scale(X, rows, cols, 0, ceil, -1)
+    assert fl == 0
+    d = orc.oz1_slices(X, rows, cols, 0, dA, p, radix, dmax)
+    assert np.abs(d.astype(np.int32)).max() <= dmax
+    R = Fraction(dmax, radix - 1)
+    for r in range(rows):
+        for c in range(cols):
+            x = Fraction(float(X[r, c])) * Fraction(2) ** int(dA[r])
+            s = sum(Fraction(int(d[i, r, c])) / Fraction(radix) ** (i + 1) for i in range(p))
+            assert abs(x) <= Fraction(1, 2) * (1 + Fraction(1, 128))
+            assert abs(x - s) <= R / Fraction(radix) ** p * (1 + Fraction(1, 2 ** 20)), (r, c)
+
+
+def test_scheme1_recon_scale_constant(orc):
+    """radix^-(L+2) as W 2^qw: W has its top bit set and W 2^qw is within 2^-60 of the exact value; a
+    power-of-two radix gives W = 2^63 exactly (plan.hpp:446-460)."""
+    for radix, L in [(254, 7), (254, 12), (64, 9), (14, 15)]:
+        whi, wlo, qw = orc.oz1_scale_w(radix, L)
+        W = (whi << 32) | wlo
+        assert W >> 63 == 1
+        exact = Fraction(1, radix ** (L + 2))
+        assert abs(Fraction(W) * Fraction(2) ** qw - exact) <= exact * Fraction(2) ** -60
+    assert orc.oz1_scale_w(64, 9)[:2] == (1 << 31, 0)
+
+
+def test_scheme1_recon_against_exact_horner(orc):
+    """For random diagonal sums the oracle's reconstruction is the exact S radix^-(L+2) 2^-(dA+dB) to within
+    the triple-float working precision (~2^-66 of the largest term) plus the final rounding."""
+    rng = np.random.default_rng(11)
+    ndiag, M, N = 8, 3, 50
+    Pd = rng.integers(-(2 ** 30), 2 ** 30, (ndiag, M, N)).astype(np.int32)
+    dA = rng.integers(-3, 3, M).astype(np.int32)
+    dB = rng.integers(-3, 3, N).astype(np.int32)
+    out = orc.oz1_recon(Pd, 254, 1, 0, dA, dB).reshape(M, N)
+    for i in range(M):
+        for j in range(N):
+            S = sum(Fraction(int(Pd[d, i, j])) * 254 ** (ndiag - 1 - d) for d in range(ndiag))
+            v = S / Fraction(254) ** (ndiag + 1) * Fraction(2) ** -(int(dA[i]) + int(dB[j]))
+            top = Fraction(2 ** 30) * Fraction(254) ** (ndiag - 1) / Fraction(254) ** (ndiag + 1)
+            assert abs(Fraction(float(out[i, j])) - v) <= abs(v) * Fraction(2) ** -52 + top * Fraction(2) ** -60

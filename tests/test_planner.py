@@ -119,3 +119,52 @@ def test_eval_inputs_match_reference_hashes():
     n = 4096
     a, b = oz.eval_inputs(7, 1.0, n * n, n * n)
     assert oz.eval_hash(a) == 0x108dbf997fae1816 and oz.eval_hash(b) == 0x292d509b232b2c21  # dgemm_ref.log:18
+
+
+# ---- Scheme I ----------------------------------------------------------------------------------
+# phi_sweep.log / phi_sweep_05.log (I-INT8, 4096^3, seed 7): the automatic p and the two model estimates
+# at p (OZ_FP64 lines :47, :191, :335, :479, :623, :767 and phi_sweep_05.log:47).
+OZ1_RECORDS = [  # phi, p, independent-sign bits, sampled bits
+    (0.0, 7, 53.9, 53.8), (0.5, 8, 57.0, 54.2), (1.0, 8, 54.1, 53.9), (2.0, 9, 59.2, 56.2),
+    (4.0, 9, 57.4, 55.2), (8.0, 9, 54.7, 53.9), (16.0, 11, 57.8, 58.1),
+]
+
+
+@pytest.mark.parametrize("phi,p,bi,bs", [OZ1_RECORDS[i] for i in (0, 2, 6)])
+def test_scheme1_auto_p_matches_reference_records(phi, p, bi, bs):
+    n = 4096
+    a, b = oz.eval_inputs(7, phi, n * n, n * n)
+    pl = oz.plan1(a, b, n, n, n)
+    assert pl.p == p
+    assert pl.pmax == 22  # ceil(160 / log2 254) + 1
+    assert abs(pl.bits_indep - bi) <= 0.05 and abs(pl.bits_sampled - bs) <= 0.05
+    assert (pl.Kc, pl.nkb, pl.pairloop, pl.pairwise, pl.fuse, pl.defer) == (n, 1, 0, 0, 0, 0)
+
+
+def test_scheme1_issue_plans():
+    """Closed forms of plan.hpp:130-206 and format.hpp:136-183 for the configurations of the BASELINE
+    and the error paths."""
+    z = np.zeros(64 * 64)
+    # INT8, single K block up to (L+1) K 127^2 < 2^31
+    pl = oz.plan1(z, z, 64, 64, 64, slices=8)
+    assert (pl.p, pl.Kc, pl.nkb, pl.defer, pl.nsmall) == (8, 64, 1, 0, 0)
+    # BF16 at C5's k = 65536 with 8 slices: pairwise issue, K blocks of 16384, int32 accumulation, deferred
+    # reconstruction, no diagonal small enough to be read whole
+    big = np.zeros(64 * 65536)
+    pl = oz.plan1(big, big, 64, 64, 65536, slices=8, fmt=oz.Format.BF16)
+    assert (pl.Kc, pl.nkb, pl.pairloop, pl.pairwise, pl.fuse, pl.defer, pl.nsmall) == (16384, 4, 0, 1, 1, 1, 0)
+    # BF16 at 128^3 with 10 slices: the pair loop, all ten diagonals read whole (quick.csv:2)
+    z128 = np.zeros(128 * 128)
+    pl = oz.plan1(z128, z128, 128, 128, 128, slices=10, fmt=oz.Format.BF16)
+    assert (pl.Kc, pl.nkb, pl.pairloop, pl.defer, pl.nsmall) == (128, 1, 1, 1, 10)
+
+
+def test_scheme1_rejects_unsupported_plans():
+    # INT8 would need two K blocks at k = 32768 with 8 slices (plan.hpp:187-195)
+    z = np.zeros(64 * 32768)
+    with pytest.raises(RuntimeError, match="K blocking"):
+        oz.plan1(z, z, 64, 64, 32768, slices=8)
+    # 16 slices of radix 254 overflow the FP32 exponent of the Horner evaluation (format.hpp:160-171)
+    z = np.zeros(64 * 64)
+    with pytest.raises(RuntimeError, match="overflow FP32"):
+        oz.plan1(z, z, 64, 64, 64, slices=16)
