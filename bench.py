@@ -1,6 +1,10 @@
 #!/usr/bin/env python3
 """Headline benchmark: Ozaki-II INT8 FP64 GEMM at m = n = k = 8192 on one MI355X.
 
+`--config C1|C2|C5` measures the other built BASELINE configs the same way (C1: II-INT8 1024^3 one
+pass; C2: I-INT8 4096^3 automatic slices; C5: I-BF16 8192 x 8192 x 65536, 8 slices, 1% zero rows and
+columns); the default line is C3.
+
 Workload: row-major FP64 A, B with entries (U(0,1)-0.5)*exp(0.5*N(0,1)),
 the reference's evaluation generator with seed 3; Scheme II, INT8 residues, automatic moduli (<= 24),
 forced two-pass reconstruction (the reconstruction here is exact, which serves both pass modes).
@@ -45,17 +49,18 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(a, b, n: int, rows: int) -> dict:
+def cpu_baseline(a, b, m: int, n: int, k: int, rows: int) -> dict:
     """Reference host path (evaluation/numerics.hpp:58-93 Dot2, OpenMP) on rows [0, rows) of C."""
     from tests.oracle_lib import load_oracle
     orc = load_oracle()
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    rows = min(rows, m)
     t0 = time.perf_counter()
-    orc.dot2(a, b, n, n, n, 0, rows)
+    orc.dot2(a, b, m, n, k, 0, rows)
     dt = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * n * n / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+    return {"value": round(2.0 * rows * n * k / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port", "sample": f"Dot2 compensated FP64 GEMM (reference_gemm restated in oracle/) on rows "
-                                     f"0..{rows - 1} of C (full N={n}, K={n}), {dt:.2f} s; value = 2*rows*N*K/t"}
+                                     f"0..{rows - 1} of C (full N={n}, K={k}), {dt:.2f} s; value = 2*rows*N*K/t"}
 
 
 def copy_probe(nbytes: int) -> int:
@@ -71,13 +76,31 @@ def copy_probe(nbytes: int) -> int:
     return 0
 
 
+# name -> (scheme, format, m, n, k, seed, phi, options, peak of the product format, rows of
+# the CPU baseline slab, sample edge of the binary128 check). C3 is the headline and the default.
+CONFIGS = {
+    "C1": ("II", "INT8", 1024, 1024, 1024, 1, 0.5, dict(reconstruction="OnePass"), INT8_PEAK_TOPS, 1024, 64),
+    "C2": ("I", "INT8", 4096, 4096, 4096, 2, 1.0, dict(), INT8_PEAK_TOPS, 4096, 64),
+    "C3": ("II", "INT8", 8192, 8192, 8192, 3, 0.5, dict(reconstruction="TwoPass"), INT8_PEAK_TOPS, 1024, 64),
+    # BF16 digits (+-32) run on the INT8 matrix cores, so the product roofline is the INT8 peak
+    "C5": ("I", "BF16", 8192, 8192, 65536, 5, 4.0, dict(slices=8), INT8_PEAK_TOPS, 128, 32),
+}
+WORKLOADS = {
+    "C1": "C1 Ozaki-II INT8 m=n=k=1024, auto moduli, one-pass reconstruction",
+    "C2": "C2 Ozaki-I INT8 m=n=k=4096, automatic slices",
+    "C3": "C3 Ozaki-II INT8 m=n=k=8192, auto moduli (<=24), two-pass reconstruction",
+    "C5": "C5 Ozaki-I BF16 m=n=8192 k=65536, 8 slices, rows i%100==0 of A and columns j%100==0 of B zero",
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--n", type=int, default=8192)
-    ap.add_argument("--cpu-rows", type=int, default=1024, help="rows of the CPU baseline slab (0: skip)")
+    ap.add_argument("--config", default="C3", choices=sorted(CONFIGS), help="BASELINE config (C3: the headline)")
+    ap.add_argument("--cpu-rows", type=int, default=-1, help="rows of the CPU baseline slab (0: skip; -1: the "
+                                                             "config's default, about 1.4e11 Dot2 flops)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy BYTES device-to-device with the plain copy kernel (calibrates HBM counters)")
     args = ap.parse_args()
@@ -89,49 +112,58 @@ def main() -> int:
         return 2
     import oztt_amd as oz
 
-    n = args.n
-    log(f"generating inputs {n}x{n} (seed 3, phi 0.5)")
-    a, b = oz.eval_inputs(3, 0.5, n * n, n * n)
-    opts = oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, reconstruction=oz.Reconstruction.TwoPass)
+    scheme, fmt, m, n, k, seed, phi, extra, peak, cpu_rows, edge = CONFIGS[args.config]
+    if args.cpu_rows >= 0:
+        cpu_rows = args.cpu_rows
+    log(f"{args.config}: generating inputs {m}x{k} and {k}x{n} (seed {seed}, phi {phi})")
+    a, b = oz.eval_inputs(seed, phi, m * k, k * n)
+    if args.config == "C5":  # 1% of A's rows and B's columns set to zero (82 of 8192 each)
+        a.reshape(m, k)[::100, :] = 0.0
+        b.reshape(k, n)[:, ::100] = 0.0
+    opts = oz.Options(scheme=oz.Scheme[scheme], format=oz.Format[fmt])
+    for key, v in extra.items():
+        setattr(opts, key, oz.Reconstruction[v] if key == "reconstruction" else v)
     ctx = oz.Context(0)
     log("planning, first pass, whole-pass replays")
     t0 = time.perf_counter()
-    c, info, ev = ctx.evaluate(a, b, n, n, n, opts, warmup=args.warmup, repeats=args.steps)
-    log(f"call done in {time.perf_counter() - t0:.1f} s: moduli={info.moduli} b={info.integer_bits} "
-        f"whole={ev.whole_ms:.3f} ms checked={ev.whole_checked}")
+    c, info, ev = ctx.evaluate(a, b, m, n, k, opts, warmup=args.warmup, repeats=args.steps)
+    log(f"call done in {time.perf_counter() - t0:.1f} s: slices={info.slices} moduli={info.moduli} "
+        f"b={info.integer_bits} whole={ev.whole_ms:.3f} ms checked={ev.whole_checked}")
     if not ev.whole_checked:
         raise SystemExit("whole-pass replay output differs from the first pass")
     ms = ev.whole_ms
-    value = 2.0 * n * n * n / (ms * 1e-3) / 1e12
+    value = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     # one plain Context.gemm from host buffers: planning + PCIe transfers + the pass (not the metric)
-    c2 = np.empty(n * n)
+    c2 = np.empty(m * n)
     t0 = time.perf_counter()
-    ctx.gemm(a, b, c2, n, n, n, opts)
+    ctx.gemm(a, b, c2, m, n, k, opts)
     call_ms = (time.perf_counter() - t0) * 1e3
     if not np.array_equal(c2.view(np.uint64), c.view(np.uint64)):
         raise SystemExit("Context.gemm output differs from the evaluated pass")
     del c2
 
-    # accuracy on a 64 x 64 sample at full K against binary128, next to a native FP64 dot product
+    # accuracy on an edge x edge sample at full K against binary128, next to a native FP64 dot product
     log("accuracy sample (binary128)")
     rng = np.random.default_rng(0)
-    rs = np.sort(rng.choice(n, 64, replace=False))
-    cs = np.sort(rng.choice(n, 64, replace=False))
-    rows = np.repeat(rs, 64).astype(np.int32)
-    cols = np.tile(cs, 64).astype(np.int32)
-    q = oz.eval_quad_sample(a, b, n, n, n, rows, cols)
-    A = a.reshape(n, n)
-    B = b.reshape(n, n)
-    got = c.reshape(n, n)[rows, cols]
+    rs = np.sort(rng.choice(m, edge, replace=False))
+    cs = np.sort(rng.choice(n, edge, replace=False))
+    rows = np.repeat(rs, edge).astype(np.int32)
+    cols = np.tile(cs, edge).astype(np.int32)
+    q = oz.eval_quad_sample(a, b, m, n, k, rows, cols)
+    A = a.reshape(m, k)
+    B = b.reshape(k, n)
+    got = c.reshape(m, n)[rows, cols]
     fp64 = np.einsum("ij,ij->i", A[rows], B[:, cols].T)  # native FP64 dot products
     absab = np.einsum("ij,ij->i", np.abs(A[rows]), np.abs(B[:, cols].T))
-    rel = np.abs(got - q) / np.abs(q)
-    rel64 = np.abs(fp64 - q) / np.abs(q)
-    bound = n * 2.0 ** -53 * absab / np.abs(q)  # FP64 GEMM error bound gamma_k |A||B| relative to |C|
+    nz = q != 0
+    rel = np.abs(got - q)[nz] / np.abs(q[nz])
+    rel64 = np.abs(fp64 - q)[nz] / np.abs(q[nz])
+    bound = k * 2.0 ** -53 * absab[nz] / np.abs(q[nz])  # FP64 GEMM error bound gamma_k |A||B| relative to |C|
     gemm_ms = ev.gemm_launch_ms
     achieved = ev.product_ops / (gemm_ms * 1e-3) / 1e12
+    headline = args.config == "C3"
     out = {
-        "metric": METRIC,
+        "metric": METRIC if headline else f"effective FP64 TFLOP/s (2mnk/t), {WORKLOADS[args.config]}",
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -141,26 +173,27 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic: reference evaluation generator, seed 3, (U(0,1)-0.5)*exp(0.5*N(0,1))",
-        "config": {"workload": f"C3 Ozaki-II INT8 m=n=k={n}, auto moduli (<=24), two-pass reconstruction",
-                   "m": n, "n": n, "k": n, "moduli": info.moduli, "integer_bits": info.integer_bits,
+        "dtype": "int8",  # every product runs on the INT8 matrix cores (C5's BF16-format digits are int8 values)
+        "data": f"synthetic: reference evaluation generator, seed {seed}, (U(0,1)-0.5)*exp({phi}*N(0,1))",
+        "config": {"workload": WORKLOADS[args.config], "m": m, "n": n, "k": k, "scheme": scheme, "format": fmt,
+                   "slices": info.slices, "moduli": info.moduli, "integer_bits": info.integer_bits,
                    "reconstruction_passes": info.reconstruction_passes},
         "max_rel_err_vs_binary128": float(rel.max()),
         "fp64_max_rel_err_vs_binary128": float(rel64.max()),
         "max_err_over_fp64_bound": float((rel / bound).max()),
-        "phases_ms": {k: round(ev.phase_ms[i], 4) for i, k in enumerate(["scale", "slice", "gemm", "compose", "recon"])},
+        "phases_ms": {key: round(ev.phase_ms[i], 4) for i, key in enumerate(["scale", "slice", "gemm", "compose", "recon"])},
         "host_call_ms": round(call_ms, 2),
-        "host_call_tflops": round(2.0 * n * n * n / (call_ms * 1e-3) / 1e12, 3),
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "traffic": C3_GEMM_TRAFFIC_BYTES if (n == 8192 and info.moduli == 17) else None,
-                     "kernel": "gemm_i8_kernel<true> (oz2_gemm_digits)", "launch_ms": round(gemm_ms, 4),
-                     "ops_per_launch": ev.product_ops},
+        "host_call_tflops": round(2.0 * m * n * k / (call_ms * 1e-3) / 1e12, 3),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4),
+                     "traffic": C3_GEMM_TRAFFIC_BYTES if (headline and info.moduli == 17) else None,
+                     "kernel": "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II"
+                                                   else "<DIAG> (oz1_gemm_diag_i8)"),
+                     "launch_ms": round(gemm_ms, 4), "ops_per_launch": ev.product_ops},
     }
-    if args.cpu_rows > 0:
-        log(f"CPU baseline: Dot2 on {args.cpu_rows} rows")
-        out["cpu_baseline"] = cpu_baseline(a, b, n, args.cpu_rows)
+    if cpu_rows > 0:
+        log(f"CPU baseline: Dot2 on {cpu_rows} rows")
+        out["cpu_baseline"] = cpu_baseline(a, b, m, n, k, cpu_rows)
     ctx.close()
     print(json.dumps(out), flush=True)
     return 0

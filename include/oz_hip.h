@@ -147,16 +147,17 @@ int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, lon
  * t *= radix (tfMulR, or tfMulP2 for a power of two), d = clamp(round(t_hi), +-dmax), t_hi -= d.
  * Plane i holds digit i (weight radix^-(i+1)) as int8, in OZ_BLOCK tiles: layout 2 (planes of
  * rows x cols) or layout 3 (transposed, cols x rows); geometry rules as oz2_split_int8's blocked
- * layouts. radix <= 254, dmax <= 127, p <= 64. */
+ * layouts. radix <= 254, dmax <= 127, p <= 256. */
 int oz1_split_int8(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int p,
                    int radix, int dmax, int8_t* planes, int layout, int prow, int pld, long long plane_stride);
 
 /* ---- A16: diagonal partial products (reference ozaki1/gemm.hpp:315, stages.hpp:157) ----------
- * C[d] = sum_{i=0..d} A[i] * Bt[d-i]^T for d < ndiag, exact int32 (the d+1 pairs concatenated along
- * K in one accumulation; requires ndiag*K*127^2 < 2^31, the reference's single-K-block INT8 plan).
+ * C[d] = sum_{i=0..d} A[i] * Bt[d-i]^T for d < ndiag, exact int32: the d+1 pairs concatenated along
+ * K in one accumulation, which requires ndiag*K*dmax^2 < 2^31 for digits |A|, |Bt| <= dmax (the
+ * reference's single-K-block INT8 plan, and its int32 sums S_d of the other formats).
  * A[i]: M x K, Bt[i]: N x K int8 in OZ_BLOCK tiles; operand rules as oz_gemm_i8. */
 int oz1_gemm_diag_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K, int ndiag,
-                     int ldc, long long strideA, long long strideB, long long strideC);
+                     int dmax, int ldc, long long strideA, long long strideB, long long strideC);
 
 /* ---- A17: reconstruction (reference recon_tf_i32in.cpp:116-157, recon_f64_writer.cpp:148-160) -
  * out[i][j] = S * radix^-(L+2) * 2^-(dA[i]+dB[j]) with S = sum_d radix^(L-d) P_d (L = ndiag-1)

@@ -68,6 +68,6 @@ bool scheme_available(Format format, Scheme scheme) noexcept;
 
 // Backends.
 Output ozaki2_int8_run(Device& dev, const Problem& p);
-Output ozaki1_int8_run(Device& dev, const Problem& p);
+Output ozaki1_run(Device& dev, const Problem& p);
 
 }  // namespace ozTTgemm::detail

@@ -186,7 +186,7 @@ int ozt_choose_moduli_int8(unsigned K, int num_moduli, int b_cap, ozt_plan2* out
     return 0;
 }
 
-// Scheme I planner on padded row-major A (M x K) and B (K x N); format 5 = INT8, 0 = BF16 constants.
+// Scheme I planner on padded row-major A (M x K) and B (K x N) with the constants of `format`.
 struct ozt_plan1 {
     int p, pmax, nsmall;
     unsigned Kc, nkb;
@@ -198,7 +198,7 @@ struct ozt_plan1 {
 int ozt_plan1(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned slices, int format,
               ozt_plan1* out, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
-        const auto& f = format == 0 ? ozTTgemm::detail::kOz1Bf16 : ozTTgemm::detail::kOz1Int8;
+        const auto& f = ozTTgemm::detail::oz1_format(format);
         const auto pl = ozTTgemm::detail::plan_scheme1(A, B, M, N, K, slices, f);
         std::memset(out, 0, sizeof(*out));
         out->p = pl.p;

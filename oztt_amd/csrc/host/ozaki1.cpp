@@ -1,12 +1,17 @@
-// Ozaki scheme I driver (INT8 slices): one FP64 GEMM on the GPU.
+// Ozaki scheme I driver: one FP64 GEMM on the GPU, for every format.
 //
 // Pipeline of the reference's src/ozaki1.cpp run(): number of slices p (given, or chosen from the
 // input, auto_precision.hpp:506) and the issue plan (plan.hpp:223) -> upload the FP64 operands ->
-// scale (row/column maxima rounded up to BF16, deltas nshift - e with nshift = -1) -> p slices of
-// radix 254 per operand -> the diagonal partial products P_d = sum_{i<=d} A_i B_{d-i}, each one
-// exact int32 accumulation over the d+1 pairs concatenated along K -> Horner reconstruction in
-// triple-float and FP64 assembly. INT8 admits a single K block only (plan.hpp:187-195), so the
-// reference's panels and row bands reduce to one launch per stage on one MI355X.
+// scale (row/column maxima to BF16, deltas nshift - e) -> p slices per operand (radix 254 for INT8,
+// 64 for BF16/FP16/TF32/BFP8, 32 for FP8, 14 for BFP4, 2 for BFP2) -> the diagonal partial products
+// P_d = sum_{i<=d} A_i B_{d-i} -> Horner reconstruction in triple-float and FP64 assembly.
+//
+// The digits of every format are integers of at most 7 bits, so all products run on the INT8 matrix
+// cores: one exact int32 accumulation per diagonal over its d+1 pairs concatenated along K. For INT8
+// that is the reference's single-K-block plan (plan.hpp:187-195); for the FP32-product formats it is
+// the exact int32 sum S_d the reference accumulates over pairs and K blocks before its deferred
+// reconstruction (plan.hpp:95-128), so the reconstruction reads the same integers. The reference's
+// panels and row bands reduce to one launch per stage on one MI355X.
 //
 // Device layout: A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2]; slices of A: p planes of
 // Mg x Kg int8, of B: p planes of Ng x Kg (B transposed), both in the GEMM's OZ_BLOCK tiles (Mg, Ng
@@ -29,15 +34,15 @@ std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / 
 
 }  // namespace
 
-Output ozaki1_int8_run(Device& D, const Problem& p) {
+Output ozaki1_run(Device& D, const Problem& p) {
     oz_dev* dev = D.dev;
-    const Oz1Format& f = kOz1Int8;
+    const Oz1Format& f = oz1_format((int)p.options.format);
     const Plan1 plan = plan_scheme1(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.slices, f);
     const std::uint32_t M = p.m, N = p.n, K = p.k, P = (std::uint32_t)plan.p;
     const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
-    if ((std::uint64_t)P * Kg * 127 * 127 > 0x7FFFFFFFull)
-        throw std::logic_error("scheme I plan: padded K breaks the single-block exactness");
-    const oz1_recon_dev rdesc{(int)P, f.radix, 1, 0, plan.Whi, plan.Wlo, plan.qw};
+    if ((std::uint64_t)P * Kg * f.dmax * f.dmax > 0x7FFFFFFFull)
+        throw std::logic_error("scheme I plan: the padded K breaks the int32 exactness of a diagonal");
+    const oz1_recon_dev rdesc{(int)P, f.radix, plan.signmag ? 1 : 0, plan.nsmall, plan.Whi, plan.Wlo, plan.qw};
 
     Workspace& ws = *D.ws;
     auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
@@ -57,7 +62,7 @@ Output ozaki1_int8_run(Device& D, const Problem& p) {
     std::vector<Step> steps;
     steps.push_back({ev::Scale, [=] {
                          device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
-                         // INT8 rounds the BF16 of the maxima up; target 1/2 (format.hpp:76-101)
+                         // BF16 of the maxima rounded as the format requires, target 2^nshift (format.hpp:76-101)
                          device_check(dev, oz_scale_f64(dev, dAf, (int)M, (int)K, (int)K, 0, (int)f.ceil, f.nshift,
                                                         dltA, flags),
                                       "scale A");
@@ -77,8 +82,8 @@ Output ozaki1_int8_run(Device& D, const Problem& p) {
                      }});
     steps.push_back({ev::Gemm, [=] {
                          device_check(dev,
-                                      oz1_gemm_diag_i8(dev, slA, slB, part, (int)Mg, (int)Ng, (int)Kg, (int)P, (int)Ng,
-                                                       strideA, strideB, strideP),
+                                      oz1_gemm_diag_i8(dev, slA, slB, part, (int)Mg, (int)Ng, (int)Kg, (int)P, f.dmax,
+                                                       (int)Ng, strideA, strideB, strideP),
                                       "diagonal products");
                      }});
     steps.push_back({ev::Recon, [=] {
@@ -91,7 +96,7 @@ Output ozaki1_int8_run(Device& D, const Problem& p) {
     const unsigned pairs = P * (P + 1) / 2;
     std::vector<double> values =
         run_pipeline(dev, steps, 2, out, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
-    Info info{Scheme::I, Format::INT8};
+    Info info{Scheme::I, p.options.format};
     info.slices = P;
     return {std::move(values), info};
 }

@@ -432,6 +432,17 @@ bool exact_check(std::uint32_t K, int L, const Oz1Format& f) {
 
 }  // namespace
 
+const Oz1Format& oz1_format(int format) {
+    switch (format) {
+    case 0: case 1: case 2: case 3: return kOz1Bf16;  // BF16, FP16, TF32, BFP8
+    case 4: return kOz1Fp8;
+    case 5: return kOz1Int8;
+    case 6: return kOz1Bfp4;
+    case 7: return kOz1Bfp2;
+    default: throw std::invalid_argument("unknown format");
+    }
+}
+
 std::uint32_t oz1_block_k(std::uint32_t K, int L, const Oz1Format& f) {
     const std::uint32_t pb = prod_bits((std::uint32_t)f.dmax);
     if (f.acc_bits < pb + 1) return 0;
@@ -513,6 +524,14 @@ Plan1 plan_scheme1(const double* A, const double* B, std::uint32_t M, std::uint3
                                  "): log2(k) + slices*log2(radix) + 12 must be below 128. Use fewer slices "
                                  "(Options::slices) or a smaller k.");
     if (!exact_check(ip.Kc, per_pair ? 0 : L, f)) throw std::logic_error("scheme I plan: K block violates exactness");
+    // The products run as exact int8 x int8 -> int32 accumulations over all pairs and K of a diagonal.
+    // That reproduces the reference's int32 sums S_d (deferred reconstruction) and its single-block INT8
+    // products; the reference's remaining plan, per-block Horner over FP32 products, is not built.
+    if (!f.int32_partial && !ip.defer)
+        throw std::runtime_error("Ozaki scheme I: k=" + std::to_string(K) + " with " + std::to_string(pl.p) +
+                                 " slices exceeds the int32 range of a diagonal's sum in this format; this build does "
+                                 "not reconstruct K block by K block. Use fewer slices (Options::slices) or a smaller k.");
+    pl.signmag = f.int32_partial;
     // reconstruction constants (plan.hpp:424-460)
     if (ip.defer) {
         const std::uint64_t per = (std::uint64_t)K * f.dmax * f.dmax;

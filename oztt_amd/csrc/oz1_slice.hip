@@ -62,7 +62,7 @@ extern "C" int oz1_split_int8(oz_dev* dev, const double* X, int rows, int cols, 
                               int pld, long long plane_stride) {
     if (int st = oz::use(dev)) return st;
     if (!X || !delta || !planes || rows <= 0 || cols <= 0 || ld < cols || (mode != 0 && mode != 1) ||
-        (layout != 2 && layout != 3) || p < 1 || p > 64 || radix < 2 || radix > 254 || dmax < 1 || dmax > 127)
+        (layout != 2 && layout != 3) || p < 1 || p > 256 || radix < 2 || radix > 254 || dmax < 1 || dmax > 127)
         return oz::fail(dev, OZ_ERR_ARG, "oz1_split_int8: invalid arguments");
     const bool tran = layout == 3;
     const int need_rows = tran ? cols : rows, need_ld = tran ? rows : cols;

@@ -308,12 +308,14 @@ extern "C" int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, u
 }
 
 extern "C" int oz1_gemm_diag_i8(oz_dev* dev, const int8_t* A, const int8_t* Bt, int32_t* C, int M, int N, int K,
-                                int ndiag, int ldc, long long strideA, long long strideB, long long strideC) {
+                                int ndiag, int dmax, int ldc, long long strideA, long long strideB,
+                                long long strideC) {
     if (int st = oz::use(dev)) return st;
     if (const char* e = check_gemm(A, Bt, C, M, N, K, ndiag, ldc, strideA, strideB, strideC))
         return oz::fail(dev, OZ_ERR_ARG, "oz1_gemm_diag_i8: %s (M=%d N=%d K=%d ndiag=%d)", e, M, N, K, ndiag);
-    // one accumulation covers ndiag*K products of at most 127^2: it must stay exact in int32
-    if ((long long)ndiag * K * 127 * 127 > 0x7FFFFFFFll)
-        return oz::fail(dev, OZ_ERR_ARG, "oz1_gemm_diag_i8: %d pairs of K=%d can overflow int32", ndiag, K);
+    // one accumulation covers ndiag*K products of at most dmax^2: it must stay exact in int32
+    if (dmax < 1 || dmax > 127 || (long long)ndiag * K * dmax * dmax > 0x7FFFFFFFll)
+        return oz::fail(dev, OZ_ERR_ARG, "oz1_gemm_diag_i8: %d pairs of K=%d with digits up to %d can overflow int32",
+                        ndiag, K, dmax);
     return launch_gemm<DIAG>(dev, A, Bt, C, M, N, K, ndiag, ldc, strideA, strideB, strideC, oz2::DigitConsts{});
 }

@@ -164,8 +164,8 @@ class Device:
         self._check(hip().oz1_split_int8(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, p, radix, dmax, planes.ptr,
                                          layout, prow, pld, ctypes.c_longlong(pstride)), "oz1_split_int8")
 
-    def oz1_gemm_diag(self, A: Buffer, Bt: Buffer, C: Buffer, M, N, K, ndiag, ldc, sA, sB, sC):
-        self._check(hip().oz1_gemm_diag_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, ndiag, ldc, ctypes.c_longlong(sA),
+    def oz1_gemm_diag(self, A: Buffer, Bt: Buffer, C: Buffer, M, N, K, ndiag, ldc, sA, sB, sC, dmax=127):
+        self._check(hip().oz1_gemm_diag_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, ndiag, dmax, ldc, ctypes.c_longlong(sA),
                                            ctypes.c_longlong(sB), ctypes.c_longlong(sC)), "oz1_gemm_diag_i8")
 
     def oz1_recon(self, P: Buffer, M, N, ldp, sP, desc: "Oz1ReconDesc", dA: Buffer, dB: Buffer, out: Buffer, ldo):

@@ -128,6 +128,24 @@ def test_reference_hash_int8_128(ctx):
     assert oz.eval_hash(c) == 0x6C9693442BFC11B0
 
 
+# tools/validated/quick.csv, scheme I at 128^3, uniform seed 7 (format, slices, output hash): the four radix-64
+# formats share the hash (lines 2, 4, 6, 8), FP8 line 10, BFP4 line 14, BFP2 line 16.
+QUICK_I = [(oz.Format.BF16, 10, 0xBE6558FA9F435FA0), (oz.Format.FP16, 10, 0xBE6558FA9F435FA0),
+           (oz.Format.TF32, 10, 0xBE6558FA9F435FA0), (oz.Format.BFP8, 10, 0xBE6558FA9F435FA0),
+           (oz.Format.FP8, 12, 0x4D24ADD106258287), (oz.Format.BFP4, 16, 0xF353DBD6B57F8B99),
+           (oz.Format.BFP2, 59, 0x13CD8E69EDCA2911)]
+
+
+@pytest.mark.parametrize("fmt,slices,h", QUICK_I)
+def test_reference_hashes_other_formats_128(ctx, fmt, slices, h):
+    n = 128
+    a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
+    c = np.empty(n * n)
+    info = ctx.gemm(a, b, c, n, n, n, oz.Options(scheme=oz.Scheme.I, format=fmt, slices=slices))
+    assert (info.format, info.slices) == (fmt, slices)
+    assert oz.eval_hash(c) == h
+
+
 # phi_sweep.log CONFIG lines of I-INT8 at 4096^3, seed 7: (phi, slices option, p used, chash)
 PHI_HASHES = [(0.0, 8, 8, 0x2D5687AE78334480), (0.0, 0, 7, 0x16D398E7A7E7AB7E), (16.0, 0, 11, 0x53768BF42D24E8DE),
               (2.0, 8, 8, 0xB94DEA61BA62020B)]
@@ -186,3 +204,32 @@ def test_c2_bit_exact_chain(ctx, dev, oracle):
     got = c.reshape(n, n)[r_, c_]
     absab = np.einsum("ij,ij->i", np.abs(A[r_]), np.abs(B[:, c_].T))
     assert np.all(np.abs(got - q) <= n * 2.0 ** -53 * absab)
+
+
+def test_c5_shape_bit_exact(ctx, oracle):
+    """The C5 class (BF16 format, 8 slices, k = 65536, seed 5, phi 4, rows i%100 == 0 of A and columns
+    j%100 == 0 of B zero) at m = n = 512: the whole output of a row slab equals the oracle's chain (radix-64
+    slices, exact int32 diagonal sums S_d, deferred reconstruction with no diagonal read whole)."""
+    m = n = 512
+    k = 65536
+    a, b = oz.eval_inputs(5, 4.0, m * k, k * n)
+    A, B = a.reshape(m, k), b.reshape(k, n)
+    A[::100, :] = 0.0
+    B[:, ::100] = 0.0
+    c = np.empty(m * n)
+    info = ctx.gemm(a, b, c, m, n, k, oz.Options(scheme=oz.Scheme.I, format=oz.Format.BF16, slices=8))
+    assert (info.format, info.slices) == (oz.Format.BF16, 8)
+    pl = oz.plan1(a, b, m, n, k, slices=8, fmt=oz.Format.BF16)
+    assert (pl.pairwise, pl.defer, pl.nsmall) == (1, 1, 0)
+    rows = slice(0, 64)
+    dA, _ = oracle.scale(A, m, k, 0, 0, -1)
+    dB, _ = oracle.scale(B, k, n, 1, 0, -1)
+    sa = oracle.oz1_slices(np.ascontiguousarray(A[rows]), 64, k, 0, dA[rows], 8, 64, 32)
+    sb = oracle.oz1_slices(B, k, n, 1, dB, 8, 64, 32)
+    Pd = np.empty((8, 64, n), dtype=np.int32)
+    for d in range(8):
+        s = sum(sa[i].astype(np.float64) @ sb[d - i].astype(np.float64) for i in range(d + 1))  # exact: < 2^53
+        Pd[d] = s.astype(np.int64)
+    want = oracle.oz1_recon(Pd, 64, 0, 0, dA[rows], dB)
+    np.testing.assert_array_equal(c.reshape(m, n)[rows].reshape(-1).view(np.uint64), want.view(np.uint64))
+    assert not c.reshape(m, n)[::100, :].any() and not c.reshape(m, n)[:, ::100].any()

@@ -246,3 +246,19 @@ def test_scheme1_recon_against_exact_horner(orc):
             v = S / Fraction(254) ** (ndiag + 1) * Fraction(2) ** -(int(dA[i]) + int(dB[j]))
             top = Fraction(2 ** 30) * Fraction(254) ** (ndiag - 1) / Fraction(254) ** (ndiag + 1)
             assert abs(Fraction(float(out[i, j])) - v) <= abs(v) * Fraction(2) ** -52 + top * Fraction(2) ** -60
+
+
+@pytest.mark.parametrize("radix,dmax,ceil,nshift,p,h", [(32, 16, 0, -1, 12, 0x4D24ADD106258287),
+                                                        (14, 7, 0, -1, 16, 0xF353DBD6B57F8B99)])
+def test_scheme1_other_formats_reference_hash(orc, radix, dmax, ceil, nshift, p, h):
+    """quick.csv:10 (I FP8, p = 12) and :14 (I BFP4, p = 16) at 128^3, uniform seed 7: digits within +-dmax,
+    int32 sums S_d of the deferred reconstruction, all diagonals read whole (nsmall = p)."""
+    n = 128
+    a, b = orc.inputs(7, -1.0, n * n, n * n)
+    A, B = a.reshape(n, n), b.reshape(n, n)
+    dA, _ = orc.scale(A, n, n, 0, ceil, nshift)
+    dB, _ = orc.scale(B, n, n, 1, ceil, nshift)
+    sa = orc.oz1_slices(A, n, n, 0, dA, p, radix, dmax)
+    sb = orc.oz1_slices(B, n, n, 1, dB, p, radix, dmax)
+    Pd, _ = orc.oz1_gemm_diag(sa, sb, p)
+    assert orc.hash(orc.oz1_recon(Pd, radix, 0, min((1 << 24) // (n * dmax * dmax), p), dA, dB)) == h
