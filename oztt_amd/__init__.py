@@ -88,7 +88,11 @@ class Plan2(ctypes.Structure):
                 ("two_pass", ctypes.c_int), ("m_cap", ctypes.c_int), ("m", ctypes.c_int * 24),
                 ("log2M", ctypes.c_double), ("recon1_log2", ctypes.c_double), ("TA", ctypes.c_double),
                 ("TB", ctypes.c_double), ("nA", ctypes.c_double), ("nB", ctypes.c_double), ("nC", ctypes.c_double),
-                ("wA", ctypes.c_double), ("wB", ctypes.c_double), ("b_cap", ctypes.c_int)]
+                ("wA", ctypes.c_double), ("wB", ctypes.c_double), ("b_cap", ctypes.c_int),
+                ("rS", ctypes.c_int), ("rsparse", ctypes.c_int), ("rfold_first", ctypes.c_int), ("rmaxg", ctypes.c_int),
+                ("rnprod", ctypes.c_int), ("rnplane", ctypes.c_int), ("rnout", ctypes.c_int),
+                ("rm", ctypes.c_int * 24), ("rmode", ctypes.c_int * 24), ("rmaxg_m", ctypes.c_int * 24),
+                ("rlog2M", ctypes.c_double)]
 
 
 class Plan1(ctypes.Structure):
@@ -216,14 +220,28 @@ class Context:
         return c, info, ev
 
 
-def plan2_int8(a, b, M: int, N: int, K: int, max_moduli: int = 0,
-               reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0) -> Plan2:
-    """Scheme II INT8 planner on padded row-major A (M x K) and B (K x N)."""
+def plan2(a, b, M: int, N: int, K: int, fmt: Format = Format.INT8, max_moduli: int = 0,
+          reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0) -> Plan2:
+    """Scheme II planner on padded row-major A (M x K) and B (K x N): the execution set (m, S, b, ...)
+    and the route's plan of the format (rm, rS, rmode, ...)."""
     a, b = _f64(a), _f64(b)
     out = Plan2()
     err = ctypes.create_string_buffer(2048)
-    _raise(host().ozt_plan2_int8(_ptr(a), _ptr(b), M, N, K, max_moduli, int(reconstruction), fixed_bits,
-                                 ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
+    _raise(host().ozt_plan_scheme2(_ptr(a), _ptr(b), M, N, K, int(fmt), max_moduli, int(reconstruction), fixed_bits,
+                            ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
+    return out
+
+
+def plan2_int8(a, b, M: int, N: int, K: int, max_moduli: int = 0,
+               reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0) -> Plan2:
+    """Scheme II INT8 planner on padded row-major A (M x K) and B (K x N)."""
+    return plan2(a, b, M, N, K, Format.INT8, max_moduli, reconstruction, fixed_bits)
+
+
+def choose_moduli_fp8(K: int, num_moduli: int, b_cap: int, window_log2: float = 0.0) -> Plan2:
+    """FP8-route moduli selection (route fields r*); window_log2 > 0 replaces the CRT window log2 K."""
+    out = Plan2()
+    host().ozt_choose_moduli_fp8(K, num_moduli, b_cap, ctypes.c_double(window_log2), ctypes.byref(out))
     return out
 
 

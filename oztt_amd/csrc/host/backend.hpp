@@ -67,7 +67,7 @@ Backend backend_for(Format format, Scheme scheme);
 bool scheme_available(Format format, Scheme scheme) noexcept;
 
 // Backends.
-Output ozaki2_int8_run(Device& dev, const Problem& p);
+Output ozaki2_run(Device& dev, const Problem& p);
 Output ozaki1_run(Device& dev, const Problem& p);
 
 }  // namespace ozTTgemm::detail

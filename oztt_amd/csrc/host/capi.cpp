@@ -3,6 +3,7 @@
 // the Scheme II planner. Each function returns 0 on success or one of the OZT_E* codes, mapping the
 // C++ exception types of the public API, and copies the exception's message into err.
 #include <cstring>
+#include <limits>
 #include <new>
 #include <optional>
 #include <stdexcept>
@@ -80,7 +81,27 @@ struct ozt_plan2 {
     double log2M, recon1_log2;
     double TA, TB, nA, nB, nC, wA, wB;
     int b_cap;
+    // the route's plan (FP8: the reference's FP8 moduli; INT8: as above)
+    int rS, rsparse, rfold_first, rmaxg, rnprod, rnplane, rnout;
+    int rm[24], rmode[24], rmaxg_m[24];
+    double rlog2M;
 };
+
+static void fill_route(const ozTTgemm::detail::ModuliSet& r, ozt_plan2* out) {
+    out->rS = (int)r.m.size();
+    out->rsparse = r.sparse;
+    out->rfold_first = r.fold_first;
+    out->rmaxg = r.maxg;
+    out->rnprod = r.nprod;
+    out->rnplane = r.nplane;
+    out->rnout = r.nout;
+    for (int s = 0; s < out->rS && s < 24; s++) {
+        out->rm[s] = r.m[s];
+        out->rmode[s] = s < (int)r.mode.size() ? r.mode[s] : 0;
+        out->rmaxg_m[s] = s < (int)r.maxg_m.size() ? r.maxg_m[s] : 1;
+    }
+    out->rlog2M = r.log2M;
+}
 
 int ozt_context_new(int device_id, const char* kernel_dir, void** out, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
@@ -144,14 +165,14 @@ int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, s
 int ozt_is_available(int format) { return ozTTgemm::is_available(static_cast<ozTTgemm::Format>(format)) ? 1 : 0; }
 const char* ozt_format_name(int format) { return ozTTgemm::format_name(static_cast<ozTTgemm::Format>(format)); }
 
-// Scheme II INT8 planner on padded row-major A (M x K) and B (K x N).
-int ozt_plan2_int8(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned max_moduli,
-                   int recon, unsigned fixed_b, ozt_plan2* out, char* err, std::size_t errlen) {
+// Scheme II planner on padded row-major A (M x K) and B (K x N) for `format` (INT8 or FP8).
+int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, unsigned K, int format, unsigned max_moduli,
+              int recon, unsigned fixed_b, ozt_plan2* out, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
-        const auto p = ozTTgemm::detail::plan_scheme2_int8(A, B, M, N, K, max_moduli,
-                                                             static_cast<ozTTgemm::Reconstruction>(recon), fb);
+        const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, static_cast<ozTTgemm::Format>(format), max_moduli,
+                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb);
         std::memset(out, 0, sizeof(*out));
         out->ok = p.mo.ok;
         out->b = p.b;
@@ -170,7 +191,23 @@ int ozt_plan2_int8(const double* A, const double* B, unsigned M, unsigned N, uns
         out->wA = p.stats.wA;
         out->wB = p.stats.wB;
         out->b_cap = p.stats.measured ? ozTTgemm::detail::precision_cap(p.stats) : 0;
+        fill_route(p.route, out);
     });
+}
+
+// FP8-route moduli selection alone (no input statistics); window_log2 <= 0 selects log2 K.
+int ozt_choose_moduli_fp8(unsigned K, int num_moduli, int b_cap, double window_log2, ozt_plan2* out) {
+    const auto mo = ozTTgemm::detail::choose_moduli_fp8(
+        K, num_moduli, b_cap, window_log2 > 0 ? window_log2 : std::numeric_limits<double>::quiet_NaN());
+    std::memset(out, 0, sizeof(*out));
+    out->ok = mo.ok;
+    out->b = mo.b;
+    out->S = (int)mo.m.size();
+    out->m_cap = mo.m_cap;
+    for (int s = 0; s < out->S && s < 24; s++) out->m[s] = mo.m[s];
+    out->log2M = mo.log2M;
+    fill_route(mo, out);
+    return 0;
 }
 
 // Moduli selection alone (no input statistics).

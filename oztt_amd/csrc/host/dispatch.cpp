@@ -36,15 +36,15 @@ void Workspace::release_all() {
     bufs_.clear();
 }
 
-// Scheme I runs every format (its digits are int8 values); Scheme II runs INT8.
+// Scheme I runs every format (its digits are int8 values); Scheme II runs INT8 and FP8.
 bool scheme_available(Format format, Scheme scheme) noexcept {
     if ((int)format < 0 || (int)format > (int)Format::BFP2) return false;
-    return scheme == Scheme::I || format == Format::INT8;
+    return scheme == Scheme::I || format == Format::INT8 || format == Format::FP8;
 }
 
 Backend backend_for(Format format, Scheme scheme) {
     if (scheme == Scheme::I && scheme_available(format, scheme)) return ozaki1_run;
-    if (scheme == Scheme::II && format == Format::INT8) return ozaki2_int8_run;
+    if (scheme == Scheme::II && scheme_available(format, scheme)) return ozaki2_run;
     throw std::invalid_argument("requested format was not built");
 }
 

@@ -1,4 +1,5 @@
-// Ozaki scheme II driver (INT8 residues): one FP64 GEMM on the GPU.
+// Ozaki scheme II driver (INT8 residues; the FP8 format plans its width on the FP8 route and computes
+// with INT8 residues, see plan2.hpp): one FP64 GEMM on the GPU.
 //
 // Pipeline of the reference's ozaki2.cpp:439-478: plan (moduli, width b, passes) -> upload the FP64
 // operands -> scale (row/column maxima, exponent deltas) -> slice (int8 residue planes per
@@ -34,13 +35,13 @@ std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / 
 
 }  // namespace
 
-Output ozaki2_int8_run(Device& D, const Problem& p) {
+Output ozaki2_run(Device& D, const Problem& p) {
     oz_dev* dev = D.dev;
     ev::Settings* es = ev::active();
     std::optional<unsigned> fixed_b;
     if (es && es->fixed_bits) fixed_b = es->fixed_bits;
-    const Plan2 plan = plan_scheme2_int8(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.max_moduli,
-                                         p.options.reconstruction, fixed_b);
+    const Plan2 plan = plan_scheme2(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.format, p.options.max_moduli,
+                                    p.options.reconstruction, fixed_b);
     const std::uint32_t M = p.m, N = p.n, K = p.k, S = (std::uint32_t)plan.S;
     const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
     const oz2_moduli_dev mdesc = split_descriptor(plan);
@@ -96,8 +97,8 @@ Output ozaki2_int8_run(Device& D, const Problem& p) {
 
     std::vector<double> values = run_pipeline(dev, steps, 2, out, (std::size_t)M * N, flags,
                                               2.0 * M * (double)N * K * S, S);
-    Info info{Scheme::II, Format::INT8};
-    info.moduli = S;
+    Info info{Scheme::II, p.options.format};
+    info.moduli = (std::uint32_t)plan.route.m.size();
     info.integer_bits = (std::uint32_t)plan.b;
     info.reconstruction_passes = plan.two_pass ? 2 : 1;
     return {std::move(values), info};

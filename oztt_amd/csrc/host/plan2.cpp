@@ -215,12 +215,16 @@ double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st) {
     return kRecon1EpsLog2 + l2m - 2.0 * b + 0.5 * (std::log2(st.TA) + std::log2(st.TB) - std::log2(st.nC));
 }
 
-Plan2 plan_scheme2_int8(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K,
-                        std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b) {
+Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
+                   std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b) {
+    if (format != Format::INT8 && format != Format::FP8)
+        throw std::invalid_argument("Ozaki II is built for INT8 and FP8 only");
+    const bool fp8 = format == Format::FP8;
     Plan2 p;
     p.M = M;
     p.N = N;
     p.K = K;
+    p.format = format;
     int b_cap = kDefaultBits;
     const bool b_fixed = fixed_b.has_value();
     if (b_fixed)
@@ -229,18 +233,20 @@ Plan2 plan_scheme2_int8(const double* A, const double* B, std::uint32_t M, std::
         p.stats = measure_stats(A, B, M, N, K);
         b_cap = precision_cap(p.stats);
     }
-    // limit on the number of moduli (plan.hpp:281): the caller's, else 16 with a fixed width, else 24
-    p.S_req = max_moduli ? max_moduli : (b_fixed ? 16u : (std::uint32_t)kMaxModuli);
+    // limit on the number of moduli (plan.hpp:281): the caller's, else the route's default with a fixed
+    // width (16 for INT8, 14 for FP8; split.hpp:73-76), else 24
+    p.S_req = max_moduli ? max_moduli : (b_fixed ? (fp8 ? 14u : 16u) : (std::uint32_t)kMaxModuli);
     if (b_fixed && passes == Reconstruction::Automatic) p.stats = measure_stats(A, B, M, N, K);
-    p.mo = choose_moduli_int8(K, (int)p.S_req, b_cap);
-    if (!p.mo.ok) {
-        if (!p.mo.acc_ok)
+    p.route = fp8 ? choose_moduli_fp8(K, (int)p.S_req, b_cap) : choose_moduli_int8(K, (int)p.S_req, b_cap);
+    const ModuliSet& r = p.route;
+    if (!r.ok) {
+        if (!r.acc_ok)
             throw std::runtime_error("Ozaki II: the padded inner dimension K=" + std::to_string(K) +
-                                     " is too large for this format: " + p.mo.acc_fail +
+                                     " is too large for this format: " + r.acc_fail +
                                      ". Use a smaller K or a different format; Options::max_moduli does not change "
                                      "this limit.");
         std::string cause;
-        if ((std::uint32_t)p.mo.ncand < std::min<std::uint32_t>(p.S_req, kMaxModuli))
+        if ((std::uint32_t)r.ncand < std::min<std::uint32_t>(p.S_req, kMaxModuli))
             cause = "Every candidate modulus is in use, so a larger Options::max_moduli does not help.";
         else if (p.S_req < (std::uint32_t)kMaxModuli)
             cause = "The limit of " + std::to_string(p.S_req) + " moduli is too small; raise Options::max_moduli.";
@@ -250,15 +256,25 @@ Plan2 plan_scheme2_int8(const double* A, const double* B, std::uint32_t M, std::
                                  "dimension K=" +
                                  std::to_string(K) + ". " + cause);
     }
-    if (!b_fixed && p.mo.b < kTargetBits)
+    if (!b_fixed && r.b < kTargetBits)
         throw std::runtime_error("Ozaki II: for the padded inner dimension K=" + std::to_string(K) + " the " +
-                                 std::to_string(p.mo.m.size()) + " selected moduli cover a width of only " +
-                                 std::to_string(p.mo.b) + " bits, below the 53 bits of FP64-equivalent accuracy; "
+                                 std::to_string(r.m.size()) + " selected moduli cover a width of only " +
+                                 std::to_string(r.b) + " bits, below the 53 bits of FP64-equivalent accuracy; "
                                  "raise Options::max_moduli or use a smaller K.");
-    p.b = p.mo.b;
+    p.b = r.b;
+    // the set the device computes with: the route's own (INT8), or INT8 moduli covering the window of
+    // the FP8 route's width
+    if (fp8) {
+        p.mo = choose_moduli_int8(K, kMaxModuli, p.b);
+        if (!p.mo.ok || p.mo.b != p.b)
+            throw std::runtime_error("Ozaki II: the width b=" + std::to_string(p.b) + " of the FP8 plan for K=" +
+                                     std::to_string(K) + " exceeds what 24 int8-sized moduli carry in this build");
+    } else {
+        p.mo = r;
+    }
     p.S = (int)p.mo.m.size();
-    // passes (plan.hpp:245-252)
-    p.recon1_log2 = p.stats.measured ? recon1_log2(p.mo, p.b, p.stats) : -INFINITY;
+    // passes (plan.hpp:245-252), from the route's moduli
+    p.recon1_log2 = p.stats.measured ? recon1_log2(r, p.b, p.stats) : -INFINITY;
     if (passes != Reconstruction::Automatic)
         p.two_pass = passes == Reconstruction::TwoPass;
     else

@@ -8,6 +8,7 @@
 #pragma once
 
 #include <cstdint>
+#include <limits>
 #include <optional>
 #include <string>
 #include <vector>
@@ -34,7 +35,11 @@ struct OperandStats {
     bool measured = false;
 };
 
-// Result of the moduli selection (the subset of the reference's Ozaki2Moduli that the INT8 path uses).
+// Carrying methods of a modulus on the FP8 route (split.hpp:176-214 OZ2_SPLIT_*): square modulus with
+// balanced digits (3 products), radix-16 Karatsuba (3), wide two-digit (4), square with sparse digits (3).
+inline constexpr int kFp8SplitSq = 0, kFp8SplitKar = 1, kFp8SplitWide = 2, kFp8SplitSqs = 4;
+
+// Result of the moduli selection (the subset of the reference's Ozaki2Moduli that this build uses).
 struct ModuliSet {
     bool ok = false;
     bool acc_ok = true;
@@ -43,12 +48,22 @@ struct ModuliSet {
     double log2M = 0;
     int m_cap = 0, ncand = 0;
     std::string acc_fail;  // first failed accumulation condition (empty when all hold)
+    // FP8 route only
+    bool fp8 = false, sparse = false, fold_first = false;
+    std::vector<int> mode, maxg_m;  // carrying method and concatenation bound per modulus
+    int maxg = 1, nprod = 0, nplane = 0, nout = 0;
 };
 
-// The plan of one Scheme II call.
+// The plan of one Scheme II call. `route` is the reference's plan for the requested format (its moduli
+// count, width and passes are what Info reports); `mo` is the set the device computes with. For INT8
+// they are the same. For FP8 the width b comes from the FP8 route and the exact product A'B' is
+// computed with INT8 moduli covering the same window (one int8 GEMM per modulus): the CRT is exact,
+// so the result depends on b (and the digits of A', B') only, not on the moduli that carry it.
 struct Plan2 {
     std::uint32_t M = 0, N = 0, K = 0;  // padded dimensions
     std::uint32_t S_req = 0;
+    Format format = Format::INT8;
+    ModuliSet route;
     ModuliSet mo;
     int b = 0, nd = 3, S = 0;
     bool two_pass = false;
@@ -68,14 +83,19 @@ int precision_cap(const OperandStats& st);
 
 // Moduli selection for the INT8 path (moduli.hpp:719-769 with the INT8 route of split.hpp:73).
 ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap);
+// Moduli selection for the FP8 route (moduli.hpp:719-769 with OZ2_ROUTE_FP8, split.hpp:72-76). The CRT
+// window is log2 K (the library's rule); window_log2 replaces it (used to restate the research planner
+// that wrote the reference's accuracy logs, which measured the window from the input).
+ModuliSet choose_moduli_fp8(std::uint32_t K, int num_moduli, int b_cap,
+                            double window_log2 = std::numeric_limits<double>::quiet_NaN());
 
 // log2 of the expected relative error of one reconstruction pass (auto_precision.hpp:128-139).
 double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st);
 
 // The whole plan (plan.hpp:258-306). fixed_b: width fixed by the caller (evaluator only).
 // Throws std::runtime_error when no exact configuration exists.
-Plan2 plan_scheme2_int8(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K,
-                        std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b);
+Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
+                   std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b);
 
 // Device descriptors of the plan.
 oz2_moduli_dev split_descriptor(const Plan2& p);

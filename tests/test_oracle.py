@@ -262,3 +262,33 @@ def test_scheme1_other_formats_reference_hash(orc, radix, dmax, ceil, nshift, p,
     sb = orc.oz1_slices(B, n, n, 1, dB, p, radix, dmax)
     Pd, _ = orc.oz1_gemm_diag(sa, sb, p)
     assert orc.hash(orc.oz1_recon(Pd, radix, 0, min((1 << 24) // (n * dmax * dmax), p), dA, dB)) == h
+
+
+def test_fp8_reference_hash_from_exact_residues(orc):
+    """quick.csv:11: II FP8 128^3, uniform seed 7, b = 54, one pass -> 20046e5bb3816cbb. The FP8 route's set
+    at K = 128 (the library planner), residues of the exact product A'B' modulo those moduli, and the oracle's
+    restatement of the reference reconstruction reproduce the reference's output: its digit split, products
+    and composition deliver exactly the residue classes of A'B', which is what this build computes."""
+    import oztt_amd as oz
+    n, b, nd = 128, 54, 3
+    a, bb = orc.inputs(7, -1.0, n * n, n * n)
+    A, B = a.reshape(n, n), bb.reshape(n, n)
+    fp8 = oz.choose_moduli_fp8(n, 14, b)
+    ms = [fp8.rm[i] for i in range(fp8.rS)]
+    assert fp8.ok and len(ms) == 12
+    shift = b - 20 * (nd - 1)
+    dA, _ = orc.scale(A, n, n, 0, 1, shift)
+    dB, _ = orc.scale(B, n, n, 1, 1, shift)
+    dgA = orc.digits(A, n, n, 0, dA, nd).reshape(n, n, nd).astype(np.int64)
+    dgB = orc.digits(B, n, n, 1, dB, nd).reshape(n, n, nd).astype(np.int64)
+    w = [1 << 40, 1 << 20, 1]
+    Ap = [[sum(int(dgA[i, k, j]) * w[j] for j in range(nd)) for k in range(n)] for i in range(n)]
+    Bp = [[sum(int(dgB[k, c, j]) * w[j] for j in range(nd)) for c in range(n)] for k in range(n)]
+    C = np.zeros((len(ms), n, n), dtype=np.int32)
+    for i in range(n):
+        for c in range(n):
+            v = sum(Ap[i][k] * Bp[k][c] for k in range(n))
+            for s, m in enumerate(ms):
+                r = v % m
+                C[s, i, c] = r - m if r > m // 2 else r
+    assert orc.hash(orc.crt_ref(C, n, n, ms, b, nd, 0, dA, dB)) == 0x20046E5BB3816CBB

@@ -168,3 +168,60 @@ def test_scheme1_rejects_unsupported_plans():
     z = np.zeros(64 * 64)
     with pytest.raises(RuntimeError, match="overflow FP32"):
         oz.plan1(z, z, 64, 64, 64, slices=16)
+
+
+# ---- Scheme II, FP8 route ----------------------------------------------------------------------
+# cool_oz2fp8_{3520,7040,14080}.log:22 (fixed b = 54, 14 moduli requested): the set with its carrying
+# methods (s sparse square, * square, k Karatsuba, w wide), matrix products, GEMM outputs after
+# concatenation, and the concatenation bounds.
+FP8_RECORDS = [
+    (3520, "2401s 2209s 1849s 1681s 1521s 1369s 1024* 961* 841* 625* 289* 529*", 36, 24, 74,
+     [4, 5, 7, 8, 9, 11, 18, 21, 24, 33, 74, 39]),
+    (7040, "2401s 2209s 1849s 1681s 1521s 1369s 1024* 961* 841* 625* 529* 487k", 36, 25, 19,
+     [2, 2, 3, 4, 4, 5, 9, 10, 12, 16, 19, 9]),
+    (14080, "2401s 2209s 1849s 1681s 1521s 1369s 1024* 961* 841* 625* 529* 977w", 37, 28, 9,
+     [1, 1, 1, 2, 2, 2, 4, 5, 6, 8, 9, 4]),
+]
+FP8_CODES = {0: "*", 1: "k", 2: "w", 4: "s"}
+
+
+@pytest.mark.parametrize("K,mods,gemms,outs,maxg,maxg_m", FP8_RECORDS)
+def test_fp8_moduli_records(K, mods, gemms, outs, maxg, maxg_m):
+    p = oz.choose_moduli_fp8(K, 14, 54)
+    assert p.ok and p.b == 54 and p.rsparse == 1 and p.rfold_first == 1
+    got = " ".join(f"{p.rm[i]}{FP8_CODES[p.rmode[i]]}" for i in range(p.rS))
+    assert got == mods
+    assert (p.rnprod, p.rnout, p.rmaxg) == (gemms, outs, maxg)
+    assert [p.rmaxg_m[i] for i in range(p.rS)] == maxg_m
+
+
+def test_fp8_dense_digits_at_large_k():
+    """K*32^2 + 2401 > 2^24 (K > 16381) returns to dense digits, the table up to 33^2 = 1089
+    (moduli.hpp:724-731); every modulus then carries digits within 16."""
+    p = oz.choose_moduli_fp8(16384, 24, 59)
+    assert p.ok and p.b == 59 and p.rsparse == 0
+    ms = [p.rm[i] for i in range(p.rS)]
+    assert max(ms) <= 1089 and ms[:6] == [1089, 1024, 961, 841, 625, 529]
+    assert all(math.gcd(x, y) == 1 for i, x in enumerate(ms) for y in ms[i + 1:])
+    assert sum(math.log2(x) for x in ms) >= 2 * 59 + 1 + math.log2(16384)
+
+
+# phi_sweep.log II-FP8 auto lines (4096^3, seed 7, two-pass forced): phi, b, moduli (CONFIG :110, :254, :398, :542)
+FP8_PHI = [(0.0, 53, 12), (1.0, 57, 12), (2.0, 59, 12), (4.0, 61, 13)]
+
+
+@pytest.mark.parametrize("phi,b,S", [FP8_PHI[i] for i in (0, 3)])
+def test_fp8_auto_precision_records(phi, b, S):
+    """The FP8 plan's width b equals the record; its set with the research planner's measured window has the
+    recorded size; the execution set (INT8 moduli) covers the same width."""
+    n = 4096
+    a, bb = oz.eval_inputs(7, phi, n * n, n * n)
+    p = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass)
+    assert p.b == b and p.two_pass == 1
+    r = math.sqrt(n)
+    f = (1 + r / math.ldexp(p.wA, b)) * (1 + r / math.ldexp(p.wB, b))
+    wlog2 = math.log2(p.wA * p.wB * max(f, 1.001))
+    research = oz.choose_moduli_fp8(n, 24, b, wlog2)
+    assert research.b == b and research.rS == S
+    lib = oz.choose_moduli_int8(n, 24, b)
+    assert p.S == lib.S and [p.m[i] for i in range(p.S)] == [lib.m[i] for i in range(lib.S)]
