@@ -1,9 +1,9 @@
 #!/usr/bin/env python3
 """Headline benchmark: Ozaki-II INT8 FP64 GEMM at m = n = k = 8192 on one MI355X.
 
-`--config C1|C2|C5` measures the other built BASELINE configs the same way (C1: II-INT8 1024^3 one
-pass; C2: I-INT8 4096^3 automatic slices; C5: I-BF16 8192 x 8192 x 65536, 8 slices, 1% zero rows and
-columns); the default line is C3.
+`--config C1|C2|C4|C5` measures the other BASELINE configs the same way (C1: II-INT8 1024^3 one
+pass; C2: I-INT8 4096^3 automatic slices; C4: II-FP8 16384^3, phi 2; C5: I-BF16 8192 x 8192 x 65536,
+8 slices, 1% zero rows and columns); the default line is C3.
 
 Workload: row-major FP64 A, B with entries (U(0,1)-0.5)*exp(0.5*N(0,1)),
 the reference's evaluation generator with seed 3; Scheme II, INT8 residues, automatic moduli (<= 24),
@@ -39,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "effective FP64 TFLOP/s (2mnk/t) + max rel err vs binary128, Ozaki-II INT8 8192³"
 INT8_PEAK_TOPS = 5000.0  # MI355X dense INT8 MFMA, 5.0 POP/s
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, 5.0 PFLOP/s
 # HBM bytes per launch of the product kernel at n = 8192 (17 moduli), from the rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes over this script scaled by the counters' readings for a plain 1 GiB copy
 # (factors 2.000 and 1.000): profiles/scheme2_int8_c3_8192_traffic.md.
@@ -82,6 +83,8 @@ CONFIGS = {
     "C1": ("II", "INT8", 1024, 1024, 1024, 1, 0.5, dict(reconstruction="OnePass"), INT8_PEAK_TOPS, 1024, 64),
     "C2": ("I", "INT8", 4096, 4096, 4096, 2, 1.0, dict(), INT8_PEAK_TOPS, 4096, 64),
     "C3": ("II", "INT8", 8192, 8192, 8192, 3, 0.5, dict(reconstruction="TwoPass"), INT8_PEAK_TOPS, 1024, 64),
+    # e4m3 digit products on the FP8 matrix cores (dense FP8 peak 5.0 PFLOP/s)
+    "C4": ("II", "FP8", 16384, 16384, 16384, 4, 2.0, dict(), FP8_PEAK_TFLOPS, 256, 32),
     # BF16 digits (+-32) run on the INT8 matrix cores, so the product roofline is the INT8 peak
     "C5": ("I", "BF16", 8192, 8192, 65536, 5, 4.0, dict(slices=8), INT8_PEAK_TOPS, 128, 32),
 }
@@ -89,6 +92,7 @@ WORKLOADS = {
     "C1": "C1 Ozaki-II INT8 m=n=k=1024, auto moduli, one-pass reconstruction",
     "C2": "C2 Ozaki-I INT8 m=n=k=4096, automatic slices",
     "C3": "C3 Ozaki-II INT8 m=n=k=8192, auto moduli (<=24), two-pass reconstruction",
+    "C4": "C4 Ozaki-II FP8 m=n=k=16384, auto moduli (FP8 route), wide dynamic range phi=2",
     "C5": "C5 Ozaki-I BF16 m=n=8192 k=65536, 8 slices, rows i%100==0 of A and columns j%100==0 of B zero",
 }
 
@@ -173,7 +177,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",  # every product runs on the INT8 matrix cores (C5's BF16-format digits are int8 values)
+        # the products' arithmetic: int8 (C5's BF16-format digits are int8 values) or e4m3 digits (C4)
+        "dtype": "fp8_e4m3" if fmt == "FP8" else "int8",
         "data": f"synthetic: reference evaluation generator, seed {seed}, (U(0,1)-0.5)*exp({phi}*N(0,1))",
         "config": {"workload": WORKLOADS[args.config], "m": m, "n": n, "k": k, "scheme": scheme, "format": fmt,
                    "slices": info.slices, "moduli": info.moduli, "integer_bits": info.integer_bits,
@@ -187,10 +192,21 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": C3_GEMM_TRAFFIC_BYTES if (headline and info.moduli == 17) else None,
-                     "kernel": "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II"
-                                                   else "<DIAG> (oz1_gemm_diag_i8)"),
+                     "kernel": ("gemm_f8_groups_kernel<1> (oz2_gemm_groups_f8)" if fmt == "FP8" else
+                                "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II"
+                                                    else "<DIAG> (oz1_gemm_diag_i8)")),
                      "launch_ms": round(gemm_ms, 4), "ops_per_launch": ev.product_ops},
     }
+    if fmt == "FP8":
+        # the same exact C' at the same width carried by INT8 residues (one int8 product per modulus)
+        log("INT8 residues at the FP8 plan's width")
+        o8 = oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, max_moduli=24)
+        c8, i8, e8 = ctx.evaluate(a, b, m, n, k, o8, fixed_bits=info.integer_bits, warmup=1, repeats=3)
+        out["int8_same_width"] = {"ms_per_step": round(e8.whole_ms, 4), "moduli": i8.moduli,
+                                  "integer_bits": i8.integer_bits,
+                                  "value": round(2.0 * m * n * k / (e8.whole_ms * 1e-3) / 1e12, 3),
+                                  "identical_output": bool(np.array_equal(c8.view(np.uint64), c.view(np.uint64)))}
+        del c8
     if cpu_rows > 0:
         log(f"CPU baseline: Dot2 on {cpu_rows} rows")
         out["cpu_baseline"] = cpu_baseline(a, b, m, n, k, cpu_rows)

@@ -139,6 +139,66 @@ int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, 
 int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long strideD,
                        const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo);
 
+/* ==== Scheme II digit formats: residues carried as small digits (reference FP8 route) ========= */
+
+#define OZ2_MAXPLANES 72  /* digit planes (at most 3 per modulus) */
+#define OZ2_MAXOUT 96     /* product outputs (at most 4 per modulus) */
+
+/* ---- A18 split (reference modslice_digit.cpp:142-243, sparse_fix.h:48-78, split.hpp:157-279) ---
+ * As oz2_split_int8 (same residues r = A' mod m_s, m_s <= 2401), then r split into digits per
+ * modulus, planes l, h (and s = h + l for xmode 1) in modulus order:
+ *   xmode 0 (rounded, square or wide modulus): h = Rnd(r*qinv), l = r - q*h;
+ *   xmode 1 (Karatsuba): h = Rnd((r + sgn(r)*(q/2 - 1/2))*qinv), l = r - q*h, s = h + l;
+ *   xmode 2 (sparse square, q odd): the rounded digits moved into {|x| <= 16} U {even, |x| <= 32}.
+ * Every operation is one binary32 operation as in the reference. encoding 1 stores e4m3 bytes
+ * (gfx950 FP8, exact for these digits), 0 int8 values. Layouts 2 and 3 only (OZ_BLOCK tiles). */
+typedef struct oz2_digit_dev {
+    oz2_moduli_dev mo;       /* moduli (m <= 2401), rinv, weights, nd */
+    int xmode[OZ2_MAXS];     /* 0 rounded, 1 Karatsuba, 2 sparse square */
+    float q[OZ2_MAXS];       /* digit radix */
+    float qinv[OZ2_MAXS];    /* 1.0f / q (stages.hpp:223) */
+    int encoding;            /* 1 e4m3, 0 int8 */
+} oz2_digit_dev;
+/* Number of digit planes of a descriptor (2 per modulus, 3 for Karatsuba), or -1. */
+int oz2_digit_planes(const oz2_digit_dev* dd);
+int oz2_split_digits(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
+                     const oz2_digit_dev* dd, uint8_t* planes, int layout, int prow, int pld, long long plane_stride);
+
+/* ---- A18 products + composition (reference ozaki2.cpp:228-285 run_digit_modulus, compose.cpp,
+ * split.hpp:541-661 product terms and groups) ------------------------------------------------
+ * Output o sums npairs digit products over the full K on the FP8 matrix cores (e4m3 x e4m3,
+ * FP32 accumulation; exact while the sum stays below 2^24, which `bound` states and the entry
+ * point checks):  P_o = sum_t A[a[t]] * Bt[b[t]]^T  (the reference's concatenation along K).
+ * out_kind 0 stores P_o as int32 (M x N per output, element strides); out_kind 1 stores the CRT
+ * term w_o = (coef * P_o) mod m in [0, m) as uint16, where coef is the composition coefficient
+ * times y_s (mod m): for modulus s, sum over its outputs of w_o == D_s * y_s (mod m_s), D_s the
+ * composed residue. A and Bt are e4m3 digit planes of oz2_split_digits (layouts 2 and 3);
+ * strideA/strideB are the byte distances between planes (multiples of 1024), strideO between
+ * outputs in elements. M, N multiples of 256, K of 64. */
+typedef struct oz2_group_dev {
+    int npairs;              /* 1..4 */
+    int modulus;             /* s: the modulus this output composes into */
+    unsigned char a[4], b[4];/* digit planes of A and of B, pair t = (a[t], b[t]) */
+    uint32_t m;              /* m_s */
+    uint32_t coef;           /* (coefficient * y_s) mod m_s */
+    float bound;             /* upper bound of |P_o| (sum over pairs of K * |digit| bounds) */
+} oz2_group_dev;
+typedef struct oz2_groups_dev {
+    int nout;                /* outputs, 1..OZ2_MAXOUT */
+    int nplanes;             /* digit planes in A and in Bt (every a[t], b[t] is below it) */
+    oz2_group_dev g[OZ2_MAXOUT];
+} oz2_groups_dev;
+int oz2_gemm_groups_f8(oz_dev* dev, const uint8_t* A, const uint8_t* Bt, void* out, int M, int N, int K,
+                       const oz2_groups_dev* gd, int out_kind, int ldo, long long strideA, long long strideB,
+                       long long strideO);
+
+/* CRT reconstruction from the uint16 terms of oz2_gemm_groups_f8 (out_kind 1): term plane o adds
+ * w_o * Q_{modulus(o)}; then as oz2_crt_f64 (moduli up to 2401; crt->nw must hold nterms * M).
+ * ldw and strideW in elements, multiples of 4; W 8-byte aligned. */
+int oz2_crt_terms_f64(oz_dev* dev, const uint16_t* W, int M, int N, int ldw, long long strideW, int nterms,
+                      const unsigned char* term_modulus, const oz2_crt_dev* crt, const int32_t* dA,
+                      const int32_t* dB, double* out, int ldo);
+
 /* ==== Scheme I (reference src/ozaki1.cpp run(): scale, slice, diagonal products, Horner) ==== */
 
 /* ---- A15: slicing (reference ozaki1/kernels/slice_tf_body.h:86-131, slice_tf_sm8.cpp) --------

@@ -748,6 +748,70 @@ void orc_oz2_residues(const double* X, int rows, int cols, int ld, int mode, con
     }
 }
 
+// modslice_digit.cpp:195-218 + sparse_fix.h:53-73: the digits of residue r (d[0] = l, d[1] = h,
+// d[2] = s), in the FP32 operation model. xmode 0 rounded, 1 Karatsuba, 2 sparse square.
+static int split_residue(float r, int xmode, float q, float qinv, float* d) {
+    if (xmode == 1) {
+        float sgn = std::signbit(r) ? 1.0f : 0.0f;          // Ltz
+        sgn = f_add(f_mul(sgn, -2.0f), 1.0f);                // MulS -2, AddS 1
+        const float t = f_mul(sgn, f_sub(f_mul(q, 0.5f), 0.5f));
+        const float h = f_rnd(f_mul(f_add(r, t), qinv));
+        const float l = f_sub(r, f_mul(h, q));
+        d[0] = l;
+        d[1] = h;
+        d[2] = f_add(h, l);
+        return 3;
+    }
+    float h = f_rnd(f_mul(r, qinv));
+    float l = f_sub(r, f_mul(h, q));
+    if (xmode == 2) {
+        const float al = std::fabs(l);
+        if (al > 16.5f && ((int)al & 1)) {
+            if (l < 0.0f) {
+                l = f_add(l, q);
+                h = f_sub(h, 1.0f);
+            } else {
+                l = f_sub(l, q);
+                h = f_add(h, 1.0f);
+            }
+        }
+        const float ah = std::fabs(h);
+        if (ah > 16.5f && ((int)ah & 1)) h = h < 0.0f ? f_add(h, q) : f_sub(h, q);
+    }
+    d[0] = l;
+    d[1] = h;
+    return 2;
+}
+
+void orc_oz2_digit_planes(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
+                          const int* m, const int* q, const int* xmode, int8_t* planes) {
+    std::vector<float> rinv(S), cw((size_t)S * 4);
+    std::vector<int> poff(S);
+    int np = 0;
+    for (int s = 0; s < S; s++) {
+        const __float128 qq = (__float128)1 / (__float128)m[s];
+        rinv[s] = (float)(double)qq;
+        for (int j = 0; j < 4; j++) cw[(size_t)s * 4 + j] = pow2mod(20 * (j + 1), m[s]);
+        poff[s] = np;
+        np += xmode[s] == 1 ? 3 : 2;
+    }
+    const size_t plane = (size_t)rows * cols;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        float dig[5], d[3];
+        for (int c = 0; c < cols; c++) {
+            make_digits(X[(size_t)r * ld + c], delta_of(delta, mode, r, c), nd, dig);
+            for (int s = 0; s < S; s++) {
+                const float v = residue(dig, nd, (float)m[s], rinv[s], &cw[(size_t)s * 4]);
+                const float qf = (float)q[s];
+                const int n = split_residue(v, xmode[s], qf, 1.0f / qf, d);
+                for (int j = 0; j < n; j++)
+                    planes[(size_t)(poff[s] + j) * plane + (size_t)r * cols + c] = (int8_t)(int)d[j];
+            }
+        }
+    }
+}
+
 float orc_modround(float d, float m, float rinv) { return mod_round(d, m, rinv); }
 
 int64_t orc_gemm_i8(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K) {

@@ -10,6 +10,9 @@
 //   orc_split_f64                 exactness hi+mid+lo == x*2^d (binary128) over random and edge inputs
 //   orc_oz2_digits/residues       digits.h:44 KAT, ModRound KATs (sfpu_tf_proc.h:271,303,312),
 //                                 residue-class invariants, and end to end by the output hashes
+//   orc_oz2_digit_planes          closed forms (h = round(r/q) or the Karatsuba ceiling, l + q h == r,
+//                                 the sparse-set moves checked against an integer restatement), and end
+//                                 to end by the FP8 output hash (tools/validated/quick.csv:11)
 //   orc_gemm_i8                   brute force int64 (its own definition)
 //   orc_oz2_crt_ref               reference output hashes (tools/validated/quick.csv:13,
 //                                 phi_sweep.log:116,122)
@@ -44,6 +47,11 @@ void orc_oz2_digits(const double* X, int rows, int cols, int ld, int mode, const
 // A8: residues A' mod m_s for S moduli, planes[s][r][c] (digits.h:165-179, modslice_int8.cpp:60-95).
 void orc_oz2_residues(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
                       const int* m, int8_t* planes);
+// A18: the residues split into digit planes (modslice_digit.cpp:195-218, sparse_fix.h:53-73):
+// per modulus s with digit radix q[s] and mode xmode[s] (0 rounded, 1 Karatsuba, 2 sparse square),
+// planes l, h (and s = h + l for Karatsuba) as int8 values, planes[p][r][c], moduli in order.
+void orc_oz2_digit_planes(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
+                          const int* m, const int* q, const int* xmode, int8_t* planes);
 // The reference's ModRound on one value (sfpu_tf_proc.h:316-319).
 float orc_modround(float d, float m, float rinv);
 // A9: C = A*B exactly (int64 accumulation; returns the largest |C| seen). A: MxK, B: KxN, row-major.

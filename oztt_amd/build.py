@@ -40,6 +40,8 @@ HIP_SOURCES = {
     "oz2_crt.hip": [],
     "oz1_slice.hip": ["-fgpu-flush-denormals-to-zero"],
     "oz1_recon.hip": ["-fgpu-flush-denormals-to-zero"],
+    "oz2_digits.hip": ["-fgpu-flush-denormals-to-zero"],
+    "oz2_gemm_f8.hip": [],
 }
 HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
               "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{CSRC / 'host'}"]

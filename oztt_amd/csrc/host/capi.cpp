@@ -195,6 +195,23 @@ int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, u
     });
 }
 
+// The device descriptors of a Scheme II FP8 plan (digit split, product outputs, CRT, term moduli).
+int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned max_moduli,
+                         int recon, unsigned fixed_b, oz2_digit_dev* dd, oz2_groups_dev* gd, oz2_crt_dev* crt,
+                         unsigned char* term_modulus, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        std::optional<unsigned> fb;
+        if (fixed_b) fb = fixed_b;
+        const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, ozTTgemm::Format::FP8, max_moduli,
+                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb);
+        *crt = ozTTgemm::detail::crt_descriptor(p);
+        *dd = ozTTgemm::detail::digit_descriptor(p);
+        std::vector<unsigned char> tm;
+        *gd = ozTTgemm::detail::groups_descriptor(p, *crt, tm);
+        std::memcpy(term_modulus, tm.data(), tm.size());
+    });
+}
+
 // FP8-route moduli selection alone (no input statistics); window_log2 <= 0 selects log2 K.
 int ozt_choose_moduli_fp8(unsigned K, int num_moduli, int b_cap, double window_log2, ozt_plan2* out) {
     const auto mo = ozTTgemm::detail::choose_moduli_fp8(

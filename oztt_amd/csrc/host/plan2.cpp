@@ -262,18 +262,11 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
                                  std::to_string(r.b) + " bits, below the 53 bits of FP64-equivalent accuracy; "
                                  "raise Options::max_moduli or use a smaller K.");
     p.b = r.b;
-    // the set the device computes with: the route's own (INT8), or INT8 moduli covering the window of
-    // the FP8 route's width
-    if (fp8) {
-        p.mo = choose_moduli_int8(K, kMaxModuli, p.b);
-        if (!p.mo.ok || p.mo.b != p.b)
-            throw std::runtime_error("Ozaki II: the width b=" + std::to_string(p.b) + " of the FP8 plan for K=" +
-                                     std::to_string(K) + " exceeds what 24 int8-sized moduli carry in this build");
-    } else {
-        p.mo = r;
-    }
+    p.mo = r;
     p.S = (int)p.mo.m.size();
-    // passes (plan.hpp:245-252), from the route's moduli
+    if (fp8 && (p.mo.nplane > OZ2_MAXPLANES || p.mo.nout > OZ2_MAXOUT))
+        throw std::runtime_error("Ozaki II: the FP8 plan needs more digit planes or outputs than the device tables hold");
+    // passes (plan.hpp:245-252)
     p.recon1_log2 = p.stats.measured ? recon1_log2(r, p.b, p.stats) : -INFINITY;
     if (passes != Reconstruction::Automatic)
         p.two_pass = passes == Reconstruction::TwoPass;
@@ -317,9 +310,10 @@ oz2_crt_dev crt_descriptor(const Plan2& p) {
     };
     std::vector<std::uint32_t> Mw{1};
     for (int m : p.mo.m) mul_small(Mw, (std::uint32_t)m);
-    // accumulator width: (S+1)*M plus a sign bit
+    // accumulator width: (terms+1)*M plus a sign bit; a term is a CRT digit (below m_s, one per
+    // modulus) or, on the FP8 route, one product output's share of it
     std::vector<std::uint32_t> bound = Mw;
-    mul_small(bound, (std::uint32_t)(p.S + 1));
+    mul_small(bound, (std::uint32_t)(std::max(p.S, p.mo.nout) + 1));
     int bits = 32 * ((int)bound.size() - 1) + (32 - __builtin_clz(bound.back())) + 1;
     d.nw = std::max(3, (bits + 31) / 32);
     if (d.nw > 8) throw std::runtime_error("Ozaki II: the CRT modulus exceeds the 256-bit reconstruction width");
@@ -349,6 +343,49 @@ oz2_crt_dev crt_descriptor(const Plan2& p) {
         d.y[s] = y;
     }
     return d;
+}
+
+oz2_digit_dev digit_descriptor(const Plan2& p) {
+    oz2_digit_dev d{};
+    d.mo = split_descriptor(p);
+    for (int s = 0; s < p.S; s++) {
+        const int mode = p.mo.mode[s];
+        // digit-making modes of the slicer (split.hpp:218-227 oz2_xmode): rounded digits for the square
+        // and wide methods, Karatsuba, sparse square
+        d.xmode[s] = mode == kFp8SplitKar ? 1 : (mode == kFp8SplitSqs ? 2 : 0);
+        d.q[s] = (float)p.mo.q[s];
+        d.qinv[s] = 1.0f / (float)p.mo.q[s];  // stages.hpp:223
+    }
+    d.encoding = 1;
+    return d;
+}
+
+oz2_groups_dev groups_descriptor(const Plan2& p, const oz2_crt_dev& crt, std::vector<unsigned char>& term_modulus) {
+    oz2_groups_dev g{};
+    const std::vector<Fp8Output>& outs = p.mo.outputs;
+    g.nout = (int)outs.size();
+    g.nplanes = p.mo.nplane;
+    // heavier outputs (more pairs) are dispatched first; ties keep the reference's order
+    std::vector<int> order(outs.size());
+    for (std::size_t i = 0; i < order.size(); i++) order[i] = (int)i;
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return outs[x].npairs > outs[y].npairs; });
+    term_modulus.assign(outs.size(), 0);
+    for (std::size_t j = 0; j < order.size(); j++) {
+        const Fp8Output& o = outs[order[j]];
+        oz2_group_dev& d = g.g[j];
+        d.npairs = o.npairs;
+        d.modulus = o.s;
+        for (int t = 0; t < o.npairs; t++) {
+            d.a[t] = (unsigned char)o.a[t];
+            d.b[t] = (unsigned char)o.b[t];
+        }
+        const std::uint64_t m = (std::uint64_t)p.mo.m[o.s];
+        d.m = (std::uint32_t)m;
+        d.coef = (std::uint32_t)(((std::uint64_t)o.coef % m) * crt.y[o.s] % m);
+        d.bound = (float)o.bound;
+        term_modulus[j] = (unsigned char)o.s;
+    }
+    return g;
 }
 
 }  // namespace ozTTgemm::detail

@@ -39,6 +39,16 @@ struct OperandStats {
 // balanced digits (3 products), radix-16 Karatsuba (3), wide two-digit (4), square with sparse digits (3).
 inline constexpr int kFp8SplitSq = 0, kFp8SplitKar = 1, kFp8SplitWide = 2, kFp8SplitSqs = 4;
 
+// One product output of the FP8 route (split.hpp:628-661 oz2_product_groups): the sum of npairs
+// digit products over K, A digit plane a[t] times B digit plane b[t] (global plane indices, the
+// moduli's planes one after the other), composed into modulus s with coefficient coef (mod m_s).
+struct Fp8Output {
+    int s = 0, npairs = 0;
+    int a[4] = {0, 0, 0, 0}, b[4] = {0, 0, 0, 0};
+    long coef = 0;
+    double bound = 0;  // largest |sum| (oz2_group_bound)
+};
+
 // Result of the moduli selection (the subset of the reference's Ozaki2Moduli that this build uses).
 struct ModuliSet {
     bool ok = false;
@@ -51,14 +61,13 @@ struct ModuliSet {
     // FP8 route only
     bool fp8 = false, sparse = false, fold_first = false;
     std::vector<int> mode, maxg_m;  // carrying method and concatenation bound per modulus
+    std::vector<int> q;             // digit radix per modulus
+    std::vector<Fp8Output> outputs; // product outputs in the reference's order (modulus by modulus)
     int maxg = 1, nprod = 0, nplane = 0, nout = 0;
 };
 
-// The plan of one Scheme II call. `route` is the reference's plan for the requested format (its moduli
-// count, width and passes are what Info reports); `mo` is the set the device computes with. For INT8
-// they are the same. For FP8 the width b comes from the FP8 route and the exact product A'B' is
-// computed with INT8 moduli covering the same window (one int8 GEMM per modulus): the CRT is exact,
-// so the result depends on b (and the digits of A', B') only, not on the moduli that carry it.
+// The plan of one Scheme II call: the moduli set of the requested format's route (`route`, which is
+// also the set the device computes with, `mo`), the width b, digits of A' and passes.
 struct Plan2 {
     std::uint32_t M = 0, N = 0, K = 0;  // padded dimensions
     std::uint32_t S_req = 0;
@@ -100,5 +109,10 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
 // Device descriptors of the plan.
 oz2_moduli_dev split_descriptor(const Plan2& p);
 oz2_crt_dev crt_descriptor(const Plan2& p);
+// FP8 route: the digit split (e4m3 planes) and the product outputs with their CRT coefficients
+// (coefficient * y_s mod m_s, y_s from crt), ordered with the outputs of more pairs first;
+// term_modulus receives the modulus of each output in that order.
+oz2_digit_dev digit_descriptor(const Plan2& p);
+oz2_groups_dev groups_descriptor(const Plan2& p, const oz2_crt_dev& crt, std::vector<unsigned char>& term_modulus);
 
 }  // namespace ozTTgemm::detail

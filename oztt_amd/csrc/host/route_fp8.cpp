@@ -373,15 +373,31 @@ ModuliSet choose_moduli_fp8(std::uint32_t K, int num_moduli, int b_cap, double w
                 }
         break;
     }
-    // per-modulus layout (moduli.hpp:583-606)
+    // per-modulus layout (moduli.hpp:583-606) and the product outputs: group (a0, b0, g) pairs A digit
+    // a0+t with B digit np-1-(b0+t) (the B planes are read in reversed order, LAYOUT_B_PERM)
     o.nprod = o.nplane = o.nout = 0;
     for (int i = 0; i < s; ++i) {
         Term t[4];
         Group gr[4];
+        const int np = planes(o.m[i], smax);
         o.mode.push_back(split_mode(o.m[i], smax));
+        o.q.push_back(digit_base(o.m[i], smax));
         o.nprod += product_terms(o.m[i], smax, t);
-        o.nplane += planes(o.m[i], smax);
-        o.nout += product_groups(o.m[i], smax, o.maxg_m[i], gr);
+        const int ng = product_groups(o.m[i], smax, o.maxg_m[i], gr);
+        for (int j = 0; j < ng; ++j) {
+            Fp8Output out;
+            out.s = i;
+            out.npairs = gr[j].g;
+            for (int u = 0; u < gr[j].g; ++u) {
+                out.a[u] = o.nplane + gr[j].a0 + u;
+                out.b[u] = o.nplane + np - 1 - (gr[j].b0 + u);
+            }
+            out.coef = gr[j].lo;
+            out.bound = group_bound(o.m[i], gr[j], (double)K, smax);
+            o.outputs.push_back(out);
+        }
+        o.nplane += np;
+        o.nout += ng;
     }
     return o;
 }

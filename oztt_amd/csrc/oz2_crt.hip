@@ -207,6 +207,51 @@ __global__ void __launch_bounds__(256) crt_digits_kernel(const uint8_t* __restri
         if (j0 + e < N) out[(long long)i * ldo + j0 + e] = crt_finish<NW>(acc[e], a, gi - dB[j0 + e]);
 }
 
+// Plane -> modulus of the uint16 CRT terms (digit formats).
+struct TermMap {
+    unsigned char mod[OZ2_MAXOUT];
+};
+
+// From the uint16 CRT terms w_o of the digit formats (oz2_gemm_groups_f8): acc = sum_o w_o Q_{s(o)},
+// which is congruent to sum_s k_s Q_s modulo M because the terms of modulus s add up to k_s modulo
+// m_s and m_s Q_s = M. One thread per 4 consecutive output elements (one 8-byte load per term).
+template <int NW>
+__global__ void __launch_bounds__(256) crt_terms_kernel(const uint16_t* __restrict__ W, int M, int N, int ldw,
+                                                        long long sW, int nterms, CrtArgs a, TermMap tmap,
+                                                        const int32_t* __restrict__ dA, const int32_t* __restrict__ dB,
+                                                        double* __restrict__ out, int ldo) {
+    const int j0 = 4 * (blockIdx.x * 256 + threadIdx.x);
+    const int i = blockIdx.y;
+    if (j0 >= N) return;
+    const uint2* w = reinterpret_cast<const uint2*>(W + (long long)i * ldw + j0);
+    const long long sw = sW / 4;
+    uint32_t acc[4][NW];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int q = 0; q < NW; q++) acc[e][q] = 0;
+    for (int o = 0; o < nterms; o++) {
+        const uint2 v = w[(long long)o * sw];
+        const uint32_t* Q = a.k.Q[tmap.mod[o]];
+        crt_add<NW>(acc[0], v.x & 0xFFFFu, Q);
+        crt_add<NW>(acc[1], v.x >> 16, Q);
+        crt_add<NW>(acc[2], v.y & 0xFFFFu, Q);
+        crt_add<NW>(acc[3], v.y >> 16, Q);
+    }
+    const int gi = 2 * a.k.shift - dA[i] - 2 * a.k.b;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (j0 + e < N) out[(long long)i * ldo + j0 + e] = crt_finish<NW>(acc[e], a, gi - dB[j0 + e]);
+}
+
+template <int NW>
+int launch_terms(oz_dev* dev, const uint16_t* W, int M, int N, int ldw, long long sW, int nterms, const CrtArgs& a,
+                 const TermMap& tmap, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    hipLaunchKernelGGL(crt_terms_kernel<NW>, dim3(oz::ceil_div(N, 1024), M), dim3(256), 0, dev->stream, W, M, N, ldw,
+                       sW, nterms, a, tmap, dA, dB, out, ldo);
+    return oz::launch_check(dev, "crt_terms_kernel");
+}
+
 template <int NW>
 int launch_crt(oz_dev* dev, const void* C, bool digits, int M, int N, int ldc, long long sC, const CrtArgs& a,
                const int32_t* dA, const int32_t* dB, double* out, int ldo) {
@@ -220,18 +265,12 @@ int launch_crt(oz_dev* dev, const void* C, bool digits, int M, int N, int ldc, l
     return oz::launch_check(dev, "crt_kernel");
 }
 
-// Both entry points: C is int32 products (element strides) or uint8 digits (byte strides).
-int crt_f64(oz_dev* dev, const char* name, const void* C, bool digits, int M, int N, int ldc, long long strideC,
-            const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
-    if (int st = oz::use(dev)) return st;
-    if (!C || !crt || !dA || !dB || !out || M <= 0 || N <= 0 || ldc < N || ldo < N || crt->S < 1 ||
-        crt->S > OZ2_MAXS || crt->nw < 3 || crt->nw > 8 || crt->Mtop <= 0.0 ||
-        (digits && (ldc % 4 || strideC % 4 || ((uintptr_t)C & 3))))
-        return oz::fail(dev, OZ_ERR_ARG, "%s: invalid arguments", name);
-    CrtArgs a{};
+// Kernel constants of a CRT descriptor whose moduli are at most mmax.
+int crt_args(oz_dev* dev, const char* name, const oz2_crt_dev* crt, uint32_t mmax, CrtArgs& a) {
+    a = CrtArgs{};
     a.k = *crt;
     for (int s = 0; s < crt->S; s++) {
-        if (crt->m[s] < 2 || crt->m[s] > 255) return oz::fail(dev, OZ_ERR_ARG, "%s: modulus out of range", name);
+        if (crt->m[s] < 2 || crt->m[s] > mmax) return oz::fail(dev, OZ_ERR_ARG, "%s: modulus out of range", name);
         a.magic[s] = (uint32_t)(0x100000000ull / crt->m[s]);
     }
     // floor(M/2)
@@ -241,6 +280,19 @@ int crt_f64(oz_dev* dev, const char* name, const void* C, bool digits, int M, in
         a.Mhalf[w] = (uint32_t)(cur >> 1);
         r = (uint32_t)(cur & 1u);
     }
+    return OZ_OK;
+}
+
+// Both entry points: C is int32 products (element strides) or uint8 digits (byte strides).
+int crt_f64(oz_dev* dev, const char* name, const void* C, bool digits, int M, int N, int ldc, long long strideC,
+            const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    if (int st = oz::use(dev)) return st;
+    if (!C || !crt || !dA || !dB || !out || M <= 0 || N <= 0 || ldc < N || ldo < N || crt->S < 1 ||
+        crt->S > OZ2_MAXS || crt->nw < 3 || crt->nw > 8 || crt->Mtop <= 0.0 ||
+        (digits && (ldc % 4 || strideC % 4 || ((uintptr_t)C & 3))))
+        return oz::fail(dev, OZ_ERR_ARG, "%s: invalid arguments", name);
+    CrtArgs a{};
+    if (int st = crt_args(dev, name, crt, 255u, a)) return st;
     const size_t esz = digits ? 1 : 4;
     // the grid puts rows on y (at most 65535 per launch): launch in row chunks
     for (int i0 = 0; i0 < M; i0 += 65535) {
@@ -271,4 +323,38 @@ extern "C" int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc,
 extern "C" int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long strideD,
                                   const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
     return crt_f64(dev, "oz2_crt_digits_f64", D, true, M, N, ldd, strideD, crt, dA, dB, out, ldo);
+}
+
+extern "C" int oz2_crt_terms_f64(oz_dev* dev, const uint16_t* W, int M, int N, int ldw, long long strideW, int nterms,
+                                 const unsigned char* term_modulus, const oz2_crt_dev* crt, const int32_t* dA,
+                                 const int32_t* dB, double* out, int ldo) {
+    const char* name = "oz2_crt_terms_f64";
+    if (int st = oz::use(dev)) return st;
+    if (!W || !term_modulus || !crt || !dA || !dB || !out || M <= 0 || N <= 0 || ldw < N || ldo < N || nterms < 1 ||
+        nterms > OZ2_MAXOUT || crt->S < 1 || crt->S > OZ2_MAXS || crt->nw < 3 || crt->nw > 8 || crt->Mtop <= 0.0 ||
+        ldw % 4 || strideW % 4 || ((uintptr_t)W & 7) || (nterms > 1 && strideW < (long long)M * ldw))
+        return oz::fail(dev, OZ_ERR_ARG, "%s: invalid arguments", name);
+    CrtArgs a;
+    if (int st = crt_args(dev, name, crt, 2401u, a)) return st;
+    TermMap tmap{};
+    for (int o = 0; o < nterms; o++) {
+        if (term_modulus[o] >= crt->S) return oz::fail(dev, OZ_ERR_ARG, "%s: term %d names modulus %d", name, o, term_modulus[o]);
+        tmap.mod[o] = term_modulus[o];
+    }
+    for (int i0 = 0; i0 < M; i0 += 65535) {
+        const int rows = std::min(65535, M - i0);
+        const uint16_t* Wi = W + (size_t)i0 * ldw;
+        double* oi = out + (long long)i0 * ldo;
+        int st;
+        switch (crt->nw) {
+        case 3: st = launch_terms<3>(dev, Wi, rows, N, ldw, strideW, nterms, a, tmap, dA + i0, dB, oi, ldo); break;
+        case 4: st = launch_terms<4>(dev, Wi, rows, N, ldw, strideW, nterms, a, tmap, dA + i0, dB, oi, ldo); break;
+        case 5: st = launch_terms<5>(dev, Wi, rows, N, ldw, strideW, nterms, a, tmap, dA + i0, dB, oi, ldo); break;
+        case 6: st = launch_terms<6>(dev, Wi, rows, N, ldw, strideW, nterms, a, tmap, dA + i0, dB, oi, ldo); break;
+        case 7: st = launch_terms<7>(dev, Wi, rows, N, ldw, strideW, nterms, a, tmap, dA + i0, dB, oi, ldo); break;
+        default: st = launch_terms<8>(dev, Wi, rows, N, ldw, strideW, nterms, a, tmap, dA + i0, dB, oi, ldo); break;
+        }
+        if (st) return st;
+    }
+    return OZ_OK;
 }

@@ -23,66 +23,12 @@
 //     (ds_read_b128, rows r..r+31, two chunk columns) spread evenly over the LDS banks.
 //   - Workgroups are mapped to tiles XCD-aware (tile_of below).
 #include "oz2_modular.hpp"
+#include "oz_gemm_common.hpp"
 #include "oz_internal.hpp"
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Workgroup -> (batch, tile row, tile column). Workgroups are dispatched round-robin over the 8
-// XCDs (workgroup w runs on XCD w % 8), and each XCD has its own L2. The map gives every XCD one
-// contiguous range of the logical tile sequence, and orders that sequence batch-major, then in
-// groups of GROUP_M tile rows walked column by column, so the ~32 workgroups an XCD runs at a time
-// cover a compact block of tiles and share their A rows and B columns in that L2. It is a
-// bijection for any workgroup count.
-constexpr int XCDS = 8, GROUP_M = 4;
-__device__ __forceinline__ void tile_of(int w, int tiles_m, int tiles_n, int nbatch, int& batch, int& tm, int& tn) {
-    const int total = tiles_m * tiles_n * nbatch;
-    const int q = total / XCDS, r = total % XCDS;
-    const int x = w % XCDS, j = w / XCDS;
-    const int t = x * q + min(x, r) + j;  // logical index
-    const int per_batch = tiles_m * tiles_n;
-    batch = t / per_batch;
-    const int u = t % per_batch;
-    const int group = u / (GROUP_M * tiles_n);
-    const int first_m = group * GROUP_M;
-    const int gm = min(tiles_m - first_m, GROUP_M);
-    const int v = u % (GROUP_M * tiles_n);
-    tm = first_m + v % gm;
-    tn = v / gm;
-}
-
-// Workgroup barrier without the memory fences of __syncthreads(): those would wait for every
-// outstanding load, including the direct-to-LDS loads of the stages still in flight. Each wave
-// first waits (vmcnt) for its own loads of the stage about to be read, so after the barrier the
-// whole stage is in LDS; the empty asm statements keep the compiler from moving LDS accesses
-// across the barrier.
-__device__ __forceinline__ void stage_barrier() {
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-}
-
-// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding of simm16: vmcnt
-// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-// vmcnt = N and lgkmcnt = 0 (this wave's LDS reads complete).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
-}
-
-constexpr int BM = 256, BN = 256, BK = 64, NS = 4, THREADS = 256;
-constexpr int STAGE_A = BM * BK, STAGE_B = BN * BK, STAGE = STAGE_A + STAGE_B;  // bytes
-constexpr int LOADS_A = STAGE_A / 16 / THREADS, LOADS_B = STAGE_B / 16 / THREADS;  // per thread per stage
-static_assert(LOADS_A == 4 && LOADS_B == 4, "each thread moves 4+4 chunks of 16 bytes per stage");
+using namespace ozg;
 
 // Output modes. PRODUCTS: C[b] = A[b] Bt[b]^T as int32. DIGITS: the same products reduced in the
 // epilogue to the CRT digit for modulus b (oz2::crt_digit with dc.m/y/magic[b]), C as uint8. DIAG
@@ -142,16 +88,8 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
     } while (0)
 
     const int wm = wave >> 1, wn = wave & 1;
-    // fragment addresses: row r = lane%32 of each 32-row block, logical chunk c = 2*ks + lane/32,
-    // stored at chunk position c ^ f(r) (f sees bits 1..3 of r only, so r%16 or r gives the same)
-    const int frow = lane & 31;
     int offA[2], offB[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-        const int pos = 16 * ((2 * ks + (lane >> 5)) ^ (((frow >> 1) ^ (frow >> 2)) & 3));
-        offA[ks] = (wm * 128 + frow) * BK + pos;
-        offB[ks] = STAGE_A + (wn * 128 + frow) * BK + pos;
-    }
+    fragment_offsets(lane, wm, wn, offA, offB);
 
     v16i acc[4][4];
 #pragma unroll

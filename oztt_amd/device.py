@@ -28,6 +28,38 @@ class CrtDesc(ctypes.Structure):
                 ("Q", (ctypes.c_uint32 * 8) * OZ2_MAXS), ("Mw", ctypes.c_uint32 * 8), ("Mtop", ctypes.c_double)]
 
 
+OZ2_MAXPLANES = 72
+OZ2_MAXOUT = 96
+
+
+class DigitDesc(ctypes.Structure):
+    _fields_ = [("mo", ModuliDesc), ("xmode", ctypes.c_int * OZ2_MAXS), ("q", ctypes.c_float * OZ2_MAXS),
+                ("qinv", ctypes.c_float * OZ2_MAXS), ("encoding", ctypes.c_int)]
+
+
+class GroupDesc(ctypes.Structure):
+    _fields_ = [("npairs", ctypes.c_int), ("modulus", ctypes.c_int), ("a", ctypes.c_ubyte * 4),
+                ("b", ctypes.c_ubyte * 4), ("m", ctypes.c_uint32), ("coef", ctypes.c_uint32), ("bound", ctypes.c_float)]
+
+
+class GroupsDesc(ctypes.Structure):
+    _fields_ = [("nout", ctypes.c_int), ("nplanes", ctypes.c_int), ("g", GroupDesc * OZ2_MAXOUT)]
+
+
+# OCP e4m3 (the gfx950 FP8 format): byte -> value
+def _e4m3_table() -> np.ndarray:
+    t = np.zeros(256)
+    for u in range(256):
+        s, e, f = u >> 7, (u >> 3) & 15, u & 7
+        v = (f / 8.0) * 2.0 ** -6 if e == 0 else (1 + f / 8.0) * 2.0 ** (e - 7)
+        t[u] = -v if s else v
+    t[0x7F] = t[0xFF] = np.nan
+    return t
+
+
+E4M3 = _e4m3_table()
+
+
 def moduli_desc(moduli, nd: int) -> ModuliDesc:
     d = ModuliDesc()
     d.S, d.nd = len(moduli), nd
@@ -171,6 +203,23 @@ class Device:
     def oz1_recon(self, P: Buffer, M, N, ldp, sP, desc: "Oz1ReconDesc", dA: Buffer, dB: Buffer, out: Buffer, ldo):
         self._check(hip().oz1_recon_f64(self.h, P.ptr, M, N, ldp, ctypes.c_longlong(sP), ctypes.byref(desc), dA.ptr,
                                         dB.ptr, out.ptr, ldo), "oz1_recon_f64")
+
+    def split_digits(self, X: Buffer, rows, cols, ld, mode, delta: Buffer, desc: DigitDesc, planes: Buffer, layout,
+                     prow, pld, pstride):
+        self._check(hip().oz2_split_digits(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, ctypes.byref(desc),
+                                              planes.ptr, layout, prow, pld, ctypes.c_longlong(pstride)),
+                    "oz2_split_digits")
+
+    def gemm_groups_f8(self, A: Buffer, Bt: Buffer, out: Buffer, M, N, K, desc: GroupsDesc, kind, ldo, sA, sB, sO):
+        self._check(hip().oz2_gemm_groups_f8(self.h, A.ptr, Bt.ptr, out.ptr, M, N, K, ctypes.byref(desc), kind, ldo,
+                                                ctypes.c_longlong(sA), ctypes.c_longlong(sB), ctypes.c_longlong(sO)),
+                    "oz2_gemm_groups_f8")
+
+    def crt_terms(self, W: Buffer, M, N, ldw, sW, nterms, term_modulus, desc: CrtDesc, dA: Buffer, dB: Buffer,
+                  out: Buffer, ldo):
+        tm = (ctypes.c_ubyte * OZ2_MAXOUT)(*[int(x) for x in term_modulus])
+        self._check(hip().oz2_crt_terms_f64(self.h, W.ptr, M, N, ldw, ctypes.c_longlong(sW), nterms, tm,
+                                               ctypes.byref(desc), dA.ptr, dB.ptr, out.ptr, ldo), "oz2_crt_terms_f64")
 
     def crt(self, C: Buffer, M, N, ldc, sC, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
         self._check(hip().oz2_crt_f64(self.h, C.ptr, M, N, ldc, ctypes.c_longlong(sC), ctypes.byref(desc), dA.ptr,

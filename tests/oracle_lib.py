@@ -72,6 +72,18 @@ class Oracle:
                                   P(m), P(out))
         return out
 
+    def digit_planes(self, X, rows, cols, mode, delta, nd, moduli, q, xmode):
+        """FP8-route digit planes (l, h[, s] per modulus) as int8 values, shape (planes, rows, cols)."""
+        X = np.ascontiguousarray(X, dtype=np.float64)
+        m = np.array(moduli, dtype=np.int32)
+        qa = np.array(q, dtype=np.int32)
+        xa = np.array(xmode, dtype=np.int32)
+        n = int(sum(3 if x == 1 else 2 for x in xmode))
+        out = np.empty((n, rows, cols), dtype=np.int8)
+        self.lib.orc_oz2_digit_planes(P(X), rows, cols, cols, mode, P(np.ascontiguousarray(delta, np.int32)), nd,
+                                      len(moduli), P(m), P(qa), P(xa), P(out))
+        return out
+
     def modround(self, d, m, rinv) -> float:
         return float(self.lib.orc_modround(d, m, rinv))
 

@@ -1,0 +1,171 @@
+"""Scheme II with the FP8 format on the GPU: e4m3 digit planes, digit products on the FP8 matrix
+cores, composition in the product epilogue, exact CRT.
+
+1. Stage parity against the oracle (reference modslice_digit.cpp / compose.cpp restated): the digit
+   planes are bit-exact (decoded e4m3 values), every product output equals the int64 sum of its
+   digit products, every uint16 term is coef * P mod m; the reference's published FP8 output hash
+   (quick.csv:11, 20046e5bb3816cbb) follows from the GPU terms through the oracle's restatement of
+   the reference reconstruction.
+2. The public API: the FP8 output is bit-identical to the INT8 output at the same width b (both
+   reconstruct the exact C' = A'B'), Info reports the FP8 route, accuracy on the C4 generator.
+"""
+import numpy as np
+import pytest
+
+import oztt_amd as oz
+from oztt_amd.device import E4M3, from_blocks
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = oz.Context()
+    yield c
+    c.close()
+
+
+def opts(fmt, **kw):
+    o = oz.Options(scheme=oz.Scheme.II, format=fmt)
+    for key, v in kw.items():
+        setattr(o, key, v)
+    return o
+
+
+def test_fp8_quick_case_matches_int8_bits(ctx):
+    """quick.csv:11 / :13 settings: 128^3, uniform seed 7, b = 54, one pass; S_req 14 (FP8), 16 (INT8)."""
+    n = 128
+    a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
+    one = oz.Reconstruction.OnePass
+    c8, i8, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.FP8, max_moduli=14, reconstruction=one), fixed_bits=54)
+    ci, ii, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.INT8, max_moduli=16, reconstruction=one), fixed_bits=54)
+    assert i8.format == oz.Format.FP8 and i8.moduli == 12 and i8.integer_bits == 54
+    assert ii.moduli == 15 and ii.integer_bits == 54
+    np.testing.assert_array_equal(c8.view(np.uint64), ci.view(np.uint64))
+
+
+@pytest.mark.parametrize("n", [1024, 2048])
+def test_fp8_wide_range_auto(ctx, oracle, n):
+    """C4 generator (seed 4, phi 2) at reduced size: automatic b, FP8 route moduli, accuracy."""
+    a, b = oz.eval_inputs(4, 2.0, n * n, n * n)
+    p = oz.plan2(a, b, n, n, n, oz.Format.FP8)
+    c = np.empty(n * n)
+    info = ctx.gemm(a, b, c, n, n, n, opts(oz.Format.FP8))
+    assert info.format == oz.Format.FP8 and info.moduli == p.rS and info.integer_bits == p.b
+    assert info.reconstruction_passes == (2 if p.two_pass else 1)
+    ci = np.empty(n * n)
+    ii = ctx.gemm(a, b, ci, n, n, n, opts(oz.Format.INT8))
+    if ii.integer_bits == info.integer_bits:
+        np.testing.assert_array_equal(c.view(np.uint64), ci.view(np.uint64))
+    rs = np.random.default_rng(0).integers(0, n, 256)
+    cs = np.random.default_rng(1).integers(0, n, 256)
+    q = oracle.quad_sample(a, b, n, n, n, rs, cs)
+    got = c.reshape(n, n)[rs, cs]
+    absab = (np.abs(a.reshape(n, n)[rs]) * np.abs(b.reshape(n, n)[:, cs].T)).sum(axis=1)
+    assert np.all(np.abs(got - q) <= absab * n * 2.0 ** -53)
+
+
+def run_fp8_stages(dev, a, b, n, max_moduli=0, fixed_bits=0, one_pass=True):
+    """scale -> digit planes -> product outputs (int32 and uint16 terms) -> CRT on the GPU."""
+    rec = oz.Reconstruction.OnePass if one_pass else oz.Reconstruction.Automatic
+    dd, gd, crt, tm = oz.plan2_fp8_device(a, b, n, n, n, max_moduli=max_moduli, reconstruction=rec,
+                                          fixed_bits=fixed_bits)
+    nd, b_ = dd.mo.nd, crt.b
+    shift = b_ - 20 * (nd - 1)
+    Mg = -(-n // 256) * 256
+    Kg = -(-n // 64) * 64
+    P, O = gd.nplanes, gd.nout
+    bA, bB = dev.upload(a), dev.upload(b)
+    bdA, bdB, bfl = dev.alloc(4 * n), dev.alloc(4 * n), dev.alloc(8)
+    dev.fill_u32(bfl, 0, 2)
+    dev.scale(bA, n, n, n, 0, 1, shift, bdA, bfl, 0)
+    dev.scale(bB, n, n, n, 1, 1, shift, bdB, bfl, 1)
+    pA, pB = dev.alloc(P * Mg * Kg), dev.alloc(P * Mg * Kg)
+    dev.split_digits(bA, n, n, n, 0, bdA, dd, pA, 2, Mg, Kg, Mg * Kg)
+    dev.split_digits(bB, n, n, n, 1, bdB, dd, pB, 3, Mg, Kg, Mg * Kg)
+    bP = dev.alloc(4 * O * Mg * Mg)
+    dev.gemm_groups_f8(pA, pB, bP, Mg, Mg, Kg, gd, 0, Mg, Mg * Kg, Mg * Kg, Mg * Mg)
+    bW = dev.alloc(2 * O * Mg * Mg)
+    dev.gemm_groups_f8(pA, pB, bW, Mg, Mg, Kg, gd, 1, Mg, Mg * Kg, Mg * Kg, Mg * Mg)
+    bo = dev.alloc(8 * n * n)
+    dev.crt_terms(bW, n, n, Mg, Mg * Mg, O, tm, crt, bdA, bdB, bo, n)
+    r = dict(dd=dd, gd=gd, crt=crt, tm=tm, nd=nd, b=b_,
+             dA=dev.download(bdA, np.int32, n), dB=dev.download(bdB, np.int32, n),
+             flags=dev.download(bfl, np.uint32, 2),
+             planesA=E4M3[from_blocks(dev.download(pA, np.uint8, P * Mg * Kg).reshape(P, -1), Mg, Kg)[:, :n, :n]],
+             planesB=E4M3[from_blocks(dev.download(pB, np.uint8, P * Mg * Kg).reshape(P, -1), Mg, Kg)[:, :n, :n]],
+             P=dev.download(bP, np.int32, O * Mg * Mg).reshape(O, Mg, Mg)[:, :n, :n],
+             W=dev.download(bW, np.uint16, O * Mg * Mg).reshape(O, Mg, Mg)[:, :n, :n],
+             out=dev.download(bo, np.float64, n * n))
+    for buf in (bA, bB, bdA, bdB, bfl, pA, pB, bP, bW, bo):
+        buf.free()
+    dev.bufs.clear()
+    return r
+
+
+def check_fp8_chain(oracle, r, a, b, n):
+    """Every stage of run_fp8_stages against the oracle; returns the composed residues (S, n, n)."""
+    dd, gd, crt, tm, nd, b_ = r["dd"], r["gd"], r["crt"], r["tm"], r["nd"], r["b"]
+    S = dd.mo.S
+    ms = [int(crt.m[s]) for s in range(S)]
+    qs = [int(dd.q[s]) for s in range(S)]
+    xm = [int(dd.xmode[s]) for s in range(S)]
+    A, B = a.reshape(n, n), b.reshape(n, n)
+    shift = b_ - 20 * (nd - 1)
+    dA, fA = oracle.scale(A, n, n, 0, 1, shift)
+    dB, fB = oracle.scale(B, n, n, 1, 1, shift)
+    np.testing.assert_array_equal(r["dA"], dA)
+    np.testing.assert_array_equal(r["dB"], dB)
+    assert fA == fB == 0 and not r["flags"].any()
+    pa = oracle.digit_planes(A, n, n, 0, dA, nd, ms, qs, xm)
+    pb = oracle.digit_planes(B, n, n, 1, dB, nd, ms, qs, xm)
+    np.testing.assert_array_equal(r["planesA"], pa.astype(np.float64))
+    np.testing.assert_array_equal(r["planesB"], pb.transpose(0, 2, 1).astype(np.float64))
+    k = [np.zeros((n, n), dtype=np.int64) for _ in ms]
+    for o in range(gd.nout):
+        g = gd.g[o]
+        P = sum(oracle.gemm_i8(pa[g.a[t]], pb[g.b[t]])[0].astype(np.int64) for t in range(g.npairs))
+        np.testing.assert_array_equal(r["P"][o].astype(np.int64), P)
+        w = (g.coef * (P % g.m)) % g.m
+        np.testing.assert_array_equal(r["W"][o].astype(np.int64), w)
+        k[tm[o]] = (k[tm[o]] + w) % g.m
+    C = np.zeros((S, n, n), dtype=np.int32)
+    for s, m in enumerate(ms):
+        res = (k[s] * pow(int(crt.y[s]), -1, m)) % m
+        C[s] = np.where(res > m // 2, res - m, res)
+    ex = oracle.crt_exact(C, n, n, ms, b_, nd, dA, dB)
+    np.testing.assert_array_equal(r["out"].view(np.uint64), ex.view(np.uint64))
+    return C, ms, dA, dB
+
+
+def test_fp8_stages_quick_case_reference_hash(dev, oracle):
+    """quick.csv:11: II FP8 128^3, uniform seed 7, b = 54, 14 moduli requested, one pass."""
+    n = 128
+    a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
+    r = run_fp8_stages(dev, a, b, n, max_moduli=14, fixed_bits=54)
+    assert r["dd"].mo.S == 12 and r["b"] == 54 and sorted(set(r["dd"].xmode[s] for s in range(12))) == [0, 1, 2]
+    C, ms, dA, dB = check_fp8_chain(oracle, r, a, b, n)
+    assert oracle.hash(oracle.crt_ref(C, n, n, ms, 54, r["nd"], 0, dA, dB)) == 0x20046E5BB3816CBB
+
+
+@pytest.mark.parametrize("n,seed,phi,fixed", [(1024, 4, 2.0, 60), (256, 4, 2.0, 0), (320, 9, 1.0, 0)])
+def test_fp8_stages_bit_exact(dev, oracle, n, seed, phi, fixed):
+    """C4 generator; b = 60 at K = 1024 brings a wide (non-square, 4-product) modulus, 803."""
+    a, b = oz.eval_inputs(seed, phi, n * n, n * n)
+    r = run_fp8_stages(dev, a, b, n, fixed_bits=fixed, one_pass=False)
+    if fixed == 60:
+        assert 803 in [r["crt"].m[s] for s in range(r["dd"].mo.S)]
+        assert any(r["gd"].g[o].m == 803 for o in range(r["gd"].nout))
+    check_fp8_chain(oracle, r, a, b, n)
+
+
+def test_fp8_gemm_rejects_inexact_bound(dev):
+    _, gd, _, _ = oz.plan2_fp8_device(*oz.eval_inputs(7, -1.0, 64 * 64, 64 * 64), 64, 64, 64)
+    gd.g[0].bound = 2.0 ** 24
+    A = dev.alloc(gd.nplanes * 256 * 64)
+    P = dev.alloc(4 * gd.nout * 256 * 256)
+    with pytest.raises(RuntimeError, match="exact FP32"):
+        dev.gemm_groups_f8(A, A, P, 256, 256, 64, gd, 0, 256, 256 * 64, 256 * 64, 256 * 256)
+    A.free()
+    P.free()
+    dev.bufs.clear()

@@ -292,3 +292,94 @@ def test_fp8_reference_hash_from_exact_residues(orc):
                 r = v % m
                 C[s, i, c] = r - m if r > m // 2 else r
     assert orc.hash(orc.crt_ref(C, n, n, ms, b, nd, 0, dA, dB)) == 0x20046E5BB3816CBB
+
+
+def _fp8_quick_plan():
+    import oztt_amd as oz
+    n, b = 128, 54
+    a, bb = oz.eval_inputs(7, -1.0, n * n, n * n)
+    dd, gd, crt, tm = oz.plan2_fp8_device(a, bb, n, n, n, max_moduli=14, reconstruction=oz.Reconstruction.OnePass,
+                                          fixed_bits=b)
+    S = dd.mo.S
+    ms = [int(crt.m[s]) for s in range(S)]
+    qs = [int(dd.q[s]) for s in range(S)]
+    xm = [int(dd.xmode[s]) for s in range(S)]
+    return n, b, dd.mo.nd, a.reshape(n, n), bb.reshape(n, n), dd, gd, crt, tm, ms, qs, xm
+
+
+def _sparse_split(r, q):
+    """sparse_fix.h:12-18 in integer arithmetic: rounded digits, then the odd ones >= 17 moved by q."""
+    num = 2 * r + (q if r >= 0 else -q)  # round half away from zero (q odd: no ties)
+    h = (abs(num) // (2 * q)) * (1 if num >= 0 else -1)
+    t = r - q * h
+    if t % 2 and abs(t) >= 17:
+        s = 1 if t > 0 else -1
+        t -= s * q
+        h += s
+    if h % 2 and abs(h) >= 17:
+        h -= (1 if h > 0 else -1) * q
+    return t, h
+
+
+def test_fp8_digit_planes_closed_forms(orc):
+    """The FP8-route digits of every element (quick case: six sparse squares, five dense squares and a
+    Karatsuba modulus) equal the closed forms of split.hpp:157-279 applied to a residue of A'."""
+    n, b, nd, A, B, dd, gd, crt, tm, ms, qs, xm = _fp8_quick_plan()
+    assert sorted(set(xm)) == [0, 1, 2]
+    shift = b - 20 * (nd - 1)
+    for X, mode in ((A, 0), (B, 1)):
+        dl, _ = orc.scale(X, n, n, mode, 1, shift)
+        pl = orc.digit_planes(X, n, n, mode, dl, nd, ms, qs, xm).astype(np.int64)
+        dig = orc.digits(X, n, n, mode, dl, nd).reshape(n, n, nd).astype(np.int64)
+        Ap = sum(dig[:, :, j] << (20 * (nd - 1 - j)) for j in range(nd))  # exact A' (|A'| < 2^55)
+        p = 0
+        for m, q, x in zip(ms, qs, xm):
+            l, h = pl[p], pl[p + 1]
+            r = l + (16 if x == 1 else q) * h
+            assert np.all((r - Ap) % m == 0), m
+            if x == 2:  # the sparse moves change l + q h by multiples of q^2 = m: back to |r| <= m/2 + 1
+                r = (r + m // 2) % m - m // 2
+            assert np.all(np.abs(r) <= m // 2 + 1), m
+            if x == 1:  # Karatsuba: h = sgn(r) ceil(|r|/16), s = h + l, all within 16
+                assert np.all(h == np.sign(r) * (-(-np.abs(r) // 16))) and np.all(pl[p + 2] == h + l)
+                assert np.abs(pl[p:p + 3]).max() <= 16
+                p += 3
+                continue
+            if x == 0:  # rounded: h = round-half-even(r/q), |l| <= q/2, digits within 16
+                hh = np.rint(r / q).astype(np.int64)
+                assert np.all(h == hh) and np.all(l == r - q * hh) and np.abs(pl[p:p + 2]).max() <= 16
+            else:  # sparse square: the integer restatement, digits in the exact e4m3 integers
+                # r is one of the representatives within m/2 + 1 (both ends exist only for +-(m+1)/2)
+                for v, lv, hv in zip(r.ravel(), l.ravel(), h.ravel()):
+                    cands = [int(v)] + ([int(v) - m] if abs(int(v) - m) <= m // 2 + 1 else [])
+                    assert (int(lv), int(hv)) in [_sparse_split(c, q) for c in cands], (m, v, lv, hv)
+                for d in (l, h):
+                    a_ = np.abs(d)
+                    assert np.all((a_ <= 16) | ((a_ <= 32) & (a_ % 2 == 0)))
+            p += 2
+        assert p == gd.nplanes
+
+
+def test_fp8_reference_hash_from_digit_products(orc):
+    """quick.csv:11 end to end through the digit path: oracle digit planes, the planned product outputs
+    (int64), their CRT terms w_o = coef_o P_o mod m, k_s = sum of the terms of modulus s, the residue
+    k_s y_s^-1 mod m_s, and the reference reconstruction give the reference's output hash."""
+    n, b, nd, A, B, dd, gd, crt, tm, ms, qs, xm = _fp8_quick_plan()
+    shift = b - 20 * (nd - 1)
+    dA, _ = orc.scale(A, n, n, 0, 1, shift)
+    dB, _ = orc.scale(B, n, n, 1, 1, shift)
+    pa = orc.digit_planes(A, n, n, 0, dA, nd, ms, qs, xm)
+    pb = orc.digit_planes(B, n, n, 1, dB, nd, ms, qs, xm)
+    k = [np.zeros((n, n), dtype=np.int64) for _ in ms]
+    for o in range(gd.nout):
+        g = gd.g[o]
+        P = sum(orc.gemm_i8(pa[g.a[t]], pb[g.b[t]])[0].astype(np.int64) for t in range(g.npairs))
+        assert np.abs(P).max() <= g.bound and g.bound + g.m <= 2 ** 24
+        s = tm[o]
+        assert g.modulus == s and g.m == ms[s]
+        k[s] = (k[s] + (g.coef * (P % g.m)) % g.m) % g.m
+    C = np.zeros((len(ms), n, n), dtype=np.int32)
+    for s, m in enumerate(ms):
+        r = (k[s] * pow(int(crt.y[s]), -1, m)) % m
+        C[s] = np.where(r > m // 2, r - m, r)
+    assert orc.hash(orc.crt_ref(C, n, n, ms, b, nd, 0, dA, dB)) == 0x20046E5BB3816CBB

@@ -213,7 +213,7 @@ FP8_PHI = [(0.0, 53, 12), (1.0, 57, 12), (2.0, 59, 12), (4.0, 61, 13)]
 @pytest.mark.parametrize("phi,b,S", [FP8_PHI[i] for i in (0, 3)])
 def test_fp8_auto_precision_records(phi, b, S):
     """The FP8 plan's width b equals the record; its set with the research planner's measured window has the
-    recorded size; the execution set (INT8 moduli) covers the same width."""
+    recorded size; the execution set is the route's FP8 set."""
     n = 4096
     a, bb = oz.eval_inputs(7, phi, n * n, n * n)
     p = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass)
@@ -223,5 +223,4 @@ def test_fp8_auto_precision_records(phi, b, S):
     wlog2 = math.log2(p.wA * p.wB * max(f, 1.001))
     research = oz.choose_moduli_fp8(n, 24, b, wlog2)
     assert research.b == b and research.rS == S
-    lib = oz.choose_moduli_int8(n, 24, b)
-    assert p.S == lib.S and [p.m[i] for i in range(p.S)] == [lib.m[i] for i in range(lib.S)]
+    assert p.S == p.rS and [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
