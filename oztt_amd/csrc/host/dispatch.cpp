@@ -36,10 +36,13 @@ void Workspace::release_all() {
     bufs_.clear();
 }
 
-// Scheme I runs every format (its digits are int8 values); Scheme II runs INT8 and FP8.
+// Every format runs with both schemes. Scheme I runs every format's digits (int8 values) on the INT8
+// matrix cores; Scheme II runs FP8 on the FP8 matrix cores and every other format with INT8 residues
+// (the formats without their own MI355X matrix instructions, and BF16/FP16, whose matrix rate is half
+// the INT8 rate: see plan_scheme2).
 bool scheme_available(Format format, Scheme scheme) noexcept {
     if ((int)format < 0 || (int)format > (int)Format::BFP2) return false;
-    return scheme == Scheme::I || format == Format::INT8 || format == Format::FP8;
+    return scheme == Scheme::I || scheme == Scheme::II;
 }
 
 Backend backend_for(Format format, Scheme scheme) {

@@ -217,8 +217,12 @@ double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st) {
 
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
                    std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b) {
-    if (format != Format::INT8 && format != Format::FP8)
-        throw std::invalid_argument("Ozaki II is built for INT8 and FP8 only");
+    // FP8 plans on the reference's FP8 route (e4m3 digits). Every other format plans on the INT8 route:
+    // on MI355X their digits are int8 values (BFP8, BFP4, BFP2, TF32 have no matrix instructions of
+    // their own; BF16/FP16 run at half the INT8 rate and need about twice the products), and INT8
+    // residues are the cheapest exact int8 transport. The exact reconstruction makes the result a
+    // function of the width b alone, which the INT8 route sets the same way.
+    if ((int)format < 0 || (int)format > (int)Format::BFP2) throw std::invalid_argument("unknown format");
     const bool fp8 = format == Format::FP8;
     Plan2 p;
     p.M = M;

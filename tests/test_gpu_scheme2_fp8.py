@@ -169,3 +169,30 @@ def test_fp8_gemm_rejects_inexact_bound(dev):
     A.free()
     P.free()
     dev.bufs.clear()
+
+
+@pytest.mark.parametrize("fmt", [oz.Format.BFP8, oz.Format.BF16, oz.Format.FP16, oz.Format.TF32, oz.Format.BFP4,
+                                 oz.Format.BFP2])
+def test_other_formats_run_int8_residues(ctx, fmt):
+    """Scheme II with the formats that have no e4m3 route here: INT8 residues at the same width, so the
+    output is bit-identical to Format::INT8; Info reports the requested format."""
+    n = 256
+    a, b = oz.eval_inputs(5, 1.0, n * n, n * n)
+    c = np.empty(n * n)
+    info = ctx.gemm(a, b, c, n, n, n, opts(fmt))
+    ci = np.empty(n * n)
+    ii = ctx.gemm(a, b, ci, n, n, n, opts(oz.Format.INT8))
+    assert info.format == fmt and info.scheme == oz.Scheme.II
+    assert (info.moduli, info.integer_bits, info.reconstruction_passes) == (ii.moduli, ii.integer_bits,
+                                                                              ii.reconstruction_passes)
+    np.testing.assert_array_equal(c.view(np.uint64), ci.view(np.uint64))
+
+
+def test_default_options_run(ctx):
+    """Options{} (Scheme II, BFP8, automatic) works as the reference's default."""
+    n = 128
+    a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
+    c = ctx.multiply(a, b, n, n, n, oz.Options())
+    R = a.reshape(n, n).astype(np.longdouble) @ b.reshape(n, n).astype(np.longdouble)
+    err = float(np.sqrt(np.sum((c.reshape(n, n) - R) ** 2) / np.sum(R ** 2)))
+    assert err <= 8 * np.finfo(float).eps
