@@ -57,11 +57,27 @@ def cpu_baseline(a, b, m: int, n: int, k: int, rows: int) -> dict:
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     rows = min(rows, m)
     t0 = time.perf_counter()
-    orc.dot2(a, b, m, n, k, 0, rows)
+    hi, lo = orc.dot2(a, b, m, n, k, 0, rows)
     dt = time.perf_counter() - t0
     return {"value": round(2.0 * rows * n * k / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port", "sample": f"Dot2 compensated FP64 GEMM (reference_gemm restated in oracle/) on rows "
-                                     f"0..{rows - 1} of C (full N={n}, K={k}), {dt:.2f} s; value = 2*rows*N*K/t"}
+                                     f"0..{rows - 1} of C (full N={n}, K={k}), {dt:.2f} s; value = 2*rows*N*K/t"}, \
+        hi[:rows * n], lo[:rows * n]
+
+
+def effective_bits(c, hi, lo) -> float:
+    """The reference's accuracy measure (evaluation/numerics.hpp:98-127): -log2 ||C - Cref||_F / ||Cref||_F with
+    Cref = hi + lo renormalized, sums scaled by the largest magnitude."""
+    s = hi + lo
+    bb = s - hi
+    rlo = (hi - (s - bb)) + (lo - bb)
+    d = (c - s) - rlo
+    mx = max(float(np.max(np.abs(s))), float(np.max(np.abs(d))))
+    sc = 2.0 ** -np.floor(np.log2(mx)) if mx > 0 and np.isfinite(mx) else 1.0
+    num = float(np.sum((d * sc) ** 2))
+    den = float(np.sum((s * sc) ** 2))
+    rel = np.sqrt(num) / np.sqrt(den) if den > 0 else (np.inf if num > 0 else 0.0)
+    return float(-np.log2(rel)) if rel > 0 and np.isfinite(rel) else (99.0 if rel == 0 else -1.0)
 
 
 def copy_probe(nbytes: int) -> int:
@@ -209,7 +225,13 @@ def main() -> int:
         del c8
     if cpu_rows > 0:
         log(f"CPU baseline: Dot2 on {cpu_rows} rows")
-        out["cpu_baseline"] = cpu_baseline(a, b, m, n, k, cpu_rows)
+        out["cpu_baseline"], hi, lo = cpu_baseline(a, b, m, n, k, cpu_rows)
+        rows = min(cpu_rows, m)
+        # effective bits on the Dot2 slab, next to a native FP64 GEMM (BLAS through numpy) of the same rows
+        native = a.reshape(m, k)[:rows] @ b.reshape(k, n)
+        out["effective_bits"] = {"ozaki": round(effective_bits(c[:rows * n], hi, lo), 3),
+                                 "native_fp64": round(effective_bits(native.ravel(), hi, lo), 3),
+                                 "rows": rows}
     ctx.close()
     print(json.dumps(out), flush=True)
     return 0

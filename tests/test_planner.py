@@ -224,3 +224,27 @@ def test_fp8_auto_precision_records(phi, b, S):
     research = oz.choose_moduli_fp8(n, 24, b, wlog2)
     assert research.b == b and research.rS == S
     assert p.S == p.rS and [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
+
+
+def test_fp8_composition_coefficients_kat():
+    """split.hpp:579: the radix-16 Karatsuba coefficients are (1-B, B^2-B, B) = (-15, 240, 16); squares use
+    (1, q) with HL and LH concatenated. The device terms carry coefficient * y_s mod m_s."""
+    M = N = 64
+    K = 16384
+    a, b = oz.eval_inputs(4, 2.0, M * K, K * N)
+    dd, gd, crt, tm = oz.plan2_fp8_device(a, b, M, N, K, fixed_bits=60)
+    S = dd.mo.S
+    kar = [s for s in range(S) if dd.xmode[s] == 1]
+    sq = [s for s in range(S) if dd.xmode[s] == 0]
+    assert kar and sq
+    for s in range(S):
+        m, y = int(crt.m[s]), int(crt.y[s])
+        outs = [gd.g[o] for o in range(gd.nout) if tm[o] == s]
+        raw = sorted((g.coef * pow(y, -1, m)) % m for g in outs)
+        if s in kar:
+            assert raw == sorted(c % m for c in (-15, 240, 16)), (m, raw)
+            assert all(g.npairs == 1 and g.a[0] - g.b[0] == 0 for g in outs)
+        else:
+            q = int(dd.q[s])
+            assert q * q == m and raw == sorted([1, q % m]), (m, raw)
+            assert sorted(g.npairs for g in outs) == [1, 2]
