@@ -109,25 +109,34 @@ __global__ void __launch_bounds__(256) recon_kernel(const int32_t* __restrict__ 
     if (j >= N) return;
     const int32_t* p = P + (long long)i * ldp + j;
     float hi = 0.0f, mid = 0.0f, lo = 0.0f;
-    for (int d = 0; d < ndiag; d++) {
-        if (d > 0) tf_mul_radix<POW2>(hi, mid, lo, radix);
-        const int32_t v = p[(long long)d * sP];
-        if (!SIGNMAG && d < nsingle) {
-            tf_add_s(hi, mid, lo, (float)v);
-            continue;
+    // batches of 8 diagonals: the 8 loads are in flight together
+    for (int d0 = 0; d0 < ndiag; d0 += 8) {
+        int32_t vb[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) vb[t] = d0 + t < ndiag ? p[(long long)(d0 + t) * sP] : 0;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int d = d0 + t;
+            if (d >= ndiag) break;
+            if (d > 0) tf_mul_radix<POW2>(hi, mid, lo, radix);
+            const int32_t v = vb[t];
+            if (!SIGNMAG && d < nsingle) {
+                tf_add_s(hi, mid, lo, (float)v);
+                continue;
+            }
+            float vh, vl;
+            if constexpr (SIGNMAG) {
+                const uint32_t mag = v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
+                const float sg = v > 0 ? 1.0f : (v < 0 ? -1.0f : 0.0f);
+                vh = (float)(int32_t)(mag & 0x7FFFFF00u) * sg;
+                vl = (float)(int32_t)(mag & 0xFFu) * sg;
+            } else {
+                vh = (float)(int32_t)((uint32_t)v & 0xFFFFFF00u);
+                vl = (float)(int32_t)((uint32_t)v & 0xFFu);
+            }
+            tf_add_s(hi, mid, lo, vh);
+            tf_add_s(hi, mid, lo, vl);
         }
-        float vh, vl;
-        if constexpr (SIGNMAG) {
-            const uint32_t mag = v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
-            const float sg = v > 0 ? 1.0f : (v < 0 ? -1.0f : 0.0f);
-            vh = (float)(int32_t)(mag & 0x7FFFFF00u) * sg;
-            vl = (float)(int32_t)(mag & 0xFFu) * sg;
-        } else {
-            vh = (float)(int32_t)((uint32_t)v & 0xFFFFFF00u);
-            vl = (float)(int32_t)((uint32_t)v & 0xFFu);
-        }
-        tf_add_s(hi, mid, lo, vh);
-        tf_add_s(hi, mid, lo, vl);
     }
     const uint64_t u = assemble_tf_f64(hi, mid, lo, -(dA[i] + dB[j]), W, qw);
     out[(long long)i * ldo + j] = __longlong_as_double((long long)u);

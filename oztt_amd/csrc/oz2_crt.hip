@@ -84,6 +84,13 @@ struct CrtArgs {
     oz2_crt_dev k;
     uint32_t magic[OZ2_MAXS];  // floor(2^32/m)
     uint32_t Mhalf[8];         // floor(M/2)
+    double invM;               // 1 / Mprod (quotient estimate)
+    // Moduli in groups of consecutive moduli whose product mG stays below 2^32 (the digit kernel):
+    // sum_{s in g} k_s Q_s = QG_g * sum_{s in g} k_s w_s with w_s = mG_g / m_s and QG_g = Mprod / mG_g.
+    int G;
+    unsigned char gid[OZ2_MAXS], glast[OZ2_MAXS];  // group of modulus s; s is its group's last
+    uint32_t mG[OZ2_MAXS], w[OZ2_MAXS];
+    uint32_t QG[OZ2_MAXS][8];
 };
 
 // acc = sum_s k_s Q_s (< S*M) -> the symmetric representative of acc mod M, scaled by 2^e2, as FP64.
@@ -93,7 +100,7 @@ __device__ __forceinline__ double crt_finish(uint32_t* acc, const CrtArgs& a, in
     double ahi = 0.0;
 #pragma unroll
     for (int w = NW - 1; w >= 0; w--) ahi = ahi * 4294967296.0 + (double)acc[w];
-    uint32_t q = (uint32_t)__builtin_floor(ahi / a.k.Mtop);
+    uint32_t q = (uint32_t)__builtin_floor(ahi * a.invM);
     {
         uint32_t carry = 0, borrow = 0;
 #pragma unroll
@@ -196,10 +203,34 @@ __global__ void __launch_bounds__(256) crt_digits_kernel(const uint8_t* __restri
     for (int e = 0; e < 4; e++)
 #pragma unroll
         for (int w = 0; w < NW; w++) acc[e][w] = 0;
-    for (int s = 0; s < a.k.S; s++) {
-        const uint32_t v = d[(long long)s * sw];
+    // every plane's word is requested before the first is used (S loads in flight per thread)
+    const int S = a.k.S;
+    uint32_t v[OZ2_MAXS];
 #pragma unroll
-        for (int e = 0; e < 4; e++) crt_add<NW>(acc[e], (v >> (8 * e)) & 0xFFu, a.k.Q[s]);
+    for (int s = 0; s < OZ2_MAXS; s++) v[s] = s < S ? d[(long long)s * sw] : 0u;
+    // per group g: u = sum_{s in g} k_s w_s < count * mG < 2^34, reduced mod mG (at most three
+    // subtractions), then acc += u * QG_g
+    uint64_t u[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < OZ2_MAXS; s++) {
+        if (s < S) {
+            const uint32_t ws = a.w[s];
+#pragma unroll
+            for (int e = 0; e < 4; e++) u[e] += (uint64_t)(((v[s] >> (8 * e)) & 0xFFu) * ws);
+            if (a.glast[s]) {
+                const int g = a.gid[s];
+                const uint64_t mg = a.mG[g];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    uint64_t x = u[e];
+                    x = x >= mg ? x - mg : x;
+                    x = x >= mg ? x - mg : x;
+                    x = x >= mg ? x - mg : x;
+                    crt_add<NW>(acc[e], (uint32_t)x, a.QG[g]);
+                    u[e] = 0;
+                }
+            }
+        }
     }
     const int gi = 2 * a.k.shift - dA[i] - 2 * a.k.b;
 #pragma unroll
@@ -230,13 +261,21 @@ __global__ void __launch_bounds__(256) crt_terms_kernel(const uint16_t* __restri
     for (int e = 0; e < 4; e++)
 #pragma unroll
         for (int q = 0; q < NW; q++) acc[e][q] = 0;
-    for (int o = 0; o < nterms; o++) {
-        const uint2 v = w[(long long)o * sw];
-        const uint32_t* Q = a.k.Q[tmap.mod[o]];
-        crt_add<NW>(acc[0], v.x & 0xFFFFu, Q);
-        crt_add<NW>(acc[1], v.x >> 16, Q);
-        crt_add<NW>(acc[2], v.y & 0xFFFFu, Q);
-        crt_add<NW>(acc[3], v.y >> 16, Q);
+    // batches of 8 terms: the 8 loads are in flight together
+    for (int o0 = 0; o0 < nterms; o0 += 8) {
+        uint2 v[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) v[t] = o0 + t < nterms ? w[(long long)(o0 + t) * sw] : make_uint2(0u, 0u);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            if (o0 + t < nterms) {
+                const uint32_t* Q = a.k.Q[tmap.mod[o0 + t]];
+                crt_add<NW>(acc[0], v[t].x & 0xFFFFu, Q);
+                crt_add<NW>(acc[1], v[t].x >> 16, Q);
+                crt_add<NW>(acc[2], v[t].y & 0xFFFFu, Q);
+                crt_add<NW>(acc[3], v[t].y >> 16, Q);
+            }
+        }
     }
     const int gi = 2 * a.k.shift - dA[i] - 2 * a.k.b;
 #pragma unroll
@@ -279,6 +318,29 @@ int crt_args(oz_dev* dev, const char* name, const oz2_crt_dev* crt, uint32_t mma
         const uint64_t cur = ((uint64_t)r << 32) | crt->Mw[w];
         a.Mhalf[w] = (uint32_t)(cur >> 1);
         r = (uint32_t)(cur & 1u);
+    }
+    a.invM = 1.0 / crt->Mtop;
+    // groups of consecutive moduli with product below 2^32; QG = Mprod / mG by long division
+    a.G = 0;
+    for (int s = 0; s < crt->S;) {
+        uint64_t mg = 1;
+        int n = 0;
+        while (s + n < crt->S && mg * crt->m[s + n] < 0x100000000ull) mg *= crt->m[s + n++];
+        const int g = a.G++;
+        a.mG[g] = (uint32_t)mg;
+        for (int t = 0; t < n; t++) {
+            a.w[s + t] = (uint32_t)(mg / crt->m[s + t]);
+            a.gid[s + t] = (unsigned char)g;
+            a.glast[s + t] = t == n - 1;
+        }
+        uint64_t rem = 0;
+        for (int w = 7; w >= 0; w--) {
+            const uint64_t cur = (rem << 32) | crt->Mw[w];
+            a.QG[g][w] = (uint32_t)(cur / mg);
+            rem = cur % mg;
+        }
+        if (rem) return oz::fail(dev, OZ_ERR_ARG, "%s: Mprod is not the product of the moduli", name);
+        s += n;
     }
     return OZ_OK;
 }
