@@ -67,11 +67,13 @@ CASES = [("uniform", 64, 64, 64), ("nonnegative", 3, 5, 7), ("scaled", 65, 67, 9
          ("largest-maximum", 1, 1, 1), ("uniform", 5056, 64, 32)]
 
 
+@pytest.mark.parametrize("fmt", [oz.Format.INT8, oz.Format.FP8])
 @pytest.mark.parametrize("mode,m,n,k", CASES)
-def test_reference_correctness_cases(ctx, mode, m, n, k):
+def test_reference_correctness_cases(ctx, mode, m, n, k, fmt):
     a, b = pattern(mode, m, n, k)
     c = np.full(m * n, 123.0)
-    info = ctx.gemm(a, b, c, m, n, k, II_INT8)
+    info = ctx.gemm(a, b, c, m, n, k, oz.Options(scheme=oz.Scheme.II, format=fmt))
+    assert info.format == fmt
     assert np.all(np.isfinite(c))
     err = ref_error(a, b, c, m, n, k)
     assert err <= 8 * EPS, (mode, err)

@@ -248,3 +248,16 @@ def test_fp8_composition_coefficients_kat():
             q = int(dd.q[s])
             assert q * q == m and raw == sorted([1, q % m]), (m, raw)
             assert sorted(g.npairs for g in outs) == [1, 2]
+
+
+def test_fp8_rejects_k_beyond_exact_fp32():
+    """moduli.hpp:472-500: K * 16^2 must stay within the exact FP32 integers; beyond, the plan fails with
+    runtime_error naming the limit (no device work)."""
+    M = N = 64
+    K = 65600
+    a = np.ones(M * K)
+    b = np.ones(K * N)
+    with pytest.raises(RuntimeError, match="too large for this format"):
+        oz.plan2(a, b, M, N, K, oz.Format.FP8, fixed_bits=54)
+    p = oz.plan2(a, b, M, N, K, oz.Format.INT8, fixed_bits=54)  # INT8 residues carry this K
+    assert p.ok and p.b == 54
