@@ -289,6 +289,24 @@ def eval_hash(c) -> int:
     return int(host().ozt_eval_hash(_ptr(c), ctypes.c_size_t(c.size)))
 
 
+def eval_reference_gemm(a, b, M: int, K: int, N: int, r0: int = 0, r1: int | None = None):
+    """Dot2 reference GEMM of the evaluator (numerics.hpp:58-93) for rows [r0, r1): (hi, lo), each (r1-r0)*N."""
+    a, b = _f64(a), _f64(b)
+    r1 = M if r1 is None else min(r1, M)
+    hi = np.empty((r1 - r0) * N)
+    lo = np.empty((r1 - r0) * N)
+    host().ozt_eval_reference_gemm(_ptr(a), _ptr(b), M, K, N, r0, r1, _ptr(hi), _ptr(lo))
+    return hi, lo
+
+
+def eval_accuracy(c, hi, lo):
+    """(relative Frobenius error, effective bits) of C against the Dot2 reference (numerics.hpp:98-127)."""
+    c, hi, lo = _f64(c), _f64(hi), _f64(lo)
+    rel, eb = ctypes.c_double(), ctypes.c_double()
+    host().ozt_eval_accuracy(_ptr(c), _ptr(hi), _ptr(lo), ctypes.c_size_t(c.size), ctypes.byref(rel), ctypes.byref(eb))
+    return rel.value, eb.value
+
+
 def eval_quad_sample(a, b, M: int, N: int, K: int, rows, cols) -> np.ndarray:
     a, b = _f64(a), _f64(b)
     rows = np.ascontiguousarray(rows, dtype=np.int32)

@@ -276,6 +276,16 @@ void ozt_eval_inputs(unsigned seed, double phi, std::size_t na, std::size_t nb, 
     ozTTgemm::evaluation::inputs(seed, phi, na, nb, a, b);
 }
 unsigned long long ozt_eval_hash(const double* c, std::size_t n) { return ozTTgemm::evaluation::output_hash(c, n); }
+void ozt_eval_reference_gemm(const double* A, const double* B, unsigned M, unsigned K, unsigned N, unsigned r0,
+                             unsigned r1, double* Chi, double* Clo) {
+    ozTTgemm::evaluation::reference_gemm(A, B, M, K, N, r0, r1, Chi, Clo);
+}
+void ozt_eval_accuracy(const double* C, const double* Chi, const double* Clo, std::size_t n, double* rel_fro,
+                       double* ebits) {
+    const auto a = ozTTgemm::evaluation::accuracy(C, Chi, Clo, n);
+    *rel_fro = a.rel_fro;
+    *ebits = a.ebits;
+}
 void ozt_eval_quad_sample(const double* A, const double* B, int M, int N, int K, int nsample, const int* rows,
                           const int* cols, double* out) {
     ozTTgemm::evaluation::gemm_quad_sample(A, B, M, N, K, nsample, rows, cols, out);

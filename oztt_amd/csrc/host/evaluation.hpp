@@ -53,6 +53,16 @@ Settings* active() noexcept;
 void inputs(unsigned seed, double phi, std::size_t na, std::size_t nb, double* a, double* b);
 // FNV-style hash of the bit patterns (numerics.hpp:46-57).
 std::uint64_t output_hash(const double* c, std::size_t n);
+// The Dot2 reference GEMM (numerics.hpp:58-93) for rows [r0, r1) of C = A B (A: M x K, B: K x N,
+// row-major): head and tail of each compensated dot product, Chi/Clo hold (r1 - r0) x N.
+void reference_gemm(const double* A, const double* B, std::uint32_t M, std::uint32_t K, std::uint32_t N,
+                    std::uint32_t r0, std::uint32_t r1, double* Chi, double* Clo);
+// Relative Frobenius error of C against the Dot2 reference and effective bits -log2 of it
+// (numerics.hpp:98-127).
+struct Accuracy {
+    double rel_fro = 0, ebits = 0;
+};
+Accuracy accuracy(const double* C, const double* Chi, const double* Clo, std::size_t n);
 // Binary128 products for sampled output elements (rows[t], cols[t]).
 void gemm_quad_sample(const double* A, const double* B, int M, int N, int K, int nsample, const int* rows,
                       const int* cols, double* out);
