@@ -239,7 +239,13 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
     }
     // limit on the number of moduli (plan.hpp:281): the caller's, else the route's default with a fixed
     // width (16 for INT8, 14 for FP8; split.hpp:73-76), else 24
-    p.S_req = max_moduli ? max_moduli : (b_fixed ? (fp8 ? 14u : 16u) : (std::uint32_t)kMaxModuli);
+    // For the formats carried by INT8 residues, a moduli limit counts the moduli of the format's own route
+    // (residues of up to 12 bits there, 8 here): the INT8 set takes as many as the width needs (<= 24).
+    const bool transported = !fp8 && format != Format::INT8;
+    if (transported)
+        p.S_req = (std::uint32_t)kMaxModuli;
+    else
+        p.S_req = max_moduli ? max_moduli : (b_fixed ? (fp8 ? 14u : 16u) : (std::uint32_t)kMaxModuli);
     if (b_fixed && passes == Reconstruction::Automatic) p.stats = measure_stats(A, B, M, N, K);
     p.route = fp8 ? choose_moduli_fp8(K, (int)p.S_req, b_cap) : choose_moduli_int8(K, (int)p.S_req, b_cap);
     const ModuliSet& r = p.route;
