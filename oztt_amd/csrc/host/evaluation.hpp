@@ -3,7 +3,8 @@
 //
 // Counterpart of the reference's evaluation_hooks.hpp:29-219 and evaluation/numerics.hpp. While a
 // Scope is active on the calling thread, a backend
-//   - times each phase (scale, slice, gemm, compose, recon) with HIP events on its stream,
+//   - times each phase (scale, slice, gemm, compose, recon) with HIP events around every device
+//     step on its stream (in warm passes after the replays, when there are replays),
 //   - records every device step of the call and afterwards replays the whole pass `warmup` times
 //     untimed and `repeats` times between two events (inputs and intermediates resident in HBM,
 //     no host work inside), checks that the replayed output is bit-identical to the first pass,
@@ -26,7 +27,8 @@ struct Settings {
     int warmup = 0;           // untimed whole-pass replays
     int repeats = 0;          // timed whole-pass replays (0: no replay)
     // outputs
-    double phase_ms[PhaseCount] = {};  // device time of each phase in the first pass
+    double phase_ms[PhaseCount] = {};  // device time of each phase: the average of up to 5 warm passes
+                                       // after the replays (the first pass when there are none)
     double whole_ms = 0;               // average time of one replayed whole pass
     bool whole_checked = false;        // replayed output bit-identical to the first pass
     unsigned partial_products = 0;     // low-precision matrix products per call (S or slice pairs)

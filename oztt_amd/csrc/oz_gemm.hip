@@ -10,18 +10,24 @@
 //     rows x 64 K-bytes, the K/64 blocks of each 16-row band consecutive, zero-padded to the tile
 //     grid, so no load is guarded. Inside a block, 16-byte chunk c of row r sits at chunk position
 //     c ^ f(r), f(r) = ((r >> 1) ^ (r >> 2)) & 3.
-//   - A workgroup of 4 waves (one per SIMD) computes a 256 x 256 tile; each wave owns 128 x 128
-//     (4 x 4 blocks of v_mfma_i32_32x32x32_i8, 256 accumulator registers). A single wave keeps the
-//     32x32x32 MFMA pipe close to full, unlike the 16x16x64 form (measured on MI355X). Lane l holds
-//     row l%32 and the 16 K-bytes 16*(l/32).. of a 32-byte K slice of both operands; output register
-//     q of lane l is row 8*(q/4) + 4*(l/32) + q%4, column l%32.
-//   - K advances in 64-byte steps through a ring of NS LDS stages filled by direct global->LDS
-//     loads (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS base + 16*l),
-//     NS-1 stages ahead of the MFMAs, with no register staging. One wave instruction copies one
-//     whole 1 KB block, contiguous in HBM and in LDS, so a stage's 256 rows are 16 blocks per
-//     operand and the swizzle comes with the data: the 64 lanes of each fragment read
-//     (ds_read_b128, rows r..r+31, two chunk columns) spread evenly over the LDS banks.
-//   - Workgroups are mapped to tiles XCD-aware (tile_of below).
+//   - A workgroup of 4 waves (one per SIMD) computes a 256 x 256 tile; each wave owns 128 x 128 as
+//     8 x 8 blocks of v_mfma_i32_16x16x64_i8 (256 accumulator registers). One MFMA operand is one
+//     whole OZ_BLOCK: lane l holds row l%16 and K-bytes 16*(l/16)..+15 of both operands (A and B use
+//     the same lane -> K map, so the sum runs over every K index once whatever order the matrix core
+//     takes them in); output register q of lane l is row 4*(l/16) + q, column l%16. The 64 lanes of a
+//     fragment read (ds_read_b128) cover one 1 KB block, so they fall on every LDS bank equally.
+//     On MI355X the 16x16x64 form runs the same products at a higher clock under the power limit
+//     than 32x32x32 (measured with random residues, which is what the matrix cores see).
+//   - K advances in 64-byte steps through a ring of NS = 4 LDS stages (32 KB each) filled by direct
+//     global->LDS loads (lds_copy_block: one wave instruction copies one block, contiguous in HBM and
+//     in LDS, the swizzle included), NS-1 stages ahead of the MFMAs, with no register staging. The
+//     load addresses are wave-uniform SGPR pairs plus one per-lane offset register.
+//   - Each K step is one barrier and 64 MFMAs per wave; the 16 fragment reads of the next step (one
+//     per 4 MFMAs) and the 8 loads that refill the ring (one per 8 MFMAs) are spread over them in a
+//     fixed order (sched_barrier fences; left alone, the compiler bunches them).
+//   - Workgroups are mapped to tiles so that all XCDs sweep the moduli in step (tile_of_lockstep):
+//     the operands in flight then stay in the Infinity Cache, which keeps HBM traffic, and with it
+//     power, down; the matrix cores are power-limited, so that raises their clock.
 #include "oz2_modular.hpp"
 #include "oz_gemm_common.hpp"
 #include "oz_internal.hpp"
@@ -36,161 +42,213 @@ using namespace ozg;
 // slice pairs concatenated along K in one accumulation.
 enum GemmMode { PRODUCTS = 0, DIGITS = 1, DIAG = 2 };
 
-template <int MODE>
+constexpr int LOADS = LOADS_A + LOADS_B;  // global->LDS loads per wave per K step
+
+template <int MODE, bool EVEN>
 __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ Bt,
                                                           void* __restrict__ C, int K, int ldc, long long sA,
                                                           long long sB, long long sC, int tiles_m, int tiles_n,
                                                           int nbatch, oz2::DigitConsts dc) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * STAGE];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int batch, tm, tn;
-    if constexpr (MODE == DIAG) {
-        // Diagonal d has d+1 pairs: the heaviest go first (workgroups start in index order), and
-        // within a diagonal the XCD-aware order applies.
-        const int per = tiles_m * tiles_n, b = blockIdx.x / per;
-        int unused;
-        tile_of(blockIdx.x - b * per, tiles_m, tiles_n, 1, unused, tm, tn);
-        batch = nbatch - 1 - b;
-    } else {
-        tile_of(blockIdx.x, tiles_m, tiles_n, nbatch, batch, tm, tn);
-    }
-    const int nk = K / BK;  // blocks per 16-row band
-    const int nsteps = MODE == DIAG ? (batch + 1) * nk : nk;  // K steps of this tile
-    const long long band = (long long)nk * 1024;  // bytes of one 16-row band
-    // Lane l copies bytes 16l..16l+15 of each block; the tile's first band is 16*tm (A), 16*tn (B).
-    const int8_t* Ab = A + (MODE == DIAG ? 0 : batch * sA) + (long long)tm * (BM / 16) * band + 16 * lane;
-    const int8_t* Bb = Bt + (MODE == DIAG ? 0 : batch * sB) + (long long)tn * (BN / 16) * band + 16 * lane;
-    // Byte offsets of K step u: block u of the bands, or for DIAG block u%nk of pair i = u/nk
-    // (A plane i, B plane batch-i).
-    auto step_off = [&](int u, long long& oa, long long& ob) {
+    tile_of_lockstep(blockIdx.x, tiles_m, tiles_n, nbatch, batch, tm, tn);
+    // Scheme I: diagonal d has d+1 pairs; the heaviest are dispatched first.
+    if constexpr (MODE == DIAG) batch = nbatch - 1 - batch;
+    // The map divides with VALU code; its results are wave-uniform, so they are moved to SGPRs
+    // (left in VGPRs, every address derived from them is too, and the register allocator then
+    // shuffles accumulators between AGPRs and VGPRs inside the main loop).
+    batch = __builtin_amdgcn_readfirstlane(batch);
+    tm = __builtin_amdgcn_readfirstlane(tm);
+    tn = __builtin_amdgcn_readfirstlane(tn);
+    const int nk = K / BK;                                 // blocks per 16-row band
+    const int nst = MODE == DIAG ? (batch + 1) * nk : nk;  // K steps of this tile
+    const long long band = (long long)nk * 1024;           // bytes of one 16-row band
+    const int8_t* Ab = A + (MODE == DIAG ? 0 : batch * sA) + (long long)tm * 16 * band;
+    const int8_t* Bb = Bt + (MODE == DIAG ? 0 : batch * sB) + (long long)tn * 16 * band;
+    const unsigned lane16 = 16u * lane;
+    // DIAG: the K step being loaded is block lk of the bands of pair li (A plane li, B plane
+    // batch-li), at byte offsets oA = li sA + 1024 lk and oB = (batch-li) sB + 1024 lk from the tile's
+    // bands; lcount counts the steps loaded so far and stops at the last one (past the end the last
+    // step is loaded again, so every step issues the same number of loads and the wait counts never
+    // change). Running counters and offsets instead of st / nk and products: integer division runs
+    // on the VALU, and all of this must stay on the SALU. The other modes load block
+    // st = min(step, nst - 1) directly.
+    int lk = 0, lcount = 0;
+    long long oA = 0, oB = MODE == DIAG ? batch * sB : 0;
+    auto next_stage = [&]() {  // branch-free: selects only
         if constexpr (MODE == DIAG) {
-            const int i = u / nk, kt = u - i * nk;
-            oa = i * sA + (long long)kt * 1024;
-            ob = (batch - i) * sB + (long long)kt * 1024;
-        } else {
-            oa = ob = (long long)u * 1024;
+            const int adv = lcount < nst - 1;
+            lcount += adv;
+            lk += adv;
+            oA += adv ? 1024 : 0;
+            oB += adv ? 1024 : 0;
+            const int wrap = lk == nk;
+            lk = wrap ? 0 : lk;
+            oA += wrap ? sA - band : 0;
+            oB -= wrap ? sB + band : 0;
         }
     };
-
-    // Loader: wave instruction j (= 4*i + wave) copies block (band j of the tile, K step kstep) to
-    // bytes 1024j.. of the stage, i.e. rows 16j..16j+15 of the 256 x 64 stage, swizzle included.
-#define OZ_GEMM_ISSUE(kstep, buf)                                                                                 \
-    do {                                                                                                          \
-        long long oa, ob;                                                                                         \
-        step_off(kstep, oa, ob);                                                                                  \
-        int8_t* sa = lds + (buf) * STAGE;                                                                         \
-        _Pragma("unroll") for (int i = 0; i < LOADS_A; i++)                                                       \
-            __builtin_amdgcn_global_load_lds(Ab + (4 * i + wave) * band + oa, (lds_void*)(sa + 1024 * (4 * i + wave)), \
-                                             16, 0, 0);                                                           \
-        _Pragma("unroll") for (int i = 0; i < LOADS_B; i++)                                                       \
-            __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + ob,                                     \
-                                             (lds_void*)(sa + STAGE_A + 1024 * (4 * i + wave)), 16, 0, 0);        \
-    } while (0)
-
+    // Load j (0..3) of this wave for A (issue) or B (issueB) of K step st: the block of band
+    // q = 4*j + wave, rows 16q.. of the 256 x 64 stage, to byte 1024 q of the operand's half of
+    // stage buffer buf. (The expressions are written with bnd = q & 15 and kb = q >> 4, kb being 0:
+    // in this form the compiler keeps the address arithmetic in the loop on the SALU;
+    // tests/test_gemm_asm.py checks the generated main loops.)
+    auto issue = [&](int buf, int j, int st) {
+        const int q = 4 * j + wave, bnd = q & 15, kb = q >> 4;
+        long long go;
+        if constexpr (MODE == DIAG)
+            go = (long long)bnd * band + oA + (long long)kb * 1024;
+        else
+            go = (long long)bnd * band + (long long)(st + kb) * 1024;
+        lds_copy_block(Ab + go, lds + buf * STAGE + (kb * 16 + bnd) * 1024, lane16);
+    };
+    auto issueB = [&](int buf, int j, int st) {
+        const int q = 4 * j + wave, bnd = q & 15, kb = q >> 4;
+        long long go;
+        if constexpr (MODE == DIAG)
+            go = (long long)bnd * band + oB + (long long)kb * 1024;
+        else
+            go = (long long)bnd * band + (long long)(st + kb) * 1024;
+        lds_copy_block(Bb + go, lds + buf * STAGE + STAGE_A + (kb * 16 + bnd) * 1024, lane16);
+    };
     const int wm = wave >> 1, wn = wave & 1;
-    int offA[2], offB[2];
-    fragment_offsets(lane, wm, wn, offA, offB);
+    // Fragment reads: lane l takes the 16 bytes of row r = l%16, logical chunk c = l/16 of a block,
+    // stored at byte 64 r + 16 (c ^ f(r)).
+    const int r = lane & 15, c = lane >> 4;
+    const int foff = 64 * r + 16 * (c ^ (((r >> 1) ^ (r >> 2)) & 3));
+    v4i acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
-    v16i acc[4][4];
+    // Prologue: stages 0..NS-1 in flight, then the fragments of stage 0.
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int s = 0; s < NS; s++) {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int q = 0; q < 16; q++) acc[i][j][q] = 0;
-
-    // Pipeline. Loads run NS stages ahead: while stage kt is consumed, stages kt+1 .. kt+NS-1 are in
-    // flight or landed. Fragments are double-buffered per 32-byte K substep (F, G: 8 fragments of
-    // 4 registers each): substep (kt, 0) reads G = substep (kt, 1) while its MFMAs run on F;
-    // substep (kt, 1) waits for stage kt+1, makes sure every wave has finished reading stage kt
-    // (own LDS reads complete, then the barrier), refills that buffer with stage kt+NS, and reads
-    // F = substep (kt+1, 0) while its MFMAs run on G. The tail re-loads the last valid stage
-    // (clamped), so every step has the same number of loads in flight and the same wait count.
-#pragma unroll
-    for (int s = 0; s < NS; s++) OZ_GEMM_ISSUE(min(s, nsteps - 1), s);
-    v4i fa[4], fb[4], ga[4], gb[4];
-    wait_vmcnt<(LOADS_A + LOADS_B) * (NS - 1)>();  // stage 0
-    stage_barrier();
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        fa[i] = *reinterpret_cast<const v4i*>(lds + offA[0] + i * 32 * BK);
-        fb[i] = *reinterpret_cast<const v4i*>(lds + offB[0] + i * 32 * BK);
-    }
-    // The issue order inside a step is fixed with sched_barrier fences (left alone, the compiler
-    // sinks every fragment read to just before its first use, which stalls the MFMAs on LDS
-    // latency): the 8 fragment reads of the other buffer, and after the barrier the 8 global->LDS
-    // loads, go one per MFMA over the first 8 of the 16 MFMAs of each substep.
-    for (int kt = 0; kt < nsteps; kt++) {
-        const int8_t* cur = lds + (kt % NS) * STAGE;
-        const int8_t* nxt = lds + ((kt + 1) % NS) * STAGE;
-        // substep (kt, 0): MFMAs on F, reads of G = substep (kt, 1)
-#pragma unroll
-        for (int g = 0; g < 16; g++) {
-            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[g >> 2], fb[g & 3], acc[g >> 2][g & 3], 0, 0, 0);
-            if (g < 4) ga[g] = *reinterpret_cast<const v4i*>(cur + offA[1] + g * 32 * BK);
-            else if (g < 8) gb[g - 4] = *reinterpret_cast<const v4i*>(cur + offB[1] + (g - 4) * 32 * BK);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < LOADS_A; j++) {
+            issue(s, j, min(s, nst - 1));
+            issueB(s, j, min(s, nst - 1));
         }
-        wait_vmcnt_lgkm0<(LOADS_A + LOADS_B) * (NS - 2)>();  // stage kt+1 landed; own reads of stage kt done
-        stage_barrier();                                      // ... for every wave
-        // substep (kt, 1): MFMAs on G, refill of stage kt's buffer, reads of F = substep (kt+1, 0)
-        long long oa, ob;
-        step_off(min(kt + NS, nsteps - 1), oa, ob);
-        int8_t* sa = lds + (kt % NS) * STAGE;
+        next_stage();
+    }
+    v4i fa[8], fb[8], ga[8], gb[8];
+    wait_vmcnt<LOADS * (NS - 1)>();
+    stage_barrier();
+    // fragment blk (0..7) of the wave's A rows (op 0) or B rows (op 1) in stage buffer buf
+    auto rd = [&](int buf, int op, int blk) -> v4i {
+        const int bnd = (op ? wn : wm) * 8 + blk;
+        return *reinterpret_cast<const v4i*>(lds + buf * STAGE + op * STAGE_A + bnd * 1024 + foff);
+    };
 #pragma unroll
-        for (int g = 0; g < 16; g++) {
-            acc[g >> 2][g & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ga[g >> 2], gb[g & 3], acc[g >> 2][g & 3], 0, 0, 0);
-            if (g < 4) {
-                __builtin_amdgcn_global_load_lds(Ab + (4 * g + wave) * band + oa, (lds_void*)(sa + 1024 * (4 * g + wave)),
-                                                 16, 0, 0);
-                fa[g] = *reinterpret_cast<const v4i*>(nxt + offA[0] + g * 32 * BK);
-            } else if (g < 8) {
-                const int i = g - 4;
-                __builtin_amdgcn_global_load_lds(Bb + (4 * i + wave) * band + ob,
-                                                 (lds_void*)(sa + STAGE_A + 1024 * (4 * i + wave)), 16, 0, 0);
-                fb[i] = *reinterpret_cast<const v4i*>(nxt + offB[0] + i * 32 * BK);
+    for (int i = 0; i < 8; i++) {
+        fa[i] = rd(0, 0, i);
+        fb[i] = rd(0, 1, i);
+    }
+
+    // One K step: 64 MFMAs on (xa, xb); the 16 reads of (ya, yb) from stage buffer rbuf, one per 4
+    // MFMAs in the order a0, b0..b7, a1..a7 (the first MFMAs of the next step need a0 and the b's);
+    // the 8 loads of the next stage to load into buffer lbuf, one per 8 MFMAs.
+    auto substep = [&](v4i* xa, v4i* xb, v4i* ya, v4i* yb, int rbuf, int lbuf, int lst) {
+#pragma unroll
+        for (int g = 0; g < 64; g++) {
+            const int i = g >> 3, j = g & 7;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i], xb[j], acc[i][j], 0, 0, 0);
+            if (g % 4 == 0) {
+                const int t = g / 4;
+                if (t == 0) ya[0] = rd(rbuf, 0, 0);
+                else if (t <= 8) yb[t - 1] = rd(rbuf, 1, t - 1);
+                else ya[t - 8] = rd(rbuf, 0, t - 8);
+            }
+            if (g % 8 == 6) {
+                const int t = g / 8;
+                if (t & 1) issueB(lbuf, t >> 1, lst);
+                else issue(lbuf, t >> 1, lst);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    // K step kt: wait until stage kt+1 has landed and this wave's reads of stage kt (into X) are
+    // complete, then the barrier: every wave is done with stage kt's buffer, which is refilled with
+    // stage kt+NS while the MFMAs run on X and Y reads stage kt+1. Two steps per trip (X and Y swap
+    // roles). EVEN kernels (an even number of K steps in every tile: K/64 even) have no tail; the
+    // others end an odd count with one more step.
+    int kt = 0;
+    for (; kt + 1 < nst; kt += 2) {
+        wait_vmcnt_lgkm0<LOADS * (NS - 2)>();
+        stage_barrier();
+        substep(fa, fb, ga, gb, (kt + 1) % NS, kt % NS, min(kt + NS, nst - 1));
+        next_stage();
+        wait_vmcnt_lgkm0<LOADS * (NS - 2)>();
+        stage_barrier();
+        substep(ga, gb, fa, fb, (kt + 2) % NS, (kt + 1) % NS, min(kt + 1 + NS, nst - 1));
+        next_stage();
     }
-#undef OZ_GEMM_ISSUE
+    if constexpr (!EVEN) {
+        if (kt < nst) {
+            wait_vmcnt_lgkm0<LOADS * (NS - 2)>();
+            stage_barrier();
+            substep(fa, fb, ga, gb, (kt + 1) % NS, kt % NS, min(kt + NS, nst - 1));
+        }
+    }
     wait_vmcnt<0>();  // drain the clamped tail loads before the workgroup ends
 
     const long long c0 = batch * sC + (long long)(tm * BM + wm * 128) * ldc + tn * BN + wn * 128;
     if constexpr (MODE == DIGITS) {
-        // Digits go through LDS (the stages are free once every wave has left the main loop) so
-        // that each lane stores 16 contiguous bytes: the wave's 128 x 128 byte tile is written
-        // with row stride 144 (rows r and r+4, written by the two lane halves, then fall on
-        // different banks) and read back as 16-byte chunks, 8 per row.
-        constexpr int TS = 144;
-        static_assert(4 * 128 * TS <= NS * STAGE, "epilogue tiles fit in the stage ring");
+        // The int32 sums go through LDS and the digits are computed there, so the accumulators are
+        // only ever stored (as in the int32 modes, which keeps them in AGPRs through the main loop;
+        // VALU arithmetic on them makes the register allocator move them into VGPRs inside it).
+        // Each wave owns 32 KB of the (now free) stage ring and writes its 128 x 128 sums in two
+        // rounds of 64 rows, row-major with 16-int column groups swizzled by bits 2..3 of the row
+        // (the four 16-lane groups of a write then cover all banks); every lane then reads 16
+        // consecutive sums, reduces them to digits and stores them as one 16-byte chunk.
         __syncthreads();
-        uint8_t* tile = reinterpret_cast<uint8_t*>(lds) + wave * (128 * TS);
-        const uint32_t m = dc.m[batch], y = dc.y[batch], mg = dc.magic[batch];
+        int32_t* tile = reinterpret_cast<int32_t*>(lds) + wave * (64 * 128);
+        uint32_t m = 0, y = 0, mg = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int q = 0; q < 16; q++)
-                    tile[(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * TS + 32 * j + (lane & 31)] =
-                        (uint8_t)oz2::crt_digit(acc[i][j][q], m, y, mg);
+        for (int s = 0; s < OZ2_MAXS; s++)
+            if (s == batch) {
+                m = dc.m[s];
+                y = dc.y[s];
+                mg = dc.magic[s];
+            }
         uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
 #pragma unroll
-        for (int t = 0; t < 16; t++) {
-            const int c = 64 * t + lane, r = c >> 3, x = 16 * (c & 7);
-            *reinterpret_cast<uint4*>(Cb + (long long)r * ldc + x) = *reinterpret_cast<const uint4*>(tile + r * TS + x);
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int row = 16 * i + 4 * (lane >> 4) + q;  // (row >> 2) & 3 == lane >> 4
+                        tile[row * 128 + ((16 * j) ^ (16 * (lane >> 4))) + (lane & 15)] = acc[4 * h + i][j][q];
+                    }
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int e = 64 * t + lane, row = e >> 3, cg = e & 7;
+                const int* src = tile + row * 128 + ((16 * cg) ^ (16 * ((row >> 2) & 3)));
+                uint32_t w[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const v4i v = *reinterpret_cast<const v4i*>(src + 4 * k);
+                    w[k] = oz2::crt_digit(v[0], m, y, mg) | oz2::crt_digit(v[1], m, y, mg) << 8 |
+                           oz2::crt_digit(v[2], m, y, mg) << 16 | oz2::crt_digit(v[3], m, y, mg) << 24;
+                }
+                *reinterpret_cast<uint4*>(Cb + (long long)(64 * h + row) * ldc + 16 * cg) = uint4{w[0], w[1], w[2], w[3]};
+            }
         }
     } else {
         int32_t* Cb = static_cast<int32_t*>(C) + c0;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 8; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
+            for (int j = 0; j < 8; j++)
 #pragma unroll
-                for (int q = 0; q < 16; q++)
-                    Cb[(long long)(32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * ldc + 32 * j + (lane & 31)] =
-                        acc[i][j][q];
+                for (int q = 0; q < 4; q++)
+                    Cb[(long long)(16 * i + 4 * (lane >> 4) + q) * ldc + 16 * j + (lane & 15)] = acc[i][j][q];
     }
 }
 
@@ -210,8 +268,13 @@ int launch_gemm(oz_dev* dev, const int8_t* A, const int8_t* Bt, void* C, int M, 
                 long long strideA, long long strideB, long long strideC, const oz2::DigitConsts& dc) {
     const int tiles_m = M / BM, tiles_n = N / BN;
     const unsigned grid = (unsigned)((long long)tiles_m * tiles_n * batch);
-    hipLaunchKernelGGL(gemm_i8_kernel<MODE>, dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc, strideA,
-                       strideB, strideC, tiles_m, tiles_n, batch, dc);
+    // K/64 even: every tile has an even number of K steps (DIAG: (d+1) K/64), no tail step
+    if ((K / BK) % 2 == 0)
+        hipLaunchKernelGGL((gemm_i8_kernel<MODE, true>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
+                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc);
+    else
+        hipLaunchKernelGGL((gemm_i8_kernel<MODE, false>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
+                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc);
     return oz::launch_check(dev, "gemm_i8_kernel");
 }
 

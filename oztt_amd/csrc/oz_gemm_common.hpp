@@ -35,6 +35,45 @@ __device__ __forceinline__ void tile_of(int w, int tiles_m, int tiles_n, int nba
     tn = v / gm;
 }
 
+// Workgroup -> (batch, tile row, tile column) with every XCD on the same batch at the same time.
+// When the tile count P of a batch is a multiple of 8, batch b's tiles, in the grouped order of
+// tile_of, are cut into 8 contiguous chunks of q = P/8 and XCD x takes chunk x: its j-th workgroup
+// (w = 8j + x) gets tile j % q of its chunk of batch j / q. The XCDs then sweep the batches in
+// step, so the operands in flight are those of one or two batches (at C3 size 2 x 64 MiB of int8
+// planes per batch), which the 256 MB Infinity Cache holds; with tile_of's ranges the 8 XCDs would
+// run 8 different batches and their L2 misses would go to HBM. Within a chunk the ~32 workgroups
+// an XCD runs at a time still cover a compact GROUP_M x 8 block of tiles. Otherwise (P % 8 != 0)
+// this is tile_of. A bijection for any workgroup count of P * nbatch.
+__device__ __forceinline__ void tile_of_lockstep(int w, int tiles_m, int tiles_n, int nbatch, int& batch, int& tm,
+                                                 int& tn) {
+    const int P = tiles_m * tiles_n;
+    if (P % XCDS) {
+        tile_of(w, tiles_m, tiles_n, nbatch, batch, tm, tn);
+        return;
+    }
+    const int q = P / XCDS, x = w % XCDS, j = w / XCDS;
+    batch = j / q;
+    const int u = x * q + (j - batch * q);
+    const int group = u / (GROUP_M * tiles_n);
+    const int first_m = group * GROUP_M;
+    const int gm = min(tiles_m - first_m, GROUP_M);
+    const int v = u % (GROUP_M * tiles_n);
+    tm = first_m + v % gm;
+    tn = v / gm;
+}
+
+// Direct copy of one 1 KB block from global memory to LDS: lane l reads the 16 bytes at
+// gbase + voff(l) and they land at LDS byte lbase + 16 l (global_load_lds_dwordx4). gbase and
+// lbase are wave-uniform, so the address stays in SGPRs (one per-lane offset register serves every
+// load). M0 carries the LDS base; the compiled kernels use M0 for nothing else, which
+// tests/test_gemm_asm.py checks on the generated code. The load is counted by vmcnt like any
+// other vector memory load; its consumers wait with wait_vmcnt.
+__device__ __forceinline__ void lds_copy_block(const void* gbase, void* lbase, unsigned voff) {
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const unsigned l = (unsigned)(uintptr_t)(lds_u8*)lbase;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(gbase) : "memory");
+}
+
 // Workgroup barrier without the memory fences of __syncthreads(): those would wait for every
 // outstanding load, including the direct-to-LDS loads of the stages still in flight. Each wave
 // first waits (vmcnt) for its own loads of the stage about to be read, so after the barrier the

@@ -1,0 +1,88 @@
+"""Checks on the gfx950 code generated for the int8 product kernels (oztt_amd/csrc/oz_gemm.hip).
+
+The kernels load operands with an inline-asm global->LDS copy (ozg::lds_copy_block) that sets M0
+itself, so the compiler must not use M0 for anything else in them; and their throughput depends on
+the main loop keeping the 256 accumulators in AGPRs and the fragments in VGPRs (when the register
+allocator mixes the two classes it adds v_accvgpr moves to every K step, or spills). Both are
+properties of the compiled code, so this test compiles the source with the build's flags and reads
+the assembly. It needs hipcc (present wherever the library is built) but no GPU.
+"""
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from oztt_amd import build as B
+
+
+def _kernels(asm: str) -> dict[str, list[str]]:
+    """Function name -> body lines (label to end marker) for every gemm_i8_kernel in the listing."""
+    out = {}
+    for m in re.finditer(r"^(_Z\S*gemm_i8_kernel\S*):.*?$(.*?)^\.Lfunc_end", asm, re.S | re.M):
+        out[m.group(1)] = m.group(2).split("\n")
+    return out
+
+
+def _main_loop(lines: list[str]) -> list[str]:
+    """Instructions of the innermost loop that contains the MFMAs (header to its last back-branch)."""
+    best = []
+    for i, l in enumerate(lines):
+        h = re.match(r"(\.LBB\d+_\d+):.*Loop Header", l)
+        if not h:
+            continue
+        ends = [k for k in range(i + 1, len(lines)) if re.search(r"s_c?branch\w*\s+" + re.escape(h.group(1)) + r"\b", lines[k])]
+        body = [x.strip() for x in lines[i:max(ends) + 1]] if ends else []
+        if sum(x.startswith("v_mfma") for x in body) > sum(x.startswith("v_mfma") for x in best):
+            best = body
+    return [x for x in best if x and not x.startswith(";")]
+
+
+@pytest.fixture(scope="module")
+def gemm_asm(tmp_path_factory) -> str:
+    if not shutil.which(B.HIPCC) and not shutil.os.path.exists(B.HIPCC):
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("asm") / "oz_gemm.s"
+    cmd = [B.HIPCC, *B.HIP_FLAGS, *B.HIP_SOURCES["oz_gemm.hip"], "--cuda-device-only", "-S",
+           str(B.CSRC / "oz_gemm.hip"), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text()
+
+
+def test_all_instantiations_present(gemm_asm):
+    names = _kernels(gemm_asm)
+    # three modes (products, digits, scheme I diagonals) x (even K/64, any K/64)
+    assert len(names) == 6, sorted(names)
+
+
+def test_m0_only_feeds_the_lds_copies(gemm_asm):
+    for name, lines in _kernels(gemm_asm).items():
+        body = [l.strip() for l in lines if l.strip() and not l.strip().startswith(";")]
+        for i, l in enumerate(body):
+            if re.search(r"\bm0\b", l):
+                assert re.match(r"s_mov_b32 m0, s\d+$", l), (name, l)
+                assert body[i + 1].startswith("global_load_lds_dwordx4"), (name, l, body[i + 1])
+
+
+def test_no_spills(gemm_asm):
+    meta = re.findall(r"\.name:\s+(_Z\S*gemm_i8_kernel\S*)\s.*?\.private_segment_fixed_size:\s+(\d+).*?"
+                      r"\.vgpr_spill_count:\s+(\d+)", gemm_asm, re.S)
+    assert len(meta) == 6
+    for name, private, spills in meta:
+        assert private == "0" and spills == "0", (name, private, spills)
+
+
+def test_even_main_loops_keep_accumulators_in_agprs(gemm_asm):
+    for name, lines in _kernels(gemm_asm).items():
+        loop = _main_loop(lines)
+        # two K steps per trip: 2 x 64 MFMAs, 2 x 16 fragment reads, 2 x 8 global->LDS copies
+        assert sum(x.startswith("v_mfma_i32_16x16x64_i8") for x in loop) == 128, name
+        assert sum(x.startswith("ds_read_b128") for x in loop) == 32, name
+        assert sum(x.startswith("global_load_lds_dwordx4") for x in loop) == 16, name
+        assert not any(x.startswith("scratch_") for x in loop), name
+        if "ELb1E" in name:  # the EVEN instantiations (every production shape with K % 128 == 0)
+            assert not any(x.startswith("v_accvgpr") for x in loop), (name, "accumulators moved in the loop")
+            assert sum(1 for x in loop if re.match(r"\.LBB", x)) == 1, (name, "branches inside the loop")
