@@ -48,6 +48,13 @@ int oz_dev_free(oz_dev* dev, void* ptr);
 int oz_memcpy_h2d(oz_dev* dev, void* dst, const void* src, size_t bytes);
 int oz_memcpy_d2h(oz_dev* dev, void* dst, const void* src, size_t bytes);
 int oz_fill_u32(oz_dev* dev, void* dst, uint32_t value, size_t count);
+/* Page-locked host memory (hipHostMalloc) for staging uploads and downloads: copies from it run at
+ * full link speed and asynchronously. */
+int oz_host_malloc(oz_dev* dev, size_t bytes, void** ptr);
+int oz_host_free(oz_dev* dev, void* ptr);
+/* Host-to-device copy ordered on the handle's stream that returns without waiting; src must be
+ * page-locked (oz_host_malloc) and stay valid and unchanged until the stream has passed the copy. */
+int oz_memcpy_h2d_async(oz_dev* dev, void* dst, const void* src, size_t bytes);
 /* Device-to-device copy by a plain streaming kernel (16-byte aligned pointers and size); also the
  * reference transfer for calibrating HBM traffic counters. */
 int oz_memcpy_d2d(oz_dev* dev, void* dst, const void* src, size_t bytes);

@@ -20,25 +20,34 @@ namespace ozTTgemm::detail {
 void device_check(oz_dev* dev, int status, const char* what);
 
 // Device allocations of one GPU kept by the Context between calls, grown on demand (the reference
-// rebuilds its buffers per call, README.md:81-85; reusing them avoids hipMalloc in repeated calls).
+// rebuilds its buffers per call, README.md:81-85; reusing them avoids hipMalloc in repeated calls),
+// and page-locked host staging buffers for the operands and the result, kept the same way.
 class Workspace {
 public:
     explicit Workspace(oz_dev* dev) : dev_(dev) {}
     ~Workspace();
     Workspace(const Workspace&) = delete;
     Workspace& operator=(const Workspace&) = delete;
-    // Buffer of at least `bytes` for role `slot` (contents undefined).
+    // Device buffer of at least `bytes` for role `slot` (contents undefined).
     void* get(int slot, std::size_t bytes);
+    // Page-locked host buffer of at least `bytes` for role `slot` (contents undefined); ordinary
+    // memory if page-locked memory is refused.
+    void* host(int slot, std::size_t bytes);
     void release_all();
 
 private:
     struct Buf {
         void* p = nullptr;
         std::size_t size = 0;
+        bool pinned = false;
     };
+    void free_host(Buf& b);
     oz_dev* dev_;
-    std::vector<Buf> bufs_;
+    std::vector<Buf> bufs_, host_;
 };
+
+// Host staging slots.
+enum HostSlot { kHostA = 0, kHostB, kHostC };
 
 // The opened GPU (the reference's Device, backend_interface.hpp:14).
 struct Device {
@@ -47,16 +56,17 @@ struct Device {
 };
 
 // One GEMM after validation and zero padding: A is m x k and B is k x n, row-major, with m and n
-// multiples of 64 and k a multiple of 32 (backend_interface.hpp:21-26).
+// multiples of 64 and k a multiple of 32 (backend_interface.hpp:21-26). The operands are in the
+// workspace's page-locked staging buffers.
 struct Problem {
     std::uint32_t m, n, k;
-    const std::vector<double>& a;
-    const std::vector<double>& b;
+    const double* a;
+    const double* b;
     const Options& options;
 };
 
 struct Output {
-    std::vector<double> values;  // padded m x n, row-major
+    const double* values;  // padded m x n, row-major, in the workspace's host staging (kHostC)
     Info info;
 };
 

@@ -113,10 +113,6 @@ Context::~Context() {
 Info Context::Impl::execute(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m,
                             std::size_t n, std::size_t k, const Options& opts, const Checked& v) {
     const auto mp = v.mp, np = v.np, kp = v.kp;
-    // zero-padded copies before the lock; C may alias A or B
-    std::vector<double> ap(checked_product(mp, kp), 0), bp(checked_product(kp, np), 0);
-    for (std::size_t i = 0; i < m; ++i) std::copy_n(a.data() + i * k, k, ap.data() + i * kp);
-    for (std::size_t i = 0; i < k; ++i) std::copy_n(b.data() + i * n, n, bp.data() + i * np);
     std::lock_guard lock(runtime_mutex);
     if (!device.dev) {
         oz_dev* d = nullptr;
@@ -127,14 +123,43 @@ Info Context::Impl::execute(std::span<const double> a, std::span<const double> b
         device.dev = d;
         device.ws = std::make_unique<detail::Workspace>(d);
     }
+    // zero-padded copies into the page-locked staging buffers (rows in parallel); they are complete
+    // before C is written, so C may alias A or B
+    auto* ap = static_cast<double*>(device.ws->host(detail::kHostA, sizeof(double) * checked_product(mp, kp)));
+    auto* bp = static_cast<double*>(device.ws->host(detail::kHostB, sizeof(double) * checked_product(kp, np)));
+    const double* ad = a.data();
+    const double* bd = b.data();
+#pragma omp parallel for schedule(static)
+    for (std::int64_t i = 0; i < (std::int64_t)mp; ++i) {
+        double* row = ap + (std::size_t)i * kp;
+        if ((std::size_t)i < m) {
+            std::copy_n(ad + (std::size_t)i * k, k, row);
+            std::fill(row + k, row + kp, 0.0);
+        } else {
+            std::fill(row, row + kp, 0.0);
+        }
+    }
+#pragma omp parallel for schedule(static)
+    for (std::int64_t i = 0; i < (std::int64_t)kp; ++i) {
+        double* row = bp + (std::size_t)i * np;
+        if ((std::size_t)i < k) {
+            std::copy_n(bd + (std::size_t)i * n, n, row);
+            std::fill(row + n, row + np, 0.0);
+        } else {
+            std::fill(row, row + np, 0.0);
+        }
+    }
     const detail::Problem problem{mp, np, kp, ap, bp, opts};
-    detail::Output output = detail::backend_for(opts.format, opts.scheme)(device, problem);
-    if (output.values.size() != std::size_t(mp) * np) throw std::runtime_error("backend returned an invalid output shape");
-    for (std::size_t i = 0; i < m; ++i) std::copy_n(output.values.data() + i * np, n, c.data() + i * n);
-    output.info.padded_m = mp;
-    output.info.padded_n = np;
-    output.info.padded_k = kp;
-    return output.info;
+    const detail::Output output = detail::backend_for(opts.format, opts.scheme)(device, problem);
+    const double* vals = output.values;
+    double* cd = c.data();
+#pragma omp parallel for schedule(static)
+    for (std::int64_t i = 0; i < (std::int64_t)m; ++i) std::copy_n(vals + (std::size_t)i * np, n, cd + (std::size_t)i * n);
+    Info info = output.info;
+    info.padded_m = mp;
+    info.padded_n = np;
+    info.padded_k = kp;
+    return info;
 }
 
 Info Context::gemm(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m,

@@ -1,5 +1,6 @@
 // (format, scheme) -> backend, format names, availability; the device workspace. Semantics of the
 // reference's dispatch.cpp:18-51: formats that are not built report is_available() == false.
+#include <new>
 #include <stdexcept>
 
 #include "backend.hpp"
@@ -30,10 +31,45 @@ void* Workspace::get(int slot, std::size_t bytes) {
     return bufs_[slot].p;
 }
 
+void* Workspace::host(int slot, std::size_t bytes) {
+    if (slot < 0) throw std::logic_error("host staging slot");
+    if ((std::size_t)slot >= host_.size()) host_.resize(slot + 1);
+    Buf& b = host_[slot];
+    bytes = (bytes + 4095) & ~std::size_t(4095);
+    if (b.size < bytes) {
+        free_host(b);
+        void* p = nullptr;
+        if (oz_host_malloc(dev_, bytes, &p) == OZ_OK) {
+            b.pinned = true;
+        } else {
+            // page-locked memory refused (limits or exhaustion): ordinary memory works the same,
+            // only the copies are slower; std::bad_alloc when even that runs out
+            p = ::operator new(bytes);
+            b.pinned = false;
+        }
+        b.p = p;
+        b.size = bytes;
+    }
+    return b.p;
+}
+
+void Workspace::free_host(Buf& b) {
+    if (b.p) {
+        if (b.pinned)
+            (void)oz_host_free(dev_, b.p);
+        else
+            ::operator delete(b.p);
+    }
+    b.p = nullptr;
+    b.size = 0;
+}
+
 void Workspace::release_all() {
     for (auto& b : bufs_)
         if (b.p) (void)oz_dev_free(dev_, b.p);
     bufs_.clear();
+    for (auto& b : host_) free_host(b);
+    host_.clear();
 }
 
 // Every format runs with both schemes. Scheme I runs every format's digits (int8 values) on the INT8

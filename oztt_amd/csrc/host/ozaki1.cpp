@@ -37,16 +37,20 @@ std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / 
 Output ozaki1_run(Device& D, const Problem& p) {
     oz_dev* dev = D.dev;
     const Oz1Format& f = oz1_format((int)p.options.format);
-    const Plan1 plan = plan_scheme1(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.slices, f);
-    const std::uint32_t M = p.m, N = p.n, K = p.k, P = (std::uint32_t)plan.p;
+    const std::uint32_t M = p.m, N = p.n, K = p.k;
+    Workspace& ws = *D.ws;
+    // the operands go up while the host plans (they are page-locked, the copies are asynchronous)
+    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
+    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
+    device_check(dev, oz_memcpy_h2d_async(dev, dAf, p.a, sizeof(double) * M * (std::size_t)K), "upload A");
+    device_check(dev, oz_memcpy_h2d_async(dev, dBf, p.b, sizeof(double) * K * (std::size_t)N), "upload B");
+    const Plan1 plan = plan_scheme1(p.a, p.b, p.m, p.n, p.k, p.options.slices, f);
+    const std::uint32_t P = (std::uint32_t)plan.p;
     const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
     if ((std::uint64_t)P * Kg * f.dmax * f.dmax > 0x7FFFFFFFull)
         throw std::logic_error("scheme I plan: the padded K breaks the int32 exactness of a diagonal");
     const oz1_recon_dev rdesc{(int)P, f.radix, plan.signmag ? 1 : 0, plan.nsmall, plan.Whi, plan.Wlo, plan.qw};
 
-    Workspace& ws = *D.ws;
-    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
-    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
     auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
     auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
     auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
@@ -55,9 +59,6 @@ Output ozaki1_run(Device& D, const Problem& p) {
     auto* slB = static_cast<std::int8_t*>(ws.get(kSlicesB, (std::size_t)P * strideB));
     auto* part = static_cast<std::int32_t*>(ws.get(kPartial, sizeof(std::int32_t) * (std::size_t)P * strideP));
     auto* out = static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
-
-    device_check(dev, oz_memcpy_h2d(dev, dAf, p.a.data(), sizeof(double) * p.a.size()), "upload A");
-    device_check(dev, oz_memcpy_h2d(dev, dBf, p.b.data(), sizeof(double) * p.b.size()), "upload B");
 
     std::vector<Step> steps;
     steps.push_back({ev::Scale, [=] {
@@ -94,11 +95,11 @@ Output ozaki1_run(Device& D, const Problem& p) {
                      }});
     // P(P+1)/2 slice-pair products of 2*M*N*K operations each
     const unsigned pairs = P * (P + 1) / 2;
-    std::vector<double> values =
-        run_pipeline(dev, steps, 2, out, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
+    auto* host = static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
+    run_pipeline(dev, steps, 2, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
     Info info{Scheme::I, p.options.format};
     info.slices = P;
-    return {std::move(values), info};
+    return {host, info};
 }
 
 }  // namespace ozTTgemm::detail

@@ -44,10 +44,17 @@ Output ozaki2_run(Device& D, const Problem& p) {
     ev::Settings* es = ev::active();
     std::optional<unsigned> fixed_b;
     if (es && es->fixed_bits) fixed_b = es->fixed_bits;
-    const Plan2 plan = plan_scheme2(p.a.data(), p.b.data(), p.m, p.n, p.k, p.options.format, p.options.max_moduli,
+    const std::uint32_t M = p.m, N = p.n, K = p.k;
+    Workspace& ws = *D.ws;
+    // the operands go up while the host plans (they are page-locked, the copies are asynchronous)
+    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
+    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
+    device_check(dev, oz_memcpy_h2d_async(dev, dAf, p.a, sizeof(double) * M * (std::size_t)K), "upload A");
+    device_check(dev, oz_memcpy_h2d_async(dev, dBf, p.b, sizeof(double) * K * (std::size_t)N), "upload B");
+    const Plan2 plan = plan_scheme2(p.a, p.b, p.m, p.n, p.k, p.options.format, p.options.max_moduli,
                                     p.options.reconstruction, fixed_b);
     const bool fp8 = p.options.format == Format::FP8;
-    const std::uint32_t M = p.m, N = p.n, K = p.k, S = (std::uint32_t)plan.S;
+    const std::uint32_t S = (std::uint32_t)plan.S;
     const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
     const oz2_crt_dev cdesc = crt_descriptor(plan);
     const oz2_moduli_dev mdesc = split_descriptor(plan);
@@ -62,9 +69,6 @@ Output ozaki2_run(Device& D, const Problem& p) {
     const std::uint32_t nterms = fp8 ? (std::uint32_t)gdesc.nout : S;
     const std::size_t term_bytes = fp8 ? 2 : 1;
 
-    Workspace& ws = *D.ws;
-    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
-    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
     auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
     auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
     auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
@@ -76,9 +80,6 @@ Output ozaki2_run(Device& D, const Problem& p) {
     auto* uA = reinterpret_cast<std::uint8_t*>(planesA);
     auto* uB = reinterpret_cast<std::uint8_t*>(planesB);
     auto* terms = reinterpret_cast<std::uint16_t*>(prod);
-
-    device_check(dev, oz_memcpy_h2d(dev, dAf, p.a.data(), sizeof(double) * p.a.size()), "upload A");
-    device_check(dev, oz_memcpy_h2d(dev, dBf, p.b.data(), sizeof(double) * p.b.size()), "upload B");
 
     const int shift = plan.shift();
     std::vector<Step> steps;
@@ -140,13 +141,13 @@ Output ozaki2_run(Device& D, const Problem& p) {
     // products: one per modulus (INT8) or the FP8 route's digit products (sum of the outputs' pairs)
     const std::uint32_t nprod = fp8 ? (std::uint32_t)plan.mo.nprod : S;
 
-    std::vector<double> values = run_pipeline(dev, steps, 2, out, (std::size_t)M * N, flags,
-                                              2.0 * M * (double)N * K * nprod, nprod);
+    auto* host = static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
+    run_pipeline(dev, steps, 2, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * nprod, nprod);
     Info info{Scheme::II, p.options.format};
     info.moduli = S;
     info.integer_bits = (std::uint32_t)plan.b;
     info.reconstruction_passes = plan.two_pass ? 2 : 1;
-    return {std::move(values), info};
+    return {host, info};
 }
 
 }  // namespace ozTTgemm::detail

@@ -11,9 +11,9 @@ namespace ozTTgemm::detail {
 
 namespace ev = ::ozTTgemm::evaluation;
 
-std::vector<double> run_pipeline(oz_dev* dev, const std::vector<Step>& steps, std::size_t gemm_step,
-                                 const double* out, std::size_t count, const std::uint32_t* flags,
-                                 double product_ops, unsigned partial_products) {
+void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, std::size_t gemm_step, const double* out,
+                  double* host, std::size_t count, const std::uint32_t* flags, double product_ops,
+                  unsigned partial_products) {
     ev::Settings* es = ev::active();
     // Per-phase device times: events around every step (slots 24 + 2i, 25 + 2i), summed by phase.
     // The events are read after the pass, so each step needs its own pair.
@@ -45,8 +45,7 @@ std::vector<double> run_pipeline(oz_dev* dev, const std::vector<Step>& steps, st
         es->product_ops = product_ops;
         es->gemm_launches = 1;
     }
-    std::vector<double> values(count);
-    device_check(dev, oz_memcpy_d2h(dev, values.data(), out, sizeof(double) * count), "read C");
+    device_check(dev, oz_memcpy_d2h(dev, host, out, sizeof(double) * count), "read C");
     std::uint32_t fl[2];
     device_check(dev, oz_memcpy_d2h(dev, fl, flags, sizeof fl), "read flags");
 
@@ -64,7 +63,7 @@ std::vector<double> run_pipeline(oz_dev* dev, const std::vector<Step>& steps, st
         es->whole_ms = ms / es->repeats;
         std::vector<double> again(count);
         device_check(dev, oz_memcpy_d2h(dev, again.data(), out, sizeof(double) * count), "read C");
-        es->whole_checked = std::memcmp(again.data(), values.data(), sizeof(double) * count) == 0;
+        es->whole_checked = std::memcmp(again.data(), host, sizeof(double) * count) == 0;
         device_check(dev, oz_event_record(dev, 22), "event");
         for (int r = 0; r < es->repeats; r++) steps[gemm_step].issue();
         device_check(dev, oz_event_record(dev, 23), "event");
@@ -87,7 +86,6 @@ std::vector<double> run_pipeline(oz_dev* dev, const std::vector<Step>& steps, st
             if (fl[t] & 2u) throw std::runtime_error(std::string("a maximum of the ") + what + " is below 2^-126");
             throw std::runtime_error(std::string("a maximum of the ") + what + " exceeds the BF16 range");
         }
-    return values;
 }
 
 }  // namespace ozTTgemm::detail

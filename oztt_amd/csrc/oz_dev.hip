@@ -92,6 +92,26 @@ int oz_memcpy_d2h(oz_dev* dev, void* dst, const void* src, size_t bytes) {
     return oz::hip_check(dev, hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
 }
 
+int oz_host_malloc(oz_dev* dev, size_t bytes, void** ptr) {
+    if (int st = oz::use(dev)) return st;
+    if (!ptr) return oz::fail(dev, OZ_ERR_ARG, "oz_host_malloc: null output pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return OZ_OK;
+    return oz::hip_check(dev, hipHostMalloc(ptr, bytes, hipHostMallocDefault), "hipHostMalloc");
+}
+
+int oz_host_free(oz_dev* dev, void* ptr) {
+    if (int st = oz::use(dev)) return st;
+    if (!ptr) return OZ_OK;
+    return oz::hip_check(dev, hipHostFree(ptr), "hipHostFree");
+}
+
+int oz_memcpy_h2d_async(oz_dev* dev, void* dst, const void* src, size_t bytes) {
+    if (int st = oz::use(dev)) return st;
+    if (!bytes) return OZ_OK;
+    return oz::hip_check(dev, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream), "hipMemcpyAsync H2D");
+}
+
 int oz_fill_u32(oz_dev* dev, void* dst, uint32_t value, size_t count) {
     if (int st = oz::use(dev)) return st;
     if (!count) return OZ_OK;
