@@ -44,6 +44,8 @@ void oz_dev_close(oz_dev* dev);
 const char* oz_last_error(const oz_dev* dev);
 int oz_device_count(int* count);
 int oz_dev_malloc(oz_dev* dev, size_t bytes, void** ptr);
+/* Free and total device memory of the handle's GPU (hipMemGetInfo). */
+int oz_mem_info(oz_dev* dev, size_t* free_bytes, size_t* total_bytes);
 int oz_dev_free(oz_dev* dev, void* ptr);
 int oz_memcpy_h2d(oz_dev* dev, void* dst, const void* src, size_t bytes);
 int oz_memcpy_d2h(oz_dev* dev, void* dst, const void* src, size_t bytes);

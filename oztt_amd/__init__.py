@@ -80,7 +80,8 @@ class EvalStats(ctypes.Structure):
     _fields_ = [("fixed_bits", ctypes.c_uint), ("warmup", ctypes.c_int), ("repeats", ctypes.c_int),
                 ("phase_ms", ctypes.c_double * 5), ("whole_ms", ctypes.c_double), ("whole_checked", ctypes.c_int),
                 ("partial_products", ctypes.c_uint), ("product_ops", ctypes.c_double),
-                ("gemm_launch_ms", ctypes.c_double), ("gemm_launches", ctypes.c_int)]
+                ("gemm_launch_ms", ctypes.c_double), ("gemm_launches", ctypes.c_int),
+                ("max_band_rows", ctypes.c_uint)]
 
 
 class Plan2(ctypes.Structure):
@@ -210,12 +211,15 @@ class Context:
         return c
 
     def evaluate(self, a, b, m: int, n: int, k: int, options: Options, fixed_bits: int = 0, warmup: int = 0,
-                 repeats: int = 0):
-        """GEMM under the evaluation hooks: returns (C, Info, EvalStats) with phase and whole-pass times."""
+                 repeats: int = 0, max_band_rows: int = 0):
+        """GEMM under the evaluation hooks: returns (C, Info, EvalStats) with phase and whole-pass times.
+        max_band_rows > 0 caps the rows of a band (row bands are otherwise used only when the problem
+        does not fit in device memory)."""
         a, b = _f64(a), _f64(b)
         c = np.empty(m * n, dtype=np.float64)
         ev = EvalStats()
         ev.fixed_bits, ev.warmup, ev.repeats = fixed_bits, warmup, repeats
+        ev.max_band_rows = max_band_rows
         info = self._call(a, b, c, m, n, k, options, ev)
         return c, info, ev
 

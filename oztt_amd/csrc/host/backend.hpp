@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <initializer_list>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -33,6 +34,9 @@ public:
     // Page-locked host buffer of at least `bytes` for role `slot` (contents undefined); ordinary
     // memory if page-locked memory is refused.
     void* host(int slot, std::size_t bytes);
+    // Device bytes held by the slots, and the release of one slot's device buffer.
+    std::size_t held() const;
+    void release(int slot);
     void release_all();
 
 private:
@@ -49,11 +53,21 @@ private:
 // Host staging slots.
 enum HostSlot { kHostA = 0, kHostB, kHostC };
 
+
 // The opened GPU (the reference's Device, backend_interface.hpp:14).
 struct Device {
     oz_dev* dev = nullptr;
     std::unique_ptr<Workspace> ws;
 };
+
+// Row bands (the reference's row bands when device memory runs short, ozaki2/plan.hpp:386-444):
+// the rows of A and C per band, either all M, or the largest multiple of 256 for which
+// `fixed` bytes plus `per_row` bytes per padded row fit in the device memory left beside the other
+// slots of the workspace (the slots listed in `band_slots` are released to make room). An active
+// evaluation Scope may cap the band (Settings::max_band_rows). std::runtime_error when not even
+// 256 rows fit.
+std::uint32_t band_rows(Device& D, std::uint32_t M, std::size_t fixed, std::size_t per_row,
+                        std::initializer_list<int> band_slots);
 
 // One GEMM after validation and zero padding: A is m x k and B is k x n, row-major, with m and n
 // multiples of 64 and k a multiple of 32 (backend_interface.hpp:21-26). The operands are in the

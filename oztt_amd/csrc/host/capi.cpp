@@ -73,6 +73,7 @@ struct ozt_eval {
     double product_ops;
     double gemm_launch_ms;
     int gemm_launches;
+    unsigned max_band_rows;  // input: cap on the rows of a band (0: bands only when memory requires)
 };
 
 struct ozt_plan2 {
@@ -145,6 +146,7 @@ int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, s
         s.fixed_bits = evo->fixed_bits;
         s.warmup = evo->warmup;
         s.repeats = evo->repeats;
+        s.max_band_rows = evo->max_band_rows;
         auto* cx = static_cast<ozTTgemm::Context*>(ctx);
         ozTTgemm::Info i;
         {

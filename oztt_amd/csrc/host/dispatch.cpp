@@ -4,6 +4,9 @@
 #include <stdexcept>
 
 #include "backend.hpp"
+#include "evaluation.hpp"
+
+#include <algorithm>
 
 namespace ozTTgemm::detail {
 
@@ -62,6 +65,42 @@ void Workspace::free_host(Buf& b) {
     }
     b.p = nullptr;
     b.size = 0;
+}
+
+std::size_t Workspace::held() const {
+    std::size_t n = 0;
+    for (const auto& b : bufs_) n += b.size;
+    return n;
+}
+
+void Workspace::release(int slot) {
+    if (slot < 0 || (std::size_t)slot >= bufs_.size()) return;
+    Buf& b = bufs_[slot];
+    if (b.p) (void)oz_dev_free(dev_, b.p);
+    b.p = nullptr;
+    b.size = 0;
+}
+
+std::uint32_t band_rows(Device& D, std::uint32_t M, std::size_t fixed, std::size_t per_row,
+                        std::initializer_list<int> band_slots) {
+    const std::uint32_t Mg = (M + 255) / 256 * 256;
+    std::uint32_t rows = M;
+    std::size_t free_b = 0, total_b = 0;
+    device_check(D.dev, oz_mem_info(D.dev, &free_b, &total_b), "device memory");
+    // bytes available: free now plus what the workspace holds (its slots are reallocated as needed),
+    // less a margin for the runtime
+    const std::size_t margin = std::max<std::size_t>(total_b / 64, std::size_t(1) << 30);
+    std::size_t avail = free_b + D.ws->held();
+    avail = avail > margin ? avail - margin : 0;
+    if (fixed + per_row * (std::size_t)Mg > avail) {
+        for (int s : band_slots) D.ws->release(s);
+        if (fixed + 256 * per_row > avail)
+            throw std::runtime_error("the problem does not fit in device memory, not even in row bands of 256 rows");
+        rows = (std::uint32_t)std::min<std::size_t>((avail - fixed) / per_row / 256 * 256, Mg);
+    }
+    if (const ::ozTTgemm::evaluation::Settings* es = ::ozTTgemm::evaluation::active())
+        if (es->max_band_rows > 0) rows = std::min(rows, std::max(256u, es->max_band_rows / 256 * 256));
+    return std::min(rows, M);
 }
 
 void Workspace::release_all() {

@@ -26,6 +26,7 @@ struct Settings {
     unsigned fixed_bits = 0;  // Scheme II: width b fixed by the caller (0: chosen from the input)
     int warmup = 0;           // untimed whole-pass replays
     int repeats = 0;          // timed whole-pass replays (0: no replay)
+    unsigned max_band_rows = 0;  // cap on the rows of a band (0: bands only when memory requires)
     // outputs
     double phase_ms[PhaseCount] = {};  // device time of each phase: the average of up to 5 warm passes
                                        // after the replays (the first pass when there are none)
@@ -33,8 +34,8 @@ struct Settings {
     bool whole_checked = false;        // replayed output bit-identical to the first pass
     unsigned partial_products = 0;     // low-precision matrix products per call (S or slice pairs)
     double product_ops = 0;            // algorithmic operations of the product phase (2*M*N*K*products)
-    double gemm_launch_ms = 0;         // average duration of one product-kernel launch in the replays
-    int gemm_launches = 0;             // product-kernel launches per pass
+    double gemm_launch_ms = 0;         // device time of the product launches of one pass, in the replays
+    int gemm_launches = 0;             // product-kernel launches per pass (one per row band)
 };
 
 // Activates `s` for the calling thread until destruction (not nestable).

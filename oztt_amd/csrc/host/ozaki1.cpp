@@ -11,11 +11,13 @@
 // that is the reference's single-K-block plan (plan.hpp:187-195); for the FP32-product formats it is
 // the exact int32 sum S_d the reference accumulates over pairs and K blocks before its deferred
 // reconstruction (plan.hpp:95-128), so the reconstruction reads the same integers. The reference's
-// panels and row bands reduce to one launch per stage on one MI355X.
+// panels reduce to one launch per stage on one MI355X; its row bands (plan.hpp:386-444) remain for
+// problems beyond the device memory (A's slices and the partial sums are then per band, band_rows).
 //
 // Device layout: A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2]; slices of A: p planes of
-// Mg x Kg int8, of B: p planes of Ng x Kg (B transposed), both in the GEMM's OZ_BLOCK tiles (Mg, Ng
-// multiples of 256, Kg of 64); partial sums: p planes of Mg x Ng int32; output: M x N f64.
+// Mbg x Kg int8 per band of rows, of B: p planes of Ng x Kg (B transposed), both in the GEMM's
+// OZ_BLOCK tiles (Mbg, Ng multiples of 256, Kg of 64); partial sums (per band): p planes of Mbg x Ng
+// int32; output: M x N f64.
 #include <stdexcept>
 
 #include "backend.hpp"
@@ -46,15 +48,24 @@ Output ozaki1_run(Device& D, const Problem& p) {
     device_check(dev, oz_memcpy_h2d_async(dev, dBf, p.b, sizeof(double) * K * (std::size_t)N), "upload B");
     const Plan1 plan = plan_scheme1(p.a, p.b, p.m, p.n, p.k, p.options.slices, f);
     const std::uint32_t P = (std::uint32_t)plan.p;
-    const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
+    const std::uint32_t Ng = round_up(N, 256), Kg = round_up(K, 64);
     if ((std::uint64_t)P * Kg * f.dmax * f.dmax > 0x7FFFFFFFull)
         throw std::logic_error("scheme I plan: the padded K breaks the int32 exactness of a diagonal");
     const oz1_recon_dev rdesc{(int)P, f.radix, plan.signmag ? 1 : 0, plan.nsmall, plan.Whi, plan.Wlo, plan.qw};
 
+    // Row bands: A's slices and the partial sums are per band of rows; A, B, B's slices, the deltas
+    // and C are whole. One band (all of M) unless device memory requires more.
+    const std::size_t fixed = sizeof(double) * ((std::size_t)M * K + (std::size_t)K * N + (std::size_t)M * N) +
+                              (std::size_t)P * Ng * Kg + sizeof(std::int32_t) * (M + N) + 256;
+    const std::size_t per_row = (std::size_t)P * Kg + sizeof(std::int32_t) * (std::size_t)P * Ng;
+    const std::uint32_t Mb = band_rows(D, M, fixed, per_row, {kSlicesA, kPartial});
+    const std::uint32_t Mbg = round_up(Mb, 256);
+    const std::uint32_t nbands = (M + Mb - 1) / Mb;
+
     auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
     auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
     auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
-    const long long strideA = (long long)Mg * Kg, strideB = (long long)Ng * Kg, strideP = (long long)Mg * Ng;
+    const long long strideA = (long long)Mbg * Kg, strideB = (long long)Ng * Kg, strideP = (long long)Mbg * Ng;
     auto* slA = static_cast<std::int8_t*>(ws.get(kSlicesA, (std::size_t)P * strideA));
     auto* slB = static_cast<std::int8_t*>(ws.get(kSlicesB, (std::size_t)P * strideB));
     auto* part = static_cast<std::int32_t*>(ws.get(kPartial, sizeof(std::int32_t) * (std::size_t)P * strideP));
@@ -71,32 +82,41 @@ Output ozaki1_run(Device& D, const Problem& p) {
                                                         dltB, flags + 1),
                                       "scale B");
                      }});
+    // B's slices once, then per band: A's slices, the diagonal products, the reconstruction
     steps.push_back({ev::Slice, [=] {
-                         device_check(dev,
-                                      oz1_split_int8(dev, dAf, (int)M, (int)K, (int)K, 0, dltA, (int)P, f.radix, f.dmax,
-                                                     slA, 2, (int)Mg, (int)Kg, strideA),
-                                      "slice A");
                          device_check(dev,
                                       oz1_split_int8(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, (int)P, f.radix, f.dmax,
                                                      slB, 3, (int)Ng, (int)Kg, strideB),
                                       "slice B");
                      }});
-    steps.push_back({ev::Gemm, [=] {
-                         device_check(dev,
-                                      oz1_gemm_diag_i8(dev, slA, slB, part, (int)Mg, (int)Ng, (int)Kg, (int)P, f.dmax,
-                                                       (int)Ng, strideA, strideB, strideP),
-                                      "diagonal products");
-                     }});
-    steps.push_back({ev::Recon, [=] {
-                         device_check(dev,
-                                      oz1_recon_f64(dev, part, (int)M, (int)N, (int)Ng, strideP, &rdesc, dltA, dltB, out,
-                                                    (int)N),
-                                      "reconstruction");
-                     }});
+    for (std::uint32_t band = 0; band < nbands; band++) {
+        const std::uint32_t r0 = band * Mb, rows = std::min(Mb, M - r0), rowsg = round_up(rows, 256);
+        const double* Ab = dAf + (std::size_t)r0 * K;
+        const std::int32_t* dAb = dltA + r0;
+        double* ob = out + (std::size_t)r0 * N;
+        steps.push_back({ev::Slice, [=] {
+                             device_check(dev,
+                                          oz1_split_int8(dev, Ab, (int)rows, (int)K, (int)K, 0, dAb, (int)P, f.radix,
+                                                         f.dmax, slA, 2, (int)rowsg, (int)Kg, strideA),
+                                          "slice A");
+                         }});
+        steps.push_back({ev::Gemm, [=] {
+                             device_check(dev,
+                                          oz1_gemm_diag_i8(dev, slA, slB, part, (int)rowsg, (int)Ng, (int)Kg, (int)P,
+                                                           f.dmax, (int)Ng, strideA, strideB, strideP),
+                                          "diagonal products");
+                         }});
+        steps.push_back({ev::Recon, [=] {
+                             device_check(dev,
+                                          oz1_recon_f64(dev, part, (int)rows, (int)N, (int)Ng, strideP, &rdesc, dAb,
+                                                        dltB, ob, (int)N),
+                                          "reconstruction");
+                         }});
+    }
     // P(P+1)/2 slice-pair products of 2*M*N*K operations each
     const unsigned pairs = P * (P + 1) / 2;
     auto* host = static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, 2, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
+    run_pipeline(dev, steps, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
     Info info{Scheme::I, p.options.format};
     info.slices = P;
     return {host, info};

@@ -2,9 +2,10 @@
 //
 // Pipeline of the reference's ozaki2.cpp:439-478: plan (moduli, width b, passes) -> upload the FP64
 // operands -> scale (row/column maxima, exponent deltas) -> slice -> products -> CRT reconstruction
-// to FP64 -> read back and check the range flags. The reference splits the output into row bands
-// when its 32 GB of DRAM is short (plan.hpp:386-444); at the sizes one MI355X (288 GB) serves, every
-// buffer is resident at once, so there are no bands.
+// to FP64 -> read back and check the range flags. Like the reference (plan.hpp:386-444), the output
+// is computed in row bands when the device memory is short: the planes of A and the product terms
+// are then per band of rows, while A, B, B's planes and C stay whole (band_rows). Up to about
+// 60000^3 (INT8, 18 moduli) one MI355X (288 GB) holds everything at once, and there is one band.
 //   INT8: slice = int8 residue planes per modulus; products = one exact int32 GEMM per modulus,
 //   reduced in the epilogue to the CRT digit (uint8); reconstruction from the S digit planes.
 //   FP8 (ozaki2.cpp:228-318 run_digit_gemms): slice = e4m3 digit planes (2 or 3 per modulus);
@@ -14,10 +15,10 @@
 //
 // Device layout (all row-major, zero-padded so that every kernel runs unguarded full tiles):
 //   A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2];
-//   planes of A: P x Mg x Kg bytes, of B: P x Ng x Kg bytes (B transposed), both K-major in the
+//   planes of A (per band of Mb rows): P x Mbg x Kg bytes, of B: P x Ng x Kg bytes (B transposed), both K-major in the
 //   GEMM's OZ_BLOCK tiles (1 KB blocks of 16 rows x 64 K-bytes), Mg, Ng multiples of 256 and Kg of
 //   64 (P = S residue planes, or the FP8 route's digit planes);
-//   product digits: S x Mg x Ng uint8 (INT8) or nout x Mg x Ng uint16 (FP8); output: M x N f64.
+//   product digits (per band): S x Mbg x Ng uint8 (INT8) or nout x Mbg x Ng uint16 (FP8); output: M x N f64.
 #include <chrono>
 #include <cstring>
 #include <functional>
@@ -55,7 +56,7 @@ Output ozaki2_run(Device& D, const Problem& p) {
                                     p.options.reconstruction, fixed_b);
     const bool fp8 = p.options.format == Format::FP8;
     const std::uint32_t S = (std::uint32_t)plan.S;
-    const std::uint32_t Mg = round_up(M, 256), Ng = round_up(N, 256), Kg = round_up(K, 64);
+    const std::uint32_t Ng = round_up(N, 256), Kg = round_up(K, 64);
     const oz2_crt_dev cdesc = crt_descriptor(plan);
     const oz2_moduli_dev mdesc = split_descriptor(plan);
     oz2_digit_dev ddesc{};
@@ -69,10 +70,19 @@ Output ozaki2_run(Device& D, const Problem& p) {
     const std::uint32_t nterms = fp8 ? (std::uint32_t)gdesc.nout : S;
     const std::size_t term_bytes = fp8 ? 2 : 1;
 
+    // Row bands: A's planes and the product terms are per band; A, B, B's planes, the deltas and C
+    // are whole. One band (all of M) unless device memory requires more.
+    const std::size_t fixed = sizeof(double) * ((std::size_t)M * K + (std::size_t)K * N + (std::size_t)M * N) +
+                              (std::size_t)nplanes * Ng * Kg + sizeof(std::int32_t) * (M + N) + 256;
+    const std::size_t per_row = (std::size_t)nplanes * Kg + (std::size_t)nterms * Ng * term_bytes;
+    const std::uint32_t Mb = band_rows(D, M, fixed, per_row, {kPlanesA, kProducts});
+    const std::uint32_t Mbg = round_up(Mb, 256);
+    const std::uint32_t nbands = (M + Mb - 1) / Mb;
+
     auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
     auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
     auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
-    const long long strideA = (long long)Mg * Kg, strideB = (long long)Ng * Kg, strideC = (long long)Mg * Ng;
+    const long long strideA = (long long)Mbg * Kg, strideB = (long long)Ng * Kg, strideC = (long long)Mbg * Ng;
     auto* planesA = static_cast<std::int8_t*>(ws.get(kPlanesA, (std::size_t)nplanes * strideA));
     auto* planesB = static_cast<std::int8_t*>(ws.get(kPlanesB, (std::size_t)nplanes * strideB));
     auto* prod = static_cast<std::uint8_t*>(ws.get(kProducts, (std::size_t)nterms * strideC * term_bytes));
@@ -91,58 +101,73 @@ Output ozaki2_run(Device& D, const Problem& p) {
                          device_check(dev, oz_scale_f64(dev, dBf, (int)K, (int)N, (int)N, 1, 1, shift, dltB, flags + 1),
                                       "scale B");
                      }});
-    if (fp8) {
+    // B's planes once, then per band: A's planes, the products, the reconstruction of the band's rows
+    if (fp8)
         steps.push_back({ev::Slice, [=] {
-                             device_check(dev,
-                                          oz2_split_digits(dev, dAf, (int)M, (int)K, (int)K, 0, dltA, &ddesc, uA, 2,
-                                                           (int)Mg, (int)Kg, strideA),
-                                          "slice A");
                              device_check(dev,
                                           oz2_split_digits(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, &ddesc, uB, 3,
                                                            (int)Ng, (int)Kg, strideB),
                                           "slice B");
                          }});
-        steps.push_back({ev::Gemm, [=] {
-                             device_check(dev,
-                                          oz2_gemm_groups_f8(dev, uA, uB, terms, (int)Mg, (int)Ng, (int)Kg, &gdesc, 1,
-                                                             (int)Ng, strideA, strideB, strideC),
-                                          "products");
-                         }});
-        steps.push_back({ev::Recon, [=] {
-                             device_check(dev,
-                                          oz2_crt_terms_f64(dev, terms, (int)M, (int)N, (int)Ng, strideC, (int)nterms,
-                                                            term_mod.data(), &cdesc, dltA, dltB, out, (int)N),
-                                          "reconstruction");
-                         }});
-    } else {
+    else
         steps.push_back({ev::Slice, [=] {
-                             device_check(dev,
-                                          oz2_split_int8(dev, dAf, (int)M, (int)K, (int)K, 0, dltA, &mdesc, planesA, 2,
-                                                         (int)Mg, (int)Kg, strideA),
-                                          "slice A");
                              device_check(dev,
                                           oz2_split_int8(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, &mdesc, planesB, 3,
                                                          (int)Ng, (int)Kg, strideB),
                                           "slice B");
                          }});
-        steps.push_back({ev::Gemm, [=] {
-                             device_check(dev,
-                                          oz2_gemm_digits(dev, planesA, planesB, prod, (int)Mg, (int)Ng, (int)Kg,
-                                                          (int)S, (int)Ng, strideA, strideB, strideC, &cdesc),
-                                          "products");
-                         }});
-        steps.push_back({ev::Recon, [=] {
-                             device_check(dev,
-                                          oz2_crt_digits_f64(dev, prod, (int)M, (int)N, (int)Ng, strideC, &cdesc, dltA,
-                                                             dltB, out, (int)N),
-                                          "reconstruction");
-                         }});
+    for (std::uint32_t band = 0; band < nbands; band++) {
+        const std::uint32_t r0 = band * Mb, rows = std::min(Mb, M - r0), rowsg = round_up(rows, 256);
+        const double* Ab = dAf + (std::size_t)r0 * K;
+        const std::int32_t* dAb = dltA + r0;
+        double* ob = out + (std::size_t)r0 * N;
+        if (fp8) {
+            steps.push_back({ev::Slice, [=] {
+                                 device_check(dev,
+                                              oz2_split_digits(dev, Ab, (int)rows, (int)K, (int)K, 0, dAb, &ddesc, uA,
+                                                               2, (int)rowsg, (int)Kg, strideA),
+                                              "slice A");
+                             }});
+            steps.push_back({ev::Gemm, [=] {
+                                 device_check(dev,
+                                              oz2_gemm_groups_f8(dev, uA, uB, terms, (int)rowsg, (int)Ng, (int)Kg,
+                                                                 &gdesc, 1, (int)Ng, strideA, strideB, strideC),
+                                              "products");
+                             }});
+            steps.push_back({ev::Recon, [=] {
+                                 device_check(dev,
+                                              oz2_crt_terms_f64(dev, terms, (int)rows, (int)N, (int)Ng, strideC,
+                                                                (int)nterms, term_mod.data(), &cdesc, dAb, dltB, ob,
+                                                                (int)N),
+                                              "reconstruction");
+                             }});
+        } else {
+            steps.push_back({ev::Slice, [=] {
+                                 device_check(dev,
+                                              oz2_split_int8(dev, Ab, (int)rows, (int)K, (int)K, 0, dAb, &mdesc,
+                                                             planesA, 2, (int)rowsg, (int)Kg, strideA),
+                                              "slice A");
+                             }});
+            steps.push_back({ev::Gemm, [=] {
+                                 device_check(dev,
+                                              oz2_gemm_digits(dev, planesA, planesB, prod, (int)rowsg, (int)Ng,
+                                                              (int)Kg, (int)S, (int)Ng, strideA, strideB, strideC,
+                                                              &cdesc),
+                                              "products");
+                             }});
+            steps.push_back({ev::Recon, [=] {
+                                 device_check(dev,
+                                              oz2_crt_digits_f64(dev, prod, (int)rows, (int)N, (int)Ng, strideC,
+                                                                 &cdesc, dAb, dltB, ob, (int)N),
+                                              "reconstruction");
+                             }});
+        }
     }
     // products: one per modulus (INT8) or the FP8 route's digit products (sum of the outputs' pairs)
     const std::uint32_t nprod = fp8 ? (std::uint32_t)plan.mo.nprod : S;
 
     auto* host = static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, 2, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * nprod, nprod);
+    run_pipeline(dev, steps, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * nprod, nprod);
     Info info{Scheme::II, p.options.format};
     info.moduli = S;
     info.integer_bits = (std::uint32_t)plan.b;

@@ -11,9 +11,8 @@ namespace ozTTgemm::detail {
 
 namespace ev = ::ozTTgemm::evaluation;
 
-void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, std::size_t gemm_step, const double* out,
-                  double* host, std::size_t count, const std::uint32_t* flags, double product_ops,
-                  unsigned partial_products) {
+void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const double* out, double* host, std::size_t count,
+                  const std::uint32_t* flags, double product_ops, unsigned partial_products) {
     ev::Settings* es = ev::active();
     // Per-phase device times: events around every step (slots 24 + 2i, 25 + 2i), summed by phase.
     // The events are read after the pass, so each step needs its own pair.
@@ -43,7 +42,8 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, std::size_t gemm_
             for (auto& s : steps) s.issue();
         es->partial_products = partial_products;
         es->product_ops = product_ops;
-        es->gemm_launches = 1;
+        es->gemm_launches = 0;
+        for (auto& s : steps) es->gemm_launches += s.phase == ev::Gemm;
     }
     device_check(dev, oz_memcpy_d2h(dev, host, out, sizeof(double) * count), "read C");
     std::uint32_t fl[2];
@@ -65,7 +65,9 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, std::size_t gemm_
         device_check(dev, oz_memcpy_d2h(dev, again.data(), out, sizeof(double) * count), "read C");
         es->whole_checked = std::memcmp(again.data(), host, sizeof(double) * count) == 0;
         device_check(dev, oz_event_record(dev, 22), "event");
-        for (int r = 0; r < es->repeats; r++) steps[gemm_step].issue();
+        for (int r = 0; r < es->repeats; r++)
+            for (auto& s : steps)
+                if (s.phase == ev::Gemm) s.issue();
         device_check(dev, oz_event_record(dev, 23), "event");
         device_check(dev, oz_event_elapsed_ms(dev, 22, 23, &ms), "event time");
         es->gemm_launch_ms = ms / es->repeats;

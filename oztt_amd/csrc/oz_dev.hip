@@ -70,6 +70,12 @@ int oz_dev_malloc(oz_dev* dev, size_t bytes, void** ptr) {
     return oz::hip_check(dev, hipMalloc(ptr, bytes), "hipMalloc");
 }
 
+int oz_mem_info(oz_dev* dev, size_t* free_bytes, size_t* total_bytes) {
+    if (int st = oz::use(dev)) return st;
+    if (!free_bytes || !total_bytes) return oz::fail(dev, OZ_ERR_ARG, "oz_mem_info: null output pointer");
+    return oz::hip_check(dev, hipMemGetInfo(free_bytes, total_bytes), "hipMemGetInfo");
+}
+
 int oz_dev_free(oz_dev* dev, void* ptr) {
     if (int st = oz::use(dev)) return st;
     if (!ptr) return OZ_OK;

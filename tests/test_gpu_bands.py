@@ -1,0 +1,46 @@
+"""Row bands on the GPU (the reference's row bands when device memory runs short,
+ozaki2/plan.hpp:386-444).
+
+A band recomputes nothing that depends on the other rows: the row maxima of A are per row, the
+column maxima and the planes of B are computed once, and the plan comes from the whole operands.
+So C must be bit-identical whether the rows run in one band or in many. The evaluation hook
+max_band_rows forces bands of 256 rows (the band logic otherwise only engages when the workspace
+exceeds the device memory); M = 1000 leaves a ragged last band of 232 rows.
+"""
+import numpy as np
+import pytest
+
+import oztt_amd as oz
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = oz.Context()
+    yield c
+    c.close()
+
+
+CASES = [
+    ("II-INT8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8)),
+    ("II-FP8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8)),
+    ("I-INT8", oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8)),
+    ("I-BF16", oz.Options(scheme=oz.Scheme.I, format=oz.Format.BF16, slices=6)),
+]
+
+
+@pytest.mark.parametrize("name,opts", CASES, ids=[c[0] for c in CASES])
+def test_bands_bit_identical(ctx, name, opts):
+    m, n, k = 1000, 384, 512
+    a, b = oz.eval_inputs(11, 1.0, m * k, k * n)
+    c1, i1, e1 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=2)
+    c4, i4, e4 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=2, max_band_rows=256)
+    assert e1.gemm_launches == 1
+    assert e4.gemm_launches == 4  # 1024 padded rows: 256 + 256 + 256 + 232
+    assert e1.whole_checked and e4.whole_checked
+    assert (i1.moduli, i1.slices, i1.integer_bits) == (i4.moduli, i4.slices, i4.integer_bits)
+    np.testing.assert_array_equal(c4.view(np.uint64), c1.view(np.uint64))
+    # and the plain call (no evaluation hooks) gives the same C
+    c0 = ctx.multiply(a, b, m, n, k, opts)
+    np.testing.assert_array_equal(c0.view(np.uint64), c1.view(np.uint64))
