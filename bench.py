@@ -208,7 +208,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": C3_GEMM_TRAFFIC_BYTES if (headline and info.moduli == 17) else None,
-                     "kernel": ("gemm_f8_groups_kernel<1> (oz2_gemm_groups_f8)" if fmt == "FP8" else
+                     "kernel": ("gemm_f8_groups_kernel<TERMS> (oz2_gemm_groups_f8)" if fmt == "FP8" else
                                 "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II"
                                                     else "<DIAG> (oz1_gemm_diag_i8)")),
                      "launch_ms": round(gemm_ms, 4), "ops_per_launch": ev.product_ops},

@@ -178,7 +178,8 @@ int oz2_split_digits(oz_dev* dev, const double* X, int rows, int cols, int ld, i
  * Output o sums npairs digit products over the full K on the FP8 matrix cores (e4m3 x e4m3,
  * FP32 accumulation; exact while the sum stays below 2^24, which `bound` states and the entry
  * point checks):  P_o = sum_t A[a[t]] * Bt[b[t]]^T  (the reference's concatenation along K).
- * out_kind 0 stores P_o as int32 (M x N per output, element strides); out_kind 1 stores the CRT
+ * out_kind 0 stores P_o as int32 (M x N per output, element strides, out 16-byte aligned and ldo,
+ * strideO multiples of 4); out_kind 1 stores the CRT
  * term w_o = (coef * P_o) mod m in [0, m) as uint16, where coef is the composition coefficient
  * times y_s (mod m): for modulus s, sum over its outputs of w_o == D_s * y_s (mod m_s), D_s the
  * composed residue. A and Bt are e4m3 digit planes of oz2_split_digits (layouts 2 and 3);
