@@ -36,7 +36,7 @@ struct GroupArgs {
     struct G {
         unsigned char a[4], b[4];
         uint32_t np_m;  // npairs << 16 | m
-        uint32_t coef, magic;
+        uint32_t coef;
     } g[OZ2_MAXOUT];
 };
 
@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(THREADS) gemm_f8_groups_kernel(const uint8_t* 
     __syncthreads();
     float* tile = reinterpret_cast<float*>(lds) + wave * (64 * 128);
     const long long c0 = (long long)o * sO + (long long)(tm * BM + wm * 128) * ldo + tn * BN + wn * 128;
-    const uint32_t m = g.np_m & 0xFFFFu, coef = g.coef, mg = g.magic;
+    const double md = (double)(g.np_m & 0xFFFFu), cf = (double)g.coef, rinv = 1.0 / md;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
 #pragma unroll
@@ -227,19 +227,20 @@ __global__ void __launch_bounds__(THREADS) gemm_f8_groups_kernel(const uint8_t* 
             const int e = 64 * t + lane, row = e >> 4, cg = e & 15;
             const float* src = tile + row * 128 + ((8 * cg) ^ (32 * ((row >> 2) & 1)));
             const v4f v0 = *reinterpret_cast<const v4f*>(src), v1 = *reinterpret_cast<const v4f*>(src + 4);
-            const int32_t s[8] = {(int32_t)v0[0], (int32_t)v0[1], (int32_t)v0[2], (int32_t)v0[3],
-                                  (int32_t)v1[0], (int32_t)v1[1], (int32_t)v1[2], (int32_t)v1[3]};
             const long long at = c0 + (long long)(64 * h + row) * ldo + 8 * cg;
             if constexpr (KIND == 1) {
+                // |P_o| < 2^24 and coef < m <= 2401: |P_o coef| < 2^36, within mod_mul_f64's range
+                const float s[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 uint32_t w[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++)
-                    w[k] = oz2::crt_digit(s[2 * k], m, coef, mg) | oz2::crt_digit(s[2 * k + 1], m, coef, mg) << 16;
+                    w[k] = oz2::mod_mul_f64((double)s[2 * k], cf, md, rinv) |
+                           oz2::mod_mul_f64((double)s[2 * k + 1], cf, md, rinv) << 16;
                 *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + at) = uint4{w[0], w[1], w[2], w[3]};
             } else {
                 int32_t* d = static_cast<int32_t*>(out) + at;
-                *reinterpret_cast<v4i*>(d) = v4i{s[0], s[1], s[2], s[3]};
-                *reinterpret_cast<v4i*>(d + 4) = v4i{s[4], s[5], s[6], s[7]};
+                *reinterpret_cast<v4i*>(d) = v4i{(int32_t)v0[0], (int32_t)v0[1], (int32_t)v0[2], (int32_t)v0[3]};
+                *reinterpret_cast<v4i*>(d + 4) = v4i{(int32_t)v1[0], (int32_t)v1[1], (int32_t)v1[2], (int32_t)v1[3]};
             }
         }
     }
@@ -281,7 +282,6 @@ extern "C" int oz2_gemm_groups_f8(oz_dev* dev, const uint8_t* A, const uint8_t* 
                             (double)g.bound);
         ga.g[o].np_m = ((uint32_t)g.npairs << 16) | g.m;
         ga.g[o].coef = g.coef;
-        ga.g[o].magic = (uint32_t)(0x100000000ull / g.m);
     }
     const int tiles_m = M / BM, tiles_n = N / BN;
     const unsigned grid = (unsigned)((long long)tiles_m * tiles_n * gd->nout);

@@ -37,7 +37,7 @@ namespace {
 using namespace ozg;
 
 // Output modes. PRODUCTS: C[b] = A[b] Bt[b]^T as int32. DIGITS: the same products reduced in the
-// epilogue to the CRT digit for modulus b (oz2::crt_digit with dc.m/y/magic[b]), C as uint8. DIAG
+// epilogue to the CRT digit for modulus b ((C mod m_b) y_b mod m_b, from dc.m/y[b]), C as uint8. DIAG
 // (scheme I): C[d] = sum_{i <= d} A[i] Bt[d-i]^T as int32 for the diagonals d < nbatch, the d+1
 // slice pairs concatenated along K in one accumulation.
 enum GemmMode { PRODUCTS = 0, DIGITS = 1, DIAG = 2 };
@@ -206,15 +206,16 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
         // consecutive sums, reduces them to digits and stores them as one 16-byte chunk.
         __syncthreads();
         int32_t* tile = reinterpret_cast<int32_t*>(lds) + wave * (64 * 128);
-        uint32_t m = 0, y = 0, mg = 0;
+        uint32_t m = 2, y = 0;
 #pragma unroll
         for (int s = 0; s < OZ2_MAXS; s++)
             if (s == batch) {
                 m = dc.m[s];
                 y = dc.y[s];
-                mg = dc.magic[s];
             }
         uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
+        const double md = (double)m, yd = (double)y, rinv = 1.0 / md;
+        auto dg = [&](int32_t c) -> uint32_t { return oz2::mod_mul_f64((double)c, yd, md, rinv); };
 #pragma unroll
         for (int h = 0; h < 2; h++) {
 #pragma unroll
@@ -234,8 +235,7 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const v4i v = *reinterpret_cast<const v4i*>(src + 4 * k);
-                    w[k] = oz2::crt_digit(v[0], m, y, mg) | oz2::crt_digit(v[1], m, y, mg) << 8 |
-                           oz2::crt_digit(v[2], m, y, mg) << 16 | oz2::crt_digit(v[3], m, y, mg) << 24;
+                    w[k] = dg(v[0]) | dg(v[1]) << 8 | dg(v[2]) << 16 | dg(v[3]) << 24;
                 }
                 *reinterpret_cast<uint4*>(Cb + (long long)(64 * h + row) * ldc + 16 * cg) = uint4{w[0], w[1], w[2], w[3]};
             }
@@ -303,7 +303,6 @@ extern "C" int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, u
         if (m < 2 || m > 255 || crt->y[s] >= m) return oz::fail(dev, OZ_ERR_ARG, "oz2_gemm_digits: bad modulus %u", m);
         dc.m[s] = m;
         dc.y[s] = crt->y[s];
-        dc.magic[s] = (uint32_t)(0x100000000ull / m);
     }
     return launch_gemm<DIGITS>(dev, A, Bt, D, M, N, K, S, ldd, strideA, strideB, strideD, dc);
 }

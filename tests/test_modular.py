@@ -1,0 +1,64 @@
+"""The FP64 modular product of the product kernels' epilogues (oz2::mod_mul_f64 in
+oztt_amd/csrc/oz2_modular.hpp), emulated with numpy's IEEE binary64 operations and checked against
+exact integer arithmetic.
+
+The device function computes r = x - floor(RN(x * RN(1/m))) * m for x = c * y, then maps r = m to 0.
+Its FMA rounds an exact small integer, so plain binary64 subtraction of the exact product q * m
+(an integer below 2^40) gives the same value here. The kernels use it for the CRT digit of an int32
+product (|c| < 2^31, y < m <= 255: reference recon_crt.cpp:293's residue step) and for the FP8
+route's terms (|P| < 2^24, coef < m <= 2401). CPU only.
+"""
+import numpy as np
+
+
+def mod_mul_f64(c: np.ndarray, y: np.ndarray, m: np.ndarray) -> np.ndarray:
+    x = c.astype(np.float64) * y.astype(np.float64)
+    md = m.astype(np.float64)
+    rinv = 1.0 / md
+    r = x - np.floor(x * rinv) * md
+    return np.where(r >= md, r - md, r).astype(np.int64)
+
+
+def _check(c, y, m):
+    got = mod_mul_f64(c, y, m)
+    want = np.array([(int(a) * int(b)) % int(q) for a, b, q in zip(c, y, m)], dtype=np.int64)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_int8_digit_range_random():
+    rng = np.random.default_rng(7)
+    n = 200_000
+    m = rng.integers(2, 256, n)
+    y = rng.integers(0, 1 << 30, n) % m
+    c = rng.integers(-(1 << 31), 1 << 31, n)
+    _check(c, y, m)
+
+
+def test_fp8_term_range_random():
+    rng = np.random.default_rng(8)
+    n = 200_000
+    m = rng.integers(2, 2402, n)
+    y = rng.integers(0, 1 << 30, n) % m
+    c = rng.integers(-(1 << 24) + 1, 1 << 24, n)
+    _check(c, y, m)
+
+
+def test_exact_multiples_and_extremes():
+    # x/m an integer: the floor may land one below, the select must map r = m back to 0
+    rows = []
+    for m in (2, 3, 5, 7, 127, 251, 253, 255, 256, 1021, 2401):
+        for y in (1, 2, m - 1, (m - 1) // 2 or 1):
+            for c in (0, m, -m, 3 * m, -(3 * m), (2**31 - 1) // m * m, -((2**31) // m) * m,
+                      2**31 - 1, -(2**31), 2**31 - 2, -(2**31) + 1, (1 << 24) - 1, -(1 << 24) + 1):
+                rows.append((c, y, m))
+    c, y, m = (np.array(v, dtype=np.int64) for v in zip(*rows))
+    _check(c, y, m)
+
+
+def test_every_product_for_small_moduli():
+    # all residues c mod m and all y < m, for a few moduli, shifted by large multiples of m
+    for m in (2, 9, 251, 255):
+        c0 = np.arange(m, dtype=np.int64)
+        cc, yy = np.meshgrid(c0, np.arange(m, dtype=np.int64))
+        for shift in (0, (2**31 - m) // m * m, -((2**31) // m) * m):
+            _check(cc.ravel() + shift, yy.ravel(), np.full(cc.size, m))
