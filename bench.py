@@ -20,8 +20,8 @@ value = 2*m*n*k / (time of one whole pass)  [effective FP64 TFLOP/s]
 Also reported: accuracy against binary128 on a 64x64 sample of C at full K (and the same numbers
 for a native FP64 dot product), the per-phase device times, the roofline of the product kernel
 (algorithmic int8 operations per launch / its average launch time, against 5.0 POP/s dense INT8),
-and the reference's host OpenMP Dot2 GEMM (the oracle's restatement) timed on this host on a row
-slab of the same problem.
+the reference's host OpenMP Dot2 GEMM (the oracle's restatement) timed on this host on a row
+slab of the same problem, and the GPU's own FP64 GEMM (rocBLAS dgemm) on the same operands.
 """
 from __future__ import annotations
 
@@ -91,6 +91,54 @@ def copy_probe(nbytes: int) -> int:
     dev.sync()
     print(json.dumps({"copy_probe_bytes": nbytes, "launches": 3}), flush=True)
     return 0
+
+
+def native_fp64_gemm(a, b, m: int, n: int, k: int, reps: int = 3) -> dict:
+    """The GPU's own FP64 GEMM on the same operands, as a yardstick for `value`: rocBLAS dgemm (its
+    kernels on the FP64 matrix cores) on device-resident operands, timed with HIP events over `reps`
+    calls after one warm-up call. Row 0 of the result is checked against numpy."""
+    import ctypes
+    try:
+        hiprt = ctypes.CDLL("libamdhip64.so")
+        rb = ctypes.CDLL("librocblas.so")
+    except OSError as e:
+        return {"error": str(e)}
+    from oztt_amd.device import Device
+    dev = Device(0)
+    h = ctypes.c_void_p()
+    try:
+        bA, bB, bC = dev.upload(a), dev.upload(b), dev.alloc(8 * m * n)
+        if rb.rocblas_create_handle(ctypes.byref(h)) != 0:
+            return {"error": "rocblas_create_handle failed"}
+        alpha, beta = ctypes.c_double(1.0), ctypes.c_double(0.0)
+        none = 111  # rocblas_operation_none
+        # row-major C = A B is the column-major product C^T = B^T A^T: (n x k) times (k x m)
+        call = lambda: rb.rocblas_dgemm(h, none, none, n, m, k, ctypes.byref(alpha), bB.ptr, n, bA.ptr, k,
+                                        ctypes.byref(beta), bC.ptr, n)
+        if call() != 0:
+            return {"error": "rocblas_dgemm failed"}
+        hiprt.hipDeviceSynchronize()
+        e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+        hiprt.hipEventCreate(ctypes.byref(e0))
+        hiprt.hipEventCreate(ctypes.byref(e1))
+        hiprt.hipEventRecord(e0, None)
+        for _ in range(reps):
+            call()
+        hiprt.hipEventRecord(e1, None)
+        hiprt.hipEventSynchronize(e1)
+        t = ctypes.c_float()
+        hiprt.hipEventElapsedTime(ctypes.byref(t), e0, e1)
+        hiprt.hipEventDestroy(e0)
+        hiprt.hipEventDestroy(e1)
+        ms = t.value / reps
+        row0 = dev.download(bC, np.float64, n)
+        ok = bool(np.allclose(row0, a[:k] @ b.reshape(k, n), rtol=1e-10, atol=1e-300))
+        return {"library": "rocBLAS dgemm", "ms": round(ms, 4), "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 3),
+                "row0_checked": ok}
+    finally:
+        if h:
+            rb.rocblas_destroy_handle(h)
+        dev.close()
 
 
 # BASELINE.json configs: name -> (scheme, format, m, n, k, seed, phi, options, peak of the product format, rows of
@@ -223,6 +271,8 @@ def main() -> int:
                                   "value": round(2.0 * m * n * k / (e8.whole_ms * 1e-3) / 1e12, 3),
                                   "identical_output": bool(np.array_equal(c8.view(np.uint64), c.view(np.uint64)))}
         del c8
+    log("native FP64 GEMM on the GPU (rocBLAS dgemm)")
+    out["native_fp64_gemm"] = native_fp64_gemm(a, b, m, n, k)
     if cpu_rows > 0:
         log(f"CPU baseline: Dot2 on {cpu_rows} rows")
         out["cpu_baseline"], hi, lo = cpu_baseline(a, b, m, n, k, cpu_rows)
