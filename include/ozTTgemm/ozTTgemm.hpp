@@ -71,6 +71,27 @@ bool is_available(Format format) noexcept;
 // "BF16", "FP16", "TF32", "BFP8", "FP8", "INT8", "BFP4" or "BFP2".
 const char* format_name(Format format) noexcept;
 
+class Context;
+
+// A matrix kept on the GPU of a Context between calls: an extension of the reference's interface,
+// which takes host spans only and moves and plans everything per call. A Matrix is immutable; it is
+// made by Context::upload or as the result of Context::gemm, and belongs to that Context (using it
+// with another Context throws std::invalid_argument). Copies share the same matrix. It may outlive
+// its Context: the GPU stays open until the last Matrix is gone.
+class Matrix {
+public:
+    Matrix() = default;  // empty
+    std::size_t rows() const noexcept;
+    std::size_t cols() const noexcept;
+    explicit operator bool() const noexcept { return static_cast<bool>(s_); }
+
+    struct State;  // opaque
+
+private:
+    friend class Context;
+    std::shared_ptr<State> s_;
+};
+
 // Owns one GPU, opened lazily by the first valid GEMM. Calls through all contexts of a process are
 // serialized.
 class Context {
@@ -96,6 +117,23 @@ public:
     // Same as gemm(), returning C as a new vector.
     std::vector<double> multiply(std::span<const double> a, std::span<const double> b, std::size_t m, std::size_t n,
                                  std::size_t k, const Options& options = {});
+
+    // ---- resident operands (extension) -------------------------------------------------------
+    // Copies the row-major rows x cols matrix x to the GPU. Throws std::invalid_argument for zero or
+    // mismatched dimensions and for NaN or infinite entries, std::runtime_error when the GPU cannot
+    // be used.
+    Matrix upload(std::span<const double> x, std::size_t rows, std::size_t cols);
+    // C = A*B with A = a (m x k) and B = b (k x n) on the GPU: the same result, bit for bit, and the
+    // same Info as gemm() on the host copies of a and b, with the same checks (the row maxima of a
+    // and the column maxima of b in [2^-126, largest finite BF16]). Nothing is moved over PCIe but C
+    // (none of it for the second form), and the plan of the pair (a, b) for these options is kept,
+    // so later calls on the same pair skip the host planning.
+    Info gemm(const Matrix& a, const Matrix& b, std::span<double> c, const Options& options = {});
+    // Same, with C kept on the GPU as a new Matrix in c (its previous matrix, if c was the only
+    // holder of it and it has C's shape, lends its device memory).
+    Info gemm(const Matrix& a, const Matrix& b, Matrix& c, const Options& options = {});
+    // Copies x back into out (rows*cols elements, row-major).
+    void download(const Matrix& x, std::span<double> out);
 
 private:
     struct Impl;

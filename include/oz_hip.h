@@ -60,6 +60,11 @@ int oz_memcpy_h2d_async(oz_dev* dev, void* dst, const void* src, size_t bytes);
 /* Device-to-device copy by a plain streaming kernel (16-byte aligned pointers and size); also the
  * reference transfer for calibrating HBM traffic counters. */
 int oz_memcpy_d2d(oz_dev* dev, void* dst, const void* src, size_t bytes);
+/* dst (drows x dcols, row-major, leading dimension dcols) = the top-left min(drows, srows) x
+ * min(dcols, scols) of src (srows x scols, leading dimension sld), zero elsewhere; stream-ordered.
+ * No counterpart in the reference: it lays out the resident operands (ozTTgemm::Matrix) in the
+ * zero-padded shapes of the products. */
+int oz_pad_copy_f64(oz_dev* dev, double* dst, int drows, int dcols, const double* src, int srows, int scols, int sld);
 int oz_sync(oz_dev* dev);
 /* Stream-ordered timing (64 event slots per handle). */
 int oz_event_record(oz_dev* dev, int slot);

@@ -81,7 +81,7 @@ class EvalStats(ctypes.Structure):
                 ("phase_ms", ctypes.c_double * 5), ("whole_ms", ctypes.c_double), ("whole_checked", ctypes.c_int),
                 ("partial_products", ctypes.c_uint), ("product_ops", ctypes.c_double),
                 ("gemm_launch_ms", ctypes.c_double), ("gemm_launches", ctypes.c_int),
-                ("max_band_rows", ctypes.c_uint)]
+                ("max_band_rows", ctypes.c_uint), ("plan_reused", ctypes.c_int)]
 
 
 class Plan2(ctypes.Structure):
@@ -132,6 +132,7 @@ def host() -> ctypes.CDLL:
         h = _load("libozTTgemm.so")
         h.ozt_format_name.restype = ctypes.c_char_p
         h.ozt_eval_hash.restype = ctypes.c_ulonglong
+        h.ozt_matrix_new.restype = ctypes.c_void_p
         _host = h
     return _host
 
@@ -158,6 +159,34 @@ def _f64(x) -> np.ndarray:
 
 def _ptr(a: np.ndarray) -> ctypes.c_void_p:
     return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Matrix:
+    """A matrix kept on the GPU of a Context between calls (ozTTgemm::Matrix, an extension of the
+    reference's interface). Made by Context.upload, or filled as the result of Context.gemm_resident
+    (pass an empty Matrix() as c)."""
+
+    def __init__(self):
+        self._m = ctypes.c_void_p(host().ozt_matrix_new())
+        if not self._m:
+            raise MemoryError("ozt_matrix_new")
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        r, c = ctypes.c_size_t(), ctypes.c_size_t()
+        host().ozt_matrix_dims(self._m, ctypes.byref(r), ctypes.byref(c))
+        return r.value, c.value
+
+    def close(self) -> None:
+        if self._m:
+            host().ozt_matrix_free(self._m)
+            self._m = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Context:
@@ -222,6 +251,47 @@ class Context:
         ev.max_band_rows = max_band_rows
         info = self._call(a, b, c, m, n, k, options, ev)
         return c, info, ev
+
+
+    # ---- resident operands (extension) --------------------------------------------------------
+    def upload(self, x, rows: int, cols: int) -> Matrix:
+        """Copies the row-major rows x cols float64 matrix x to the GPU (Context::upload)."""
+        x = _f64(x)
+        m = Matrix()
+        err = ctypes.create_string_buffer(2048)
+        _raise(host().ozt_upload(self._ctx, _ptr(x), ctypes.c_size_t(x.size), ctypes.c_size_t(rows),
+                                 ctypes.c_size_t(cols), m._m, err, ctypes.c_size_t(2048)), err)
+        return m
+
+    def download(self, m: Matrix) -> np.ndarray:
+        rows, cols = m.shape
+        out = np.empty(rows * cols, dtype=np.float64)
+        err = ctypes.create_string_buffer(2048)
+        _raise(host().ozt_download(self._ctx, m._m, _ptr(out), ctypes.c_size_t(out.size), err,
+                                   ctypes.c_size_t(2048)), err)
+        return out
+
+    def gemm_resident(self, a: Matrix, b: Matrix, c, options: Options | None = None,
+                      evaluation: EvalStats | None = None) -> Info:
+        """C = A*B for resident a, b (Context::gemm on Matrix operands): c is a contiguous float64 array
+        of m*n elements (C read back) or a Matrix (C stays on the GPU; an empty Matrix() receives it).
+        With an EvalStats the call runs under the evaluation hooks."""
+        o = options or Options()
+        err = ctypes.create_string_buffer(4096)
+        info = _Info()
+        if isinstance(c, Matrix):
+            cptr, nc, cm = ctypes.c_void_p(), 0, c._m
+        else:
+            if not (isinstance(c, np.ndarray) and c.dtype == np.float64 and c.flags.c_contiguous):
+                raise ValueError("c must be a Matrix or a contiguous float64 numpy array")
+            cptr, nc, cm = _ptr(c), c.size, ctypes.c_void_p()
+        _raise(host().ozt_gemm_resident(self._ctx, a._m, b._m, cptr, ctypes.c_size_t(nc), cm, int(o.scheme),
+                                        int(o.format), ctypes.c_uint(o.slices), ctypes.c_uint(o.max_moduli),
+                                        int(o.reconstruction), ctypes.byref(info),
+                                        ctypes.byref(evaluation) if evaluation is not None else None, err,
+                                        ctypes.c_size_t(4096)), err)
+        return Info(Scheme(info.scheme), Format(info.format), info.slices, info.moduli, info.integer_bits,
+                    info.reconstruction_passes, info.padded_m, info.padded_n, info.padded_k)
 
 
 def plan2(a, b, M: int, N: int, K: int, fmt: Format = Format.INT8, max_moduli: int = 0,

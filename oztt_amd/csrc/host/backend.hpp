@@ -71,17 +71,26 @@ std::uint32_t band_rows(Device& D, std::uint32_t M, std::size_t fixed, std::size
 
 // One GEMM after validation and zero padding: A is m x k and B is k x n, row-major, with m and n
 // multiples of 64 and k a multiple of 32 (backend_interface.hpp:21-26). The operands are in the
-// workspace's page-locked staging buffers.
+// workspace's page-locked staging buffers (a, b: what the planner reads).
+// Resident operands (Context::Matrix) add device copies in the same padded layout (a_dev, b_dev:
+// the backend then uploads nothing) and may bring the plan made for them earlier (plan: the
+// planner is skipped, and a and b may be null); c_dev receives the padded m x n result on the
+// device instead of the host staging.
 struct Problem {
     std::uint32_t m, n, k;
     const double* a;
     const double* b;
     const Options& options;
+    const double* a_dev = nullptr;
+    const double* b_dev = nullptr;
+    double* c_dev = nullptr;
+    std::shared_ptr<const void> plan;  // a Plan1 (scheme I) or Plan2 (scheme II) of this backend
 };
 
 struct Output {
-    const double* values;  // padded m x n, row-major, in the workspace's host staging (kHostC)
+    const double* values;  // padded m x n, row-major, in the workspace's host staging (kHostC); null with c_dev
     Info info;
+    std::shared_ptr<const void> plan;  // the plan the call ran (for the Context's cache)
 };
 
 using Backend = Output (*)(Device&, const Problem&);

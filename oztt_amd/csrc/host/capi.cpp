@@ -74,6 +74,7 @@ struct ozt_eval {
     double gemm_launch_ms;
     int gemm_launches;
     unsigned max_band_rows;  // input: cap on the rows of a band (0: bands only when memory requires)
+    int plan_reused;         // resident operands: the plan kept from an earlier call was used
 };
 
 struct ozt_plan2 {
@@ -138,6 +139,62 @@ int ozt_gemm(void* ctx, const double* a, std::size_t na, const double* b, std::s
     });
 }
 
+// ---- resident operands (ozTTgemm::Matrix) -----------------------------------------------------
+void* ozt_matrix_new() { return new (std::nothrow) ozTTgemm::Matrix(); }
+void ozt_matrix_free(void* m) { delete static_cast<ozTTgemm::Matrix*>(m); }
+void ozt_matrix_dims(void* m, std::size_t* rows, std::size_t* cols) {
+    const auto* x = static_cast<const ozTTgemm::Matrix*>(m);
+    *rows = x->rows();
+    *cols = x->cols();
+}
+
+int ozt_upload(void* ctx, const double* x, std::size_t n, std::size_t rows, std::size_t cols, void* m, char* err,
+               std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        *static_cast<ozTTgemm::Matrix*>(m) = static_cast<ozTTgemm::Context*>(ctx)->upload({x, n}, rows, cols);
+    });
+}
+
+int ozt_download(void* ctx, void* m, double* out, std::size_t n, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        static_cast<ozTTgemm::Context*>(ctx)->download(*static_cast<const ozTTgemm::Matrix*>(m), {out, n});
+    });
+}
+
+static void fill_eval(const ozTTgemm::evaluation::Settings& s, ozt_eval* evo);
+
+// C = A B for resident A and B: into the host array c (nc elements) when cm is null, else into the
+// Matrix cm. evo, when not null, runs the call under the evaluation hooks.
+int ozt_gemm_resident(void* ctx, void* a, void* b, double* c, std::size_t nc, void* cm, int scheme, int format,
+                      unsigned slices, unsigned max_moduli, int recon, ozt_info* info, ozt_eval* evo, char* err,
+                      std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        auto* cx = static_cast<ozTTgemm::Context*>(ctx);
+        const auto& A = *static_cast<const ozTTgemm::Matrix*>(a);
+        const auto& B = *static_cast<const ozTTgemm::Matrix*>(b);
+        const auto o = make_options(scheme, format, slices, max_moduli, recon);
+        auto run = [&] {
+            return cm ? cx->gemm(A, B, *static_cast<ozTTgemm::Matrix*>(cm), o) : cx->gemm(A, B, {c, nc}, o);
+        };
+        ozTTgemm::Info i;
+        if (evo) {
+            ozTTgemm::evaluation::Settings s;
+            s.fixed_bits = evo->fixed_bits;
+            s.warmup = evo->warmup;
+            s.repeats = evo->repeats;
+            s.max_band_rows = evo->max_band_rows;
+            {
+                ozTTgemm::evaluation::Scope scope(s);
+                i = run();
+            }
+            fill_eval(s, evo);
+        } else {
+            i = run();
+        }
+        fill_info(i, info);
+    });
+}
+
 int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, std::size_t nb, double* c,
                   std::size_t nc, std::size_t m, std::size_t n, std::size_t k, int scheme, int format, unsigned slices,
                   unsigned max_moduli, int recon, ozt_info* info, ozt_eval* evo, char* err, std::size_t errlen) {
@@ -154,14 +211,19 @@ int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, s
             i = cx->gemm({a, na}, {b, nb}, {c, nc}, m, n, k, make_options(scheme, format, slices, max_moduli, recon));
         }
         fill_info(i, info);
-        for (int p = 0; p < 5; p++) evo->phase_ms[p] = s.phase_ms[p];
-        evo->whole_ms = s.whole_ms;
-        evo->whole_checked = s.whole_checked ? 1 : 0;
-        evo->partial_products = s.partial_products;
-        evo->product_ops = s.product_ops;
-        evo->gemm_launch_ms = s.gemm_launch_ms;
-        evo->gemm_launches = s.gemm_launches;
+        fill_eval(s, evo);
     });
+}
+
+static void fill_eval(const ozTTgemm::evaluation::Settings& s, ozt_eval* evo) {
+    for (int p = 0; p < 5; p++) evo->phase_ms[p] = s.phase_ms[p];
+    evo->whole_ms = s.whole_ms;
+    evo->whole_checked = s.whole_checked ? 1 : 0;
+    evo->partial_products = s.partial_products;
+    evo->product_ops = s.product_ops;
+    evo->gemm_launch_ms = s.gemm_launch_ms;
+    evo->gemm_launches = s.gemm_launches;
+    evo->plan_reused = s.plan_reused ? 1 : 0;
 }
 
 int ozt_is_available(int format) { return ozTTgemm::is_available(static_cast<ozTTgemm::Format>(format)) ? 1 : 0; }

@@ -2,7 +2,10 @@
 // Semantics of the reference's context.cpp:19-194: the same checks in the same order, the same
 // exception types, padding of m and n to multiples of 64 and k to a multiple of 32, inputs copied
 // before the lock so that C may alias A or B, one process-wide lock, the device opened lazily.
+// Resident operands (Matrix, an extension) keep device copies in the padded layouts of the
+// products, a host copy for the planner, and the plans of the pairs they were multiplied in.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <filesystem>
 #include <limits>
@@ -12,10 +15,14 @@
 #include <string>
 
 #include "backend.hpp"
+#include "evaluation.hpp"
 
 namespace ozTTgemm {
 namespace {
-std::mutex runtime_mutex;  // serializes device use by all contexts of the process
+// Serializes device use by all contexts of the process. Recursive: a resident Matrix frees its
+// device memory under it, and may be released while the lock is held.
+std::recursive_mutex runtime_mutex;
+std::atomic<std::uint64_t> next_matrix_id{1};
 
 std::size_t checked_product(std::size_t a, std::size_t b) {
     if (a == 0 || b == 0 || a > std::numeric_limits<std::size_t>::max() / sizeof(double) / b)
@@ -85,7 +92,100 @@ Checked validate(const Options& options, std::span<const double> a, std::span<co
     check_values(a, b, m, n, k);
     return v;
 }
+
 }  // namespace
+
+namespace detail {
+// The opened GPU, shared by a Context and its resident matrices; it is closed by the last of them
+// (always under runtime_mutex).
+struct DeviceHandle {
+    oz_dev* dev = nullptr;
+    ~DeviceHandle() {
+        if (dev) oz_dev_close(dev);
+    }
+};
+
+// What the checks of gemm() need to know about a resident operand (check_values on its host copy).
+struct Facts {
+    bool finite = true, rows_ok = true, cols_ok = true;
+};
+Facts facts_of(const double* x, std::size_t rows, std::size_t cols) {
+    constexpr double maximum = 0x1.fep127, minimum = 0x1p-126;
+    auto ok = [&](double v) { return v == 0 || (v >= minimum && v <= maximum); };
+    bool finite = true, rows_ok = true;
+    std::vector<double> colmax(cols, 0);
+    // rows in parallel; each thread keeps its own column maxima (maxima do not depend on the order)
+#pragma omp parallel
+    {
+        std::vector<double> cm(cols, 0);
+        bool fin = true, rok = true;
+#pragma omp for schedule(static) nowait
+        for (std::int64_t i = 0; i < (std::int64_t)rows; ++i) {
+            const double* r = x + (std::size_t)i * cols;
+            double mx = 0;
+            for (std::size_t j = 0; j < cols; ++j) {
+                const double v = r[j];
+                fin = fin && std::isfinite(v);
+                const double av = std::abs(v);
+                mx = std::max(mx, av);
+                cm[j] = std::max(cm[j], av);
+            }
+            rok = rok && ok(mx);
+        }
+#pragma omp critical
+        {
+            finite = finite && fin;
+            rows_ok = rows_ok && rok;
+            for (std::size_t j = 0; j < cols; ++j) colmax[j] = std::max(colmax[j], cm[j]);
+        }
+    }
+    Facts f;
+    f.finite = finite;
+    f.rows_ok = rows_ok;
+    for (double v : colmax) f.cols_ok = f.cols_ok && ok(v);
+    return f;
+}
+}  // namespace detail
+
+using detail::DeviceHandle;
+using detail::Facts;
+using detail::facts_of;
+
+struct Matrix::State {
+    std::uint64_t id = 0;
+    const void* owner = nullptr;  // the Context::Impl that made it
+    std::shared_ptr<DeviceHandle> device;
+    std::size_t rows = 0, cols = 0;
+    // host copy (row-major rows x cols) and its facts; a result has them only once it is needed
+    std::unique_ptr<double[]> host;
+    bool have_host = false;
+    Facts facts;
+    // device copies: the first one (src, leading dimension src_ld) and the zero-padded layouts
+    // (prow x pcol, leading dimension pcol) made from it; src is one of them or the raw upload
+    struct Copy {
+        std::uint32_t prow, pcol;
+        double* p;
+    };
+    double* raw = nullptr;
+    const double* src = nullptr;
+    std::size_t src_ld = 0;
+    std::vector<Copy> copies;
+    // zero-padded host copies for the planner, by layout
+    std::vector<std::pair<std::pair<std::uint32_t, std::uint32_t>, std::unique_ptr<double[]>>> padded_host;
+
+    ~State() {
+        std::lock_guard lock(runtime_mutex);
+        if (device && device->dev) {
+            for (auto& c : copies) oz_dev_free(device->dev, c.p);
+            if (raw) oz_dev_free(device->dev, raw);
+        }
+        copies.clear();
+        device.reset();
+    }
+};
+
+std::size_t Matrix::rows() const noexcept { return s_ ? s_->rows : 0; }
+std::size_t Matrix::cols() const noexcept { return s_ ? s_->cols : 0; }
 
 struct Context::Impl {
     explicit Impl(DeviceOptions o) : options(std::move(o)) {
@@ -95,7 +195,29 @@ struct Context::Impl {
     }
     Info execute(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m,
                  std::size_t n, std::size_t k, const Options& options, const Checked& v);
+    void open();
+    // resident operands (under the lock)
+    const double* layout(Matrix::State& x, std::uint32_t prow, std::uint32_t pcol);
+    void fetch_host(Matrix::State& x);
+    const double* padded_host(Matrix::State& x, std::uint32_t prow, std::uint32_t pcol);
+    Info resident(Matrix::State& A, Matrix::State& B, std::span<double>* c, std::shared_ptr<Matrix::State>* cslot,
+                  const Options& opts);
+
+    // plans of resident pairs, most recent last
+    struct CachedPlan {
+        std::uint64_t a, b;
+        Scheme scheme;
+        Format format;
+        std::uint32_t slices, max_moduli;
+        Reconstruction reconstruction;
+        std::shared_ptr<const void> plan;
+    };
+    static constexpr std::size_t kPlanCacheSize = 16;
+    std::vector<CachedPlan> plans;
+    std::size_t plan_hits = 0;
+
     DeviceOptions options;
+    std::shared_ptr<DeviceHandle> handle;
     detail::Device device;
 };
 
@@ -105,24 +227,29 @@ Context::~Context() {
     std::lock_guard lock(runtime_mutex);
     if (impl_->device.dev) {
         impl_->device.ws.reset();  // frees the workspace
-        oz_dev_close(impl_->device.dev);
         impl_->device.dev = nullptr;
+        impl_->handle.reset();  // closes the GPU unless resident matrices still hold it
     }
+}
+
+void Context::Impl::open() {
+    if (device.dev) return;
+    oz_dev* d = nullptr;
+    const int st = oz_dev_open(options.device_id, &d);
+    if (st != OZ_OK)
+        throw std::runtime_error("could not open HIP device " + std::to_string(options.device_id) +
+                                 " (no MI355X visible, or the device id is out of range)");
+    handle = std::make_shared<DeviceHandle>();
+    handle->dev = d;
+    device.dev = d;
+    device.ws = std::make_unique<detail::Workspace>(d);
 }
 
 Info Context::Impl::execute(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m,
                             std::size_t n, std::size_t k, const Options& opts, const Checked& v) {
     const auto mp = v.mp, np = v.np, kp = v.kp;
     std::lock_guard lock(runtime_mutex);
-    if (!device.dev) {
-        oz_dev* d = nullptr;
-        const int st = oz_dev_open(options.device_id, &d);
-        if (st != OZ_OK)
-            throw std::runtime_error("could not open HIP device " + std::to_string(options.device_id) +
-                                     " (no MI355X visible, or the device id is out of range)");
-        device.dev = d;
-        device.ws = std::make_unique<detail::Workspace>(d);
-    }
+    open();
     // zero-padded copies into the page-locked staging buffers (rows in parallel); they are complete
     // before C is written, so C may alias A or B
     auto* ap = static_cast<double*>(device.ws->host(detail::kHostA, sizeof(double) * checked_product(mp, kp)));
@@ -174,6 +301,205 @@ std::vector<double> Context::multiply(std::span<const double> a, std::span<const
     std::vector<double> c(v.c_size);
     impl_->execute(a, b, c, m, n, k, options, v);
     return c;
+}
+
+// ---- resident operands ------------------------------------------------------------------------
+
+// x's device copy in the zero-padded layout prow x pcol, made from its first device copy on first use.
+const double* Context::Impl::layout(Matrix::State& x, std::uint32_t prow, std::uint32_t pcol) {
+    for (const auto& c : x.copies)
+        if (c.prow == prow && c.pcol == pcol) return c.p;
+    void* p = nullptr;
+    detail::device_check(device.dev, oz_dev_malloc(device.dev, sizeof(double) * (std::size_t)prow * pcol, &p),
+                         "resident matrix");
+    x.copies.push_back({prow, pcol, static_cast<double*>(p)});
+    detail::device_check(device.dev,
+                         oz_pad_copy_f64(device.dev, static_cast<double*>(p), (int)prow, (int)pcol, x.src, (int)x.rows,
+                                         (int)x.cols, (int)x.src_ld),
+                         "resident matrix layout");
+    return static_cast<double*>(p);
+}
+
+// x's host copy and its facts (a result is downloaded the first time they are needed).
+void Context::Impl::fetch_host(Matrix::State& x) {
+    if (x.have_host) return;
+    // (new double[]: no zero-filling of buffers that are overwritten anyway)
+    std::unique_ptr<double[]> buf(new double[x.rows * x.src_ld]);
+    detail::device_check(device.dev,
+                         oz_memcpy_d2h(device.dev, buf.get(), x.src, sizeof(double) * x.rows * x.src_ld), "download");
+    x.host.reset(new double[x.rows * x.cols]);
+#pragma omp parallel for schedule(static)
+    for (std::int64_t i = 0; i < (std::int64_t)x.rows; ++i)
+        std::copy_n(buf.get() + (std::size_t)i * x.src_ld, x.cols, x.host.get() + (std::size_t)i * x.cols);
+    x.facts = facts_of(x.host.get(), x.rows, x.cols);
+    x.have_host = true;
+}
+
+// x's host copy zero-padded to prow x pcol: what the planner reads.
+const double* Context::Impl::padded_host(Matrix::State& x, std::uint32_t prow, std::uint32_t pcol) {
+    for (const auto& e : x.padded_host)
+        if (e.first == std::make_pair(prow, pcol)) return e.second.get();
+    fetch_host(x);
+    std::unique_ptr<double[]> v(new double[(std::size_t)prow * pcol]);
+#pragma omp parallel for schedule(static)
+    for (std::int64_t i = 0; i < (std::int64_t)prow; ++i) {
+        double* row = v.get() + (std::size_t)i * pcol;
+        if ((std::size_t)i < x.rows) {
+            std::copy_n(x.host.get() + (std::size_t)i * x.cols, x.cols, row);
+            std::fill(row + x.cols, row + pcol, 0.0);
+        } else {
+            std::fill(row, row + pcol, 0.0);
+        }
+    }
+    x.padded_host.emplace_back(std::make_pair(prow, pcol), std::move(v));
+    return x.padded_host.back().second.get();
+}
+
+Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<double>* c,
+                             std::shared_ptr<Matrix::State>* cslot, const Options& opts) {
+    check_options(opts);
+    if (A.owner != this || B.owner != this) throw std::invalid_argument("the Matrix belongs to another Context");
+    const std::size_t m = A.rows, k = A.cols, n = B.cols;
+    if (B.rows != k) throw std::invalid_argument("matrix dimensions do not match: a is m x k and b must be k x n");
+    const std::size_t mn = checked_product(m, n);
+    if (c && c->size() != mn) throw std::invalid_argument("matrix span sizes do not match m, n, k");
+    const std::uint32_t mp = padded(m, 64), np = padded(n, 64), kp = padded(k, 32);
+    std::lock_guard lock(runtime_mutex);
+    open();
+    // the plan of this pair and these options, if an earlier call made one (not when the
+    // evaluation hooks fix the width b)
+    evaluation::Settings* es = evaluation::active();
+    const bool cacheable = !es || es->fixed_bits == 0;
+    std::shared_ptr<const void> plan;
+    if (cacheable)
+        for (std::size_t i = plans.size(); i-- > 0;) {
+            const CachedPlan& e = plans[i];
+            if (e.a == A.id && e.b == B.id && e.scheme == opts.scheme && e.format == opts.format &&
+                e.slices == opts.slices && e.max_moduli == opts.max_moduli && e.reconstruction == opts.reconstruction) {
+                plan = e.plan;
+                std::rotate(plans.begin() + (std::ptrdiff_t)i, plans.begin() + (std::ptrdiff_t)i + 1, plans.end());
+                ++plan_hits;
+                break;
+            }
+        }
+    // the checks of gemm() (check_values), on the operands' facts
+    fetch_host(A);
+    fetch_host(B);
+    if (!A.facts.finite) throw std::invalid_argument("A contains NaN or infinity");
+    if (!B.facts.finite) throw std::invalid_argument("B contains NaN or infinity");
+    if (!A.facts.rows_ok || !B.facts.cols_ok)
+        throw std::invalid_argument("each nonzero row maximum of A and column maximum of B must be in [2^-126, max_BF16]");
+    const double* ah = plan ? nullptr : padded_host(A, mp, kp);
+    const double* bh = plan ? nullptr : padded_host(B, kp, np);
+    const double* ad = layout(A, mp, kp);
+    const double* bd = layout(B, kp, np);
+    // a resident result: the device memory of c's previous matrix when nobody else holds it
+    std::shared_ptr<Matrix::State> out;
+    double* cdev = nullptr;
+    if (cslot) {
+        out = std::make_shared<Matrix::State>();
+        out->id = next_matrix_id++;
+        out->owner = this;
+        out->device = handle;
+        out->rows = m;
+        out->cols = n;
+        const std::shared_ptr<Matrix::State>& old = *cslot;
+        if (old && old.use_count() == 1 && old->owner == this && old.get() != &A && old.get() != &B)
+            for (const auto& cp : old->copies)
+                if (cp.prow == mp && cp.pcol == np) cdev = cp.p;  // moves to out once the call succeeded
+        if (!cdev) {
+            void* p = nullptr;
+            detail::device_check(device.dev, oz_dev_malloc(device.dev, sizeof(double) * (std::size_t)mp * np, &p),
+                                 "resident result");
+            cdev = static_cast<double*>(p);
+            out->copies.push_back({mp, np, cdev});  // out frees it if the call fails
+        }
+        out->src = cdev;
+        out->src_ld = np;
+    }
+    detail::Problem problem{mp, np, kp, ah, bh, opts, ad, bd, cdev, plan};
+    const detail::Output output = detail::backend_for(opts.format, opts.scheme)(device, problem);
+    if (cslot && out->copies.empty()) {  // the previous matrix's memory: hand it over
+        auto& oc = (*cslot)->copies;
+        oc.erase(std::find_if(oc.begin(), oc.end(), [&](const Matrix::State::Copy& cp) { return cp.p == cdev; }));
+        out->copies.push_back({mp, np, cdev});
+    }
+    if (es) es->plan_reused = plan != nullptr;
+    if (!plan && cacheable) {
+        if (plans.size() == kPlanCacheSize) plans.erase(plans.begin());
+        plans.push_back({A.id, B.id, opts.scheme, opts.format, opts.slices, opts.max_moduli, opts.reconstruction,
+                         output.plan});
+    }
+    if (c) {
+        const double* vals = output.values;
+        double* cd = c->data();
+#pragma omp parallel for schedule(static)
+        for (std::int64_t i = 0; i < (std::int64_t)m; ++i)
+            std::copy_n(vals + (std::size_t)i * np, n, cd + (std::size_t)i * n);
+    }
+    if (cslot) cslot->swap(out);  // the previous matrix (now in out) is released here
+    Info info = output.info;
+    info.padded_m = mp;
+    info.padded_n = np;
+    info.padded_k = kp;
+    return info;
+}
+
+Matrix Context::upload(std::span<const double> x, std::size_t rows, std::size_t cols) {
+    if (x.size() != checked_product(rows, cols))
+        throw std::invalid_argument("matrix span size does not match rows x cols");
+    padded(rows, 64);  // index range of either role
+    padded(cols, 64);
+    auto st = std::make_shared<Matrix::State>();
+    st->facts = facts_of(x.data(), rows, cols);
+    if (!st->facts.finite) throw std::invalid_argument("the matrix contains NaN or infinity");
+    st->id = next_matrix_id++;
+    st->owner = impl_.get();
+    st->rows = rows;
+    st->cols = cols;
+    st->host.reset(new double[x.size()]);
+    const double* xd = x.data();
+    double* hd = st->host.get();
+#pragma omp parallel for schedule(static)
+    for (std::int64_t i = 0; i < (std::int64_t)rows; ++i)
+        std::copy_n(xd + (std::size_t)i * cols, cols, hd + (std::size_t)i * cols);
+    st->have_host = true;
+    {
+        std::lock_guard lock(runtime_mutex);
+        impl_->open();
+        st->device = impl_->handle;
+        oz_dev* d = impl_->device.dev;
+        void* p = nullptr;
+        detail::device_check(d, oz_dev_malloc(d, sizeof(double) * x.size(), &p), "upload");
+        st->raw = static_cast<double*>(p);
+        detail::device_check(d, oz_memcpy_h2d(d, p, x.data(), sizeof(double) * x.size()), "upload");
+        st->src = st->raw;
+        st->src_ld = cols;
+    }
+    Matrix mx;
+    mx.s_ = std::move(st);
+    return mx;
+}
+
+Info Context::gemm(const Matrix& a, const Matrix& b, std::span<double> c, const Options& options) {
+    if (!a.s_ || !b.s_) throw std::invalid_argument("empty Matrix");
+    return impl_->resident(*a.s_, *b.s_, &c, nullptr, options);
+}
+
+Info Context::gemm(const Matrix& a, const Matrix& b, Matrix& c, const Options& options) {
+    if (!a.s_ || !b.s_) throw std::invalid_argument("empty Matrix");
+    // a and b keep their states alive even when c is one of them
+    const std::shared_ptr<Matrix::State> ka = a.s_, kb = b.s_;
+    return impl_->resident(*ka, *kb, nullptr, &c.s_, options);
+}
+
+void Context::download(const Matrix& x, std::span<double> out) {
+    if (!x.s_) throw std::invalid_argument("empty Matrix");
+    if (x.s_->owner != impl_.get()) throw std::invalid_argument("the Matrix belongs to another Context");
+    if (out.size() != x.s_->rows * x.s_->cols) throw std::invalid_argument("span size does not match the Matrix");
+    std::lock_guard lock(runtime_mutex);
+    impl_->fetch_host(*x.s_);
+    std::copy_n(x.s_->host.get(), out.size(), out.begin());
 }
 
 }  // namespace ozTTgemm

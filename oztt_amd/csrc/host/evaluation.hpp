@@ -36,6 +36,7 @@ struct Settings {
     double product_ops = 0;            // algorithmic operations of the product phase (2*M*N*K*products)
     double gemm_launch_ms = 0;         // device time of the product launches of one pass, in the replays
     int gemm_launches = 0;             // product-kernel launches per pass (one per row band)
+    bool plan_reused = false;          // resident operands: the call ran the plan kept from an earlier call
 };
 
 // Activates `s` for the calling thread until destruction (not nestable).

@@ -18,6 +18,7 @@
 // Mbg x Kg int8 per band of rows, of B: p planes of Ng x Kg (B transposed), both in the GEMM's
 // OZ_BLOCK tiles (Mbg, Ng multiples of 256, Kg of 64); partial sums (per band): p planes of Mbg x Ng
 // int32; output: M x N f64.
+#include <memory>
 #include <stdexcept>
 
 #include "backend.hpp"
@@ -41,12 +42,22 @@ Output ozaki1_run(Device& D, const Problem& p) {
     const Oz1Format& f = oz1_format((int)p.options.format);
     const std::uint32_t M = p.m, N = p.n, K = p.k;
     Workspace& ws = *D.ws;
-    // the operands go up while the host plans (they are page-locked, the copies are asynchronous)
-    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
-    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
-    device_check(dev, oz_memcpy_h2d_async(dev, dAf, p.a, sizeof(double) * M * (std::size_t)K), "upload A");
-    device_check(dev, oz_memcpy_h2d_async(dev, dBf, p.b, sizeof(double) * K * (std::size_t)N), "upload B");
-    const Plan1 plan = plan_scheme1(p.a, p.b, p.m, p.n, p.k, p.options.slices, f);
+    // the operands go up while the host plans (they are page-locked, the copies are asynchronous);
+    // resident operands are already there
+    const double* dAf = p.a_dev;
+    const double* dBf = p.b_dev;
+    if (!dAf) {
+        auto* a = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
+        auto* b = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
+        device_check(dev, oz_memcpy_h2d_async(dev, a, p.a, sizeof(double) * M * (std::size_t)K), "upload A");
+        device_check(dev, oz_memcpy_h2d_async(dev, b, p.b, sizeof(double) * K * (std::size_t)N), "upload B");
+        dAf = a;
+        dBf = b;
+    }
+    const std::shared_ptr<const Plan1> planp =
+        p.plan ? std::static_pointer_cast<const Plan1>(p.plan)
+               : std::make_shared<const Plan1>(plan_scheme1(p.a, p.b, p.m, p.n, p.k, p.options.slices, f));
+    const Plan1& plan = *planp;
     const std::uint32_t P = (std::uint32_t)plan.p;
     const std::uint32_t Ng = round_up(N, 256), Kg = round_up(K, 64);
     if ((std::uint64_t)P * Kg * f.dmax * f.dmax > 0x7FFFFFFFull)
@@ -55,7 +66,8 @@ Output ozaki1_run(Device& D, const Problem& p) {
 
     // Row bands: A's slices and the partial sums are per band of rows; A, B, B's slices, the deltas
     // and C are whole. One band (all of M) unless device memory requires more.
-    const std::size_t fixed = sizeof(double) * ((std::size_t)M * K + (std::size_t)K * N + (std::size_t)M * N) +
+    const std::size_t fixed = sizeof(double) * ((p.a_dev ? 0 : (std::size_t)M * K + (std::size_t)K * N) +
+                                                (p.c_dev ? 0 : (std::size_t)M * N)) +
                               (std::size_t)P * Ng * Kg + sizeof(std::int32_t) * (M + N) + 256;
     const std::size_t per_row = (std::size_t)P * Kg + sizeof(std::int32_t) * (std::size_t)P * Ng;
     const std::uint32_t Mb = band_rows(D, M, fixed, per_row, {kSlicesA, kPartial});
@@ -69,7 +81,7 @@ Output ozaki1_run(Device& D, const Problem& p) {
     auto* slA = static_cast<std::int8_t*>(ws.get(kSlicesA, (std::size_t)P * strideA));
     auto* slB = static_cast<std::int8_t*>(ws.get(kSlicesB, (std::size_t)P * strideB));
     auto* part = static_cast<std::int32_t*>(ws.get(kPartial, sizeof(std::int32_t) * (std::size_t)P * strideP));
-    auto* out = static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
+    auto* out = p.c_dev ? p.c_dev : static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
 
     std::vector<Step> steps;
     steps.push_back({ev::Scale, [=] {
@@ -115,11 +127,11 @@ Output ozaki1_run(Device& D, const Problem& p) {
     }
     // P(P+1)/2 slice-pair products of 2*M*N*K operations each
     const unsigned pairs = P * (P + 1) / 2;
-    auto* host = static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
+    auto* host = p.c_dev ? nullptr : static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
+    run_pipeline(dev, steps, out, host, host ? (std::size_t)M * N : 0, flags, 2.0 * M * (double)N * K * pairs, pairs);
     Info info{Scheme::I, p.options.format};
     info.slices = P;
-    return {host, info};
+    return {host, info, planp};
 }
 
 }  // namespace ozTTgemm::detail

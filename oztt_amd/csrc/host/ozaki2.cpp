@@ -22,6 +22,7 @@
 #include <chrono>
 #include <cstring>
 #include <functional>
+#include <memory>
 #include <stdexcept>
 
 #include "backend.hpp"
@@ -47,13 +48,23 @@ Output ozaki2_run(Device& D, const Problem& p) {
     if (es && es->fixed_bits) fixed_b = es->fixed_bits;
     const std::uint32_t M = p.m, N = p.n, K = p.k;
     Workspace& ws = *D.ws;
-    // the operands go up while the host plans (they are page-locked, the copies are asynchronous)
-    auto* dAf = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
-    auto* dBf = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
-    device_check(dev, oz_memcpy_h2d_async(dev, dAf, p.a, sizeof(double) * M * (std::size_t)K), "upload A");
-    device_check(dev, oz_memcpy_h2d_async(dev, dBf, p.b, sizeof(double) * K * (std::size_t)N), "upload B");
-    const Plan2 plan = plan_scheme2(p.a, p.b, p.m, p.n, p.k, p.options.format, p.options.max_moduli,
-                                    p.options.reconstruction, fixed_b);
+    // the operands go up while the host plans (they are page-locked, the copies are asynchronous);
+    // resident operands are already there
+    const double* dAf = p.a_dev;
+    const double* dBf = p.b_dev;
+    if (!dAf) {
+        auto* a = static_cast<double*>(ws.get(kA, sizeof(double) * M * (std::size_t)K));
+        auto* b = static_cast<double*>(ws.get(kB, sizeof(double) * K * (std::size_t)N));
+        device_check(dev, oz_memcpy_h2d_async(dev, a, p.a, sizeof(double) * M * (std::size_t)K), "upload A");
+        device_check(dev, oz_memcpy_h2d_async(dev, b, p.b, sizeof(double) * K * (std::size_t)N), "upload B");
+        dAf = a;
+        dBf = b;
+    }
+    const std::shared_ptr<const Plan2> planp =
+        p.plan ? std::static_pointer_cast<const Plan2>(p.plan)
+               : std::make_shared<const Plan2>(plan_scheme2(p.a, p.b, p.m, p.n, p.k, p.options.format,
+                                                            p.options.max_moduli, p.options.reconstruction, fixed_b));
+    const Plan2& plan = *planp;
     const bool fp8 = p.options.format == Format::FP8;
     const std::uint32_t S = (std::uint32_t)plan.S;
     const std::uint32_t Ng = round_up(N, 256), Kg = round_up(K, 64);
@@ -72,7 +83,8 @@ Output ozaki2_run(Device& D, const Problem& p) {
 
     // Row bands: A's planes and the product terms are per band; A, B, B's planes, the deltas and C
     // are whole. One band (all of M) unless device memory requires more.
-    const std::size_t fixed = sizeof(double) * ((std::size_t)M * K + (std::size_t)K * N + (std::size_t)M * N) +
+    const std::size_t fixed = sizeof(double) * ((p.a_dev ? 0 : (std::size_t)M * K + (std::size_t)K * N) +
+                                                (p.c_dev ? 0 : (std::size_t)M * N)) +
                               (std::size_t)nplanes * Ng * Kg + sizeof(std::int32_t) * (M + N) + 256;
     const std::size_t per_row = (std::size_t)nplanes * Kg + (std::size_t)nterms * Ng * term_bytes;
     const std::uint32_t Mb = band_rows(D, M, fixed, per_row, {kPlanesA, kProducts});
@@ -86,7 +98,7 @@ Output ozaki2_run(Device& D, const Problem& p) {
     auto* planesA = static_cast<std::int8_t*>(ws.get(kPlanesA, (std::size_t)nplanes * strideA));
     auto* planesB = static_cast<std::int8_t*>(ws.get(kPlanesB, (std::size_t)nplanes * strideB));
     auto* prod = static_cast<std::uint8_t*>(ws.get(kProducts, (std::size_t)nterms * strideC * term_bytes));
-    auto* out = static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
+    auto* out = p.c_dev ? p.c_dev : static_cast<double*>(ws.get(kOut, sizeof(double) * M * (std::size_t)N));
     auto* uA = reinterpret_cast<std::uint8_t*>(planesA);
     auto* uB = reinterpret_cast<std::uint8_t*>(planesB);
     auto* terms = reinterpret_cast<std::uint16_t*>(prod);
@@ -166,13 +178,13 @@ Output ozaki2_run(Device& D, const Problem& p) {
     // products: one per modulus (INT8) or the FP8 route's digit products (sum of the outputs' pairs)
     const std::uint32_t nprod = fp8 ? (std::uint32_t)plan.mo.nprod : S;
 
-    auto* host = static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * nprod, nprod);
+    auto* host = p.c_dev ? nullptr : static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
+    run_pipeline(dev, steps, out, host, host ? (std::size_t)M * N : 0, flags, 2.0 * M * (double)N * K * nprod, nprod);
     Info info{Scheme::II, p.options.format};
     info.moduli = S;
     info.integer_bits = (std::uint32_t)plan.b;
     info.reconstruction_passes = plan.two_pass ? 2 : 1;
-    return {host, info};
+    return {host, info, planp};
 }
 
 }  // namespace ozTTgemm::detail

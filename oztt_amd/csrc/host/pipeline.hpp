@@ -21,7 +21,8 @@ struct Step {
 
 // Issues `steps` (timing each phase, then replaying the whole pass and the product steps, those of
 // phase Gemm, under an active evaluation Scope), reads back the `count` result values of `out` into
-// `host` and the two range flags, and throws std::runtime_error for a set flag (scale.hpp:187-208).
+// `host` (none for a result that stays on the device) and the two range flags, and throws
+// std::runtime_error for a set flag (scale.hpp:187-208).
 // product_ops / partial_products describe the product phase for the evaluation record.
 void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const double* out, double* host, std::size_t count,
                   const std::uint32_t* flags, double product_ops, unsigned partial_products);

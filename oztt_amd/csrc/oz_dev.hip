@@ -16,6 +16,16 @@ __global__ void copy16_kernel(uint4* __restrict__ dst, const uint4* __restrict__
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
+
+// Row r of dst: blockIdx.y + j gridDim.y; 256 columns per block along x. Rows and columns outside
+// src are zero.
+__global__ void pad_copy_f64_kernel(double* __restrict__ dst, int drows, int dcols, const double* __restrict__ src,
+                                    int srows, int scols, int sld) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= dcols) return;
+    for (int r = blockIdx.y; r < drows; r += gridDim.y)
+        dst[(size_t)r * dcols + c] = (r < srows && c < scols) ? src[(size_t)r * sld + c] : 0.0;
+}
 }  // namespace
 
 extern "C" {
@@ -136,6 +146,16 @@ int oz_memcpy_d2d(oz_dev* dev, void* dst, const void* src, size_t bytes) {
     const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 8192);
     hipLaunchKernelGGL(copy16_kernel, dim3(blocks), dim3(256), 0, dev->stream, (uint4*)dst, (const uint4*)src, n16);
     return oz::launch_check(dev, "copy16_kernel");
+}
+
+int oz_pad_copy_f64(oz_dev* dev, double* dst, int drows, int dcols, const double* src, int srows, int scols,
+                    int sld) {
+    if (int st = oz::use(dev)) return st;
+    if (!dst || drows <= 0 || dcols <= 0 || srows < 0 || scols < 0 || (srows && scols && (!src || sld < scols)))
+        return oz::fail(dev, OZ_ERR_ARG, "oz_pad_copy_f64: invalid arguments");
+    const dim3 grid((unsigned)((dcols + 255) / 256), (unsigned)std::min(drows, 65535));
+    hipLaunchKernelGGL(pad_copy_f64_kernel, grid, dim3(256), 0, dev->stream, dst, drows, dcols, src, srows, scols, sld);
+    return oz::launch_check(dev, "pad_copy_f64_kernel");
 }
 
 int oz_sync(oz_dev* dev) {

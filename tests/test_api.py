@@ -70,3 +70,20 @@ def test_host_validation_leaves_c_untouched(ctx):
     with pytest.raises(ValueError):
         ctx.gemm(np.full(4, 2.0 ** 128), b, c, 2, 2, 2, OPT)   # row maximum above the BF16 range
     assert np.all(c == 123.0)
+
+
+def test_resident_upload_validation(ctx):
+    """Context.upload (the resident-operand extension) rejects bad input before it touches the GPU."""
+    with pytest.raises(ValueError):
+        ctx.upload(np.ones(6), 2, 4)          # span size
+    with pytest.raises(ValueError):
+        ctx.upload(np.ones(4), 0, 4)          # zero dimension
+    for bad in (np.nan, np.inf, -np.inf):
+        with pytest.raises(ValueError):
+            ctx.upload(np.array([1.0, bad, 0.0, 0.0]), 2, 2)
+    empty = oz.Matrix()
+    assert empty.shape == (0, 0)
+    with pytest.raises(ValueError):
+        ctx.gemm_resident(empty, empty, np.empty(1))  # empty operands
+    with pytest.raises(ValueError):
+        ctx.download(empty)
