@@ -115,3 +115,26 @@ def test_resident_checks(ctx):
         ctx.gemm_resident(X, ctx.upload(np.ones(4), 2, 2), np.empty(4), opts)
     other.close()
     X.close()  # a Matrix may outlive its Context: it holds the GPU open until it is freed
+
+
+@pytest.mark.parametrize("name,opts", CASES[:2] + CASES[3:4], ids=["II-INT8", "II-FP8", "I-INT8"])
+def test_resident_row_bands(ctx, name, opts):
+    """Resident operands through row bands (forced by the evaluation hook max_band_rows): the band
+    loop reads A's rows from the resident copy and writes C's rows into the result."""
+    m, n, k = 1000, 384, 512
+    a, b = oz.eval_inputs(11, 1.0, m * k, k * n)
+    want = np.empty(m * n)
+    ctx.gemm(a, b, want, m, n, k, opts)
+    A, B = ctx.upload(a, m, k), ctx.upload(b, k, n)
+    ev = oz.EvalStats()
+    ev.max_band_rows = 256
+    got = np.empty(m * n)
+    ctx.gemm_resident(A, B, got, opts, evaluation=ev)
+    assert ev.gemm_launches == 4
+    np.testing.assert_array_equal(bits(got), bits(want))
+    C = oz.Matrix()
+    ev2 = oz.EvalStats()
+    ev2.max_band_rows = 256
+    ctx.gemm_resident(A, B, C, opts, evaluation=ev2)
+    assert ev2.gemm_launches == 4
+    np.testing.assert_array_equal(bits(ctx.download(C)), bits(want))
