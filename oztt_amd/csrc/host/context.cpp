@@ -153,8 +153,7 @@ using detail::facts_of;
 
 struct Matrix::State {
     std::uint64_t id = 0;
-    const void* owner = nullptr;  // the Context::Impl that made it
-    std::shared_ptr<DeviceHandle> device;
+    std::shared_ptr<DeviceHandle> device;  // the GPU of the Context that made it (identifies that Context)
     std::size_t rows = 0, cols = 0;
     // host copy (row-major rows x cols) and its facts; a result has them only once it is needed
     std::unique_ptr<double[]> host;
@@ -214,7 +213,6 @@ struct Context::Impl {
     };
     static constexpr std::size_t kPlanCacheSize = 16;
     std::vector<CachedPlan> plans;
-    std::size_t plan_hits = 0;
 
     DeviceOptions options;
     std::shared_ptr<DeviceHandle> handle;
@@ -358,14 +356,16 @@ const double* Context::Impl::padded_host(Matrix::State& x, std::uint32_t prow, s
 Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<double>* c,
                              std::shared_ptr<Matrix::State>* cslot, const Options& opts) {
     check_options(opts);
-    if (A.owner != this || B.owner != this) throw std::invalid_argument("the Matrix belongs to another Context");
     const std::size_t m = A.rows, k = A.cols, n = B.cols;
     if (B.rows != k) throw std::invalid_argument("matrix dimensions do not match: a is m x k and b must be k x n");
     const std::size_t mn = checked_product(m, n);
     if (c && c->size() != mn) throw std::invalid_argument("matrix span sizes do not match m, n, k");
     const std::uint32_t mp = padded(m, 64), np = padded(n, 64), kp = padded(k, 32);
     std::lock_guard lock(runtime_mutex);
-    open();
+    // a Context's matrices hold its device handle, which no other Context shares (and a Context
+    // that made no Matrix has none yet)
+    if (!handle || A.device != handle || B.device != handle)
+        throw std::invalid_argument("the Matrix belongs to another Context");
     // the plan of this pair and these options, if an earlier call made one (not when the
     // evaluation hooks fix the width b)
     evaluation::Settings* es = evaluation::active();
@@ -378,7 +378,6 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
                 e.slices == opts.slices && e.max_moduli == opts.max_moduli && e.reconstruction == opts.reconstruction) {
                 plan = e.plan;
                 std::rotate(plans.begin() + (std::ptrdiff_t)i, plans.begin() + (std::ptrdiff_t)i + 1, plans.end());
-                ++plan_hits;
                 break;
             }
         }
@@ -399,12 +398,11 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
     if (cslot) {
         out = std::make_shared<Matrix::State>();
         out->id = next_matrix_id++;
-        out->owner = this;
         out->device = handle;
         out->rows = m;
         out->cols = n;
         const std::shared_ptr<Matrix::State>& old = *cslot;
-        if (old && old.use_count() == 1 && old->owner == this && old.get() != &A && old.get() != &B)
+        if (old && old.use_count() == 1 && old->device == handle && old.get() != &A && old.get() != &B)
             for (const auto& cp : old->copies)
                 if (cp.prow == mp && cp.pcol == np) cdev = cp.p;  // moves to out once the call succeeded
         if (!cdev) {
@@ -454,7 +452,6 @@ Matrix Context::upload(std::span<const double> x, std::size_t rows, std::size_t 
     st->facts = facts_of(x.data(), rows, cols);
     if (!st->facts.finite) throw std::invalid_argument("the matrix contains NaN or infinity");
     st->id = next_matrix_id++;
-    st->owner = impl_.get();
     st->rows = rows;
     st->cols = cols;
     st->host.reset(new double[x.size()]);
@@ -495,9 +492,10 @@ Info Context::gemm(const Matrix& a, const Matrix& b, Matrix& c, const Options& o
 
 void Context::download(const Matrix& x, std::span<double> out) {
     if (!x.s_) throw std::invalid_argument("empty Matrix");
-    if (x.s_->owner != impl_.get()) throw std::invalid_argument("the Matrix belongs to another Context");
     if (out.size() != x.s_->rows * x.s_->cols) throw std::invalid_argument("span size does not match the Matrix");
     std::lock_guard lock(runtime_mutex);
+    if (!impl_->handle || x.s_->device != impl_->handle)
+        throw std::invalid_argument("the Matrix belongs to another Context");
     impl_->fetch_host(*x.s_);
     std::copy_n(x.s_->host.get(), out.size(), out.begin());
 }
