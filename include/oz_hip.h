@@ -251,6 +251,16 @@ typedef struct oz1_recon_dev {
 } oz1_recon_dev;
 int oz1_recon_f64(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long strideP, const oz1_recon_dev* r,
                   const int32_t* dA, const int32_t* dB, double* out, int ldo);
+/* The reconstruction run K block by K block (reference ozaki1/kernels/recon_tf_f32in.cpp:54-89 and
+ * recon_f64_writer.cpp, ozaki1/plan.hpp:104-109: FP32 products whose int32 sum over all of K could
+ * overflow). P holds one K block's diagonal sums, exact integers of at most 2^24 that enter whole;
+ * after the first block (first = 0) the limbs carried in `limbs` (hi, mid, lo planes of M x N floats,
+ * leading dimension ldl, limb_stride elements apart) are added in the order lo, mid, hi. Every block
+ * but the last (last = 0) writes the limbs back; the last assembles C as oz1_recon_f64 does.
+ * r->signmag must be 0 (nsingle is not read: every diagonal enters whole). */
+int oz1_recon_block_f64(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long strideP,
+                        const oz1_recon_dev* r, int first, int last, float* limbs, long long limb_stride, int ldl,
+                        const int32_t* dA, const int32_t* dB, double* out, int ldo);
 
 #ifdef __cplusplus
 }

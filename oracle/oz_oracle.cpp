@@ -1095,6 +1095,36 @@ void orc_oz1_recon(const int32_t* P, int M, int N, int ndiag, int radix, int sig
         }
 }
 
+void orc_oz1_recon_blocks(const int32_t* P, int M, int N, int ndiag, int nkb, int radix, const int32_t* dA,
+                          const int32_t* dB, double* out) {
+    uint32_t Whi, Wlo;
+    int32_t qw;
+    oz1_scale_w(radix, ndiag - 1, Whi, Wlo, qw);
+    const float r = (float)radix;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float ph = 0.0f, pm = 0.0f, pl = 0.0f;  // limbs carried from the previous blocks
+            for (int kb = 0; kb < nkb; kb++) {
+                float hi = 0.0f, mid = 0.0f, lo = 0.0f;
+                for (int d = 0; d < ndiag; d++) {
+                    if (d > 0) tf_mul_radix(hi, mid, lo, r);
+                    tf_add_s(hi, mid, lo, (float)P[(((size_t)kb * ndiag + d) * M + i) * N + j]);
+                }
+                if (kb > 0) {
+                    tf_add_s(hi, mid, lo, pl);
+                    tf_add_s(hi, mid, lo, pm);
+                    tf_add_s(hi, mid, lo, ph);
+                }
+                ph = hi;
+                pm = mid;
+                pl = lo;
+            }
+            const uint64_t u = assemble_tf_f64(f_bits(ph), f_bits(pm), f_bits(pl), -(dA[i] + dB[j]), Whi, Wlo, qw);
+            std::memcpy(&out[(size_t)i * N + j], &u, 8);
+        }
+}
+
 void orc_oz1_scale_w(int radix, int L, uint32_t* Whi, uint32_t* Wlo, int32_t* qw) { oz1_scale_w(radix, L, *Whi, *Wlo, *qw); }
 
 // Scheme I INT8 end to end (ozaki1.cpp run(): scale with nshift -1 and rounding up, p slices of

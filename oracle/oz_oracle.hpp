@@ -101,6 +101,13 @@ int64_t orc_oz1_gemm_diag(const int8_t* A, const int8_t* B, int32_t* P, int M, i
 // Horner reconstruction + FP64 assembly (recon_tf_i32in.cpp:116-157, recon_f64_writer.cpp:148-160).
 void orc_oz1_recon(const int32_t* P, int M, int N, int ndiag, int radix, int signmag, int nsingle, const int32_t* dA,
                    const int32_t* dB, double* out);
+// The reconstruction K block by K block (recon_tf_f32in.cpp:54-89, plan.hpp:104-109): P holds nkb
+// blocks of ndiag planes of exact sums of at most 2^24; per block the Horner sum with every P_d
+// whole, then from the second block on the previous limbs added (lo, mid, hi); the last block is
+// assembled to FP64. Parity unpinned: no reference record runs this plan; pinned by agreement with
+// the single-block reconstruction up to its last bits (tests/test_oracle.py).
+void orc_oz1_recon_blocks(const int32_t* P, int M, int N, int ndiag, int nkb, int radix, const int32_t* dA,
+                          const int32_t* dB, double* out);
 // radix^-(L+2) as W = Whi:Wlo (64-bit significand) and 2^qw (ozaki1/plan.hpp:446-460).
 void orc_oz1_scale_w(int radix, int L, uint32_t* Whi, uint32_t* Wlo, int32_t* qw);
 // Scheme I INT8 end to end with p slices on padded row-major A, B; returns max |P_d|.

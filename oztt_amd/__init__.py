@@ -81,7 +81,7 @@ class EvalStats(ctypes.Structure):
                 ("phase_ms", ctypes.c_double * 5), ("whole_ms", ctypes.c_double), ("whole_checked", ctypes.c_int),
                 ("partial_products", ctypes.c_uint), ("product_ops", ctypes.c_double),
                 ("gemm_launch_ms", ctypes.c_double), ("gemm_launches", ctypes.c_int),
-                ("max_band_rows", ctypes.c_uint), ("plan_reused", ctypes.c_int)]
+                ("max_band_rows", ctypes.c_uint), ("plan_reused", ctypes.c_int), ("force_kc", ctypes.c_uint)]
 
 
 class Plan2(ctypes.Structure):
@@ -240,15 +240,17 @@ class Context:
         return c
 
     def evaluate(self, a, b, m: int, n: int, k: int, options: Options, fixed_bits: int = 0, warmup: int = 0,
-                 repeats: int = 0, max_band_rows: int = 0):
+                 repeats: int = 0, max_band_rows: int = 0, force_kc: int = 0):
         """GEMM under the evaluation hooks: returns (C, Info, EvalStats) with phase and whole-pass times.
         max_band_rows > 0 caps the rows of a band (row bands are otherwise used only when the problem
-        does not fit in device memory)."""
+        does not fit in device memory); force_kc > 0 makes Scheme I with an FP32-product format
+        reconstruct K block by K block with blocks of that length."""
         a, b = _f64(a), _f64(b)
         c = np.empty(m * n, dtype=np.float64)
         ev = EvalStats()
         ev.fixed_bits, ev.warmup, ev.repeats = fixed_bits, warmup, repeats
         ev.max_band_rows = max_band_rows
+        ev.force_kc = force_kc
         info = self._call(a, b, c, m, n, k, options, ev)
         return c, info, ev
 

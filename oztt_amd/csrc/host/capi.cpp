@@ -75,6 +75,7 @@ struct ozt_eval {
     int gemm_launches;
     unsigned max_band_rows;  // input: cap on the rows of a band (0: bands only when memory requires)
     int plan_reused;         // resident operands: the plan kept from an earlier call was used
+    unsigned force_kc;       // input: Scheme I block-by-block reconstruction with this K block (0: as planned)
 };
 
 struct ozt_plan2 {
@@ -183,6 +184,7 @@ int ozt_gemm_resident(void* ctx, void* a, void* b, double* c, std::size_t nc, vo
             s.warmup = evo->warmup;
             s.repeats = evo->repeats;
             s.max_band_rows = evo->max_band_rows;
+        s.force_kc = evo->force_kc;
             {
                 ozTTgemm::evaluation::Scope scope(s);
                 i = run();
@@ -204,6 +206,7 @@ int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, s
         s.warmup = evo->warmup;
         s.repeats = evo->repeats;
         s.max_band_rows = evo->max_band_rows;
+        s.force_kc = evo->force_kc;
         auto* cx = static_cast<ozTTgemm::Context*>(ctx);
         ozTTgemm::Info i;
         {

@@ -27,6 +27,8 @@ struct Settings {
     int warmup = 0;           // untimed whole-pass replays
     int repeats = 0;          // timed whole-pass replays (0: no replay)
     unsigned max_band_rows = 0;  // cap on the rows of a band (0: bands only when memory requires)
+    unsigned force_kc = 0;       // Scheme I, FP32-product formats: reconstruct K block by K block with
+                                 // blocks of this length (0: as planned; it must divide the padded K)
     // outputs
     double phase_ms[PhaseCount] = {};  // device time of each phase: the average of up to 5 warm passes
                                        // after the replays (the first pass when there are none)

@@ -526,11 +526,9 @@ Plan1 plan_scheme1(const double* A, const double* B, std::uint32_t M, std::uint3
     if (!exact_check(ip.Kc, per_pair ? 0 : L, f)) throw std::logic_error("scheme I plan: K block violates exactness");
     // The products run as exact int8 x int8 -> int32 accumulations over all pairs and K of a diagonal.
     // That reproduces the reference's int32 sums S_d (deferred reconstruction) and its single-block INT8
-    // products; the reference's remaining plan, per-block Horner over FP32 products, is not built.
-    if (!f.int32_partial && !ip.defer)
-        throw std::runtime_error("Ozaki scheme I: k=" + std::to_string(K) + " with " + std::to_string(pl.p) +
-                                 " slices exceeds the int32 range of a diagonal's sum in this format; this build does "
-                                 "not reconstruct K block by K block. Use fewer slices (Options::slices) or a smaller k.");
+    // products. The remaining plan (FP32 products whose sum over all of K could overflow int32:
+    // !defer, several K blocks of the concatenated issue) reconstructs K block by K block
+    // (plan.hpp:104-109): the driver sums each block's diagonals exactly and carries the Horner limbs.
     pl.signmag = f.int32_partial;
     // reconstruction constants (plan.hpp:424-460)
     if (ip.defer) {

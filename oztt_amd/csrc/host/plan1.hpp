@@ -70,9 +70,8 @@ struct Plan1 {
 std::uint32_t oz1_block_k(std::uint32_t K, int L, const Oz1Format& f);
 
 // The whole plan: p (slices, or automatic when 0), issue, reconstruction constants. Throws
-// std::runtime_error when the configuration cannot be executed (plan.hpp:177-240), and for the one
-// plan of the reference this build does not run: FP32 products whose int32 sum could overflow, which
-// the reference reconstructs block by block (recon_limbs).
+// std::runtime_error when the configuration cannot be executed (plan.hpp:177-240). issue.defer false
+// for a format with FP32 products means the reconstruction runs K block by K block (recon_limbs).
 Plan1 plan_scheme1(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K,
                    std::uint32_t slices, const Oz1Format& f);
 

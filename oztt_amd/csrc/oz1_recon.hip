@@ -142,6 +142,77 @@ __global__ void __launch_bounds__(256) recon_kernel(const int32_t* __restrict__ 
     out[(long long)i * ldo + j] = __longlong_as_double((long long)u);
 }
 
+// One K block of the reconstruction that runs block by block (reference recon_tf_f32in.cpp:54-89
+// with recon_f64_writer.cpp; ozaki1/plan.hpp:104-109): the block's diagonal sums P_d, exact
+// integers of at most 2^24 (the FP32 products of the reference), enter whole into the Horner
+// evaluation; then, after the first block, the three limbs carried from the previous blocks are
+// added (lo, then mid, then hi). Every block but the last stores the limbs; the last assembles C.
+template <bool POW2, bool ACC, bool EMIT>
+__global__ void __launch_bounds__(256) recon_block_kernel(const int32_t* __restrict__ P, int M, int N, int ldp,
+                                                          long long sP, int ndiag, float radix, float* __restrict__ L,
+                                                          long long sL, int ldl, uint64_t W, int32_t qw,
+                                                          const int32_t* __restrict__ dA,
+                                                          const int32_t* __restrict__ dB, double* __restrict__ out,
+                                                          int ldo) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.y;
+    if (j >= N) return;
+    const int32_t* p = P + (long long)i * ldp + j;
+    float hi = 0.0f, mid = 0.0f, lo = 0.0f;
+    for (int d0 = 0; d0 < ndiag; d0 += 8) {
+        int32_t vb[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) vb[t] = d0 + t < ndiag ? p[(long long)(d0 + t) * sP] : 0;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int d = d0 + t;
+            if (d >= ndiag) break;
+            if (d > 0) tf_mul_radix<POW2>(hi, mid, lo, radix);
+            tf_add_s(hi, mid, lo, (float)vb[t]);
+        }
+    }
+    float* l = L + (long long)i * ldl + j;
+    if constexpr (ACC) {
+        const float ph = l[0], pm = l[sL], pl = l[2 * sL];
+        tf_add_s(hi, mid, lo, pl);
+        tf_add_s(hi, mid, lo, pm);
+        tf_add_s(hi, mid, lo, ph);
+    }
+    if constexpr (EMIT) {
+        l[0] = hi;
+        l[sL] = mid;
+        l[2 * sL] = lo;
+    } else {
+        const uint64_t u = assemble_tf_f64(hi, mid, lo, -(dA[i] + dB[j]), W, qw);
+        out[(long long)i * ldo + j] = __longlong_as_double((long long)u);
+    }
+}
+
+template <bool POW2, bool ACC, bool EMIT>
+int launch_block(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long sP, const oz1_recon_dev* r, float* L,
+                 long long sL, int ldl, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    const uint64_t W = ((uint64_t)r->Whi << 32) | r->Wlo;
+    for (int i0 = 0; i0 < M; i0 += 65535) {
+        const int rows = min(65535, M - i0);
+        hipLaunchKernelGGL((recon_block_kernel<POW2, ACC, EMIT>), dim3(oz::ceil_div(N, 256), rows), dim3(256), 0,
+                           dev->stream, P + (long long)i0 * ldp, rows, N, ldp, sP, r->ndiag, (float)r->radix,
+                           L + (long long)i0 * ldl, sL, ldl, W, r->qw, dA ? dA + i0 : dA, dB,
+                           out ? out + (long long)i0 * ldo : out, ldo);
+        if (int st = oz::launch_check(dev, "recon_block_kernel")) return st;
+    }
+    return OZ_OK;
+}
+
+template <bool POW2>
+int launch_block_mode(oz_dev* dev, int first, int last, const int32_t* P, int M, int N, int ldp, long long sP,
+                      const oz1_recon_dev* r, float* L, long long sL, int ldl, const int32_t* dA, const int32_t* dB,
+                      double* out, int ldo) {
+    if (first && last) return launch_block<POW2, false, false>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+    if (first) return launch_block<POW2, false, true>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+    if (last) return launch_block<POW2, true, false>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+    return launch_block<POW2, true, true>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+}
+
 template <bool POW2, bool SIGNMAG>
 int launch_recon(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long sP, const oz1_recon_dev* r,
                  const int32_t* dA, const int32_t* dB, double* out, int ldo) {
@@ -171,4 +242,19 @@ extern "C" int oz1_recon_f64(oz_dev* dev, const int32_t* P, int M, int N, int ld
                     : launch_recon<false, true>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo);
     return pow2 ? launch_recon<true, false>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo)
                 : launch_recon<false, false>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo);
+}
+
+extern "C" int oz1_recon_block_f64(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long strideP,
+                                   const oz1_recon_dev* r, int first, int last, float* limbs, long long limb_stride,
+                                   int ldl, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    if (int st = oz::use(dev)) return st;
+    if (!P || !r || !limbs || M <= 0 || N <= 0 || ldp < N || ldl < N || r->ndiag < 1 || r->radix < 2 ||
+        r->radix > 254 || r->signmag || (r->ndiag > 1 && strideP < (long long)M * ldp) ||
+        limb_stride < (long long)M * ldl || (last && (!dA || !dB || !out || ldo < N || !(r->Whi >> 31))))
+        return oz::fail(dev, OZ_ERR_ARG, "oz1_recon_block_f64: invalid arguments");
+    const bool pow2 = (r->radix & (r->radix - 1)) == 0;
+    return pow2 ? launch_block_mode<true>(dev, first, last, P, M, N, ldp, strideP, r, limbs, limb_stride, ldl, dA, dB,
+                                          out, ldo)
+                : launch_block_mode<false>(dev, first, last, P, M, N, ldp, strideP, r, limbs, limb_stride, ldl, dA,
+                                           dB, out, ldo);
 }

@@ -161,6 +161,16 @@ def _oz1_recon(self, Pd, radix, signmag, nsingle, dA, dB):
     return out
 
 
+def _oz1_recon_blocks(self, Pb, radix, dA, dB):
+    """Block-by-block reconstruction: Pb [nkb][ndiag][M][N] int32 -> C (M*N)."""
+    Pb = np.ascontiguousarray(Pb, dtype=np.int32)
+    nkb, ndiag, M, N = Pb.shape
+    out = np.empty(M * N)
+    self.lib.orc_oz1_recon_blocks(P(Pb), M, N, ndiag, nkb, radix, P(np.ascontiguousarray(dA, dtype=np.int32)),
+                                  P(np.ascontiguousarray(dB, dtype=np.int32)), P(out))
+    return out
+
+
 def _oz1_scale_w(self, radix, L):
     whi, wlo, qw = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_int32()
     self.lib.orc_oz1_scale_w(radix, L, ctypes.byref(whi), ctypes.byref(wlo), ctypes.byref(qw))
@@ -178,6 +188,7 @@ def _oz1_int8_gemm(self, A, B, M, N, K, p):
 Oracle.oz1_slices = _oz1_slices
 Oracle.oz1_gemm_diag = _oz1_gemm_diag
 Oracle.oz1_recon = _oz1_recon
+Oracle.oz1_recon_blocks = _oz1_recon_blocks
 Oracle.oz1_scale_w = _oz1_scale_w
 Oracle.oz1_int8_gemm = _oz1_int8_gemm
 

@@ -233,3 +233,68 @@ def test_c5_shape_bit_exact(ctx, oracle):
     want = oracle.oz1_recon(Pd, 64, 0, 0, dA[rows], dB)
     np.testing.assert_array_equal(c.reshape(m, n)[rows].reshape(-1).view(np.uint64), want.view(np.uint64))
     assert not c.reshape(m, n)[::100, :].any() and not c.reshape(m, n)[:, ::100].any()
+
+
+def _block_chain(oracle, A, B, rows, dA, dB, p, radix, dmax, Kc):
+    """The oracle's block-by-block chain on the rows `rows` of C: slices, exact per-block diagonal sums,
+    reconstruction with the limbs carried from block to block."""
+    m, k = A.shape
+    n = B.shape[1]
+    sa = oracle.oz1_slices(np.ascontiguousarray(A[rows]), A[rows].shape[0], k, 0, dA[rows], p, radix, dmax)
+    sb = oracle.oz1_slices(B, k, n, 1, dB, p, radix, dmax)
+    nkb = k // Kc
+    Pb = np.empty((nkb, p, sa.shape[1], n), dtype=np.int32)
+    for kb in range(nkb):
+        ks = slice(kb * Kc, (kb + 1) * Kc)
+        ga = [sa[i][:, ks].astype(np.float64) for i in range(p)]
+        gb = [sb[i][ks].astype(np.float64) for i in range(p)]
+        for d in range(p):
+            Pb[kb, d] = sum(ga[i] @ gb[d - i] for i in range(d + 1)).astype(np.int64)  # exact: < 2^24
+    return oracle.oz1_recon_blocks(Pb, radix, dA[rows], dB)
+
+
+@pytest.mark.parametrize("fmt,p,radix,dmax", [(oz.Format.BF16, 8, 64, 32), (oz.Format.FP8, 6, 32, 16)])
+def test_block_reconstruction_forced_bit_exact(ctx, oracle, fmt, p, radix, dmax):
+    """The reconstruction K block by K block (reference plan.hpp:104-109, recon_tf_f32in.cpp), forced with
+    the evaluation hook force_kc at a size the oracle runs whole: C equals the oracle's block chain bit for
+    bit, and differs from the one-block (deferred) reconstruction by at most one unit in the last place."""
+    m, n, k, Kc = 256, 320, 2048, 512
+    a, b = oz.eval_inputs(13, 2.0, m * k, k * n)
+    A, B = a.reshape(m, k), b.reshape(k, n)
+    opts = oz.Options(scheme=oz.Scheme.I, format=fmt, slices=p)
+    c_blk, info, ev = ctx.evaluate(a, b, m, n, k, opts, force_kc=Kc)
+    assert info.slices == p and ev.gemm_launches == k // Kc
+    dA, _ = oracle.scale(A, m, k, 0, 0, -1)
+    dB, _ = oracle.scale(B, k, n, 1, 0, -1)
+    want = _block_chain(oracle, A, B, slice(0, m), dA, dB, p, radix, dmax, Kc)
+    np.testing.assert_array_equal(c_blk.view(np.uint64), want.view(np.uint64))
+    c_one = ctx.multiply(a, b, m, n, k, opts)
+    ulp = np.abs(np.spacing(np.maximum(np.abs(c_one), np.abs(c_blk))))
+    assert np.all(np.abs(c_blk - c_one) <= ulp)
+
+
+def test_block_reconstruction_natural(ctx, oracle):
+    """BF16 with 16 slices and k = 2^18: (L+1) k dmax^2 exceeds int32, so the plan reconstructs in K blocks
+    of 1024 (the reference's recon_limbs plan, which this build runs instead of rejecting). Two rows of C
+    equal the oracle's block chain bit for bit; a sample is within the FP64 error bound of binary128."""
+    m = n = 64
+    k = 1 << 18
+    a, b = oz.eval_inputs(17, 0.5, m * k, k * n)
+    A, B = a.reshape(m, k), b.reshape(k, n)
+    opts = oz.Options(scheme=oz.Scheme.I, format=oz.Format.BF16, slices=16)
+    pl = oz.plan1(a, b, m, n, k, slices=16, fmt=oz.Format.BF16)
+    assert pl.defer == 0 and pl.nkb > 1
+    c = np.empty(m * n)
+    info = ctx.gemm(a, b, c, m, n, k, opts)
+    assert info.slices == 16
+    dA, _ = oracle.scale(A, m, k, 0, 0, -1)
+    dB, _ = oracle.scale(B, k, n, 1, 0, -1)
+    rows = slice(5, 7)
+    want = _block_chain(oracle, A, B, rows, dA, dB, 16, 64, 32, pl.Kc)
+    np.testing.assert_array_equal(c.reshape(m, n)[rows].reshape(-1).view(np.uint64), want.view(np.uint64))
+    rng = np.random.default_rng(1)
+    r_ = rng.integers(0, m, 32).astype(np.int32)
+    c_ = rng.integers(0, n, 32).astype(np.int32)
+    q = oz.eval_quad_sample(a, b, m, n, k, r_, c_)
+    absab = np.einsum("ij,ij->i", np.abs(A[r_]), np.abs(B[:, c_].T))
+    assert np.all(np.abs(c.reshape(m, n)[r_, c_] - q) <= k * 2.0 ** -53 * absab)

@@ -219,6 +219,24 @@ def test_scheme1_slices_expand_the_element(orc, radix, dmax):
             assert abs(x - s) <= R / Fraction(radix) ** p * (1 + Fraction(1, 2 ** 20)), (r, c)
 
 
+def test_scheme1_block_recon_agrees_with_one_block(orc):
+    """orc_oz1_recon_blocks (the reconstruction K block by K block) against the one-block reconstruction
+    of the summed diagonals: with one block it is the same sequence of operations (bit-identical to
+    orc_oz1_recon reading every diagonal whole); with several blocks Horner is linear in P_d, so the
+    results agree up to the final rounding (one unit in the last place)."""
+    rng = np.random.default_rng(4)
+    nkb, ndiag, M, N = 5, 7, 6, 9
+    Pb = rng.integers(-(1 << 22), 1 << 22, (nkb, ndiag, M, N)).astype(np.int32)
+    dA = rng.integers(-3, 4, M).astype(np.int32)
+    dB = rng.integers(-3, 4, N).astype(np.int32)
+    one = orc.oz1_recon_blocks(Pb[:1], 64, dA, dB)
+    np.testing.assert_array_equal(one.view(np.uint64), orc.oz1_recon(Pb[0], 64, 0, ndiag, dA, dB).view(np.uint64))
+    blocks = orc.oz1_recon_blocks(Pb, 64, dA, dB)
+    whole = orc.oz1_recon(Pb.astype(np.int64).sum(axis=0).astype(np.int32), 64, 0, 0, dA, dB)
+    assert np.all(np.abs(blocks - whole) <= np.spacing(np.abs(whole)))
+    assert np.mean(blocks == whole) > 0.9
+
+
 def test_scheme1_recon_scale_constant(orc):
     """radix^-(L+2) as W 2^qw: W has its top bit set and W 2^qw is within 2^-60 of the exact value; a
     power-of-two radix gives W = 2^63 exactly (plan.hpp:446-460)."""
