@@ -21,7 +21,9 @@ Also reported: accuracy against binary128 on a 64x64 sample of C at full K (and 
 for a native FP64 dot product), the per-phase device times, the roofline of the product kernel
 (algorithmic int8 operations per launch / its average launch time, against 5.0 POP/s dense INT8),
 the reference's host OpenMP Dot2 GEMM (the oracle's restatement) timed on this host on a row
-slab of the same problem, the GPU's own FP64 GEMM (rocBLAS dgemm) on the same operands, and the
+slab of the same problem, the GPU's own FP64 GEMM (rocBLAS dgemm) on the same operands, the
+matrix cores' throughput with register operands (mfma_ceiling: the power-limited ceiling the
+product kernel's MFMA form reaches with no memory traffic), and the
 wall time of calls on resident operands (Context.upload once; later calls reuse the pair's plan
 and move only C over PCIe, or nothing when C stays on the GPU).
 """
@@ -141,6 +143,20 @@ def native_fp64_gemm(a, b, m: int, n: int, k: int, reps: int = 3) -> dict:
         if h:
             rb.rocblas_destroy_handle(h)
         dev.close()
+
+
+def mfma_ceiling() -> dict:
+    """The matrix cores' throughput with register operands and no memory traffic, at the clock the
+    power limit allows (oztt_amd/lib/mfma_ceiling, built from oztt_amd/csrc/mfma_ceiling.hip): TOP/s
+    (or TFLOP/s) by MFMA form. Run as a child process on the same GPU."""
+    import subprocess
+    exe = Path(__file__).resolve().parent / "oztt_amd" / "lib" / "mfma_ceiling"
+    if not exe.exists():
+        return {"error": f"{exe} is not built"}
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        return {"error": r.stderr.strip()[-300:]}
+    return {d["form"]: d["tops"] for d in (json.loads(l) for l in r.stdout.splitlines() if l.startswith("{"))}
 
 
 # BASELINE.json configs: name -> (scheme, format, m, n, k, seed, phi, options, peak of the product format, rows of
@@ -303,6 +319,14 @@ def main() -> int:
         del c8
     log("native FP64 GEMM on the GPU (rocBLAS dgemm)")
     out["native_fp64_gemm"] = native_fp64_gemm(a, b, m, n, k)
+    log("matrix-core ceiling (register operands)")
+    ceil = mfma_ceiling()
+    form = "v_mfma_f32_32x32x64_f8f6f4" if fmt == "FP8" else "v_mfma_i32_16x16x64_i8"
+    if form in ceil:
+        # the product kernel against what its MFMA form reaches with no memory traffic at all
+        out["roofline"]["measured_ceiling"] = {"form": form, "value": ceil[form],
+                                               "frac": round(achieved / ceil[form], 4)}
+    out["mfma_ceiling"] = ceil
     if cpu_rows > 0:
         log(f"CPU baseline: Dot2 on {cpu_rows} rows")
         out["cpu_baseline"], hi, lo = cpu_baseline(a, b, m, n, k, cpu_rows)

@@ -67,6 +67,9 @@ def build(jobs: int | None = None, oracle: bool = True) -> None:
         steps.append([HIPCC, *HIP_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(OBJ / (src + ".o"))])
     for src in HOST_SOURCES:
         steps.append([CXX, *HOST_FLAGS, "-c", str(CSRC / "host" / src), "-o", str(OBJ / (src + ".o"))])
+    # the matrix cores' register-only throughput (a yardstick of the bench, not part of the library)
+    steps.append([HIPCC, *[f for f in HIP_FLAGS if f != "-fPIC"], str(CSRC / "mfma_ceiling.hip"), "-o",
+                  str(LIB / "mfma_ceiling")])
     with cf.ThreadPoolExecutor(jobs) as ex:
         for f in [ex.submit(_run, s) for s in steps]:
             f.result()
