@@ -972,33 +972,44 @@ void orc_gemm_quad_sample(const double* A, const double* B, int M, int N, int K,
     }
 }
 
-void orc_dot2_gemm(const double* A, const double* B, int M, int N, int K, int r0, int r1, double* Chi, double* Clo) {
-    (void)M;
-    const int IB = 8, JB = 512;
-    for (size_t z = (size_t)r0 * N; z < (size_t)r1 * N; z++) Chi[z] = Clo[z] = 0.0;
-#pragma omp parallel for schedule(static)
-    for (int ib = r0; ib < r1; ib += IB) {
-        const int i1 = std::min(ib + IB, r1);
-        for (int j0 = 0; j0 < N; j0 += JB) {
-            const int j1 = std::min(j0 + JB, N);
-            for (int k = 0; k < K; ++k) {
-                const double* Br = B + (size_t)k * N;
-                for (int i = ib; i < i1; ++i) {
-                    const double a = A[(size_t)i * K + k];
-                    double* chi = Chi + (size_t)i * N;
-                    double* clo = Clo + (size_t)i * N;
-                    for (int j = j0; j < j1; ++j) {
-                        const double bb = Br[j];
-                        const double p = a * bb, e = std::fma(a, bb, -p);
-                        const double c0 = chi[j];
-                        const double s = c0 + p, z = s - c0;
-                        clo[j] += (c0 - (s - z)) + (p - z) + e;
-                        chi[j] = s;
-                    }
+// One block of rows [ib, i1) of the Dot2 GEMM, every column, in the reference's loop order (row
+// blocks of 8, column blocks of 512, k outermost inside a block). The reference builds its
+// evaluator with -O3 -march=native (Makefile:16, :132); this library travels to hosts other than
+// the one it is built on, so the same vectorized code is compiled for the AVX-512 and AVX2+FMA
+// instruction sets and picked at load time by the CPU's features (GCC function multiversioning),
+// with a portable fallback. No flag here changes a result: contraction stays off and the only FMA
+// is the explicit one of TwoProduct.
+__attribute__((target_clones("arch=skylake-avx512", "arch=haswell", "default")))
+static void dot2_block(const double* __restrict A, const double* __restrict B, int N, int K, int ib, int i1,
+                       double* __restrict Chi, double* __restrict Clo) {
+    const int JB = 512;
+    for (int j0 = 0; j0 < N; j0 += JB) {
+        const int j1 = std::min(j0 + JB, N);
+        for (int k = 0; k < K; ++k) {
+            const double* __restrict Br = B + (size_t)k * N;
+            for (int i = ib; i < i1; ++i) {
+                const double a = A[(size_t)i * K + k];
+                double* __restrict chi = Chi + (size_t)i * N;
+                double* __restrict clo = Clo + (size_t)i * N;
+                for (int j = j0; j < j1; ++j) {
+                    const double bb = Br[j];
+                    const double p = a * bb, e = std::fma(a, bb, -p);
+                    const double c0 = chi[j];
+                    const double s = c0 + p, z = s - c0;
+                    clo[j] += (c0 - (s - z)) + (p - z) + e;
+                    chi[j] = s;
                 }
             }
         }
     }
+}
+
+void orc_dot2_gemm(const double* A, const double* B, int M, int N, int K, int r0, int r1, double* Chi, double* Clo) {
+    (void)M;
+    const int IB = 8;
+    for (size_t z = (size_t)r0 * N; z < (size_t)r1 * N; z++) Chi[z] = Clo[z] = 0.0;
+#pragma omp parallel for schedule(static)
+    for (int ib = r0; ib < r1; ib += IB) dot2_block(A, B, N, K, ib, std::min(ib + IB, r1), Chi, Clo);
 }
 
 // Scheme I slicer (slice_tf_body.h:86-131 with the step of sfpu_tf_emu.hpp:193-198): p digits of

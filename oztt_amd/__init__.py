@@ -81,7 +81,14 @@ class EvalStats(ctypes.Structure):
                 ("phase_ms", ctypes.c_double * 5), ("whole_ms", ctypes.c_double), ("whole_checked", ctypes.c_int),
                 ("partial_products", ctypes.c_uint), ("product_ops", ctypes.c_double),
                 ("gemm_launch_ms", ctypes.c_double), ("gemm_launches", ctypes.c_int),
-                ("max_band_rows", ctypes.c_uint), ("plan_reused", ctypes.c_int), ("force_kc", ctypes.c_uint)]
+                ("max_band_rows", ctypes.c_uint), ("plan_reused", ctypes.c_int), ("force_kc", ctypes.c_uint),
+                ("replay_drop_phase", ctypes.c_int), ("whole_sentinel", ctypes.c_int),
+                ("whole_steps", ctypes.c_uint * 5), ("expected_steps", ctypes.c_uint * 5)]
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        if "replay_drop_phase" not in kw:
+            self.replay_drop_phase = -1
 
 
 class Plan2(ctypes.Structure):
@@ -240,17 +247,20 @@ class Context:
         return c
 
     def evaluate(self, a, b, m: int, n: int, k: int, options: Options, fixed_bits: int = 0, warmup: int = 0,
-                 repeats: int = 0, max_band_rows: int = 0, force_kc: int = 0):
+                 repeats: int = 0, max_band_rows: int = 0, force_kc: int = 0, replay_drop_phase: int = -1):
         """GEMM under the evaluation hooks: returns (C, Info, EvalStats) with phase and whole-pass times.
         max_band_rows > 0 caps the rows of a band (row bands are otherwise used only when the problem
         does not fit in device memory); force_kc > 0 makes Scheme I with an FP32-product format
-        reconstruct K block by K block with blocks of that length."""
+        reconstruct K block by K block with blocks of that length. replay_drop_phase >= 0 is the
+        self-test of the whole-pass check: its checking replay leaves out that phase's steps, so
+        whole_checked must be 0, and nothing is timed."""
         a, b = _f64(a), _f64(b)
         c = np.empty(m * n, dtype=np.float64)
         ev = EvalStats()
         ev.fixed_bits, ev.warmup, ev.repeats = fixed_bits, warmup, repeats
         ev.max_band_rows = max_band_rows
         ev.force_kc = force_kc
+        ev.replay_drop_phase = replay_drop_phase
         info = self._call(a, b, c, m, n, k, options, ev)
         return c, info, ev
 

@@ -67,9 +67,6 @@ def build(jobs: int | None = None, oracle: bool = True) -> None:
         steps.append([HIPCC, *HIP_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(OBJ / (src + ".o"))])
     for src in HOST_SOURCES:
         steps.append([CXX, *HOST_FLAGS, "-c", str(CSRC / "host" / src), "-o", str(OBJ / (src + ".o"))])
-    # the matrix cores' register-only throughput (a yardstick of the bench, not part of the library)
-    steps.append([HIPCC, *[f for f in HIP_FLAGS if f != "-fPIC"], str(CSRC / "mfma_ceiling.hip"), "-o",
-                  str(LIB / "mfma_ceiling")])
     with cf.ThreadPoolExecutor(jobs) as ex:
         for f in [ex.submit(_run, s) for s in steps]:
             f.result()
@@ -78,6 +75,13 @@ def build(jobs: int | None = None, oracle: bool = True) -> None:
     host_objs = [str(OBJ / (s + ".o")) for s in HOST_SOURCES]
     _run([CXX, "-shared", "-fPIC", "-fopenmp", "-o", str(LIB / "libozTTgemm.so"), *host_objs,
           f"-L{LIB}", "-loz_hip", "-Wl,-rpath,$ORIGIN", "-lquadmath"])
+    # a C++ caller of the public header (the reference's correctness cases and usage example), linked
+    # with the library as a user would link it; run by tests/test_cpp_caller.py
+    caller = ROOT / "tests" / "cpp"
+    (caller / "build").mkdir(parents=True, exist_ok=True)
+    _run([CXX, "-std=c++20", "-O2", "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{CSRC / 'host'}",
+          str(caller / "ozttgemm_caller.cpp"), "-o", str(caller / "build" / "ozttgemm_caller"), f"-L{LIB}",
+          "-lozTTgemm", "-Wl,-rpath,$ORIGIN/../../../oztt_amd/lib"])
     if oracle:
         _run(["make", "-s", "-C", str(ROOT / "oracle")])
 

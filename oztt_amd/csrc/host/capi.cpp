@@ -76,6 +76,10 @@ struct ozt_eval {
     unsigned max_band_rows;  // input: cap on the rows of a band (0: bands only when memory requires)
     int plan_reused;         // resident operands: the plan kept from an earlier call was used
     unsigned force_kc;       // input: Scheme I block-by-block reconstruction with this K block (0: as planned)
+    int replay_drop_phase;   // input: self-test of the whole-pass check (-1: off)
+    int whole_sentinel;      // the checking replay rewrote the sentinel-filled output with the first pass's bits
+    unsigned whole_steps[5];     // steps per phase issued by the checking replay
+    unsigned expected_steps[5];  // steps per phase the plan calls for
 };
 
 struct ozt_plan2 {
@@ -184,7 +188,8 @@ int ozt_gemm_resident(void* ctx, void* a, void* b, double* c, std::size_t nc, vo
             s.warmup = evo->warmup;
             s.repeats = evo->repeats;
             s.max_band_rows = evo->max_band_rows;
-        s.force_kc = evo->force_kc;
+            s.force_kc = evo->force_kc;
+            s.replay_drop_phase = evo->replay_drop_phase;
             {
                 ozTTgemm::evaluation::Scope scope(s);
                 i = run();
@@ -207,6 +212,7 @@ int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, s
         s.repeats = evo->repeats;
         s.max_band_rows = evo->max_band_rows;
         s.force_kc = evo->force_kc;
+        s.replay_drop_phase = evo->replay_drop_phase;
         auto* cx = static_cast<ozTTgemm::Context*>(ctx);
         ozTTgemm::Info i;
         {
@@ -227,6 +233,11 @@ static void fill_eval(const ozTTgemm::evaluation::Settings& s, ozt_eval* evo) {
     evo->gemm_launch_ms = s.gemm_launch_ms;
     evo->gemm_launches = s.gemm_launches;
     evo->plan_reused = s.plan_reused ? 1 : 0;
+    evo->whole_sentinel = s.whole_sentinel ? 1 : 0;
+    for (int p = 0; p < 5; p++) {
+        evo->whole_steps[p] = s.whole_steps[p];
+        evo->expected_steps[p] = s.expected_steps[p];
+    }
 }
 
 int ozt_is_available(int format) { return ozTTgemm::is_available(static_cast<ozTTgemm::Format>(format)) ? 1 : 0; }

@@ -24,73 +24,145 @@ namespace {
 std::recursive_mutex runtime_mutex;
 std::atomic<std::uint64_t> next_matrix_id{1};
 
-std::size_t checked_product(std::size_t a, std::size_t b) {
-    if (a == 0 || b == 0 || a > std::numeric_limits<std::size_t>::max() / sizeof(double) / b)
-        throw std::invalid_argument("matrix dimensions are zero or overflow the address space");
-    return a * b;
-}
-std::uint32_t padded(std::size_t value, std::size_t quantum) {
-    constexpr std::size_t limit = std::numeric_limits<std::int32_t>::max();
-    if (value == 0 || value > limit - quantum)
-        throw std::invalid_argument("matrix dimension exceeds the supported device index range");
-    return static_cast<std::uint32_t>((value + quantum - 1) / quantum * quantum);
-}
-// Every nonzero row maximum of A and column maximum of B must be a normal BF16 value, because the
-// device normalizes by BF16 maxima (context.cpp:37-63).
-void check_values(std::span<const double> a, std::span<const double> b, std::size_t m, std::size_t n, std::size_t k) {
-    constexpr double maximum = 0x1.fep127, minimum = 0x1p-126;
-    const auto check_max = [&](double x) {
-        if (x != 0 && (x < minimum || x > maximum))
-            throw std::invalid_argument(
-                "each nonzero row maximum of A and column maximum of B must be in [2^-126, max_BF16]");
-    };
-    for (std::size_t i = 0; i < m; ++i) {
-        double mx = 0;
-        for (std::size_t j = 0; j < k; ++j) {
-            const double x = a[i * k + j];
-            if (!std::isfinite(x)) throw std::invalid_argument("A contains NaN or infinity");
-            mx = std::max(mx, std::abs(x));
-        }
-        check_max(mx);
-    }
-    std::vector<double> maxima(n, 0);
-    for (std::size_t i = 0; i < k; ++i)
-        for (std::size_t j = 0; j < n; ++j) {
-            const double x = b[i * n + j];
-            if (!std::isfinite(x)) throw std::invalid_argument("B contains NaN or infinity");
-            maxima[j] = std::max(maxima[j], std::abs(x));
-        }
-    for (double x : maxima) check_max(x);
-}
-// Enum values are checked too: a caller can pass any integer through a cast (context.cpp:82-100).
-void check_options(const Options& o) {
-    if (o.scheme != Scheme::I && o.scheme != Scheme::II) throw std::invalid_argument("unknown Ozaki scheme");
-    if (!is_available(o.format)) throw std::invalid_argument("format is unknown or was not built");
-    if (o.reconstruction != Reconstruction::Automatic && o.reconstruction != Reconstruction::OnePass &&
-        o.reconstruction != Reconstruction::TwoPass)
-        throw std::invalid_argument("unknown reconstruction mode");
-    if (o.slices > 256) throw std::invalid_argument("slices must be zero (automatic) or at most 256");
-    if (o.max_moduli > 24) throw std::invalid_argument("max_moduli exceeds the supported bound of 24");
-    if (o.scheme == Scheme::I && (o.max_moduli != 0 || o.reconstruction != Reconstruction::Automatic))
-        throw std::invalid_argument("max_moduli and reconstruction apply only to Ozaki II");
-    if (o.scheme == Scheme::II && o.slices != 0) throw std::invalid_argument("slices applies only to Ozaki I");
-    if (!detail::scheme_available(o.format, o.scheme))
-        throw std::invalid_argument("this scheme is not built for the requested format");
-}
-struct Checked {
-    std::uint32_t mp, np, kp;
-    std::size_t c_size;
+// ---- Call validation -----------------------------------------------------------------------------
+// The contract is the reference's (context.cpp:17-117): a call is rejected with
+// std::invalid_argument before the device is opened and before C is written, and its checks run in
+// three rounds, in this order: the options; the shape (span sizes against m, n, k, element counts
+// that fit the address space, padded extents that fit the device's 32-bit indices); the values
+// (finite, and every nonzero row maximum of A and column maximum of B a normal BF16 value, because
+// the device normalizes each row of A and each column of B by its maximum held as BF16).
+
+// The option rules, applied in this order; the first one violated is reported.
+struct OptionRule {
+    bool (*violated)(const Options&);
+    const char* message;
 };
-Checked validate(const Options& options, std::span<const double> a, std::span<const double> b,
-                 std::optional<std::size_t> c_size, std::size_t m, std::size_t n, std::size_t k) {
-    check_options(options);
-    if (a.size() != checked_product(m, k) || b.size() != checked_product(k, n))
-        throw std::invalid_argument("matrix span sizes do not match m, n, k");
-    const std::size_t mn = checked_product(m, n);
-    if (c_size && *c_size != mn) throw std::invalid_argument("matrix span sizes do not match m, n, k");
-    const Checked v{padded(m, 64), padded(n, 64), padded(k, 32), mn};
-    check_values(a, b, m, n, k);
-    return v;
+constexpr OptionRule kOptionRules[] = {
+    // enum values are checked as numbers: a caller can pass any integer through a cast
+    {[](const Options& o) { return o.scheme != Scheme::I && o.scheme != Scheme::II; },
+     "options.scheme is not an Ozaki scheme"},
+    {[](const Options& o) { return !is_available(o.format); }, "options.format is not a format of this build"},
+    {[](const Options& o) {
+         return o.reconstruction != Reconstruction::Automatic && o.reconstruction != Reconstruction::OnePass &&
+                o.reconstruction != Reconstruction::TwoPass;
+     },
+     "options.reconstruction is not a reconstruction mode"},
+    {[](const Options& o) { return o.slices > 256; }, "options.slices must be 0 (automatic) or 1..256"},
+    {[](const Options& o) { return o.max_moduli > 24; }, "options.max_moduli must be 0 (automatic) or 1..24"},
+    {[](const Options& o) {
+         return o.scheme == Scheme::I && (o.max_moduli != 0 || o.reconstruction != Reconstruction::Automatic);
+     },
+     "options.max_moduli and options.reconstruction are Ozaki II settings"},
+    {[](const Options& o) { return o.scheme == Scheme::II && o.slices != 0; }, "options.slices is an Ozaki I setting"},
+    {[](const Options& o) { return !detail::scheme_available(o.format, o.scheme); },
+     "this build has no such scheme for options.format"},
+};
+
+void require_options(const Options& o) {
+    for (const OptionRule& rule : kOptionRules)
+        if (rule.violated(o)) throw std::invalid_argument(rule.message);
+}
+
+// rows x cols elements of 8 bytes: zero extents, and matrices whose bytes overflow size_t, are rejected.
+std::size_t element_count(std::size_t rows, std::size_t cols) {
+    std::size_t elements = 0, bytes = 0;
+    if (rows == 0 || cols == 0 || __builtin_mul_overflow(rows, cols, &elements) ||
+        __builtin_mul_overflow(elements, sizeof(double), &bytes))
+        throw std::invalid_argument("a matrix extent is zero or the matrix exceeds the address space");
+    return elements;
+}
+
+// extent rounded up to a multiple of q (64 for m and n, 32 for k); the padded extents index the
+// device with 32-bit signed integers.
+std::uint32_t padded_extent(std::size_t extent, std::size_t q) {
+    constexpr std::size_t kIndexLimit = (std::size_t)std::numeric_limits<std::int32_t>::max();
+    if (extent == 0 || extent > kIndexLimit - q)
+        throw std::invalid_argument("a matrix extent exceeds the device's 32-bit index range");
+    return (std::uint32_t)((extent + q - 1) / q * q);
+}
+
+struct CallShape {
+    std::uint32_t mp, np, kp;  // padded extents
+    std::size_t mn;            // elements of C
+};
+
+CallShape require_shape(std::size_t na, std::size_t nb, std::optional<std::size_t> nc, std::size_t m, std::size_t n,
+                        std::size_t k) {
+    const std::size_t want_a = element_count(m, k), want_b = element_count(k, n);
+    if (na != want_a || nb != want_b) throw std::invalid_argument("the sizes of a and b do not match m, n, k");
+    const std::size_t mn = element_count(m, n);
+    if (nc && *nc != mn) throw std::invalid_argument("the size of c does not match m x n");
+    return {padded_extent(m, 64), padded_extent(n, 64), padded_extent(k, 32), mn};
+}
+
+}  // namespace
+
+namespace detail {
+// What the value rules need to know of one operand (rows x cols, row-major), from one scan over it
+// with the rows split among threads. A maximum is admissible when it is zero or a normal BF16 value.
+struct OperandScan {
+    std::size_t first_bad_row = 0;    // first row with a non-finite value or an inadmissible maximum (rows: none)
+    bool first_bad_nonfinite = false; // that row holds a non-finite value
+    bool finite = true;               // no NaN or infinity anywhere
+    bool cols_ok = true;              // every column maximum is admissible
+};
+OperandScan scan_operand(const double* x, std::size_t rows, std::size_t cols) {
+    constexpr double kBf16Max = 0x1.fep127, kBf16MinNormal = 0x1p-126;
+    auto admissible = [](double v) { return v == 0 || (v >= kBf16MinNormal && v <= kBf16Max); };
+    std::vector<unsigned char> row_state(rows);  // 0 fine, 1 non-finite value, 2 inadmissible maximum
+    std::vector<double> colmax(cols, 0);
+#pragma omp parallel
+    {
+        std::vector<double> cm(cols, 0);
+#pragma omp for schedule(static) nowait
+        for (std::int64_t i = 0; i < (std::int64_t)rows; ++i) {
+            const double* r = x + (std::size_t)i * cols;
+            double mx = 0;
+            bool fin = true;
+            for (std::size_t j = 0; j < cols; ++j) {
+                const double v = std::abs(r[j]);
+                fin = fin && std::isfinite(v);
+                mx = std::max(mx, v);
+                cm[j] = std::max(cm[j], v);
+            }
+            row_state[(std::size_t)i] = !fin ? 1 : admissible(mx) ? 0 : 2;
+        }
+#pragma omp critical
+        for (std::size_t j = 0; j < cols; ++j) colmax[j] = std::max(colmax[j], cm[j]);
+    }
+    OperandScan s;
+    s.first_bad_row = rows;
+    for (std::size_t i = rows; i-- > 0;)
+        if (row_state[i]) {
+            s.first_bad_row = i;
+            s.first_bad_nonfinite = row_state[i] == 1;
+        }
+    for (unsigned char st : row_state) s.finite = s.finite && st != 1;
+    for (double v : colmax) s.cols_ok = s.cols_ok && std::isfinite(v) && admissible(v);
+    return s;
+}
+
+// The value round, in the reference's order: A row by row (a row's non-finite values before its
+// maximum), then the finiteness of all of B, then B's column maxima.
+void require_values(const OperandScan& a, std::size_t a_rows, const OperandScan& b) {
+    static const char* const kRange =
+        "every nonzero row maximum of A and column maximum of B must lie in [2^-126, the largest BF16]";
+    if (a.first_bad_row < a_rows)
+        throw std::invalid_argument(a.first_bad_nonfinite ? "A holds a NaN or an infinity" : kRange);
+    if (!b.finite) throw std::invalid_argument("B holds a NaN or an infinity");
+    if (!b.cols_ok) throw std::invalid_argument(kRange);
+}
+
+}  // namespace detail
+
+namespace {
+
+CallShape validate(const Options& options, std::span<const double> a, std::span<const double> b,
+                   std::optional<std::size_t> c_size, std::size_t m, std::size_t n, std::size_t k) {
+    require_options(options);
+    const CallShape shape = require_shape(a.size(), b.size(), c_size, m, n, k);
+    detail::require_values(detail::scan_operand(a.data(), m, k), m, detail::scan_operand(b.data(), k, n));
+    return shape;
 }
 
 }  // namespace
@@ -104,52 +176,11 @@ struct DeviceHandle {
         if (dev) oz_dev_close(dev);
     }
 };
-
-// What the checks of gemm() need to know about a resident operand (check_values on its host copy).
-struct Facts {
-    bool finite = true, rows_ok = true, cols_ok = true;
-};
-Facts facts_of(const double* x, std::size_t rows, std::size_t cols) {
-    constexpr double maximum = 0x1.fep127, minimum = 0x1p-126;
-    auto ok = [&](double v) { return v == 0 || (v >= minimum && v <= maximum); };
-    bool finite = true, rows_ok = true;
-    std::vector<double> colmax(cols, 0);
-    // rows in parallel; each thread keeps its own column maxima (maxima do not depend on the order)
-#pragma omp parallel
-    {
-        std::vector<double> cm(cols, 0);
-        bool fin = true, rok = true;
-#pragma omp for schedule(static) nowait
-        for (std::int64_t i = 0; i < (std::int64_t)rows; ++i) {
-            const double* r = x + (std::size_t)i * cols;
-            double mx = 0;
-            for (std::size_t j = 0; j < cols; ++j) {
-                const double v = r[j];
-                fin = fin && std::isfinite(v);
-                const double av = std::abs(v);
-                mx = std::max(mx, av);
-                cm[j] = std::max(cm[j], av);
-            }
-            rok = rok && ok(mx);
-        }
-#pragma omp critical
-        {
-            finite = finite && fin;
-            rows_ok = rows_ok && rok;
-            for (std::size_t j = 0; j < cols; ++j) colmax[j] = std::max(colmax[j], cm[j]);
-        }
-    }
-    Facts f;
-    f.finite = finite;
-    f.rows_ok = rows_ok;
-    for (double v : colmax) f.cols_ok = f.cols_ok && ok(v);
-    return f;
-}
 }  // namespace detail
 
 using detail::DeviceHandle;
-using detail::Facts;
-using detail::facts_of;
+using detail::OperandScan;
+using detail::scan_operand;
 
 struct Matrix::State {
     std::uint64_t id = 0;
@@ -158,7 +189,7 @@ struct Matrix::State {
     // host copy (row-major rows x cols) and its facts; a result has them only once it is needed
     std::unique_ptr<double[]> host;
     bool have_host = false;
-    Facts facts;
+    OperandScan facts;
     // device copies: the first one (src, leading dimension src_ld) and the zero-padded layouts
     // (prow x pcol, leading dimension pcol) made from it; src is one of them or the raw upload
     struct Copy {
@@ -193,7 +224,7 @@ struct Context::Impl {
             throw std::invalid_argument("kernel_directory does not name a directory");
     }
     Info execute(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m,
-                 std::size_t n, std::size_t k, const Options& options, const Checked& v);
+                 std::size_t n, std::size_t k, const Options& options, const CallShape& v);
     void open();
     // resident operands (under the lock)
     const double* layout(Matrix::State& x, std::uint32_t prow, std::uint32_t pcol);
@@ -244,14 +275,14 @@ void Context::Impl::open() {
 }
 
 Info Context::Impl::execute(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m,
-                            std::size_t n, std::size_t k, const Options& opts, const Checked& v) {
+                            std::size_t n, std::size_t k, const Options& opts, const CallShape& v) {
     const auto mp = v.mp, np = v.np, kp = v.kp;
     std::lock_guard lock(runtime_mutex);
     open();
     // zero-padded copies into the page-locked staging buffers (rows in parallel); they are complete
     // before C is written, so C may alias A or B
-    auto* ap = static_cast<double*>(device.ws->host(detail::kHostA, sizeof(double) * checked_product(mp, kp)));
-    auto* bp = static_cast<double*>(device.ws->host(detail::kHostB, sizeof(double) * checked_product(kp, np)));
+    auto* ap = static_cast<double*>(device.ws->host(detail::kHostA, sizeof(double) * element_count(mp, kp)));
+    auto* bp = static_cast<double*>(device.ws->host(detail::kHostB, sizeof(double) * element_count(kp, np)));
     const double* ad = a.data();
     const double* bd = b.data();
 #pragma omp parallel for schedule(static)
@@ -289,14 +320,14 @@ Info Context::Impl::execute(std::span<const double> a, std::span<const double> b
 
 Info Context::gemm(std::span<const double> a, std::span<const double> b, std::span<double> c, std::size_t m,
                    std::size_t n, std::size_t k, const Options& options) {
-    const Checked v = validate(options, a, b, c.size(), m, n, k);
+    const CallShape v = validate(options, a, b, c.size(), m, n, k);
     return impl_->execute(a, b, c, m, n, k, options, v);
 }
 
 std::vector<double> Context::multiply(std::span<const double> a, std::span<const double> b, std::size_t m,
                                       std::size_t n, std::size_t k, const Options& options) {
-    const Checked v = validate(options, a, b, std::nullopt, m, n, k);
-    std::vector<double> c(v.c_size);
+    const CallShape v = validate(options, a, b, std::nullopt, m, n, k);
+    std::vector<double> c(v.mn);
     impl_->execute(a, b, c, m, n, k, options, v);
     return c;
 }
@@ -329,7 +360,7 @@ void Context::Impl::fetch_host(Matrix::State& x) {
 #pragma omp parallel for schedule(static)
     for (std::int64_t i = 0; i < (std::int64_t)x.rows; ++i)
         std::copy_n(buf.get() + (std::size_t)i * x.src_ld, x.cols, x.host.get() + (std::size_t)i * x.cols);
-    x.facts = facts_of(x.host.get(), x.rows, x.cols);
+    x.facts = scan_operand(x.host.get(), x.rows, x.cols);
     x.have_host = true;
 }
 
@@ -355,12 +386,11 @@ const double* Context::Impl::padded_host(Matrix::State& x, std::uint32_t prow, s
 
 Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<double>* c,
                              std::shared_ptr<Matrix::State>* cslot, const Options& opts) {
-    check_options(opts);
+    require_options(opts);
     const std::size_t m = A.rows, k = A.cols, n = B.cols;
-    if (B.rows != k) throw std::invalid_argument("matrix dimensions do not match: a is m x k and b must be k x n");
-    const std::size_t mn = checked_product(m, n);
-    if (c && c->size() != mn) throw std::invalid_argument("matrix span sizes do not match m, n, k");
-    const std::uint32_t mp = padded(m, 64), np = padded(n, 64), kp = padded(k, 32);
+    if (B.rows != k) throw std::invalid_argument("the extents do not match: a is m x k and b must be k x n");
+    const CallShape shape = require_shape(m * k, k * n, c ? std::optional<std::size_t>(c->size()) : std::nullopt, m, n, k);
+    const std::uint32_t mp = shape.mp, np = shape.np, kp = shape.kp;
     std::lock_guard lock(runtime_mutex);
     // a Context's matrices hold its device handle, which no other Context shares (and a Context
     // that made no Matrix has none yet)
@@ -381,13 +411,10 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
                 break;
             }
         }
-    // the checks of gemm() (check_values), on the operands' facts
+    // the value round of gemm(), on the scans of the operands' host copies
     fetch_host(A);
     fetch_host(B);
-    if (!A.facts.finite) throw std::invalid_argument("A contains NaN or infinity");
-    if (!B.facts.finite) throw std::invalid_argument("B contains NaN or infinity");
-    if (!A.facts.rows_ok || !B.facts.cols_ok)
-        throw std::invalid_argument("each nonzero row maximum of A and column maximum of B must be in [2^-126, max_BF16]");
+    detail::require_values(A.facts, m, B.facts);
     const double* ah = plan ? nullptr : padded_host(A, mp, kp);
     const double* bh = plan ? nullptr : padded_host(B, kp, np);
     const double* ad = layout(A, mp, kp);
@@ -444,13 +471,13 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
 }
 
 Matrix Context::upload(std::span<const double> x, std::size_t rows, std::size_t cols) {
-    if (x.size() != checked_product(rows, cols))
+    if (x.size() != element_count(rows, cols))
         throw std::invalid_argument("matrix span size does not match rows x cols");
-    padded(rows, 64);  // index range of either role
-    padded(cols, 64);
+    padded_extent(rows, 64);  // index range of either role
+    padded_extent(cols, 64);
     auto st = std::make_shared<Matrix::State>();
-    st->facts = facts_of(x.data(), rows, cols);
-    if (!st->facts.finite) throw std::invalid_argument("the matrix contains NaN or infinity");
+    st->facts = scan_operand(x.data(), rows, cols);
+    if (!st->facts.finite) throw std::invalid_argument("the matrix holds a NaN or an infinity");
     st->id = next_matrix_id++;
     st->rows = rows;
     st->cols = cols;

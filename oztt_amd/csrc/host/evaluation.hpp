@@ -5,10 +5,11 @@
 // Scope is active on the calling thread, a backend
 //   - times each phase (scale, slice, gemm, compose, recon) with HIP events around every device
 //     step on its stream (in warm passes after the replays, when there are replays),
-//   - records every device step of the call and afterwards replays the whole pass `warmup` times
-//     untimed and `repeats` times between two events (inputs and intermediates resident in HBM,
-//     no host work inside), checks that the replayed output is bit-identical to the first pass,
-//     and reports the average whole-pass time.
+//   - records every device step of the call; fills every region the pass writes with a sentinel
+//     and replays the pass once, counting its steps per phase against the plan's; then replays it
+//     `warmup` times untimed and `repeats` times between two events (inputs and intermediates
+//     resident in HBM, no host work inside), checks that the output is still bit-identical to the
+//     first pass, and reports the average whole-pass time.
 // Without a Scope the hooks cost nothing. The library itself never activates one.
 #pragma once
 
@@ -29,11 +30,20 @@ struct Settings {
     unsigned max_band_rows = 0;  // cap on the rows of a band (0: bands only when memory requires)
     unsigned force_kc = 0;       // Scheme I, FP32-product formats: reconstruct K block by K block with
                                  // blocks of this length (0: as planned; it must divide the padded K)
+    int replay_drop_phase = -1;  // self-test of the whole-pass check: its checking replay leaves out the
+                                 // steps of this phase (so whole_checked must come out false), and
+                                 // nothing is timed; -1 (the default) replays every step
     // outputs
     double phase_ms[PhaseCount] = {};  // device time of each phase: the average of up to 5 warm passes
                                        // after the replays (the first pass when there are none)
     double whole_ms = 0;               // average time of one replayed whole pass
-    bool whole_checked = false;        // replayed output bit-identical to the first pass
+    bool whole_checked = false;        // the replays are sound: whole_sentinel, the replayed steps per
+                                       // phase equal the plan's, and the output after the timed
+                                       // replays is bit-identical to the first pass
+    bool whole_sentinel = false;       // every region the pass writes was filled with a sentinel, and one
+                                       // replay then rewrote the whole output with the first pass's bits
+    unsigned whole_steps[PhaseCount] = {};     // device steps issued per phase by the checking replay
+    unsigned expected_steps[PhaseCount] = {};  // device steps per phase that the plan calls for
     unsigned partial_products = 0;     // low-precision matrix products per call (S or slice pairs)
     double product_ops = 0;            // algorithmic operations of the product phase (2*M*N*K*products)
     double gemm_launch_ms = 0;         // device time of the product launches of one pass, in the replays

@@ -168,8 +168,23 @@ Output ozaki1_run(Device& D, const Problem& p) {
     }
     // P(P+1)/2 slice-pair products of 2*M*N*K operations each
     const unsigned pairs = P * (P + 1) / 2;
+    // the pass the configuration calls for: scale once; B's slices once per K block; per band and K
+    // block A's slices, the diagonal products and a reconstruction step; and the regions it writes
+    PassShape shape;
+    shape.steps[ev::Scale] = 1;
+    shape.steps[ev::Slice] = nkb + nbands * nkb;
+    shape.steps[ev::Gemm] = nbands * nkb;
+    shape.steps[ev::Recon] = nbands * nkb;
+    shape.written = {{flags, 2 * sizeof(std::uint32_t)},
+                     {dltA, sizeof(std::int32_t) * M},
+                     {dltB, sizeof(std::int32_t) * N},
+                     {slA, (std::size_t)P * strideA},
+                     {slB, (std::size_t)nkb * P * strideB},
+                     {part, sizeof(std::int32_t) * (std::size_t)P * strideP},
+                     {out, sizeof(double) * M * (std::size_t)N}};
+    if (limbs) shape.written.push_back({limbs, 3 * sizeof(float) * (std::size_t)M * N});
     auto* host = p.c_dev ? nullptr : static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, out, host, host ? (std::size_t)M * N : 0, flags, 2.0 * M * (double)N * K * pairs, pairs);
+    run_pipeline(dev, steps, shape, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
     Info info{Scheme::I, p.options.format};
     info.slices = P;
     return {host, info, planp};

@@ -178,8 +178,22 @@ Output ozaki2_run(Device& D, const Problem& p) {
     // products: one per modulus (INT8) or the FP8 route's digit products (sum of the outputs' pairs)
     const std::uint32_t nprod = fp8 ? (std::uint32_t)plan.mo.nprod : S;
 
+    // the pass the configuration calls for: scale once; B's slice once and A's per band; one product
+    // and one reconstruction step per band; and the regions it writes
+    PassShape shape;
+    shape.steps[ev::Scale] = 1;
+    shape.steps[ev::Slice] = 1 + nbands;
+    shape.steps[ev::Gemm] = nbands;
+    shape.steps[ev::Recon] = nbands;
+    shape.written = {{flags, 2 * sizeof(std::uint32_t)},
+                     {dltA, sizeof(std::int32_t) * M},
+                     {dltB, sizeof(std::int32_t) * N},
+                     {planesA, (std::size_t)nplanes * strideA},
+                     {planesB, (std::size_t)nplanes * strideB},
+                     {prod, (std::size_t)nterms * strideC * term_bytes},
+                     {out, sizeof(double) * M * (std::size_t)N}};
     auto* host = p.c_dev ? nullptr : static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, out, host, host ? (std::size_t)M * N : 0, flags, 2.0 * M * (double)N * K * nprod, nprod);
+    run_pipeline(dev, steps, shape, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * nprod, nprod);
     Info info{Scheme::II, p.options.format};
     info.moduli = S;
     info.integer_bits = (std::uint32_t)plan.b;

@@ -11,8 +11,34 @@ namespace ozTTgemm::detail {
 
 namespace ev = ::ozTTgemm::evaluation;
 
-void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const double* out, double* host, std::size_t count,
-                  const std::uint32_t* flags, double product_ops, unsigned partial_products) {
+namespace {
+
+// Written into every region a pass writes before the checking replay. As a double, the doubled
+// word is a NaN, which no reconstruction produces, so a value that survives is never mistaken for
+// a result.
+constexpr std::uint32_t kSentinel = 0x7FF4DEADu;
+
+std::vector<double> read_back(oz_dev* dev, const double* out, std::size_t count) {
+    std::vector<double> v(count);
+    if (count) device_check(dev, oz_memcpy_d2h(dev, v.data(), out, sizeof(double) * count), "read C");
+    return v;
+}
+
+bool same_bits(const std::vector<double>& x, const double* y, std::size_t count) {
+    return x.size() == count && (count == 0 || std::memcmp(x.data(), y, sizeof(double) * count) == 0);
+}
+
+bool whole_counts_match(const ev::Settings& s) {
+    for (int ph = 0; ph < ev::PhaseCount; ph++)
+        if (s.whole_steps[ph] != s.expected_steps[ph]) return false;
+    return true;
+}
+
+}  // namespace
+
+void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& shape, const double* out,
+                  double* host, std::size_t count, const std::uint32_t* flags, double product_ops,
+                  unsigned partial_products) {
     ev::Settings* es = ev::active();
     // Per-phase device times: events around every step (slots 24 + 2i, 25 + 2i), summed by phase.
     // The events are read after the pass, so each step needs its own pair.
@@ -44,14 +70,55 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const double* out
         es->product_ops = product_ops;
         es->gemm_launches = 0;
         for (auto& s : steps) es->gemm_launches += s.phase == ev::Gemm;
+        es->whole_checked = false;
+        es->whole_sentinel = false;
+        for (int ph = 0; ph < ev::PhaseCount; ph++) {
+            es->whole_steps[ph] = 0;
+            es->expected_steps[ph] = shape.steps[ph];
+        }
     }
-    if (count) device_check(dev, oz_memcpy_d2h(dev, host, out, sizeof(double) * count), "read C");
+    if (host && count) device_check(dev, oz_memcpy_d2h(dev, host, out, sizeof(double) * count), "read C");
     std::uint32_t fl[2];
     device_check(dev, oz_memcpy_d2h(dev, fl, flags, sizeof fl), "read flags");
 
+    // the first pass's result (when it is not in `host`), the reference of every replay
+    std::vector<double> whole_ref;
     if (es && es->repeats > 0) {
-        // whole pass: warm up, then `repeats` replays between two events; then the product step
-        // alone, for its average launch time
+        std::vector<double> first;
+        const double* ref = host;
+        if (!host) {
+            first = read_back(dev, out, count);
+            ref = first.data();
+        }
+        // 1. sentinel in every region the pass writes; the output must read back as sentinel
+        for (const Written& w : shape.written)
+            device_check(dev, oz_fill_u32(dev, w.p, kSentinel, w.bytes / 4), "sentinel fill");
+        std::vector<double> got = read_back(dev, out, count);
+        bool filled = count > 0;
+        for (std::size_t i = 0; filled && i < count; i++) {
+            std::uint64_t u;
+            std::memcpy(&u, &got[i], 8);
+            filled = u == ((std::uint64_t)kSentinel << 32 | kSentinel);
+        }
+        // 2. one checking replay, its steps counted per phase (the checker's self-test can leave out
+        //    one phase; that run then stops after the check and times nothing)
+        for (auto& s : steps) {
+            if ((int)s.phase == es->replay_drop_phase) continue;
+            s.issue();
+            es->whole_steps[s.phase]++;
+        }
+        got = read_back(dev, out, count);
+        es->whole_sentinel = filled && same_bits(got, ref, count);
+        if (!host) whole_ref = std::move(first);
+        es->whole_ms = 0;
+        es->gemm_launch_ms = 0;
+        // after the self-test's incomplete replay, one whole pass restores the result on the device
+        if (es->replay_drop_phase >= 0)
+            for (auto& s : steps) s.issue();
+    }
+    if (es && es->repeats > 0 && es->replay_drop_phase < 0) {
+        // 3. whole pass: warm up, then `repeats` replays between two events; the output must still
+        //    be the first pass's
         for (int w = 0; w < es->warmup; w++)
             for (auto& s : steps) s.issue();
         device_check(dev, oz_event_record(dev, 20), "event");
@@ -61,9 +128,10 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const double* out
         float ms = 0;
         device_check(dev, oz_event_elapsed_ms(dev, 20, 21, &ms), "event time");
         es->whole_ms = ms / es->repeats;
-        std::vector<double> again(count);
-        if (count) device_check(dev, oz_memcpy_d2h(dev, again.data(), out, sizeof(double) * count), "read C");
-        es->whole_checked = count && std::memcmp(again.data(), host, sizeof(double) * count) == 0;
+        const std::vector<double> last = read_back(dev, out, count);
+        es->whole_checked = es->whole_sentinel && whole_counts_match(*es) &&
+                            same_bits(last, host ? host : whole_ref.data(), count);
+        // 4. the product steps alone, for their average launch time
         device_check(dev, oz_event_record(dev, 22), "event");
         for (int r = 0; r < es->repeats; r++)
             for (auto& s : steps)

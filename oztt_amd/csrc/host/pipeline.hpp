@@ -19,12 +19,32 @@ struct Step {
     std::function<void()> issue;
 };
 
-// Issues `steps` (timing each phase, then replaying the whole pass and the product steps, those of
-// phase Gemm, under an active evaluation Scope), reads back the `count` result values of `out` into
-// `host` (none for a result that stays on the device) and the two range flags, and throws
-// std::runtime_error for a set flag (scale.hpp:187-208).
+// A device region that one pass writes (every intermediate and the output, never an input).
+// Sizes are whole 32-bit words.
+struct Written {
+    void* p;
+    std::size_t bytes;
+};
+
+// What one call's pass consists of, stated by the backend from its configuration (not from the
+// step list): the device steps it issues per phase, and the regions they write.
+struct PassShape {
+    unsigned steps[evaluation::PhaseCount] = {};
+    std::vector<Written> written;
+};
+
+// Issues `steps` (timing each phase, then checking and replaying the whole pass under an active
+// evaluation Scope with repeats), reads back the `count` result values of `out` into `host` (none
+// when host is null: the result stays on the device) and the two range flags, and throws
+// std::runtime_error for a set flag (scale.hpp:187-208). `out` holds `count` values in any case.
+//
+// The whole-pass check (evaluation_hooks.hpp:175-211): every region of `shape.written` is filled
+// with a sentinel, which must then be read back from the output; one checking replay issues the
+// steps, counted per phase against shape.steps; its output and the output after the timed replays
+// must both be bit-identical to the first pass. Only then is whole_checked set.
 // product_ops / partial_products describe the product phase for the evaluation record.
-void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const double* out, double* host, std::size_t count,
-                  const std::uint32_t* flags, double product_ops, unsigned partial_products);
+void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& shape, const double* out,
+                  double* host, std::size_t count, const std::uint32_t* flags, double product_ops,
+                  unsigned partial_products);
 
 }  // namespace ozTTgemm::detail

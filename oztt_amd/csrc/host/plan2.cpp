@@ -240,12 +240,28 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
     // limit on the number of moduli (plan.hpp:281): the caller's, else the route's default with a fixed
     // width (16 for INT8, 14 for FP8; split.hpp:73-76), else 24
     // For the formats carried by INT8 residues, a moduli limit counts the moduli of the format's own route
-    // (residues of up to 12 bits there, 8 here): the INT8 set takes as many as the width needs (<= 24).
+    // (residues of up to 12 bits there, 8 here; checked below): the INT8 set takes as many as the width
+    // needs (<= 24).
     const bool transported = !fp8 && format != Format::INT8;
     if (transported)
         p.S_req = (std::uint32_t)kMaxModuli;
     else
         p.S_req = max_moduli ? max_moduli : (b_fixed ? (fp8 ? 14u : 16u) : (std::uint32_t)kMaxModuli);
+    if (transported && max_moduli) {
+        // The caller's limit applies to the format's own route in the reference, whose moduli are at
+        // most the route's cap (split.hpp:86-106: 4096 for TF32, BF16, FP16 and BFP8; 3375 for BFP4;
+        // 243 for BFP2). That route's selection (a stage-time model of another device) is not
+        // restated, but a limit under which even max_moduli moduli at the cap cannot hold the CRT
+        // window log2 M >= 2b + 1 + log2 K of the smallest admissible width (53 bits, or the fixed
+        // width) fails there for certain; it is rejected here with the reference's error.
+        const double cap = format == Format::BFP2 ? 243.0 : format == Format::BFP4 ? 3375.0 : 4096.0;
+        const int width = b_fixed ? b_cap : kTargetBits;
+        if (max_moduli * std::log2(cap) < 2.0 * width + 1.0 + std::log2((double)K))
+            throw std::runtime_error("Ozaki II: the available moduli do not cover the CRT window for the padded inner "
+                                     "dimension K=" +
+                                     std::to_string(K) + ". The limit of " + std::to_string(max_moduli) +
+                                     " moduli is too small; raise Options::max_moduli.");
+    }
     if (b_fixed && passes == Reconstruction::Automatic) p.stats = measure_stats(A, B, M, N, K);
     p.route = fp8 ? choose_moduli_fp8(K, (int)p.S_req, b_cap) : choose_moduli_int8(K, (int)p.S_req, b_cap);
     const ModuliSet& r = p.route;

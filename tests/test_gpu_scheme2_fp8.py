@@ -65,38 +65,41 @@ def test_fp8_wide_range_auto(ctx, oracle, n):
     assert np.all(np.abs(got - q) <= absab * n * 2.0 ** -53)
 
 
-def run_fp8_stages(dev, a, b, n, max_moduli=0, fixed_bits=0, one_pass=True):
-    """scale -> digit planes -> product outputs (int32 and uint16 terms) -> CRT on the GPU."""
+def run_fp8_stages(dev, a, b, n, max_moduli=0, fixed_bits=0, one_pass=True, m=None, k=None):
+    """scale -> digit planes -> product outputs (int32 and uint16 terms) -> CRT on the GPU, for
+    A (m x k) and B (k x n) (m = k = n unless given)."""
+    m = n if m is None else m
+    k = n if k is None else k
     rec = oz.Reconstruction.OnePass if one_pass else oz.Reconstruction.Automatic
-    dd, gd, crt, tm = oz.plan2_fp8_device(a, b, n, n, n, max_moduli=max_moduli, reconstruction=rec,
+    dd, gd, crt, tm = oz.plan2_fp8_device(a, b, m, n, k, max_moduli=max_moduli, reconstruction=rec,
                                           fixed_bits=fixed_bits)
     nd, b_ = dd.mo.nd, crt.b
     shift = b_ - 20 * (nd - 1)
-    Mg = -(-n // 256) * 256
-    Kg = -(-n // 64) * 64
+    Mg, Ng = -(-m // 256) * 256, -(-n // 256) * 256
+    Kg = -(-k // 64) * 64
     P, O = gd.nplanes, gd.nout
     bA, bB = dev.upload(a), dev.upload(b)
-    bdA, bdB, bfl = dev.alloc(4 * n), dev.alloc(4 * n), dev.alloc(8)
+    bdA, bdB, bfl = dev.alloc(4 * m), dev.alloc(4 * n), dev.alloc(8)
     dev.fill_u32(bfl, 0, 2)
-    dev.scale(bA, n, n, n, 0, 1, shift, bdA, bfl, 0)
-    dev.scale(bB, n, n, n, 1, 1, shift, bdB, bfl, 1)
-    pA, pB = dev.alloc(P * Mg * Kg), dev.alloc(P * Mg * Kg)
-    dev.split_digits(bA, n, n, n, 0, bdA, dd, pA, 2, Mg, Kg, Mg * Kg)
-    dev.split_digits(bB, n, n, n, 1, bdB, dd, pB, 3, Mg, Kg, Mg * Kg)
-    bP = dev.alloc(4 * O * Mg * Mg)
-    dev.gemm_groups_f8(pA, pB, bP, Mg, Mg, Kg, gd, 0, Mg, Mg * Kg, Mg * Kg, Mg * Mg)
-    bW = dev.alloc(2 * O * Mg * Mg)
-    dev.gemm_groups_f8(pA, pB, bW, Mg, Mg, Kg, gd, 1, Mg, Mg * Kg, Mg * Kg, Mg * Mg)
-    bo = dev.alloc(8 * n * n)
-    dev.crt_terms(bW, n, n, Mg, Mg * Mg, O, tm, crt, bdA, bdB, bo, n)
-    r = dict(dd=dd, gd=gd, crt=crt, tm=tm, nd=nd, b=b_,
-             dA=dev.download(bdA, np.int32, n), dB=dev.download(bdB, np.int32, n),
+    dev.scale(bA, m, k, k, 0, 1, shift, bdA, bfl, 0)
+    dev.scale(bB, k, n, n, 1, 1, shift, bdB, bfl, 1)
+    pA, pB = dev.alloc(P * Mg * Kg), dev.alloc(P * Ng * Kg)
+    dev.split_digits(bA, m, k, k, 0, bdA, dd, pA, 2, Mg, Kg, Mg * Kg)
+    dev.split_digits(bB, k, n, n, 1, bdB, dd, pB, 3, Ng, Kg, Ng * Kg)
+    bP = dev.alloc(4 * O * Mg * Ng)
+    dev.gemm_groups_f8(pA, pB, bP, Mg, Ng, Kg, gd, 0, Ng, Mg * Kg, Ng * Kg, Mg * Ng)
+    bW = dev.alloc(2 * O * Mg * Ng)
+    dev.gemm_groups_f8(pA, pB, bW, Mg, Ng, Kg, gd, 1, Ng, Mg * Kg, Ng * Kg, Mg * Ng)
+    bo = dev.alloc(8 * m * n)
+    dev.crt_terms(bW, m, n, Ng, Mg * Ng, O, tm, crt, bdA, bdB, bo, n)
+    r = dict(dd=dd, gd=gd, crt=crt, tm=tm, nd=nd, b=b_, shape=(m, n, k),
+             dA=dev.download(bdA, np.int32, m), dB=dev.download(bdB, np.int32, n),
              flags=dev.download(bfl, np.uint32, 2),
-             planesA=E4M3[from_blocks(dev.download(pA, np.uint8, P * Mg * Kg).reshape(P, -1), Mg, Kg)[:, :n, :n]],
-             planesB=E4M3[from_blocks(dev.download(pB, np.uint8, P * Mg * Kg).reshape(P, -1), Mg, Kg)[:, :n, :n]],
-             P=dev.download(bP, np.int32, O * Mg * Mg).reshape(O, Mg, Mg)[:, :n, :n],
-             W=dev.download(bW, np.uint16, O * Mg * Mg).reshape(O, Mg, Mg)[:, :n, :n],
-             out=dev.download(bo, np.float64, n * n))
+             planesA=E4M3[from_blocks(dev.download(pA, np.uint8, P * Mg * Kg).reshape(P, -1), Mg, Kg)[:, :m, :k]],
+             planesB=E4M3[from_blocks(dev.download(pB, np.uint8, P * Ng * Kg).reshape(P, -1), Ng, Kg)[:, :n, :k]],
+             P=dev.download(bP, np.int32, O * Mg * Ng).reshape(O, Mg, Ng)[:, :m, :n],
+             W=dev.download(bW, np.uint16, O * Mg * Ng).reshape(O, Mg, Ng)[:, :m, :n],
+             out=dev.download(bo, np.float64, m * n))
     for buf in (bA, bB, bdA, bdB, bfl, pA, pB, bP, bW, bo):
         buf.free()
     dev.bufs.clear()
@@ -104,24 +107,25 @@ def run_fp8_stages(dev, a, b, n, max_moduli=0, fixed_bits=0, one_pass=True):
 
 
 def check_fp8_chain(oracle, r, a, b, n):
-    """Every stage of run_fp8_stages against the oracle; returns the composed residues (S, n, n)."""
+    """Every stage of run_fp8_stages against the oracle; returns the composed residues (S, m, n)."""
     dd, gd, crt, tm, nd, b_ = r["dd"], r["gd"], r["crt"], r["tm"], r["nd"], r["b"]
+    m_, n, kk = r["shape"]
     S = dd.mo.S
     ms = [int(crt.m[s]) for s in range(S)]
     qs = [int(dd.q[s]) for s in range(S)]
     xm = [int(dd.xmode[s]) for s in range(S)]
-    A, B = a.reshape(n, n), b.reshape(n, n)
+    A, B = a.reshape(m_, kk), b.reshape(kk, n)
     shift = b_ - 20 * (nd - 1)
-    dA, fA = oracle.scale(A, n, n, 0, 1, shift)
-    dB, fB = oracle.scale(B, n, n, 1, 1, shift)
+    dA, fA = oracle.scale(A, m_, kk, 0, 1, shift)
+    dB, fB = oracle.scale(B, kk, n, 1, 1, shift)
     np.testing.assert_array_equal(r["dA"], dA)
     np.testing.assert_array_equal(r["dB"], dB)
     assert fA == fB == 0 and not r["flags"].any()
-    pa = oracle.digit_planes(A, n, n, 0, dA, nd, ms, qs, xm)
-    pb = oracle.digit_planes(B, n, n, 1, dB, nd, ms, qs, xm)
+    pa = oracle.digit_planes(A, m_, kk, 0, dA, nd, ms, qs, xm)
+    pb = oracle.digit_planes(B, kk, n, 1, dB, nd, ms, qs, xm)
     np.testing.assert_array_equal(r["planesA"], pa.astype(np.float64))
     np.testing.assert_array_equal(r["planesB"], pb.transpose(0, 2, 1).astype(np.float64))
-    k = [np.zeros((n, n), dtype=np.int64) for _ in ms]
+    k = [np.zeros((m_, n), dtype=np.int64) for _ in ms]
     for o in range(gd.nout):
         g = gd.g[o]
         P = sum(oracle.gemm_i8(pa[g.a[t]], pb[g.b[t]])[0].astype(np.int64) for t in range(g.npairs))
@@ -129,11 +133,11 @@ def check_fp8_chain(oracle, r, a, b, n):
         w = (g.coef * (P % g.m)) % g.m
         np.testing.assert_array_equal(r["W"][o].astype(np.int64), w)
         k[tm[o]] = (k[tm[o]] + w) % g.m
-    C = np.zeros((S, n, n), dtype=np.int32)
+    C = np.zeros((S, m_, n), dtype=np.int32)
     for s, m in enumerate(ms):
         res = (k[s] * pow(int(crt.y[s]), -1, m)) % m
         C[s] = np.where(res > m // 2, res - m, res)
-    ex = oracle.crt_exact(C, n, n, ms, b_, nd, dA, dB)
+    ex = oracle.crt_exact(C, m_, n, ms, b_, nd, dA, dB)
     np.testing.assert_array_equal(r["out"].view(np.uint64), ex.view(np.uint64))
     return C, ms, dA, dB
 

@@ -261,3 +261,28 @@ def test_fp8_rejects_k_beyond_exact_fp32():
         oz.plan2(a, b, M, N, K, oz.Format.FP8, fixed_bits=54)
     p = oz.plan2(a, b, M, N, K, oz.Format.INT8, fixed_bits=54)  # INT8 residues carry this K
     assert p.ok and p.b == 54
+
+
+def test_moduli_limit_of_transported_formats():
+    """Formats carried by INT8 residues: Options.max_moduli bounds the format's own route. A limit under
+    which even that many moduli at the route's cap (4096 for BF16/FP16/TF32/BFP8, 3375 for BFP4, 243 for
+    BFP2; reference split.hpp:86-106) cannot hold the CRT window of 53 bits is rejected with the
+    reference's runtime error (tests/correctness.cpp:291-300 uses max_moduli = 2); a feasible limit runs
+    the INT8 set the width needs."""
+    n = 128
+    a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
+    for fmt in (oz.Format.BF16, oz.Format.FP16, oz.Format.TF32, oz.Format.BFP8, oz.Format.BFP4, oz.Format.BFP2):
+        with pytest.raises(RuntimeError, match="limit of 2 moduli is too small"):
+            oz.plan2(a, b, n, n, n, fmt=fmt, max_moduli=2)
+    # window for b = 53 at K = 128: 2*53 + 1 + 7 = 114 bits; 9 moduli of 4096 hold 108, 10 hold 120
+    with pytest.raises(RuntimeError, match="too small"):
+        oz.plan2(a, b, n, n, n, fmt=oz.Format.BF16, max_moduli=9)
+    p10 = oz.plan2(a, b, n, n, n, fmt=oz.Format.BF16, max_moduli=10)
+    p0 = oz.plan2(a, b, n, n, n, fmt=oz.Format.BF16)
+    assert (p10.S, p10.b) == (p0.S, p0.b) and p0.b >= 53
+    # BFP2: 243 = 3^5 carries 7.92 bits; 14 moduli hold 110.9 < 114, 15 hold 118.8
+    with pytest.raises(RuntimeError, match="too small"):
+        oz.plan2(a, b, n, n, n, fmt=oz.Format.BFP2, max_moduli=14)
+    assert oz.plan2(a, b, n, n, n, fmt=oz.Format.BFP2, max_moduli=15).S == p0.S
+    # the evaluator's fixed width 54 with TF32's limit of 11 (evaluate.cpp:163-177): 11 * 12 = 132 >= 116
+    assert oz.plan2(a, b, n, n, n, fmt=oz.Format.TF32, max_moduli=11, fixed_bits=54).b == 54
