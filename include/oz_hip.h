@@ -153,6 +153,23 @@ int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, 
 int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long strideD,
                        const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo);
 
+/* ---- A5-A11 in one call: the whole Scheme II INT8 pass on device-resident operands ----------
+ * (reference ozaki2.cpp:439-478: scale, slice, products, reconstruction; the plan is the caller's,
+ * made on the host as for the C++ backend.) C (M x N, leading dimension ldc) = A B for row-major A
+ * (M x K, lda) and B (K x N, ldb): flags[0..1] <- 0; oz_scale_f64 (ceil mode 1, shift crt->shift)
+ * of A's rows and B's columns, ORing their range flags into flags[0] and flags[1] (as
+ * oz_scale_f64: 1, 2, 4; the caller reads them); oz2_split_int8 of A (layout 2) and B (layout 3);
+ * oz2_gemm_digits; oz2_crt_digits_f64. Every launch is ordered on the handle's stream; nothing
+ * waits on the host. mo and crt must hold the same INT8 moduli, crt->shift = crt->b - 20 (mo->nd - 1),
+ * and K (rounded up to 64) times 127^2 must stay below 2^31. flags: two device words, 4-byte aligned.
+ * The intermediates live in `work` (256-byte aligned): the exponent deltas, the S residue planes of
+ * A and of B^T and the S digit planes, about S (Mg Kg + Ng Kg + Mg Ng) bytes with Mg, Ng = M, N
+ * rounded up to 256 and Kg = K rounded up to 64; oz2_gemm_f64_workspace gives the exact size. */
+int oz2_gemm_f64_workspace(int M, int N, int K, int S, size_t* bytes);
+int oz2_gemm_f64(oz_dev* dev, const double* A, int lda, const double* B, int ldb, double* C, int ldc, int M, int N,
+                 int K, const oz2_moduli_dev* mo, const oz2_crt_dev* crt, uint32_t* flags, void* work,
+                 size_t work_bytes);
+
 /* ==== Scheme II digit formats: residues carried as small digits (reference FP8 route) ========= */
 
 #define OZ2_MAXPLANES 72  /* digit planes (at most 3 per modulus) */

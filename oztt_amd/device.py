@@ -186,6 +186,18 @@ class Device:
                                           ctypes.c_longlong(sB), ctypes.c_longlong(sD), ctypes.byref(desc)),
                     "oz2_gemm_digits")
 
+    def gemm_f64_workspace(self, M, N, K, S) -> int:
+        n = ctypes.c_size_t()
+        self._check(hip().oz2_gemm_f64_workspace(M, N, K, S, ctypes.byref(n)), "oz2_gemm_f64_workspace")
+        return n.value
+
+    def gemm_f64(self, A: Buffer, lda, B: Buffer, ldb, C: Buffer, ldc, M, N, K, md: ModuliDesc, cd: CrtDesc,
+                 flags: Buffer, work: Buffer, work_bytes):
+        """The whole Scheme II INT8 pass C = A B on device-resident operands (oz2_gemm_f64)."""
+        self._check(hip().oz2_gemm_f64(self.h, A.ptr, lda, B.ptr, ldb, C.ptr, ldc, M, N, K, ctypes.byref(md),
+                                       ctypes.byref(cd), flags.ptr, work.ptr, ctypes.c_size_t(work_bytes)),
+                    "oz2_gemm_f64")
+
     def crt_digits(self, D: Buffer, M, N, ldd, sD, desc: CrtDesc, dA: Buffer, dB: Buffer, out: Buffer, ldo):
         self._check(hip().oz2_crt_digits_f64(self.h, D.ptr, M, N, ldd, ctypes.c_longlong(sD), ctypes.byref(desc),
                                              dA.ptr, dB.ptr, out.ptr, ldo), "oz2_crt_digits_f64")
