@@ -170,6 +170,18 @@ int oz2_gemm_f64(oz_dev* dev, const double* A, int lda, const double* B, int ldb
                  int K, const oz2_moduli_dev* mo, const oz2_crt_dev* crt, uint32_t* flags, void* work,
                  size_t work_bytes);
 
+/* The same pass for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc); it has no counterpart in the reference.
+ * It takes no workspace and allocates nothing: the intermediates live in a device array of
+ * OZ2_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on until the process ends.
+ * Shapes whose workspace (oz2_gemm_f64_workspace) exceeds it are refused with OZ_ERR_ARG; that
+ * covers for example 2048 x 2048 x 2048 with up to 20 moduli. Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (several streams or host threads) race and must be
+ * serialized by the caller. Otherwise as oz2_gemm_f64. */
+#define OZ2_NOALLOC_SCRATCH_BYTES (256u << 20)
+int oz2_gemm_f64_noalloc(oz_dev* dev, const double* A, int lda, const double* B, int ldb, double* C, int ldc, int M,
+                         int N, int K, const oz2_moduli_dev* mo, const oz2_crt_dev* crt, uint32_t* flags);
+
 /* ==== Scheme II digit formats: residues carried as small digits (reference FP8 route) ========= */
 
 #define OZ2_MAXPLANES 72  /* digit planes (at most 3 per modulus) */

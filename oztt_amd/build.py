@@ -43,6 +43,7 @@ HIP_SOURCES = {
     "oz2_digits.hip": ["-fgpu-flush-denormals-to-zero"],
     "oz2_gemm_f8.hip": [],
     "oz2_pass.hip": [],
+    "oz2_noalloc.hip": [],
 }
 HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
               "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{CSRC / 'host'}"]
