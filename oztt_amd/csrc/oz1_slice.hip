@@ -35,6 +35,7 @@ struct SliceGen {
         st.hi = st.hi - v;
         return (int)v;
     }
+    OZ_PLANES_FROM_PLANE
 };
 
 template <bool POW2>

@@ -86,6 +86,7 @@ struct DigitGen {
         else
             return (int)v;
     }
+    OZ_PLANES_FROM_PLANE
 };
 
 template <int ND, bool E4M3>

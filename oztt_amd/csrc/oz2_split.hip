@@ -99,16 +99,64 @@ __global__ void __launch_bounds__(256) split_tran_kernel(const double* __restric
     }
 }
 
-// Layouts 2/3 (OZ_BLOCK tiles): split_block_kernel of oz_tf32.hpp with this generator: the
-// state of an element is its nd digits, plane s is its residue modulo m_s.
+// Layouts 2/3 (OZ_BLOCK tiles): split_block_kernel of oz_tf32.hpp with this generator: the state of
+// an element is A' in balanced base-256 bytes and its residue modulo the even modulus, if the set
+// has one (from the reference's sequence on the digits); plane s is the residue modulo m_s (odd
+// moduli: byte dot products and one FP32 reduction, oz2_residue.hpp).
 template <int ND>
 struct ResidueGen {
+    static constexpr int W = balanced_words<ND>();
+    SplitConsts k;
+    struct State {
+        uint32_t a[W];
+        int even;
+    };
+    __device__ __forceinline__ void load(State& st, double x, int32_t d) const {
+        float dig[ND];
+        make_digits<ND>(x, d, dig);
+        balanced_bytes<ND>(dig, st.a);
+        st.even = k.even >= 0 ? residue<ND>(dig, k, k.even) : 0;
+    }
+    // one branch per plane, on the plane index (uniform); each branch hands its own values to emit.
+    // Odd moduli from 17 up give x = r + (m-1)/2, four of which the fix turns into r: adding
+    // 128 - (m-1)/2 keeps every byte in [1, 255] (no carry into the next one), and xor 0x80 then
+    // subtracts 128 from each (two's complement bytes).
+    template <class EMIT>
+    __device__ __forceinline__ void planes(State* st, int s, EMIT&& emit) const {
+        int v[16];
+        if (s == k.even) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) v[e] = st[e].even;
+            emit(v, NoFix{});
+        } else if (k.magic[s]) {
+            const uint32_t badd = k.badd[s];
+            uint32_t a[16][W];
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+#pragma unroll
+                for (int i = 0; i < W; i++) a[e][i] = st[e].a[i];
+            residues_odd_int<W>(a, k.w[s], k.dinit[s], k.magic[s], k.mneg[s], v);
+            emit(v, [badd](uint32_t w) { return (w + badd) ^ 0x80808080u; });
+        } else {
+            const float m = k.m[s], rinv = k.rinv[s];
+#pragma unroll
+            for (int e = 0; e < 16; e++) v[e] = (int)residue_odd<W>(st[e].a, k.w[s], m, rinv);
+            emit(v, NoFix{});
+        }
+    }
+};
+
+// The reference's sequence for every modulus (sets with more than one even modulus, which a
+// pairwise coprime plan never has): the state is the nd digits.
+template <int ND>
+struct ResidueChainGen {
     SplitConsts k;
     struct State {
         float dig[ND];
     };
     __device__ __forceinline__ void load(State& st, double x, int32_t d) const { make_digits<ND>(x, d, st.dig); }
     __device__ __forceinline__ int plane(State& st, int s) const { return residue<ND>(st.dig, k, s); }
+    OZ_PLANES_FROM_PLANE
 };
 
 template <int ND>
@@ -132,9 +180,24 @@ int check_moduli(oz_dev* dev, const oz2_moduli_dev* mo) {
     return OZ_OK;
 }
 
+template <class GEN>
+int launch_blocked(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
+                   const GEN& gen, int S, int8_t* planes, int layout, int pld, long long nblocks, long long pstride) {
+    const int kblocks = pld / 64;
+    const unsigned grid = oz::ceil_div(nblocks, 4);
+    if (layout == 2)
+        hipLaunchKernelGGL((split_block_kernel<GEN, false>), dim3(grid), dim3(256), 0, dev->stream, X, rows, cols, ld,
+                           mode, delta, gen, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks, pstride / 16);
+    else
+        hipLaunchKernelGGL((split_block_kernel<GEN, true>), dim3(grid), dim3(256), 0, dev->stream, X, rows, cols, ld,
+                           mode, delta, gen, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks, pstride / 16);
+    return oz::launch_check(dev, "split_block_kernel");
+}
+
 template <int ND>
 int launch_split(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
-                 const SplitConsts& k, int S, int8_t* planes, int layout, int prow, int pld, long long pstride) {
+                 const SplitConsts& k, int S, int8_t* planes, int layout, int prow, int pld, long long pstride,
+                 bool one_even) {
     if (layout == 0) {
         const int pq = pld / 4;
         const long long words = (long long)prow * pq;
@@ -143,19 +206,12 @@ int launch_split(oz_dev* dev, const double* X, int rows, int cols, int ld, int m
         return oz::launch_check(dev, "split_row_kernel");
     }
     if (layout >= 2) {
-        const int kblocks = pld / 64;
-        const long long nblocks = (long long)(prow / 16) * kblocks;
-        const unsigned grid = oz::ceil_div(nblocks, 4);
-        const ResidueGen<ND> gen{k};
-        if (layout == 2)
-            hipLaunchKernelGGL((split_block_kernel<ResidueGen<ND>, false>), dim3(grid), dim3(256), 0, dev->stream, X,
-                               rows, cols, ld, mode, delta, gen, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks,
-                               pstride / 16);
-        else
-            hipLaunchKernelGGL((split_block_kernel<ResidueGen<ND>, true>), dim3(grid), dim3(256), 0, dev->stream, X,
-                               rows, cols, ld, mode, delta, gen, S, reinterpret_cast<uint4*>(planes), kblocks, nblocks,
-                               pstride / 16);
-        return oz::launch_check(dev, "split_block_kernel");
+        const long long nblocks = (long long)(prow / 16) * (pld / 64);
+        if (one_even)
+            return launch_blocked(dev, X, rows, cols, ld, mode, delta, ResidueGen<ND>{k}, S, planes, layout, pld,
+                                  nblocks, pstride);
+        return launch_blocked(dev, X, rows, cols, ld, mode, delta, ResidueChainGen<ND>{k}, S, planes, layout, pld,
+                              nblocks, pstride);
     }
     // transposed: plane rows = columns of X (prow of them, multiple of 64); plane bytes = rows of X
     hipLaunchKernelGGL(split_tran_kernel<ND>, dim3(prow / 64, pld / 64), dim3(256), 0, dev->stream, X, rows, cols, ld,
@@ -183,15 +239,47 @@ extern "C" int oz2_split_int8(oz_dev* dev, const double* X, int rows, int cols, 
         return oz::fail(dev, OZ_ERR_ARG, "oz2_split_int8: plane geometry %dx%d (stride %lld) does not fit", prow, pld,
                         plane_stride);
     SplitConsts k{};
+    k.even = -1;
+    int evens = 0;
     for (int s = 0; s < mo->S; s++) {
         k.m[s] = mo->m[s];
         k.rinv[s] = mo->rinv[s];
         for (int j = 0; j < 4; j++) k.c[j][s] = mo->c[j][s];
+        // symmetric residues of 256^j modulo m, four to a word (signed bytes)
+        const int m = (int)mo->m[s];
+        if (m % 2 == 1 && m >= 17) {
+            const int U = mo->nd == 3 ? 18 : 19, sh = 24 - U, h = (m - 1) / 2;
+            const long long half = 1ll << (U - 1);
+            k.dinit[s] = (int)((half + m - 1) / m * m + h);
+            k.magic[s] = (uint32_t)(((1ull << (32 - sh)) + m - 1) / m);
+            k.badd[s] = (uint32_t)(128 - h) * 0x01010101u;
+            k.mneg[s] = (1 << 24) - m;
+        }
+        if (m % 2 == 0) {
+            k.even = s;
+            evens++;
+        }
+        int p = 1;  // 256^j mod m
+        for (int i = 0; i < 4; i++) {
+            uint32_t word = 0;
+            for (int j = 0; j < 4; j++) {
+                const int sym = p > m / 2 ? p - m : p;
+                word |= (uint32_t)(sym & 0xFF) << (8 * j);
+                p = p * 256 % m;
+            }
+            k.w[s][i] = word;
+        }
     }
     switch (mo->nd) {
-    case 3: return launch_split<3>(dev, X, rows, cols, ld, mode, delta, k, mo->S, planes, layout, prow, pld, plane_stride);
-    case 4: return launch_split<4>(dev, X, rows, cols, ld, mode, delta, k, mo->S, planes, layout, prow, pld, plane_stride);
-    default: return launch_split<5>(dev, X, rows, cols, ld, mode, delta, k, mo->S, planes, layout, prow, pld, plane_stride);
+    case 3:
+        return launch_split<3>(dev, X, rows, cols, ld, mode, delta, k, mo->S, planes, layout, prow, pld, plane_stride,
+                               evens <= 1);
+    case 4:
+        return launch_split<4>(dev, X, rows, cols, ld, mode, delta, k, mo->S, planes, layout, prow, pld, plane_stride,
+                               evens <= 1);
+    default:
+        return launch_split<5>(dev, X, rows, cols, ld, mode, delta, k, mo->S, planes, layout, prow, pld, plane_stride,
+                               evens <= 1);
     }
 }
 

@@ -20,12 +20,6 @@ __device__ __forceinline__ void load_triple(double x, int32_t d, float& hi, floa
     const uint32_t w1 = (uint32_t)(u >> 32), w0 = (uint32_t)u;
     const uint32_t sgn = w1 & 0x80000000u;
     const int32_t E = (int32_t)((w1 >> 20) & 0x7FFu);
-    if (E == 0) {  // zero and subnormals
-        hi = 0.0f;
-        mid = 0.0f;
-        lo = 0.0f;
-        return;
-    }
     uint32_t a = 0x400000u | ((w1 & 0x000FFFFFu) << 2) | (w0 >> 30);
     const uint32_t rem = w0 & 0x3FFFFFFFu;
     int32_t r = (int32_t)rem;
@@ -45,9 +39,11 @@ __device__ __forceinline__ void load_triple(double x, int32_t d, float& hi, floa
     const uint32_t braw = 0x4B000000u | (((uint32_t)(b + 0x400000)) & 0x7FFFFFu);
     const uint32_t craw = 0x4B000000u | c;
     const float s = __uint_as_float(sb);
-    hi = __uint_as_float(hb);
-    mid = (__uint_as_float(braw) - 12582912.0f) * s;
-    lo = ((__uint_as_float(craw) - 8388608.0f) * s) * 0.0078125f;
+    // zero and subnormals (E = 0) give the zero triple; selected at the end, so that no lane branches
+    const bool zero = E == 0;
+    hi = zero ? 0.0f : __uint_as_float(hb);
+    mid = zero ? 0.0f : (__uint_as_float(braw) - 12582912.0f) * s;
+    lo = zero ? 0.0f : ((__uint_as_float(craw) - 8388608.0f) * s) * 0.0078125f;
 }
 
 // TwoSum (Knuth) and FastTwoSum (Dekker) in the reference's operation order (sfpu_tf_proc.h:61-74).
@@ -144,7 +140,8 @@ __device__ __forceinline__ int block_swizzle(int r) { return ((r >> 1) ^ (r >> 2
 
 // One wave per block; the wave writes each plane's block with one contiguous 1 KB store (lane l ->
 // block bytes 16l..16l+15). GEN supplies the per-element state and, called with s = 0, 1, ... in
-// order, the int8 value of plane s (GEN::State, GEN::load, GEN::plane).
+// order, the int8 values of plane s for the 16 elements of a lane (GEN::State, GEN::load,
+// GEN::planes).
 //   TRAN (plane row = column of X): lane l computes plane row l/4, plane columns 16*(l%4)..+15
 //   (16 consecutive rows of X in one column; a load instruction reads 4 runs of 16 consecutive
 //   doubles) and packs its 16 values into its own stored chunk.
@@ -152,8 +149,15 @@ __device__ __forceinline__ int block_swizzle(int r) { return ((r >> 1) ^ (r >> 2
 //   contiguous 512-byte row segment of X); each plane is transposed through a 1 KB LDS image of the
 //   block (byte writes, then one 16-byte read per lane). The image is private to the wave, whose
 //   LDS operations execute in order, so no barrier is needed.
+// The 16 loads of X (and of the deltas) are issued before any element is processed. A block wholly
+// inside X (every block but those on its right and bottom edges) loads without bounds checks; an
+// edge block clamps its addresses into X and zeroes what lies outside, without branching.
+// The low bytes of a, b, c, d in one word (a lowest): two byte permutes make the pairs (a, b) and
+// (c, d), a third joins them.
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
+    const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
 template <class GEN, bool TRAN>
@@ -161,50 +165,79 @@ __global__ void __launch_bounds__(256) split_block_kernel(const double* __restri
                                                           int mode, const int32_t* __restrict__ delta, GEN gen,
                                                           int nplanes, uint4* __restrict__ planes, int kblocks,
                                                           long long nblocks, long long pstride_chunks) {
-    const long long blk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);  // block index within a plane
+    // block index within a plane, the same for the whole wave
+    const long long blk = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (blk >= nblocks) return;
     const int lane = threadIdx.x & 63;
     const int br = (int)(blk / kblocks), bk = (int)(blk % kblocks);
-    typename GEN::State st[16];
-    if constexpr (TRAN) {
-        const int pr = br * 16 + (lane >> 2);       // plane row = column of X
-        const int pc0 = bk * 64 + 16 * (lane & 3);  // first of this lane's 16 plane columns = rows of X
+    double xv[16];
+    int32_t dv[16];
+    // element e of this lane is X[xr0 + e][xc0]
+    const int xr0 = TRAN ? bk * 64 + 16 * (lane & 3) : br * 16;
+    const int xc0 = TRAN ? br * 16 + (lane >> 2) : bk * 64 + lane;
+    const bool inside = TRAN ? (bk * 64 + 64 <= rows && br * 16 + 16 <= cols) : (br * 16 + 16 <= rows && bk * 64 + 64 <= cols);
+    if (inside) {
+        const double* p = X + (size_t)xr0 * ld + xc0;
+#pragma unroll
+        for (int e = 0; e < 16; e++) xv[e] = p[(size_t)e * ld];
+#pragma unroll
+        for (int e = 0; e < 16; e++) dv[e] = mode == 0 ? delta[xr0 + e] : delta[xc0];
+    } else {
+        const int xc = min(xc0, cols - 1);
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-            const int xr = pc0 + e, xc = pr;
-            const bool in = xr < rows && xc < cols;
-            gen.load(st[e], in ? X[(size_t)xr * ld + xc] : 0.0, in ? (mode == 0 ? delta[xr] : delta[xc]) : 0);
+            const int xr = min(xr0 + e, rows - 1);
+            const bool in = xr0 + e < rows && xc0 < cols;
+            const double v = X[(size_t)xr * ld + xc];
+            const int32_t d = mode == 0 ? delta[xr] : delta[xc];
+            xv[e] = in ? v : 0.0;
+            dv[e] = in ? d : 0;
         }
+    }
+    typename GEN::State st[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) gen.load(st[e], xv[e], dv[e]);
+    // GEN::planes(st, s, emit) computes plane s's 16 values v and calls emit(v, fix) once, where
+    // fix(w) maps four packed values to the bytes stored; emit packs and stores them.
+    if constexpr (TRAN) {
         const int rr = lane >> 2;
         uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
         for (int s = 0; s < nplanes; s++) {
-            int v[16];
-#pragma unroll
-            for (int e = 0; e < 16; e++) v[e] = gen.plane(st[e], s);
-            out[(long long)s * pstride_chunks] = make_uint4(pack4(v[0], v[1], v[2], v[3]), pack4(v[4], v[5], v[6], v[7]),
-                                                            pack4(v[8], v[9], v[10], v[11]),
-                                                            pack4(v[12], v[13], v[14], v[15]));
+            gen.planes(st, s, [&](const int* v, auto fix) {
+                out[(long long)s * pstride_chunks] =
+                    make_uint4(fix(pack4(v[0], v[1], v[2], v[3])), fix(pack4(v[4], v[5], v[6], v[7])),
+                               fix(pack4(v[8], v[9], v[10], v[11])), fix(pack4(v[12], v[13], v[14], v[15])));
+            });
         }
     } else {
         __shared__ __attribute__((aligned(16))) uint8_t image[4][1024];
         uint8_t* img = image[threadIdx.x >> 6];
-        const int xc = bk * 64 + lane;  // plane column = column of X
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int xr = br * 16 + e;
-            const bool in = xr < rows && xc < cols;
-            gen.load(st[e], in ? X[(size_t)xr * ld + xc] : 0.0, in ? (mode == 0 ? delta[xr] : delta[xc]) : 0);
-        }
         // byte of (row e, column lane) inside the block image
         const int colpart = 16 * (lane >> 4), colbyte = lane & 15;
         uint4* out = planes + blk * 64 + lane;
         for (int s = 0; s < nplanes; s++) {
+            gen.planes(st, s, [&](const int* v, auto fix) {
 #pragma unroll
-            for (int e = 0; e < 16; e++)
-                img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)gen.plane(st[e], s);
-            out[(long long)s * pstride_chunks] = *reinterpret_cast<const uint4*>(img + 16 * lane);
+                for (int e = 0; e < 16; e++) img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)v[e];
+                const uint4 w = *reinterpret_cast<const uint4*>(img + 16 * lane);
+                out[(long long)s * pstride_chunks] = make_uint4(fix(w.x), fix(w.y), fix(w.z), fix(w.w));
+            });
         }
     }
 }
+
+// The identity fix: the values are the stored bytes themselves.
+struct NoFix {
+    __device__ __forceinline__ uint32_t operator()(uint32_t w) const { return w; }
+};
+
+// GEN::planes for generators that produce one element's value at a time (GEN::plane).
+#define OZ_PLANES_FROM_PLANE                                                            \
+    template <class EMIT>                                                               \
+    __device__ __forceinline__ void planes(State* st, int s, EMIT&& emit) const {      \
+        int v[16];                                                                      \
+        _Pragma("unroll") for (int e = 0; e < 16; e++) v[e] = plane(st[e], s);         \
+        emit(v, NoFix{});                                                               \
+    }
 
 }  // namespace

@@ -260,3 +260,34 @@ def test_device_copy(dev):
     np.testing.assert_array_equal(dev.download(dst, np.uint32, x.size), x)
     with pytest.raises(RuntimeError):
         dev.copy(dst, src, 20)  # not a multiple of 16
+
+
+@pytest.mark.parametrize("layout", [2, 3])
+@pytest.mark.parametrize("moduli", [[254, 128, 250, 249, 247, 3], [255, 253, 251, 2], [254]])
+def test_residues_any_parity_of_moduli(dev, oracle, layout, moduli):
+    """The blocked splitter takes odd moduli through byte dot products of A' and the one even modulus
+    of a pairwise coprime set through the reference's sequence; a set with several even moduli (no
+    plan has one) goes through the reference's sequence for all. Every case equals the oracle."""
+    nd, b = 3, 56
+    rng = np.random.default_rng(77 + layout + len(moduli))
+    tran = layout == 3
+    rows, cols = (160, 80) if tran else (80, 160)
+    X = split_inputs(rows, cols, rng, 2.0)
+    X[0, :4] = [254.0 * 2.0 ** -40, -127.0 * 2.0 ** -40, 0.0, 381.0 * 2.0 ** -40]  # values at +-m/2 of 254
+    mode = 1 if tran else 0
+    delta, _ = oracle.scale(X, rows, cols, mode, 1, b - 20 * (nd - 1))
+    want = oracle.residues(X, rows, cols, mode, delta, nd, moduli)
+    S = len(moduli)
+    prow = ((cols if tran else rows) + 63) // 64 * 64
+    pld = ((rows if tran else cols) + 63) // 64 * 64
+    bx, bd = dev.upload(X), dev.upload(delta)
+    bp = dev.alloc(S * prow * pld)
+    dev.split_int8(bx, rows, cols, cols, mode, bd, moduli_desc(moduli, nd), bp, layout, prow, pld, prow * pld)
+    got = from_blocks(dev.download(bp, np.int8, S * prow * pld).reshape(S, -1), prow, pld)
+    for buf in (bx, bd, bp):
+        buf.free()
+    dev.bufs.clear()
+    if tran:
+        np.testing.assert_array_equal(got[:, :cols, :rows], want.transpose(0, 2, 1))
+    else:
+        np.testing.assert_array_equal(got[:, :rows, :cols], want)
