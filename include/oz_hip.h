@@ -80,6 +80,13 @@ int oz_event_elapsed_ms(oz_dev* dev, int slot_begin, int slot_end, float* ms);
 int oz_scale_f64(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, int ceil_mode, int shift,
                  int32_t* delta, uint32_t* flags);
 
+/* Both operands of a product in one launch: the row maxima of A (M x K, lda) into dA[M] and the
+ * column maxima of B (K x N, ldb) into dB[N], each as oz_scale_f64 (mode 0 for A, mode 1 for B, the
+ * same ceil_mode and shift), with the range flags of A ORed into flags[0] and those of B into
+ * flags[1] (two device words, 4-byte aligned). */
+int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int lda, const double* B, int N, int ldb,
+                      int ceil_mode, int shift, int32_t* dA, int32_t* dB, uint32_t* flags);
+
 /* ---- A6-A8: Scheme II residues (reference modslice_int8.cpp:60, digits.h:80,165, f64_tf.h:141) -
  * For every element x of X (rows x cols, ld) with exponent delta d (delta[row] for mode 0,
  * delta[col] for mode 1): the triple-float of x*2^d, its nd radix-2^20 digits (nd = 3..5), and
@@ -105,6 +112,13 @@ typedef struct oz2_moduli_dev {
 } oz2_moduli_dev;
 int oz2_split_int8(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
                    const oz2_moduli_dev* mo, int8_t* planes, int layout, int prow, int pld, long long plane_stride);
+/* Both operands of a product in one launch: oz2_split_int8 of A (M x K, lda, row deltas dA, mode 0)
+ * into planesA in layout 2 (S planes of Mg x Kg, plane stride Mg*Kg bytes) and of B (K x N, ldb,
+ * column deltas dB, mode 1) into planesB in layout 3 (S planes of Ng x Kg, stride Ng*Kg). Mg >= M and
+ * Ng >= N multiples of 16, Kg >= K a multiple of 64, planes 16-byte aligned. */
+int oz2_split_pair_int8(oz_dev* dev, const double* A, int M, int K, int lda, const int32_t* dA, const double* B,
+                        int N, int ldb, const int32_t* dB, const oz2_moduli_dev* mo, int8_t* planesA, int8_t* planesB,
+                        int Mg, int Ng, int Kg);
 /* White-box view of A7: the nd digits (top first) of every element as FP32, digits[(r*cols+c)*nd+j]. */
 int oz2_digits_f32(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
                    int nd, float* digits);

@@ -109,12 +109,10 @@ Output ozaki1_run(Device& D, const Problem& p) {
     steps.push_back({ev::Scale, [=] {
                          device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
                          // BF16 of the maxima rounded as the format requires, target 2^nshift (format.hpp:76-101)
-                         device_check(dev, oz_scale_f64(dev, dAf, (int)M, (int)K, (int)K, 0, (int)f.ceil, f.nshift,
-                                                        dltA, flags),
-                                      "scale A");
-                         device_check(dev, oz_scale_f64(dev, dBf, (int)K, (int)N, (int)N, 1, (int)f.ceil, f.nshift,
-                                                        dltB, flags + 1),
-                                      "scale B");
+                         device_check(dev,
+                                      oz_scale_pair_f64(dev, dAf, (int)M, (int)K, (int)K, dBf, (int)N, (int)N,
+                                                        (int)f.ceil, f.nshift, dltA, dltB, flags),
+                                      "scale");
                      }});
     // B's slices once (per K block: rows kb Kc.. of B), then per band and K block: A's slices (columns
     // kb Kc.. of the band's rows), the diagonal products, the reconstruction

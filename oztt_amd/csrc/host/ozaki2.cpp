@@ -108,10 +108,10 @@ Output ozaki2_run(Device& D, const Problem& p) {
     steps.push_back({ev::Scale, [=] {
                          device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
                          // Scheme II rounds the BF16 of the maxima up (ozaki2.cpp:143-146)
-                         device_check(dev, oz_scale_f64(dev, dAf, (int)M, (int)K, (int)K, 0, 1, shift, dltA, flags),
-                                      "scale A");
-                         device_check(dev, oz_scale_f64(dev, dBf, (int)K, (int)N, (int)N, 1, 1, shift, dltB, flags + 1),
-                                      "scale B");
+                         device_check(dev,
+                                      oz_scale_pair_f64(dev, dAf, (int)M, (int)K, (int)K, dBf, (int)N, (int)N, 1, shift,
+                                                        dltA, dltB, flags),
+                                      "scale");
                      }});
     // B's planes once, then per band: A's planes, the products, the reconstruction of the band's rows
     if (fp8)
@@ -121,12 +121,20 @@ Output ozaki2_run(Device& D, const Problem& p) {
                                                            (int)Ng, (int)Kg, strideB),
                                           "slice B");
                          }});
-    else
+    else if (nbands > 1)
         steps.push_back({ev::Slice, [=] {
                              device_check(dev,
                                           oz2_split_int8(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, &mdesc, planesB, 3,
                                                          (int)Ng, (int)Kg, strideB),
                                           "slice B");
+                         }});
+    else  // one band: A's and B's planes in one launch
+        steps.push_back({ev::Slice, [=] {
+                             device_check(dev,
+                                          oz2_split_pair_int8(dev, dAf, (int)M, (int)K, (int)K, dltA, dBf, (int)N,
+                                                              (int)N, dltB, &mdesc, planesA, planesB, (int)Mbg,
+                                                              (int)Ng, (int)Kg),
+                                          "slice");
                          }});
     for (std::uint32_t band = 0; band < nbands; band++) {
         const std::uint32_t r0 = band * Mb, rows = std::min(Mb, M - r0), rowsg = round_up(rows, 256);
@@ -154,12 +162,13 @@ Output ozaki2_run(Device& D, const Problem& p) {
                                               "reconstruction");
                              }});
         } else {
-            steps.push_back({ev::Slice, [=] {
-                                 device_check(dev,
-                                              oz2_split_int8(dev, Ab, (int)rows, (int)K, (int)K, 0, dAb, &mdesc,
-                                                             planesA, 2, (int)rowsg, (int)Kg, strideA),
-                                              "slice A");
-                             }});
+            if (nbands > 1)
+                steps.push_back({ev::Slice, [=] {
+                                     device_check(dev,
+                                                  oz2_split_int8(dev, Ab, (int)rows, (int)K, (int)K, 0, dAb, &mdesc,
+                                                                 planesA, 2, (int)rowsg, (int)Kg, strideA),
+                                                  "slice A");
+                                 }});
             steps.push_back({ev::Gemm, [=] {
                                  device_check(dev,
                                               oz2_gemm_digits(dev, planesA, planesB, prod, (int)rowsg, (int)Ng,
@@ -178,11 +187,12 @@ Output ozaki2_run(Device& D, const Problem& p) {
     // products: one per modulus (INT8) or the FP8 route's digit products (sum of the outputs' pairs)
     const std::uint32_t nprod = fp8 ? (std::uint32_t)plan.mo.nprod : S;
 
-    // the pass the configuration calls for: scale once; B's slice once and A's per band; one product
-    // and one reconstruction step per band; and the regions it writes
+    // the pass the configuration calls for: scale once; B's slice once and A's per band (INT8 with one
+    // band: both in one step); one product and one reconstruction step per band; and the regions it
+    // writes
     PassShape shape;
     shape.steps[ev::Scale] = 1;
-    shape.steps[ev::Slice] = 1 + nbands;
+    shape.steps[ev::Slice] = (!fp8 && nbands == 1) ? 1 : 1 + nbands;
     shape.steps[ev::Gemm] = nbands;
     shape.steps[ev::Recon] = nbands;
     shape.written = {{flags, 2 * sizeof(std::uint32_t)},

@@ -2,8 +2,8 @@
 // made on the host (the moduli and CRT descriptors of include/oz_hip.h), C = A B through the same
 // stage kernels the C++ backend issues one by one (reference ozaki2.cpp:439-478: scale, slice,
 // products, reconstruction):
-//   flags <- 0; row maxima of A and column maxima of B -> exponent deltas (oz_scale_f64);
-//   residue planes of A and of B^T in OZ_BLOCK tiles (oz2_split_int8);
+//   flags <- 0; row maxima of A and column maxima of B -> exponent deltas (oz_scale_pair_f64);
+//   residue planes of A and of B^T in OZ_BLOCK tiles (oz2_split_pair_int8);
 //   products reduced to CRT digits in the GEMM epilogue (oz2_gemm_digits);
 //   exact CRT to FP64 (oz2_crt_digits_f64).
 // Every launch is ordered on the handle's stream and nothing waits on the host, so a caller that
@@ -63,14 +63,13 @@ int run_pass(oz_dev* dev, const double* A, int lda, const double* B, int ldb, do
     auto* pA = reinterpret_cast<int8_t*>(work + L.planesA);
     auto* pB = reinterpret_cast<int8_t*>(work + L.planesB);
     auto* dg = work + L.digits;
-    const long long sA = (long long)L.Mg * L.Kg, sB = (long long)L.Ng * L.Kg, sD = (long long)L.Mg * L.Ng;
+    const long long sA = (long long)L.Mg * L.Kg, sD = (long long)L.Mg * L.Ng;
     if (int st = oz_fill_u32(dev, flags, 0u, 2)) return st;
     // Scheme II rounds the BF16 of the maxima up (reference ozaki2.cpp:143-146)
-    if (int st = oz_scale_f64(dev, A, M, K, lda, 0, 1, crt->shift, dA, flags)) return st;
-    if (int st = oz_scale_f64(dev, B, K, N, ldb, 1, 1, crt->shift, dB, flags + 1)) return st;
-    if (int st = oz2_split_int8(dev, A, M, K, lda, 0, dA, mo, pA, 2, L.Mg, L.Kg, sA)) return st;
-    if (int st = oz2_split_int8(dev, B, K, N, ldb, 1, dB, mo, pB, 3, L.Ng, L.Kg, sB)) return st;
-    if (int st = oz2_gemm_digits(dev, pA, pB, dg, L.Mg, L.Ng, L.Kg, S, L.Ng, sA, sB, sD, crt)) return st;
+    if (int st = oz_scale_pair_f64(dev, A, M, K, lda, B, N, ldb, 1, crt->shift, dA, dB, flags)) return st;
+    if (int st = oz2_split_pair_int8(dev, A, M, K, lda, dA, B, N, ldb, dB, mo, pA, pB, L.Mg, L.Ng, L.Kg)) return st;
+    if (int st = oz2_gemm_digits(dev, pA, pB, dg, L.Mg, L.Ng, L.Kg, S, L.Ng, sA, (long long)L.Ng * L.Kg, sD, crt))
+        return st;
     return oz2_crt_digits_f64(dev, dg, M, N, L.Ng, sD, crt, dA, dB, C, ldc);
 }
 

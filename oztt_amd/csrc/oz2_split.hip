@@ -219,6 +219,64 @@ int launch_split(oz_dev* dev, const double* X, int rows, int cols, int ld, int m
     return oz::launch_check(dev, "split_tran_kernel");
 }
 
+// Kernel constants of a moduli descriptor (oz2_residue.hpp); *evens counts the even moduli.
+SplitConsts split_consts(const oz2_moduli_dev* mo, int* evens) {
+    SplitConsts k{};
+    k.even = -1;
+    *evens = 0;
+    for (int s = 0; s < mo->S; s++) {
+        k.m[s] = mo->m[s];
+        k.rinv[s] = mo->rinv[s];
+        for (int j = 0; j < 4; j++) k.c[j][s] = mo->c[j][s];
+        // symmetric residues of 256^j modulo m, four to a word (signed bytes)
+        const int m = (int)mo->m[s];
+        if (m % 2 == 1 && m >= 17) {
+            const int U = mo->nd == 3 ? 18 : 19, sh = 24 - U, h = (m - 1) / 2;
+            const long long half = 1ll << (U - 1);
+            k.dinit[s] = (int)((half + m - 1) / m * m + h);
+            k.magic[s] = (uint32_t)(((1ull << (32 - sh)) + m - 1) / m);
+            k.badd[s] = (uint32_t)(128 - h) * 0x01010101u;
+            k.mneg[s] = (1 << 24) - m;
+        }
+        if (m % 2 == 0) {
+            k.even = s;
+            (*evens)++;
+        }
+        int p = 1;  // 256^j mod m
+        for (int i = 0; i < 4; i++) {
+            uint32_t word = 0;
+            for (int j = 0; j < 4; j++) {
+                const int sym = p > m / 2 ? p - m : p;
+                word |= (uint32_t)(sym & 0xFF) << (8 * j);
+                p = p * 256 % m;
+            }
+            k.w[s][i] = word;
+        }
+    }
+    return k;
+}
+
+template <int ND>
+int launch_pair(oz_dev* dev, const double* A, int M, int K, int lda, const int32_t* dA, const double* B, int N,
+                int ldb, const int32_t* dB, const SplitConsts& k, int S, int8_t* pA, int8_t* pB, int Mg, int Ng,
+                int Kg, bool one_even) {
+    const int kblocks = Kg / 64;
+    const long long nbA = (long long)(Mg / 16) * kblocks, nbB = (long long)(Ng / 16) * kblocks;
+    const long long sA = (long long)Mg * Kg / 16, sB = (long long)Ng * Kg / 16;
+    const long long grid = (nbA + 3) / 4 + (nbB + 3) / 4;
+    if (grid > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz2_split_pair_int8: grid too large");
+    auto* qA = reinterpret_cast<uint4*>(pA);
+    auto* qB = reinterpret_cast<uint4*>(pB);
+    if (one_even)
+        hipLaunchKernelGGL((split_pair_kernel<ResidueGen<ND>>), dim3((unsigned)grid), dim3(256), 0, dev->stream, A, M,
+                           K, lda, dA, qA, nbA, sA, B, N, ldb, dB, qB, nbB, sB, kblocks, ResidueGen<ND>{k}, S);
+    else
+        hipLaunchKernelGGL((split_pair_kernel<ResidueChainGen<ND>>), dim3((unsigned)grid), dim3(256), 0, dev->stream,
+                           A, M, K, lda, dA, qA, nbA, sA, B, N, ldb, dB, qB, nbB, sB, kblocks, ResidueChainGen<ND>{k},
+                           S);
+    return oz::launch_check(dev, "split_pair_kernel");
+}
+
 }  // namespace
 
 extern "C" int oz2_split_int8(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode,
@@ -238,38 +296,8 @@ extern "C" int oz2_split_int8(oz_dev* dev, const double* X, int rows, int cols, 
         plane_stride % 16 != 0 || ((uintptr_t)planes & 15u))
         return oz::fail(dev, OZ_ERR_ARG, "oz2_split_int8: plane geometry %dx%d (stride %lld) does not fit", prow, pld,
                         plane_stride);
-    SplitConsts k{};
-    k.even = -1;
     int evens = 0;
-    for (int s = 0; s < mo->S; s++) {
-        k.m[s] = mo->m[s];
-        k.rinv[s] = mo->rinv[s];
-        for (int j = 0; j < 4; j++) k.c[j][s] = mo->c[j][s];
-        // symmetric residues of 256^j modulo m, four to a word (signed bytes)
-        const int m = (int)mo->m[s];
-        if (m % 2 == 1 && m >= 17) {
-            const int U = mo->nd == 3 ? 18 : 19, sh = 24 - U, h = (m - 1) / 2;
-            const long long half = 1ll << (U - 1);
-            k.dinit[s] = (int)((half + m - 1) / m * m + h);
-            k.magic[s] = (uint32_t)(((1ull << (32 - sh)) + m - 1) / m);
-            k.badd[s] = (uint32_t)(128 - h) * 0x01010101u;
-            k.mneg[s] = (1 << 24) - m;
-        }
-        if (m % 2 == 0) {
-            k.even = s;
-            evens++;
-        }
-        int p = 1;  // 256^j mod m
-        for (int i = 0; i < 4; i++) {
-            uint32_t word = 0;
-            for (int j = 0; j < 4; j++) {
-                const int sym = p > m / 2 ? p - m : p;
-                word |= (uint32_t)(sym & 0xFF) << (8 * j);
-                p = p * 256 % m;
-            }
-            k.w[s][i] = word;
-        }
-    }
+    const SplitConsts k = split_consts(mo, &evens);
     switch (mo->nd) {
     case 3:
         return launch_split<3>(dev, X, rows, cols, ld, mode, delta, k, mo->S, planes, layout, prow, pld, plane_stride,
@@ -296,4 +324,24 @@ extern "C" int oz2_digits_f32(oz_dev* dev, const double* X, int rows, int cols, 
     else
         hipLaunchKernelGGL(digits_kernel<5>, dim3(grid), dim3(256), 0, dev->stream, X, rows, cols, ld, mode, delta, digits);
     return oz::launch_check(dev, "digits_kernel");
+}
+
+extern "C" int oz2_split_pair_int8(oz_dev* dev, const double* A, int M, int K, int lda, const int32_t* dA,
+                                   const double* B, int N, int ldb, const int32_t* dB, const oz2_moduli_dev* mo,
+                                   int8_t* planesA, int8_t* planesB, int Mg, int Ng, int Kg) {
+    if (int st = oz::use(dev)) return st;
+    if (int st = check_moduli(dev, mo)) return st;
+    if (!A || !B || !dA || !dB || !planesA || !planesB || M <= 0 || N <= 0 || K <= 0 || lda < K || ldb < N)
+        return oz::fail(dev, OZ_ERR_ARG, "oz2_split_pair_int8: invalid arguments");
+    if (Mg < M || Ng < N || Kg < K || Mg % 16 || Ng % 16 || Kg % 64 || ((uintptr_t)planesA & 15u) ||
+        ((uintptr_t)planesB & 15u))
+        return oz::fail(dev, OZ_ERR_ARG, "oz2_split_pair_int8: plane geometry %dx%d / %dx%d does not fit", Mg, Kg, Ng,
+                        Kg);
+    int evens = 0;
+    const SplitConsts k = split_consts(mo, &evens);
+    switch (mo->nd) {
+    case 3: return launch_pair<3>(dev, A, M, K, lda, dA, B, N, ldb, dB, k, mo->S, planesA, planesB, Mg, Ng, Kg, evens <= 1);
+    case 4: return launch_pair<4>(dev, A, M, K, lda, dA, B, N, ldb, dB, k, mo->S, planesA, planesB, Mg, Ng, Kg, evens <= 1);
+    default: return launch_pair<5>(dev, A, M, K, lda, dA, B, N, ldb, dB, k, mo->S, planesA, planesB, Mg, Ng, Kg, evens <= 1);
+    }
 }

@@ -110,6 +110,93 @@ __global__ void zero_u32_kernel(uint32_t* __restrict__ p, int n) {
     if (i < n) p[i] = 0u;
 }
 
+// The delta and the flag bits of a maximum's key (the conversion of key_to_delta_kernel).
+__device__ __forceinline__ int32_t key_delta(uint32_t key, int shift, uint32_t& bad) {
+    int32_t e = 0;
+    bad = 0;
+    if (key == KEY_NAN)
+        bad = 4u;
+    else if (key == KEY_TINY)
+        bad = 2u;
+    else if (key >= 0x7F80u)
+        bad = 1u;
+    else if (key != 0u) {
+        const uint32_t E = (key >> 7) & 0xFFu, m = key & 0x7Fu;
+        e = (int32_t)E - 127 + (m ? 1 : 0);
+    }
+    return shift - e;
+}
+
+// A's rows and B's columns in one launch of 1024-thread workgroups, deltas written directly:
+//   workgroup r < M: row r of A, each thread a stride-1024 run of its K values;
+//   workgroup M + j: columns 16j..16j+15 of B over all of its K rows, thread t taking column t % 16
+//   and every 64th row from t / 16 (a wave reads four 128-byte row pieces per load).
+// The 16 waves' maxima meet in LDS; flags[0] (A) and flags[1] (B) collect the flag bits with atomicOr.
+template <int CEIL>
+__global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restrict__ A, int M, int K, int lda,
+                                                          const double* __restrict__ B, int N, int ldb, int shift,
+                                                          int32_t* __restrict__ dA, int32_t* __restrict__ dB,
+                                                          uint32_t* __restrict__ flags) {
+    __shared__ uint32_t part[1024];
+    const int t = threadIdx.x;
+    if ((int)blockIdx.x < M) {
+        const double* row = A + (size_t)blockIdx.x * lda;
+        uint32_t k0 = 0, k1 = 0;
+        int c = t;
+        for (; c + 1024 < K; c += 2048) {
+            k0 = max(k0, bf16_key<CEIL>(row[c]));
+            k1 = max(k1, bf16_key<CEIL>(row[c + 1024]));
+        }
+        if (c < K) k0 = max(k0, bf16_key<CEIL>(row[c]));
+        const uint32_t k = wave_max(max(k0, k1));
+        if ((t & 63) == 0) part[t >> 6] = k;
+        __syncthreads();
+        if (t == 0) {
+            uint32_t m = 0;
+#pragma unroll
+            for (int w = 0; w < 16; w++) m = max(m, part[w]);
+            uint32_t bad;
+            dA[blockIdx.x] = key_delta(m, shift, bad);
+            if (bad) atomicOr(&flags[0], bad);
+        }
+    } else {
+        const int col = ((int)blockIdx.x - M) * 16 + (t & 15);
+        const int ph = t >> 4;
+        uint32_t k0 = 0, k1 = 0, k2 = 0, k3 = 0;
+        if (col < N) {
+            const double* p = B + col;
+            int r = ph;
+            for (; r + 192 < K; r += 256) {
+                k0 = max(k0, bf16_key<CEIL>(p[(size_t)r * ldb]));
+                k1 = max(k1, bf16_key<CEIL>(p[(size_t)(r + 64) * ldb]));
+                k2 = max(k2, bf16_key<CEIL>(p[(size_t)(r + 128) * ldb]));
+                k3 = max(k3, bf16_key<CEIL>(p[(size_t)(r + 192) * ldb]));
+            }
+            for (; r < K; r += 64) k0 = max(k0, bf16_key<CEIL>(p[(size_t)r * ldb]));
+        }
+        part[t] = max(max(k0, k1), max(k2, k3));  // part[16 ph + c]
+        __syncthreads();
+        // 64 phases per column: 16 threads per column take 4 phases each, then one thread 16 of those
+        uint32_t m4 = 0;
+        if (t < 256) {
+            const int c = t & 15, q = t >> 4;
+            m4 = max(max(part[(4 * q) * 16 + c], part[(4 * q + 1) * 16 + c]),
+                     max(part[(4 * q + 2) * 16 + c], part[(4 * q + 3) * 16 + c]));
+        }
+        __syncthreads();
+        if (t < 256) part[t] = m4;  // part[16 q + c]
+        __syncthreads();
+        if (t < 16 && ((int)blockIdx.x - M) * 16 + t < N) {
+            uint32_t m = 0;
+#pragma unroll
+            for (int q = 0; q < 16; q++) m = max(m, part[q * 16 + t]);
+            uint32_t bad;
+            dB[((int)blockIdx.x - M) * 16 + t] = key_delta(m, shift, bad);
+            if (bad) atomicOr(&flags[1], bad);
+        }
+    }
+}
+
 template <int CEIL>
 int launch_keys(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, uint32_t* keys) {
     if (mode == 0) {
@@ -145,4 +232,23 @@ extern "C" int oz_scale_f64(oz_dev* dev, const double* X, int rows, int cols, in
     const int n = mode == 0 ? rows : cols;
     hipLaunchKernelGGL(key_to_delta_kernel, dim3(oz::ceil_div(n, 256)), dim3(256), 0, dev->stream, keys, n, shift, flags);
     return oz::launch_check(dev, "key_to_delta_kernel");
+}
+
+extern "C" int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int lda, const double* B, int N, int ldb,
+                                 int ceil_mode, int shift, int32_t* dA, int32_t* dB, uint32_t* flags) {
+    if (int st = oz::use(dev)) return st;
+    if (!A || !B || !dA || !dB || !flags || M <= 0 || N <= 0 || K <= 0 || lda < K || ldb < N || ceil_mode < 0 ||
+        ceil_mode > 2 || ((uintptr_t)flags & 3))
+        return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: invalid arguments (M=%d N=%d K=%d lda=%d ldb=%d ceil=%d)",
+                        M, N, K, lda, ldb, ceil_mode);
+    const long long blocks = (long long)M + (N + 15) / 16;
+    if (blocks > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: grid too large");
+    const dim3 grid((unsigned)blocks), block(1024);
+    if (ceil_mode == 0)
+        hipLaunchKernelGGL(scale_pair_kernel<0>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags);
+    else if (ceil_mode == 1)
+        hipLaunchKernelGGL(scale_pair_kernel<1>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags);
+    else
+        hipLaunchKernelGGL(scale_pair_kernel<2>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags);
+    return oz::launch_check(dev, "scale_pair_kernel");
 }

@@ -160,14 +160,12 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
+// Block blk (within a plane, the same for the whole wave) of the operand X; see split_block_kernel.
 template <class GEN, bool TRAN>
-__global__ void __launch_bounds__(256) split_block_kernel(const double* __restrict__ X, int rows, int cols, int ld,
-                                                          int mode, const int32_t* __restrict__ delta, GEN gen,
-                                                          int nplanes, uint4* __restrict__ planes, int kblocks,
-                                                          long long nblocks, long long pstride_chunks) {
-    // block index within a plane, the same for the whole wave
-    const long long blk = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (blk >= nblocks) return;
+__device__ __forceinline__ void split_block(const double* __restrict__ X, int rows, int cols, int ld, int mode,
+                                            const int32_t* __restrict__ delta, const GEN& gen, int nplanes,
+                                            uint4* __restrict__ planes, int kblocks, long long blk,
+                                            long long pstride_chunks) {
     const int lane = threadIdx.x & 63;
     const int br = (int)(blk / kblocks), bk = (int)(blk % kblocks);
     double xv[16];
@@ -223,6 +221,38 @@ __global__ void __launch_bounds__(256) split_block_kernel(const double* __restri
                 out[(long long)s * pstride_chunks] = make_uint4(fix(w.x), fix(w.y), fix(w.z), fix(w.w));
             });
         }
+    }
+}
+
+template <class GEN, bool TRAN>
+__global__ void __launch_bounds__(256) split_block_kernel(const double* __restrict__ X, int rows, int cols, int ld,
+                                                          int mode, const int32_t* __restrict__ delta, GEN gen,
+                                                          int nplanes, uint4* __restrict__ planes, int kblocks,
+                                                          long long nblocks, long long pstride_chunks) {
+    const long long blk = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (blk >= nblocks) return;
+    split_block<GEN, TRAN>(X, rows, cols, ld, mode, delta, gen, nplanes, planes, kblocks, blk, pstride_chunks);
+}
+
+// Both operands of a product in one launch: the first ceil(nbA/4) workgroups split A (M x K, row
+// deltas) into planes of Mg x Kg in OZ_BLOCK tiles, the others B (K x N, column deltas) into planes of
+// B^T, Ng x Kg. The same generator (moduli) serves both.
+template <class GEN>
+__global__ void __launch_bounds__(256) split_pair_kernel(const double* __restrict__ A, int M, int K, int lda,
+                                                         const int32_t* __restrict__ dA, uint4* __restrict__ pA,
+                                                         long long nbA, long long sA_chunks,
+                                                         const double* __restrict__ B, int N, int ldb,
+                                                         const int32_t* __restrict__ dB, uint4* __restrict__ pB,
+                                                         long long nbB, long long sB_chunks, int kblocks, GEN gen,
+                                                         int nplanes) {
+    const long long gA = (nbA + 3) / 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if ((long long)blockIdx.x < gA) {
+        const long long blk = (long long)blockIdx.x * 4 + wave;
+        if (blk < nbA) split_block<GEN, false>(A, M, K, lda, 0, dA, gen, nplanes, pA, kblocks, blk, sA_chunks);
+    } else {
+        const long long blk = ((long long)blockIdx.x - gA) * 4 + wave;
+        if (blk < nbB) split_block<GEN, true>(B, K, N, ldb, 1, dB, gen, nplanes, pB, kblocks, blk, sB_chunks);
     }
 }
 

@@ -167,6 +167,16 @@ class Device:
         self._check(hip().oz_scale_f64(self.h, X.ptr, rows, cols, ld, mode, ceil_mode, shift, delta.ptr,
                                        flags.offset(4 * flag_index)), "oz_scale_f64")
 
+    def scale_pair(self, A: Buffer, M, K, lda, B: Buffer, N, ldb, ceil_mode, shift, dA: Buffer, dB: Buffer,
+                   flags: Buffer):
+        self._check(hip().oz_scale_pair_f64(self.h, A.ptr, M, K, lda, B.ptr, N, ldb, ceil_mode, shift, dA.ptr, dB.ptr,
+                                            flags.ptr), "oz_scale_pair_f64")
+
+    def split_pair_int8(self, A: Buffer, M, K, lda, dA: Buffer, B: Buffer, N, ldb, dB: Buffer, desc: ModuliDesc,
+                        pA: Buffer, pB: Buffer, Mg, Ng, Kg):
+        self._check(hip().oz2_split_pair_int8(self.h, A.ptr, M, K, lda, dA.ptr, B.ptr, N, ldb, dB.ptr,
+                                              ctypes.byref(desc), pA.ptr, pB.ptr, Mg, Ng, Kg), "oz2_split_pair_int8")
+
     def split_int8(self, X: Buffer, rows, cols, ld, mode, delta: Buffer, desc: ModuliDesc, planes: Buffer, layout, prow,
                    pld, pstride):
         self._check(hip().oz2_split_int8(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, ctypes.byref(desc), planes.ptr,

@@ -291,3 +291,100 @@ def test_residues_any_parity_of_moduli(dev, oracle, layout, moduli):
         np.testing.assert_array_equal(got[:, :cols, :rows], want.transpose(0, 2, 1))
     else:
         np.testing.assert_array_equal(got[:, :rows, :cols], want)
+
+
+@pytest.mark.parametrize("ceil_mode", [0, 1, 2])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 1000), (64, 1100, 77), (1, 1, 1), (2048, 40, 4096)])
+def test_scale_pair_matches_oracle(dev, oracle, ceil_mode, M, N, K):
+    """oz_scale_pair_f64: A's rows and B's columns in one launch, with leading dimensions beyond the
+    extents, equal to the oracle's scale of each operand; flags 0 for finite in-range inputs."""
+    rng = np.random.default_rng(M + N + K + ceil_mode)
+    lda, ldb = K + 3, N + 5
+    A = np.zeros((M, lda))
+    B = np.zeros((K, ldb))
+    operand = lambda r, c: (split_inputs(r, c, rng, 3.0) if r >= 4 and c >= 5 else
+                            (rng.uniform(0, 1, (r, c)) - 0.5) * np.exp(3.0 * rng.standard_normal((r, c))))
+    A[:, :K] = operand(M, K)
+    B[:, :N] = operand(K, N)
+    A[M // 2, :K] = 0.0  # an all-zero row
+    B[:, N // 2] = 0.0   # an all-zero column
+    A[:, K:] = 1e300     # beyond the extents: never read
+    B[:, N:] = 1e300
+    shift = 56 - 40
+    bA, bB = dev.upload(A), dev.upload(B)
+    dA, dB, fl = dev.alloc(4 * M), dev.alloc(4 * N), dev.alloc(8)
+    dev.fill_u32(fl, 0, 2)
+    dev.scale_pair(bA, M, K, lda, bB, N, ldb, ceil_mode, shift, dA, dB, fl)
+    gA, gB = dev.download(dA, np.int32, M), dev.download(dB, np.int32, N)
+    flags = dev.download(fl, np.uint32, 2)
+    for x in (bA, bB, dA, dB, fl):
+        x.free()
+    dev.bufs.clear()
+    wA, fA = oracle.scale(np.ascontiguousarray(A[:, :K]), M, K, 0, ceil_mode, shift)
+    wB, fB = oracle.scale(np.ascontiguousarray(B[:, :N]), K, N, 1, ceil_mode, shift)
+    np.testing.assert_array_equal(gA, wA)
+    np.testing.assert_array_equal(gB, wB)
+    assert list(flags) == [fA, fB] == [0, 0]
+
+
+def test_scale_pair_flags(dev, oracle):
+    """Range flags of the pair: Inf/NaN (4), a nonzero maximum below 2^-126 (2), above the largest BF16 (1),
+    A's into flags[0] and B's into flags[1], as oz_scale_f64 reports them."""
+    M, N, K = 64, 48, 96
+    A = np.ones((M, K))
+    B = np.ones((K, N))
+    A[3, 5] = np.inf
+    A[7, :] = 2.0 ** -130
+    B[:, 9] = 2.0 ** 129
+    B[11, 2] = np.nan
+    bA, bB = dev.upload(A), dev.upload(B)
+    dA, dB, fl = dev.alloc(4 * M), dev.alloc(4 * N), dev.alloc(8)
+    dev.fill_u32(fl, 0, 2)
+    dev.scale_pair(bA, M, K, K, bB, N, N, 1, 16, dA, dB, fl)
+    flags = dev.download(fl, np.uint32, 2)
+    gA, gB = dev.download(dA, np.int32, M), dev.download(dB, np.int32, N)
+    for x in (bA, bB, dA, dB, fl):
+        x.free()
+    dev.bufs.clear()
+    wA, fA = oracle.scale(A, M, K, 0, 1, 16)
+    wB, fB = oracle.scale(B, K, N, 1, 1, 16)
+    assert list(flags) == [fA, fB] == [4 | 2, 4 | 1]
+    np.testing.assert_array_equal(gA, wA)
+    np.testing.assert_array_equal(gB, wB)
+
+
+@pytest.mark.parametrize("M,N,K,nd,b", [(300, 520, 700, 3, 56), (256, 256, 64, 4, 70), (17, 5, 33, 5, 90)])
+def test_split_pair_equals_single_splits(dev, oracle, M, N, K, nd, b):
+    """oz2_split_pair_int8 writes exactly the planes of oz2_split_int8 on A (layout 2) and B (layout 3),
+    padding zeros included, and they equal the oracle's residues."""
+    rng = np.random.default_rng(M * 7 + K)
+    A = split_inputs(M, K, rng, 1.5)
+    B = split_inputs(K, N, rng, 1.5)
+    moduli = moduli_for(b, nd, 4096)
+    md = moduli_desc(moduli, nd)
+    S = len(moduli)
+    shift = b - 20 * (nd - 1)
+    wA, _ = oracle.scale(A, M, K, 0, 1, shift)
+    wB, _ = oracle.scale(B, K, N, 1, 1, shift)
+    Mg, Ng, Kg = -(-M // 16) * 16 + 16, -(-N // 16) * 16, -(-K // 64) * 64 + 64
+    bA, bB, bdA, bdB = dev.upload(A), dev.upload(B), dev.upload(wA), dev.upload(wB)
+    pA, pB = dev.alloc(S * Mg * Kg), dev.alloc(S * Ng * Kg)
+    qA, qB = dev.alloc(S * Mg * Kg), dev.alloc(S * Ng * Kg)
+    dev.fill_u32(pA, 0x5A5A5A5A, S * Mg * Kg // 4)
+    dev.fill_u32(pB, 0x5A5A5A5A, S * Ng * Kg // 4)
+    dev.split_pair_int8(bA, M, K, K, bdA, bB, N, N, bdB, md, pA, pB, Mg, Ng, Kg)
+    dev.split_int8(bA, M, K, K, 0, bdA, md, qA, 2, Mg, Kg, Mg * Kg)
+    dev.split_int8(bB, K, N, N, 1, bdB, md, qB, 3, Ng, Kg, Ng * Kg)
+    got = [dev.download(x, np.int8, S * r * Kg) for x, r in ((pA, Mg), (pB, Ng), (qA, Mg), (qB, Ng))]
+    for x in (bA, bB, bdA, bdB, pA, pB, qA, qB):
+        x.free()
+    dev.bufs.clear()
+    np.testing.assert_array_equal(got[0], got[2])
+    np.testing.assert_array_equal(got[1], got[3])
+    want_A = oracle.residues(A, M, K, 0, wA, nd, moduli)
+    want_B = oracle.residues(B, K, N, 1, wB, nd, moduli)
+    pa = from_blocks(got[0].reshape(S, -1), Mg, Kg)
+    pb = from_blocks(got[1].reshape(S, -1), Ng, Kg)
+    np.testing.assert_array_equal(pa[:, :M, :K], want_A)
+    np.testing.assert_array_equal(pb[:, :N, :K], want_B.transpose(0, 2, 1))
+    assert not pa[:, M:, :].any() and not pa[:, :, K:].any() and not pb[:, N:, :].any() and not pb[:, :, K:].any()
