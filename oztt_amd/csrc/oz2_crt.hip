@@ -28,68 +28,53 @@ namespace {
 
 using oz2::mod_small;
 
-template <int NW>
-__device__ __forceinline__ double to_double_scaled(const uint32_t* w, int e2) {
-    // w: two's complement NW-word integer; returns w * 2^e2 rounded to nearest-even (subnormal -> 0)
-    uint32_t v[NW];
-    const bool neg = (w[NW - 1] >> 31) != 0;
-    if (neg) {
-        uint32_t c = 1;
+// V = sum_l x_l 2^(32 l) >= 0 from normalized limbs (every x_l in [0, 2^32)) -> V 2^e2 rounded to
+// nearest-even, negated if neg; 0 when V = 0, signed zero below 2^-1022 (f64_tf.h:45-47), infinity
+// above the FP64 range. The limbs are read as 64-bit words (with a zero limb below x_0 when L is
+// odd); the leading nonzero word and the one below it form a 128-bit window, everything under the
+// window only matters as the sticky bit. Selects only, no branches.
+template <int L>
+__device__ __forceinline__ double magnitude_to_double(const double* x, int e2, bool neg) {
+    constexpr int NU = (L + 1) / 2, OFF = (L & 1) ? 32 : 0;  // V = sum_k U_k 2^(64 k - OFF)
+    uint64_t U[NU];
 #pragma unroll
-        for (int i = 0; i < NW; i++) {
-            const uint64_t t = (uint64_t)(~w[i]) + c;
-            v[i] = (uint32_t)t;
-            c = (uint32_t)(t >> 32);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NW; i++) v[i] = w[i];
+    for (int k = 0; k < NU; k++) {
+        const int lo = 2 * k - (L & 1);
+        const uint64_t wl = lo >= 0 ? (uint64_t)(uint32_t)x[lo] : 0ull;
+        U[k] = ((uint64_t)(uint32_t)x[lo + 1] << 32) | wl;
     }
-    int top = -1;  // index of the highest nonzero word
+    uint64_t first = U[0], second = 0, below = 0;
+    int base = 0;
 #pragma unroll
-    for (int i = 0; i < NW; i++)
-        if (v[i]) top = i;
-    if (top < 0) return neg ? -0.0 : 0.0;
-    // gather the 96 bits below and including the leading bit: hi word, next, next
-    const uint32_t w2 = v[top];
-    const uint32_t w1 = top >= 1 ? v[top - 1] : 0u;
-    const uint32_t w0 = top >= 2 ? v[top - 2] : 0u;
-    bool sticky_low = false;
-#pragma unroll
-    for (int i = 0; i < NW; i++)
-        if (i < top - 2 && v[i]) sticky_low = true;
-    const int lz = __clz(w2);
-    // normalize the 96-bit window so that the leading bit is bit 95
-    uint64_t hi64 = ((uint64_t)w2 << 32) | w1;  // bits 95..32 of the window
-    uint32_t lo32 = w0;
-    if (lz) {
-        hi64 = (hi64 << lz) | (lo32 >> (32 - lz));
-        lo32 <<= lz;
+    for (int k = 1; k < NU; k++) {
+        const bool nz = U[k] != 0;
+        below = nz ? (below | second) : below;
+        second = nz ? first : second;
+        first = nz ? U[k] : first;
+        base = nz ? 64 * k : base;
     }
-    // hi64 holds the leading 64 bits; keep 53, round on the remaining 11 bits + lo32 + lower words
-    uint64_t mant = hi64 >> 11;
-    const uint64_t rest = hi64 & 0x7FFull;
-    const bool guard = (rest >> 10) & 1ull;
-    const bool sticky = (rest & 0x3FFull) || lo32 || sticky_low;
-    // value = mant * 2^(position of mant LSB) with the leading bit at 32*top + 31 - lz
-    int exp_lead = 32 * top + 31 - lz + e2;  // exponent of the leading bit
-    if (guard && (sticky || (mant & 1ull))) {
-        mant += 1ull;
-        if (mant >> 53) {
-            mant >>= 1;
-            exp_lead += 1;
-        }
-    }
-    if (exp_lead < -1022) return neg ? -0.0 : 0.0;
-    if (exp_lead > 1023) return neg ? -__builtin_huge_val() : __builtin_huge_val();
+    const int lz = __builtin_clzll(first | 1ull);  // 63 for first = 0 (then the result is 0 anyway)
+    const uint64_t hi = lz ? (first << lz) | (second >> (64 - lz)) : first;
+    const bool sticky = below != 0 || (second << lz) != 0;
+    uint64_t mant = hi >> 11;
+    const bool rb = (hi >> 10) & 1ull;
+    const bool st = (hi & 0x3FFull) != 0 || sticky;
+    mant += (rb && (st || (mant & 1ull))) ? 1ull : 0ull;
+    const int carry = (int)(mant >> 53);
+    mant >>= carry;
+    const int exp_lead = base - OFF + 63 - lz + e2 + carry;  // exponent of the leading bit
     const uint64_t bits = ((uint64_t)(exp_lead + 1023) << 52) | (mant & 0x000FFFFFFFFFFFFFull);
-    const double r = __longlong_as_double((long long)bits);
-    return neg ? -r : r;
+    double r = __longlong_as_double((long long)bits);
+    r = exp_lead > 1023 ? __builtin_huge_val() : r;
+    r = exp_lead < -1022 ? 0.0 : r;
+    r = neg ? -r : r;
+    return first == 0 ? 0.0 : r;
 }
 
 // Kernel constants: limbs of Q_s, M, floor(M/2), M - floor(M/2) (32-bit limbs as exact doubles).
 struct CrtLimbs {
     int S, shift, b;
+    double two32;  // 2^32 (a kernel argument, so that it sits in a scalar register)
     double invM;   // 1/M rounded
     double delta;  // exact-path threshold: 2^-28 + 2/M
     double Q[OZ2_MAXS][8];
@@ -122,18 +107,24 @@ __device__ __forceinline__ int limb_sign(const double* x) {
 }
 
 // x = V (exact limbs, each below 2^53) -> C' * 2^e2 rounded to nearest-even (subnormal -> signed 0).
+// C' = V - t M with t the nearest integer to an FP64 estimate of V/M. Its sign is that of q - t
+// whenever |C'| is not tiny, so the limbs are multiplied by that sign before the carries are
+// propagated, which leaves the magnitude in nonnegative 32-bit limbs; a tiny C' of the other sign
+// shows as a negative top limb and is negated once more (rare). An estimate near a half-integer is
+// settled exactly against floor(M/2) (rare).
 template <int L>
 __device__ __forceinline__ double crt_finish(double* x, const CrtLimbs& a, int e2) {
     double vd = x[L - 1];
 #pragma unroll
-    for (int l = L - 2; l >= 0; l--) vd = __builtin_fma(vd, kTwo32, x[l]);
+    for (int l = L - 2; l >= 0; l--) vd = __builtin_fma(vd, a.two32, x[l]);  // (2^32 from a register)
     const double q = vd * a.invM;
     const double t = __builtin_rint(q);
 #pragma unroll
     for (int l = 0; l < L; l++) x[l] = __builtin_fma(-t, a.Mw[l], x[l]);  // |t M_l| < 2^37: exact
-    normalize<L>(x);
+    bool neg = q - t < 0.0;
     if (__builtin_fabs(q - t) > 0.5 - a.delta) {
         // the estimate may pick the wrong neighbour: compare C' with floor(M/2) exactly
+        normalize<L>(x);
         double y[L];
 #pragma unroll
         for (int l = 0; l < L; l++) y[l] = x[l] - a.Mhalf[l];
@@ -152,18 +143,19 @@ __device__ __forceinline__ double crt_finish(double* x, const CrtLimbs& a, int e
                 normalize<L>(x);
             }
         }
+        neg = x[L - 1] < 0.0;
     }
-    const bool neg = x[L - 1] < 0.0;
-    if (neg) {
+    const double sg = neg ? -1.0 : 1.0;
+#pragma unroll
+    for (int l = 0; l < L; l++) x[l] *= sg;
+    normalize<L>(x);
+    if (x[L - 1] < 0.0) {  // |C'| so small that the estimate's sign was wrong
 #pragma unroll
         for (int l = 0; l < L; l++) x[l] = -x[l];
         normalize<L>(x);
+        neg = !neg;
     }
-    uint32_t w[L];
-#pragma unroll
-    for (int l = 0; l < L; l++) w[l] = (uint32_t)x[l];  // exact: every limb is in [0, 2^32)
-    const double r = to_double_scaled<L>(w, e2);      // the top bit of |C'| is clear: no negation
-    return neg ? -r : r;
+    return magnitude_to_double<L>(x, e2, neg);
 }
 
 // x += k * Q_s (k < 2^12)
@@ -204,10 +196,11 @@ __global__ void __launch_bounds__(256) crt_digits_kernel(const uint8_t* __restri
     if (j0 >= N) return;
     const uint32_t* d = reinterpret_cast<const uint32_t*>(D + (long long)i * ldd + j0);
     const long long sw = sD / 4;
-    // every plane's word is requested before the first is used (S loads in flight per thread)
+    // every plane's word is requested before the first is used (the planes past S read plane S-1
+    // again, so that no load waits on a branch)
     uint32_t v[OZ2_MAXS];
 #pragma unroll
-    for (int s = 0; s < OZ2_MAXS; s++) v[s] = s < a.S ? d[(long long)s * sw] : 0u;
+    for (int s = 0; s < OZ2_MAXS; s++) v[s] = d[(long long)min(s, a.S - 1) * sw];
     double x[4][L];
 #pragma unroll
     for (int e = 0; e < 4; e++)
@@ -278,6 +271,7 @@ __global__ void __launch_bounds__(256) crt_terms_kernel(const uint16_t* __restri
 // Kernel constants of a CRT descriptor whose moduli are at most mmax.
 int crt_limbs(oz_dev* dev, const char* name, const oz2_crt_dev* crt, uint32_t mmax, CrtLimbs& a) {
     a = CrtLimbs{};
+    a.two32 = 4294967296.0;
     a.S = crt->S;
     a.shift = crt->shift;
     a.b = crt->b;
