@@ -143,6 +143,39 @@ def native_fp64_gemm(a, b, m: int, n: int, k: int, reps: int = 3) -> dict:
         dev.close()
 
 
+def vendor_int8_gemm(m: int, n: int, k: int, reps: int = 5) -> dict:
+    """The vendor's int8 GEMM (hipBLASLt, through torch._int_mm) on one modulus's product shape,
+    m x k times k x n int8 -> int32, with operands drawn like residues (uniform on [-127, 127]), as
+    a yardstick for the product kernel: both run on the same matrix cores under the same power limit.
+    Timed with torch events on torch's current stream (where torch launches it) over `reps` calls
+    after one warm-up call; one row is checked against an int64 product."""
+    import torch
+    try:
+        g = torch.Generator(device="cuda:0").manual_seed(11)
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda:0", generator=g)
+        b = torch.randint(-127, 128, (k, n), dtype=torch.int8, device="cuda:0", generator=g)
+        c = torch._int_mm(a, b)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            c = torch._int_mm(a, b)
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        want = a[:1].cpu().to(torch.int64) @ b.cpu().to(torch.int64)
+        ok = bool(torch.equal(c[:1].cpu().to(torch.int64), want))
+        ops = 2.0 * m * n * k
+        out = {"library": "hipBLASLt int8 GEMM (torch._int_mm)", "shape": [m, n, k], "ms": round(ms, 4),
+               "tops": round(ops / (ms * 1e-3) / 1e12, 2), "frac": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+               "row0_checked": ok}
+        del a, b, c
+        torch.cuda.empty_cache()
+        return out
+    except Exception as e:  # an unsupported shape or build: report, do not fail the bench
+        return {"error": f"{type(e).__name__}: {e}"}
+
+
 # BASELINE.json configs: name -> (scheme, format, m, n, k, seed, phi, options, peak of the product format, rows of
 # the CPU baseline slab, sample edge of the binary128 check). C3 is the headline and the default.
 CONFIGS = {
@@ -303,6 +336,13 @@ def main() -> int:
         del c8
     log("native FP64 GEMM on the GPU (rocBLAS dgemm)")
     out["native_fp64_gemm"] = native_fp64_gemm(a, b, m, n, k)
+    if fmt != "FP8":
+        log("vendor int8 GEMM on one product's shape (hipBLASLt)")
+        v = vendor_int8_gemm(m, n, k)
+        if "tops" in v:
+            # the product kernel's rate per unit of int8 work next to the vendor's on the same shape
+            v["product_kernel_tops"] = round(achieved, 2)
+        out["vendor_int8_gemm"] = v
     if cpu_rows > 0:
         log(f"CPU baseline: Dot2 on {cpu_rows} rows")
         out["cpu_baseline"], hi, lo = cpu_baseline(a, b, m, n, k, cpu_rows)

@@ -268,6 +268,14 @@ int oz2_crt_terms_f64(oz_dev* dev, const uint16_t* W, int M, int N, int ldw, lon
  * layouts. radix <= 254, dmax <= 127, p <= 256. */
 int oz1_split_int8(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int p,
                    int radix, int dmax, int8_t* planes, int layout, int prow, int pld, long long plane_stride);
+/* Both operands of a product in one launch (the reference slices A and B in two kernels of the
+ * same stage, ozaki1.cpp run()): oz1_split_int8 of A (M x K, lda, row deltas dA, mode 0) into
+ * planesA in layout 2 (p planes of Mg x Kg, stride Mg*Kg bytes) and of B (K x N, ldb, column deltas
+ * dB, mode 1) into planesB in layout 3 (p planes of Ng x Kg, stride Ng*Kg). Mg >= M and Ng >= N
+ * multiples of 16, Kg >= K a multiple of 64, planes 16-byte aligned. */
+int oz1_split_pair_int8(oz_dev* dev, const double* A, int M, int K, int lda, const int32_t* dA, const double* B, int N,
+                        int ldb, const int32_t* dB, int p, int radix, int dmax, int8_t* planesA, int8_t* planesB,
+                        int Mg, int Ng, int Kg);
 
 /* ---- A16: diagonal partial products (reference ozaki1/gemm.hpp:315, stages.hpp:157) ----------
  * C[d] = sum_{i=0..d} A[i] * Bt[d-i]^T for d < ndiag, exact int32: the d+1 pairs concatenated along

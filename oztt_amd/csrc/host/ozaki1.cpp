@@ -115,8 +115,10 @@ Output ozaki1_run(Device& D, const Problem& p) {
                                       "scale");
                      }});
     // B's slices once (per K block: rows kb Kc.. of B), then per band and K block: A's slices (columns
-    // kb Kc.. of the band's rows), the diagonal products, the reconstruction
-    for (std::uint32_t kb = 0; kb < nkb; kb++) {
+    // kb Kc.. of the band's rows), the diagonal products, the reconstruction. With one K block and one
+    // band, A's and B's slices are one launch.
+    const bool paired = nkb == 1 && nbands == 1;
+    for (std::uint32_t kb = 0; kb < (paired ? 0u : nkb); kb++) {
         const double* Bk = dBf + (std::size_t)kb * Kc * N;
         std::int8_t* slBk = slB + (std::size_t)kb * P * strideB;
         steps.push_back({ev::Slice, [=] {
@@ -135,12 +137,22 @@ Output ozaki1_run(Device& D, const Problem& p) {
             const std::int8_t* slBk = slB + (std::size_t)kb * P * strideB;
             float* lb = limbs ? limbs + (std::size_t)r0 * N : nullptr;
             const int first = kb == 0, last = kb + 1 == nkb;
-            steps.push_back({ev::Slice, [=] {
-                                 device_check(dev,
-                                              oz1_split_int8(dev, Ab, (int)rows, (int)Kc, (int)K, 0, dAb, (int)P,
-                                                             f.radix, f.dmax, slA, 2, (int)rowsg, (int)Kbg, strideA),
-                                              "slice A");
-                             }});
+            if (paired)
+                steps.push_back({ev::Slice, [=] {
+                                     device_check(dev,
+                                                  oz1_split_pair_int8(dev, dAf, (int)M, (int)K, (int)K, dltA, dBf,
+                                                                      (int)N, (int)N, dltB, (int)P, f.radix, f.dmax,
+                                                                      slA, slB, (int)Mbg, (int)Ng, (int)Kbg),
+                                                  "slice A and B");
+                                 }});
+            else
+                steps.push_back({ev::Slice, [=] {
+                                     device_check(dev,
+                                                  oz1_split_int8(dev, Ab, (int)rows, (int)Kc, (int)K, 0, dAb, (int)P,
+                                                                 f.radix, f.dmax, slA, 2, (int)rowsg, (int)Kbg,
+                                                                 strideA),
+                                                  "slice A");
+                                 }});
             steps.push_back({ev::Gemm, [=] {
                                  device_check(dev,
                                               oz1_gemm_diag_i8(dev, slA, slBk, part, (int)rowsg, (int)Ng, (int)Kbg,
@@ -167,10 +179,11 @@ Output ozaki1_run(Device& D, const Problem& p) {
     // P(P+1)/2 slice-pair products of 2*M*N*K operations each
     const unsigned pairs = P * (P + 1) / 2;
     // the pass the configuration calls for: scale once; B's slices once per K block; per band and K
-    // block A's slices, the diagonal products and a reconstruction step; and the regions it writes
+    // block A's slices, the diagonal products and a reconstruction step (one band and one K block:
+    // both operands' slices in one step); and the regions it writes
     PassShape shape;
     shape.steps[ev::Scale] = 1;
-    shape.steps[ev::Slice] = nkb + nbands * nkb;
+    shape.steps[ev::Slice] = paired ? 1 : nkb + nbands * nkb;
     shape.steps[ev::Gemm] = nbands * nkb;
     shape.steps[ev::Recon] = nbands * nkb;
     shape.written = {{flags, 2 * sizeof(std::uint32_t)},

@@ -16,6 +16,8 @@
 // the Horner step is about 75 FP32 operations per diagonal, the assembly integer arithmetic.
 #pragma clang fp contract(off)
 
+#include <cmath>
+
 #include "oz_tf32.hpp"
 
 namespace {
@@ -99,7 +101,7 @@ __device__ __forceinline__ uint64_t assemble_tf_f64(float fh, float fm, float fl
     return pack_f64(A, W, qw + g + (ebase - 187) - shA, sgn);
 }
 
-template <bool POW2, bool SIGNMAG>
+template <bool POW2, bool FMA, bool SIGNMAG>
 __global__ void __launch_bounds__(256) recon_kernel(const int32_t* __restrict__ P, int M, int N, int ldp, long long sP,
                                                     int ndiag, int nsingle, float radix, uint64_t W, int32_t qw,
                                                     const int32_t* __restrict__ dA, const int32_t* __restrict__ dB,
@@ -118,7 +120,7 @@ __global__ void __launch_bounds__(256) recon_kernel(const int32_t* __restrict__ 
         for (int t = 0; t < 8; t++) {
             const int d = d0 + t;
             if (d >= ndiag) break;
-            if (d > 0) tf_mul_radix<POW2>(hi, mid, lo, radix);
+            if (d > 0) tf_mul_radix<POW2, FMA>(hi, mid, lo, radix);
             const int32_t v = vb[t];
             if (!SIGNMAG && d < nsingle) {
                 tf_add_s(hi, mid, lo, (float)v);
@@ -147,7 +149,7 @@ __global__ void __launch_bounds__(256) recon_kernel(const int32_t* __restrict__ 
 // integers of at most 2^24 (the FP32 products of the reference), enter whole into the Horner
 // evaluation; then, after the first block, the three limbs carried from the previous blocks are
 // added (lo, then mid, then hi). Every block but the last stores the limbs; the last assembles C.
-template <bool POW2, bool ACC, bool EMIT>
+template <bool POW2, bool FMA, bool ACC, bool EMIT>
 __global__ void __launch_bounds__(256) recon_block_kernel(const int32_t* __restrict__ P, int M, int N, int ldp,
                                                           long long sP, int ndiag, float radix, float* __restrict__ L,
                                                           long long sL, int ldl, uint64_t W, int32_t qw,
@@ -167,7 +169,7 @@ __global__ void __launch_bounds__(256) recon_block_kernel(const int32_t* __restr
         for (int t = 0; t < 8; t++) {
             const int d = d0 + t;
             if (d >= ndiag) break;
-            if (d > 0) tf_mul_radix<POW2>(hi, mid, lo, radix);
+            if (d > 0) tf_mul_radix<POW2, FMA>(hi, mid, lo, radix);
             tf_add_s(hi, mid, lo, (float)vb[t]);
         }
     }
@@ -188,13 +190,13 @@ __global__ void __launch_bounds__(256) recon_block_kernel(const int32_t* __restr
     }
 }
 
-template <bool POW2, bool ACC, bool EMIT>
+template <bool POW2, bool FMA, bool ACC, bool EMIT>
 int launch_block(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long sP, const oz1_recon_dev* r, float* L,
                  long long sL, int ldl, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
     const uint64_t W = ((uint64_t)r->Whi << 32) | r->Wlo;
     for (int i0 = 0; i0 < M; i0 += 65535) {
         const int rows = min(65535, M - i0);
-        hipLaunchKernelGGL((recon_block_kernel<POW2, ACC, EMIT>), dim3(oz::ceil_div(N, 256), rows), dim3(256), 0,
+        hipLaunchKernelGGL((recon_block_kernel<POW2, FMA, ACC, EMIT>), dim3(oz::ceil_div(N, 256), rows), dim3(256), 0,
                            dev->stream, P + (long long)i0 * ldp, rows, N, ldp, sP, r->ndiag, (float)r->radix,
                            L + (long long)i0 * ldl, sL, ldl, W, r->qw, dA ? dA + i0 : dA, dB,
                            out ? out + (long long)i0 * ldo : out, ldo);
@@ -203,28 +205,45 @@ int launch_block(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long
     return OZ_OK;
 }
 
-template <bool POW2>
+template <bool POW2, bool FMA>
 int launch_block_mode(oz_dev* dev, int first, int last, const int32_t* P, int M, int N, int ldp, long long sP,
                       const oz1_recon_dev* r, float* L, long long sL, int ldl, const int32_t* dA, const int32_t* dB,
                       double* out, int ldo) {
-    if (first && last) return launch_block<POW2, false, false>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
-    if (first) return launch_block<POW2, false, true>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
-    if (last) return launch_block<POW2, true, false>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
-    return launch_block<POW2, true, true>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+    if (first && last)
+        return launch_block<POW2, FMA, false, false>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+    if (first) return launch_block<POW2, FMA, false, true>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+    if (last) return launch_block<POW2, FMA, true, false>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
+    return launch_block<POW2, FMA, true, true>(dev, P, M, N, ldp, sP, r, L, sL, ldl, dA, dB, out, ldo);
 }
 
-template <bool POW2, bool SIGNMAG>
+template <bool POW2, bool FMA, bool SIGNMAG>
 int launch_recon(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long sP, const oz1_recon_dev* r,
                  const int32_t* dA, const int32_t* dB, double* out, int ldo) {
     const uint64_t W = ((uint64_t)r->Whi << 32) | r->Wlo;
     for (int i0 = 0; i0 < M; i0 += 65535) {
         const int rows = min(65535, M - i0);
-        hipLaunchKernelGGL((recon_kernel<POW2, SIGNMAG>), dim3(oz::ceil_div(N, 256), rows), dim3(256), 0, dev->stream,
-                           P + (long long)i0 * ldp, rows, N, ldp, sP, r->ndiag, r->nsingle, (float)r->radix, W, r->qw,
-                           dA + i0, dB, out + (long long)i0 * ldo, ldo);
+        hipLaunchKernelGGL((recon_kernel<POW2, FMA, SIGNMAG>), dim3(oz::ceil_div(N, 256), rows), dim3(256), 0,
+                           dev->stream, P + (long long)i0 * ldp, rows, N, ldp, sP, r->ndiag, r->nsingle,
+                           (float)r->radix, W, r->qw, dA + i0, dB, out + (long long)i0 * ldo, ldo);
         if (int st = oz::launch_check(dev, "recon_kernel")) return st;
     }
     return OZ_OK;
+}
+
+// The Horner values are integers, so no intermediate of tfMulR is subnormal, and every |value| is
+// below 2^31 r^(p-1) r/(r-1) (|P_d| < 2^31). Below 2^127 / 4097 neither form of tfMulR overflows
+// (Dekker's multiplies a limb by 4097), and its TwoProduct form gives the same triples.
+bool recon_fma_safe(const oz1_recon_dev* r) {
+    const double rad = r->radix;
+    const double bits = 31.0 + (r->ndiag - 1) * std::log2(rad) + std::log2(rad / (rad - 1.0)) + std::log2(4097.0);
+    return bits < 127.0;
+}
+
+// POW2: tfMulP2; otherwise tfMulR, in its TwoProduct form where recon_fma_safe allows
+enum RadixForm { kDekker = 0, kTwoProduct = 1, kPow2 = 2 };
+RadixForm radix_form(const oz1_recon_dev* r) {
+    if ((r->radix & (r->radix - 1)) == 0) return kPow2;
+    return recon_fma_safe(r) ? kTwoProduct : kDekker;
 }
 
 }  // namespace
@@ -236,12 +255,14 @@ extern "C" int oz1_recon_f64(oz_dev* dev, const int32_t* P, int M, int N, int ld
         r->radix > 254 || !(r->Whi >> 31) || r->nsingle < 0 || (r->signmag && r->nsingle) ||
         (r->ndiag > 1 && strideP < (long long)M * ldp))
         return oz::fail(dev, OZ_ERR_ARG, "oz1_recon_f64: invalid arguments");
-    const bool pow2 = (r->radix & (r->radix - 1)) == 0;
+    const RadixForm form = radix_form(r);
     if (r->signmag)
-        return pow2 ? launch_recon<true, true>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo)
-                    : launch_recon<false, true>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo);
-    return pow2 ? launch_recon<true, false>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo)
-                : launch_recon<false, false>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo);
+        return form == kPow2        ? launch_recon<true, false, true>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo)
+               : form == kTwoProduct ? launch_recon<false, true, true>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo)
+                                     : launch_recon<false, false, true>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo);
+    return form == kPow2        ? launch_recon<true, false, false>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo)
+           : form == kTwoProduct ? launch_recon<false, true, false>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo)
+                                 : launch_recon<false, false, false>(dev, P, M, N, ldp, strideP, r, dA, dB, out, ldo);
 }
 
 extern "C" int oz1_recon_block_f64(oz_dev* dev, const int32_t* P, int M, int N, int ldp, long long strideP,
@@ -252,9 +273,13 @@ extern "C" int oz1_recon_block_f64(oz_dev* dev, const int32_t* P, int M, int N, 
         r->radix > 254 || r->signmag || (r->ndiag > 1 && strideP < (long long)M * ldp) ||
         limb_stride < (long long)M * ldl || (last && (!dA || !dB || !out || ldo < N || !(r->Whi >> 31))))
         return oz::fail(dev, OZ_ERR_ARG, "oz1_recon_block_f64: invalid arguments");
-    const bool pow2 = (r->radix & (r->radix - 1)) == 0;
-    return pow2 ? launch_block_mode<true>(dev, first, last, P, M, N, ldp, strideP, r, limbs, limb_stride, ldl, dA, dB,
-                                          out, ldo)
-                : launch_block_mode<false>(dev, first, last, P, M, N, ldp, strideP, r, limbs, limb_stride, ldl, dA,
-                                           dB, out, ldo);
+    const RadixForm form = radix_form(r);
+    if (form == kPow2)
+        return launch_block_mode<true, false>(dev, first, last, P, M, N, ldp, strideP, r, limbs, limb_stride, ldl, dA,
+                                              dB, out, ldo);
+    if (form == kTwoProduct)
+        return launch_block_mode<false, true>(dev, first, last, P, M, N, ldp, strideP, r, limbs, limb_stride, ldl, dA,
+                                              dB, out, ldo);
+    return launch_block_mode<false, false>(dev, first, last, P, M, N, ldp, strideP, r, limbs, limb_stride, ldl, dA, dB,
+                                           out, ldo);
 }

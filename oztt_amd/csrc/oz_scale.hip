@@ -128,9 +128,11 @@ __device__ __forceinline__ int32_t key_delta(uint32_t key, int shift, uint32_t& 
 }
 
 // A's rows and B's columns in one launch of 1024-thread workgroups, deltas written directly:
-//   workgroup r < M: row r of A, each thread a stride-1024 run of its K values;
-//   workgroup M + j: columns 16j..16j+15 of B over all of its K rows, thread t taking column t % 16
-//   and every 64th row from t / 16 (a wave reads four 128-byte row pieces per load).
+//   workgroup j < ceil(N/16): columns 16j..16j+15 of B over all of its K rows, thread t taking
+//   column t % 16 and every 64th row from t / 16 (a wave reads four 128-byte row pieces per load);
+//   workgroup ceil(N/16) + r: row r of A, each thread a stride-1024 run of its K values.
+// The column strips read 16 K doubles each workgroup, the rows K: the long strips are dispatched
+// first and the short rows fill in behind them, so no strip is left running alone at the end.
 // The 16 waves' maxima meet in LDS; flags[0] (A) and flags[1] (B) collect the flag bits with atomicOr.
 template <int CEIL>
 __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restrict__ A, int M, int K, int lda,
@@ -139,16 +141,20 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
                                                           uint32_t* __restrict__ flags) {
     __shared__ uint32_t part[1024];
     const int t = threadIdx.x;
-    if ((int)blockIdx.x < M) {
-        const double* row = A + (size_t)blockIdx.x * lda;
-        uint32_t k0 = 0, k1 = 0;
+    const int strips = (N + 15) / 16;
+    if ((int)blockIdx.x >= strips) {
+        const int i = (int)blockIdx.x - strips;
+        const double* row = A + (size_t)i * lda;
+        uint32_t k0 = 0, k1 = 0, k2 = 0, k3 = 0;
         int c = t;
-        for (; c + 1024 < K; c += 2048) {
+        for (; c + 3072 < K; c += 4096) {
             k0 = max(k0, bf16_key<CEIL>(row[c]));
             k1 = max(k1, bf16_key<CEIL>(row[c + 1024]));
+            k2 = max(k2, bf16_key<CEIL>(row[c + 2048]));
+            k3 = max(k3, bf16_key<CEIL>(row[c + 3072]));
         }
-        if (c < K) k0 = max(k0, bf16_key<CEIL>(row[c]));
-        const uint32_t k = wave_max(max(k0, k1));
+        for (; c < K; c += 1024) k0 = max(k0, bf16_key<CEIL>(row[c]));
+        const uint32_t k = wave_max(max(max(k0, k1), max(k2, k3)));
         if ((t & 63) == 0) part[t >> 6] = k;
         __syncthreads();
         if (t == 0) {
@@ -156,11 +162,11 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
 #pragma unroll
             for (int w = 0; w < 16; w++) m = max(m, part[w]);
             uint32_t bad;
-            dA[blockIdx.x] = key_delta(m, shift, bad);
+            dA[i] = key_delta(m, shift, bad);
             if (bad) atomicOr(&flags[0], bad);
         }
     } else {
-        const int col = ((int)blockIdx.x - M) * 16 + (t & 15);
+        const int col = (int)blockIdx.x * 16 + (t & 15);
         const int ph = t >> 4;
         uint32_t k0 = 0, k1 = 0, k2 = 0, k3 = 0;
         if (col < N) {
@@ -186,12 +192,12 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
         __syncthreads();
         if (t < 256) part[t] = m4;  // part[16 q + c]
         __syncthreads();
-        if (t < 16 && ((int)blockIdx.x - M) * 16 + t < N) {
+        if (t < 16 && (int)blockIdx.x * 16 + t < N) {
             uint32_t m = 0;
 #pragma unroll
             for (int q = 0; q < 16; q++) m = max(m, part[q * 16 + t]);
             uint32_t bad;
-            dB[((int)blockIdx.x - M) * 16 + t] = key_delta(m, shift, bad);
+            dB[(int)blockIdx.x * 16 + t] = key_delta(m, shift, bad);
             if (bad) atomicOr(&flags[1], bad);
         }
     }

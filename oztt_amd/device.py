@@ -218,6 +218,12 @@ class Device:
         self._check(hip().oz1_split_int8(self.h, X.ptr, rows, cols, ld, mode, delta.ptr, p, radix, dmax, planes.ptr,
                                          layout, prow, pld, ctypes.c_longlong(pstride)), "oz1_split_int8")
 
+    def oz1_split_pair(self, A: Buffer, M, K, lda, dA: Buffer, B: Buffer, N, ldb, dB: Buffer, p, radix, dmax,
+                       pA: Buffer, pB: Buffer, Mg, Ng, Kg):
+        """oz1_split of A (layout 2, planes Mg x Kg) and of B (layout 3, planes Ng x Kg) in one launch."""
+        self._check(hip().oz1_split_pair_int8(self.h, A.ptr, M, K, lda, dA.ptr, B.ptr, N, ldb, dB.ptr, p, radix, dmax,
+                                              pA.ptr, pB.ptr, Mg, Ng, Kg), "oz1_split_pair_int8")
+
     def oz1_gemm_diag(self, A: Buffer, Bt: Buffer, C: Buffer, M, N, K, ndiag, ldc, sA, sB, sC, dmax=127):
         self._check(hip().oz1_gemm_diag_i8(self.h, A.ptr, Bt.ptr, C.ptr, M, N, K, ndiag, dmax, ldc, ctypes.c_longlong(sA),
                                            ctypes.c_longlong(sB), ctypes.c_longlong(sC)), "oz1_gemm_diag_i8")

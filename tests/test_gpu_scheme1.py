@@ -64,6 +64,66 @@ def test_slices_match_oracle(dev, oracle, layout, radix, dmax, ceil, p):
         assert not got[:, rows:, :].any() and not got[:, :, cols:].any()
 
 
+def test_slices_near_the_subnormal_range(dev, oracle):
+    """Digits of elements whose last significand bit sits just above and just below 2^-126 after
+    scaling (row maxima near 1/2, elements near 2^-73): deep planes reach them, and a wave takes the
+    TwoProduct form of tfMulR only when all its elements' limbs are normal, Dekker's otherwise; the
+    digits equal the oracle's either way."""
+    rng = np.random.default_rng(21)
+    rows, cols, p = 64, 256, 16
+    # |x| in [2^-k-1, 2^-k): the last bit weighs 2^(-k-53); rows 0-31 (two bands of blocks) keep
+    # k <= 73, so every limb is normal there, rows 32-63 straddle the boundary
+    k = np.where(np.arange(rows)[:, None] < 32, rng.integers(66, 74, (rows, cols)), rng.integers(70, 81, (rows, cols)))
+    X = rng.choice([-1.0, 1.0], (rows, cols)) * rng.uniform(0.5, 1.0, (rows, cols)) * np.exp2(-k.astype(np.float64))
+    X[:, 0] = 0.5
+    X[40::3, 1] = 1e-300  # far below every normal limb
+    delta, _ = oracle.scale(X, rows, cols, 0, 1, -1)
+    assert not delta.any()
+    want = oracle.oz1_slices(X, rows, cols, 0, delta, p, 254, 127)
+    assert np.count_nonzero(want[8:, :32]) > 32 * cols  # the deep planes reach the small elements
+    prow, pld = rows, cols
+    bx, bd = dev.upload(X), dev.upload(delta)
+    bp = dev.alloc(p * prow * pld)
+    dev.oz1_split(bx, rows, cols, cols, 0, bd, p, 254, 127, bp, 2, prow, pld, prow * pld)
+    got = from_blocks(dev.download(bp, np.int8, p * prow * pld).reshape(p, -1), prow, pld)
+    for x in (bx, bd, bp):
+        x.free()
+    dev.bufs.clear()
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("M,N,K,p,radix,dmax", [(300, 520, 700, 8, 254, 127), (17, 5, 33, 10, 64, 32),
+                                                (256, 256, 64, 13, 14, 7)])
+def test_split_pair_equals_single_splits(dev, oracle, M, N, K, p, radix, dmax):
+    """oz1_split_pair_int8 writes exactly the planes of oz1_split_int8 on A (layout 2) and B (layout 3),
+    padding zeros included, and they equal the oracle's slices."""
+    rng = np.random.default_rng(M + K + p)
+    A = edge_rows(M, K, rng) if M > 5 else rng.uniform(-1, 1, (M, K))
+    B = rng.uniform(-1, 1, (K, N)) * np.exp2(rng.integers(-30, 30, (1, N)))
+    dA, _ = oracle.scale(A, M, K, 0, 1, -1)
+    dB, _ = oracle.scale(B, K, N, 1, 1, -1)
+    Mg, Ng, Kg = -(-M // 16) * 16 + 16, -(-N // 16) * 16, -(-K // 64) * 64 + 64
+    bA, bB, bdA, bdB = dev.upload(A), dev.upload(B), dev.upload(dA), dev.upload(dB)
+    pA, pB = dev.alloc(p * Mg * Kg), dev.alloc(p * Ng * Kg)
+    qA, qB = dev.alloc(p * Mg * Kg), dev.alloc(p * Ng * Kg)
+    dev.fill_u32(pA, 0x5A5A5A5A, p * Mg * Kg // 4)
+    dev.fill_u32(pB, 0x5A5A5A5A, p * Ng * Kg // 4)
+    dev.oz1_split_pair(bA, M, K, K, bdA, bB, N, N, bdB, p, radix, dmax, pA, pB, Mg, Ng, Kg)
+    dev.oz1_split(bA, M, K, K, 0, bdA, p, radix, dmax, qA, 2, Mg, Kg, Mg * Kg)
+    dev.oz1_split(bB, K, N, N, 1, bdB, p, radix, dmax, qB, 3, Ng, Kg, Ng * Kg)
+    got = [dev.download(x, np.int8, p * r * Kg) for x, r in ((pA, Mg), (pB, Ng), (qA, Mg), (qB, Ng))]
+    for x in (bA, bB, bdA, bdB, pA, pB, qA, qB):
+        x.free()
+    dev.bufs.clear()
+    np.testing.assert_array_equal(got[0], got[2])
+    np.testing.assert_array_equal(got[1], got[3])
+    pa = from_blocks(got[0].reshape(p, -1), Mg, Kg)
+    pb = from_blocks(got[1].reshape(p, -1), Ng, Kg)
+    np.testing.assert_array_equal(pa[:, :M, :K], oracle.oz1_slices(A, M, K, 0, dA, p, radix, dmax))
+    np.testing.assert_array_equal(pb[:, :N, :K], oracle.oz1_slices(B, K, N, 1, dB, p, radix, dmax).transpose(0, 2, 1))
+    assert not pa[:, M:, :].any() and not pa[:, :, K:].any() and not pb[:, N:, :].any() and not pb[:, :, K:].any()
+
+
 @pytest.mark.parametrize("M,N,K,p", [(256, 512, 192, 8), (512, 256, 1024, 13), (256, 256, 64, 1)])
 def test_diagonal_products_exact(dev, M, N, K, p):
     """P_d = sum_{i<=d} A_i B_{d-i}^T with all d+1 pairs in one exact int32 accumulation; the all-127 rows
