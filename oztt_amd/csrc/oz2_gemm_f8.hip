@@ -210,7 +210,8 @@ __global__ void __launch_bounds__(THREADS) gemm_f8_groups_kernel(const uint8_t* 
     __syncthreads();
     float* tile = reinterpret_cast<float*>(lds) + wave * (64 * 128);
     const long long c0 = (long long)o * sO + (long long)(tm * BM + wm * 128) * ldo + tn * BN + wn * 128;
-    const double md = (double)(g.np_m & 0xFFFFu), cf = (double)g.coef, rinv = 1.0 / md;
+    const uint32_t mi = g.np_m & 0xFFFFu;
+    const double md = (double)mi, cf = (double)g.coef, rinv = 1.0 / md;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
 #pragma unroll
@@ -234,8 +235,8 @@ __global__ void __launch_bounds__(THREADS) gemm_f8_groups_kernel(const uint8_t* 
                 uint32_t w[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++)
-                    w[k] = oz2::mod_mul_f64((double)s[2 * k], cf, md, rinv) |
-                           oz2::mod_mul_f64((double)s[2 * k + 1], cf, md, rinv) << 16;
+                    w[k] = oz2::mod_mul_f64((double)s[2 * k], cf, md, rinv, mi) |
+                           oz2::mod_mul_f64((double)s[2 * k + 1], cf, md, rinv, mi) << 16;
                 *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + at) = uint4{w[0], w[1], w[2], w[3]};
             } else {
                 int32_t* d = static_cast<int32_t*>(out) + at;

@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
             }
         uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
         const double md = (double)m, yd = (double)y, rinv = 1.0 / md;
-        auto dg = [&](int32_t c) -> uint32_t { return oz2::mod_mul_f64((double)c, yd, md, rinv); };
+        auto dg = [&](int32_t c) -> uint32_t { return oz2::mod_mul_f64((double)c, yd, md, rinv, m); };
 #pragma unroll
         for (int h = 0; h < 2; h++) {
 #pragma unroll

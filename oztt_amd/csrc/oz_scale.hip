@@ -20,20 +20,21 @@ constexpr uint32_t KEY_NAN = 0xFFFFFFFFu;  // Inf/NaN: dominates every other key
 constexpr uint32_t KEY_TINY = 1u;          // nonzero maximum below 2^-126 (loses to any normal value)
 
 // Key of |x| for the rounding mode (the BF16 code for normal in-range magnitudes; 0x7F80 above range).
+// Branch-free: the in-range code is computed for every input, then the special cases replace it in
+// increasing priority (above range, below range, Inf/NaN), so a wave never splits over its elements.
 template <int CEIL>
 __device__ __forceinline__ uint32_t bf16_key(double x) {
     const unsigned long long u = (unsigned long long)__double_as_longlong(x);
     const uint32_t h = (uint32_t)(u >> 32) & 0x7FFFFFFFu, l = (uint32_t)u;
     const int32_t E = (int32_t)(h >> 20);
-    if (E == 0x7FF) return KEY_NAN;
     const int32_t e8 = E - 896;
-    if (e8 <= 0) return (h | l) ? KEY_TINY : 0u;
-    if (e8 >= 255) return 0x7F80u;
     uint32_t v = ((uint32_t)e8 << 7) | ((h >> 13) & 0x7Fu);
     const bool dropped = (h & 0x1FFFu) || l;
-    if (CEIL == 1 && dropped) v += 1u;
-    if (CEIL == 2 && (dropped || !(v & 0x7Fu))) v += 1u;
-    return v;
+    if (CEIL == 1) v += dropped ? 1u : 0u;
+    if (CEIL == 2) v += (dropped || !(v & 0x7Fu)) ? 1u : 0u;
+    v = e8 >= 255 ? 0x7F80u : v;
+    v = e8 <= 0 ? ((h | l) ? KEY_TINY : 0u) : v;
+    return E == 0x7FF ? KEY_NAN : v;
 }
 
 __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
@@ -145,17 +146,26 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
     if ((int)blockIdx.x >= strips) {
         const int i = (int)blockIdx.x - strips;
         const double* row = A + (size_t)i * lda;
-        uint32_t k0 = 0, k1 = 0, k2 = 0, k3 = 0;
+        // up to 8 loads in flight per thread: a whole row of K <= 8192 in one round trip
+        uint32_t k[4] = {0, 0, 0, 0};
         int c = t;
-        for (; c + 3072 < K; c += 4096) {
-            k0 = max(k0, bf16_key<CEIL>(row[c]));
-            k1 = max(k1, bf16_key<CEIL>(row[c + 1024]));
-            k2 = max(k2, bf16_key<CEIL>(row[c + 2048]));
-            k3 = max(k3, bf16_key<CEIL>(row[c + 3072]));
+        for (; c + 7168 < K; c += 8192) {
+            double v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = row[c + 1024 * u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) k[u & 3] = max(k[u & 3], bf16_key<CEIL>(v[u]));
         }
-        for (; c < K; c += 1024) k0 = max(k0, bf16_key<CEIL>(row[c]));
-        const uint32_t k = wave_max(max(max(k0, k1), max(k2, k3)));
-        if ((t & 63) == 0) part[t >> 6] = k;
+        for (; c + 3072 < K; c += 4096) {
+            double v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = row[c + 1024 * u];
+#pragma unroll
+            for (int u = 0; u < 4; u++) k[u] = max(k[u], bf16_key<CEIL>(v[u]));
+        }
+        for (; c < K; c += 1024) k[0] = max(k[0], bf16_key<CEIL>(row[c]));
+        const uint32_t kk = wave_max(max(max(k[0], k[1]), max(k[2], k[3])));
+        if ((t & 63) == 0) part[t >> 6] = kk;
         __syncthreads();
         if (t == 0) {
             uint32_t m = 0;
@@ -168,19 +178,28 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
     } else {
         const int col = (int)blockIdx.x * 16 + (t & 15);
         const int ph = t >> 4;
-        uint32_t k0 = 0, k1 = 0, k2 = 0, k3 = 0;
+        // 16 loads in flight per thread (1024 rows of the strip per round trip)
+        uint32_t k[4] = {0, 0, 0, 0};
         if (col < N) {
             const double* p = B + col;
             int r = ph;
-            for (; r + 192 < K; r += 256) {
-                k0 = max(k0, bf16_key<CEIL>(p[(size_t)r * ldb]));
-                k1 = max(k1, bf16_key<CEIL>(p[(size_t)(r + 64) * ldb]));
-                k2 = max(k2, bf16_key<CEIL>(p[(size_t)(r + 128) * ldb]));
-                k3 = max(k3, bf16_key<CEIL>(p[(size_t)(r + 192) * ldb]));
+            for (; r + 960 < K; r += 1024) {
+                double v[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) v[u] = p[(size_t)(r + 64 * u) * ldb];
+#pragma unroll
+                for (int u = 0; u < 16; u++) k[u & 3] = max(k[u & 3], bf16_key<CEIL>(v[u]));
             }
-            for (; r < K; r += 64) k0 = max(k0, bf16_key<CEIL>(p[(size_t)r * ldb]));
+            for (; r + 192 < K; r += 256) {
+                double v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = p[(size_t)(r + 64 * u) * ldb];
+#pragma unroll
+                for (int u = 0; u < 4; u++) k[u] = max(k[u], bf16_key<CEIL>(v[u]));
+            }
+            for (; r < K; r += 64) k[0] = max(k[0], bf16_key<CEIL>(p[(size_t)r * ldb]));
         }
-        part[t] = max(max(k0, k1), max(k2, k3));  // part[16 ph + c]
+        part[t] = max(max(k[0], k[1]), max(k[2], k[3]));  // part[16 ph + c]
         __syncthreads();
         // 64 phases per column: 16 threads per column take 4 phases each, then one thread 16 of those
         uint32_t m4 = 0;

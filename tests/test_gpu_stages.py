@@ -252,6 +252,37 @@ def test_gemm_digits_exact(dev, M, N, K, S):
         np.testing.assert_array_equal(D[s].astype(np.int64), want)
 
 
+@pytest.mark.parametrize("M,N,K,S,digits", [(256, 256, 256, 300, False), (256, 512, 384, 150, False),
+                                             (1024, 1024, 256, 20, True), (768, 1024, 384, 23, True)])
+def test_gemm_tile_sequences(dev, M, N, K, S, digits):
+    """More tiles than CUs (several generations of workgroups, the tile map over many batches), few
+    K steps per tile (4 and 6), tile counts that are not a multiple of the CU or XCD count; int32
+    products and CRT digits bit-exact."""
+    rng = np.random.default_rng(M + 7 * S + K)
+    A = rng.integers(-127, 128, (S, M, K), dtype=np.int8)
+    Bt = rng.integers(-127, 128, (S, N, K), dtype=np.int8)
+    A[:, 0, :] = 127
+    Bt[:, 0, :] = 127
+    A[:, 1, :] = -127
+    bA, bB = dev.upload(to_blocks(A)), dev.upload(to_blocks(Bt))
+    moduli = (INT8_16 + [193, 191, 181, 179, 173, 167, 163])[:S] if digits else None
+    out = dev.alloc((1 if digits else 4) * S * M * N)
+    if digits:
+        desc = crt_desc(moduli, 54, 3)
+        dev.gemm_digits(bA, bB, out, M, N, K, S, N, M * K, N * K, M * N, desc)
+        got = dev.download(out, np.uint8, S * M * N).reshape(S, M, N)
+    else:
+        dev.gemm_i8(bA, bB, out, M, N, K, S, N, M * K, N * K, M * N)
+        got = dev.download(out, np.int32, S * M * N).reshape(S, M, N)
+    for x in (bA, bB, out):
+        x.free()
+    dev.bufs.clear()
+    for t in range(S):
+        prod = (A[t].astype(np.float64) @ Bt[t].astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
+        want = (prod % moduli[t]) * int(desc.y[t]) % moduli[t] if digits else prod
+        np.testing.assert_array_equal(got[t].astype(np.int64), want, err_msg=f"batch {t}")
+
+
 def test_device_copy(dev):
     rng = np.random.default_rng(5)
     x = rng.integers(0, 2 ** 32, 4096 + 64, dtype=np.uint64).astype(np.uint32)
