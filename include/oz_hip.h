@@ -220,6 +220,14 @@ typedef struct oz2_digit_dev {
 int oz2_digit_planes(const oz2_digit_dev* dd);
 int oz2_split_digits(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
                      const oz2_digit_dev* dd, uint8_t* planes, int layout, int prow, int pld, long long plane_stride);
+/* Both operands of a product in one launch (the reference splits them in two kernels of the same
+ * stage, ozaki2.cpp:228-285): oz2_split_digits of A (M x K, lda, row deltas dA, mode 0) into planesA
+ * in layout 2 (planes of Mg x Kg, stride Mg*Kg bytes) and of B (K x N, ldb, column deltas dB, mode 1)
+ * into planesB in layout 3 (planes of Ng x Kg, stride Ng*Kg). Mg >= M and Ng >= N multiples of 16,
+ * Kg >= K a multiple of 64, planes 16-byte aligned. */
+int oz2_split_digits_pair(oz_dev* dev, const double* A, int M, int K, int lda, const int32_t* dA, const double* B,
+                          int N, int ldb, const int32_t* dB, const oz2_digit_dev* dd, uint8_t* planesA, uint8_t* planesB,
+                          int Mg, int Ng, int Kg);
 
 /* ---- A18 products + composition (reference ozaki2.cpp:228-285 run_digit_modulus, compose.cpp,
  * split.hpp:541-661 product terms and groups) ------------------------------------------------

@@ -114,7 +114,16 @@ Output ozaki2_run(Device& D, const Problem& p) {
                                       "scale");
                      }});
     // B's planes once, then per band: A's planes, the products, the reconstruction of the band's rows
-    if (fp8)
+    // (one band: A's and B's planes in one launch)
+    if (fp8 && nbands == 1)
+        steps.push_back({ev::Slice, [=] {
+                             device_check(dev,
+                                          oz2_split_digits_pair(dev, dAf, (int)M, (int)K, (int)K, dltA, dBf, (int)N,
+                                                                (int)N, dltB, &ddesc, uA, uB, (int)Mbg, (int)Ng,
+                                                                (int)Kg),
+                                          "slice");
+                         }});
+    else if (fp8)
         steps.push_back({ev::Slice, [=] {
                              device_check(dev,
                                           oz2_split_digits(dev, dBf, (int)K, (int)N, (int)N, 1, dltB, &ddesc, uB, 3,
@@ -142,12 +151,13 @@ Output ozaki2_run(Device& D, const Problem& p) {
         const std::int32_t* dAb = dltA + r0;
         double* ob = out + (std::size_t)r0 * N;
         if (fp8) {
-            steps.push_back({ev::Slice, [=] {
-                                 device_check(dev,
-                                              oz2_split_digits(dev, Ab, (int)rows, (int)K, (int)K, 0, dAb, &ddesc, uA,
-                                                               2, (int)rowsg, (int)Kg, strideA),
-                                              "slice A");
-                             }});
+            if (nbands > 1)
+                steps.push_back({ev::Slice, [=] {
+                                     device_check(dev,
+                                                  oz2_split_digits(dev, Ab, (int)rows, (int)K, (int)K, 0, dAb, &ddesc,
+                                                                   uA, 2, (int)rowsg, (int)Kg, strideA),
+                                                  "slice A");
+                                 }});
             steps.push_back({ev::Gemm, [=] {
                                  device_check(dev,
                                               oz2_gemm_groups_f8(dev, uA, uB, terms, (int)rowsg, (int)Ng, (int)Kg,
@@ -187,12 +197,11 @@ Output ozaki2_run(Device& D, const Problem& p) {
     // products: one per modulus (INT8) or the FP8 route's digit products (sum of the outputs' pairs)
     const std::uint32_t nprod = fp8 ? (std::uint32_t)plan.mo.nprod : S;
 
-    // the pass the configuration calls for: scale once; B's slice once and A's per band (INT8 with one
-    // band: both in one step); one product and one reconstruction step per band; and the regions it
-    // writes
+    // the pass the configuration calls for: scale once; B's slice once and A's per band (one band:
+    // both in one step); one product and one reconstruction step per band; and the regions it writes
     PassShape shape;
     shape.steps[ev::Scale] = 1;
-    shape.steps[ev::Slice] = (!fp8 && nbands == 1) ? 1 : 1 + nbands;
+    shape.steps[ev::Slice] = nbands == 1 ? 1 : 1 + nbands;
     shape.steps[ev::Gemm] = nbands;
     shape.steps[ev::Recon] = nbands;
     shape.written = {{flags, 2 * sizeof(std::uint32_t)},

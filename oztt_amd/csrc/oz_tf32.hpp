@@ -9,6 +9,8 @@
 // operation. Zero signs can differ from the model (its products with a zero factor are +0); a zero's
 // sign never changes a digit, residue or reconstructed value.
 #pragma once
+#include <type_traits>
+
 #include "oz_internal.hpp"
 
 namespace {
@@ -191,6 +193,14 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
+// Generators with kDrivesPlanes = true run the plane loop themselves: GEN::run(st, emit) calls
+// emit(p, w) for every plane p in order, w[k] holding the bytes of the lane's elements 4k..4k+3
+// (element 4k in the low byte). The others are driven plane by plane through GEN::planes.
+template <class G, class = void>
+struct drives_planes : std::false_type {};
+template <class G>
+struct drives_planes<G, std::void_t<decltype(G::kDrivesPlanes)>> : std::bool_constant<G::kDrivesPlanes> {};
+
 // Block blk (within a plane, the same for the whole wave) of the operand X; see split_block_kernel.
 template <class GEN, bool TRAN>
 __device__ __forceinline__ void split_block(const double* __restrict__ X, int rows, int cols, int ld, int mode,
@@ -226,9 +236,28 @@ __device__ __forceinline__ void split_block(const double* __restrict__ X, int ro
     typename GEN::State st[16];
 #pragma unroll
     for (int e = 0; e < 16; e++) gen.load(st[e], xv[e], dv[e]);
-    // GEN::planes(st, s, emit) computes plane s's 16 values v and calls emit(v, fix) once, where
-    // fix(w) maps four packed values to the bytes stored; emit packs and stores them.
-    if constexpr (TRAN) {
+    if constexpr (drives_planes<GEN>::value) {
+        if constexpr (TRAN) {
+            const int rr = lane >> 2;
+            uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
+            gen.run(st, [&](int p, const uint32_t* w) {
+                out[(long long)p * pstride_chunks] = make_uint4(w[0], w[1], w[2], w[3]);
+            });
+        } else {
+            __shared__ __attribute__((aligned(16))) uint8_t image[4][1024];
+            uint8_t* img = image[threadIdx.x >> 6];
+            const int colpart = 16 * (lane >> 4), colbyte = lane & 15;
+            uint4* out = planes + blk * 64 + lane;
+            gen.run(st, [&](int p, const uint32_t* w) {
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)(w[e >> 2] >> (8 * (e & 3)));
+                out[(long long)p * pstride_chunks] = *reinterpret_cast<const uint4*>(img + 16 * lane);
+            });
+        }
+    } else if constexpr (TRAN) {
+        // GEN::planes(st, s, emit) computes plane s's 16 values v and calls emit(v, fix) once, where
+        // fix(w) maps four packed values to the bytes stored; emit packs and stores them.
         const int rr = lane >> 2;
         uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
         for (int s = 0; s < nplanes; s++) {

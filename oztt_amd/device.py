@@ -238,6 +238,12 @@ class Device:
                                               planes.ptr, layout, prow, pld, ctypes.c_longlong(pstride)),
                     "oz2_split_digits")
 
+    def split_digits_pair(self, A: Buffer, M, K, lda, dA: Buffer, B: Buffer, N, ldb, dB: Buffer, desc: DigitDesc,
+                          pA: Buffer, pB: Buffer, Mg, Ng, Kg):
+        """split_digits of A (layout 2, planes Mg x Kg) and of B (layout 3, planes Ng x Kg) in one launch."""
+        self._check(hip().oz2_split_digits_pair(self.h, A.ptr, M, K, lda, dA.ptr, B.ptr, N, ldb, dB.ptr,
+                                                ctypes.byref(desc), pA.ptr, pB.ptr, Mg, Ng, Kg), "oz2_split_digits_pair")
+
     def gemm_groups_f8(self, A: Buffer, Bt: Buffer, out: Buffer, M, N, K, desc: GroupsDesc, kind, ldo, sA, sB, sO):
         self._check(hip().oz2_gemm_groups_f8(self.h, A.ptr, Bt.ptr, out.ptr, M, N, K, ctypes.byref(desc), kind, ldo,
                                                 ctypes.c_longlong(sA), ctypes.c_longlong(sB), ctypes.c_longlong(sO)),

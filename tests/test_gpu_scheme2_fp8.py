@@ -142,6 +142,37 @@ def check_fp8_chain(oracle, r, a, b, n):
     return C, ms, dA, dB
 
 
+@pytest.mark.parametrize("m,n,k,encoding", [(300, 200, 700, 1), (64, 520, 130, 1), (17, 5, 33, 0)])
+def test_split_digits_pair_equals_single_splits(dev, m, n, k, encoding):
+    """oz2_split_digits_pair writes exactly the planes of oz2_split_digits on A (layout 2) and B
+    (layout 3), padding zeros included, for both encodings."""
+    a, b = oz.eval_inputs(9, 2.0, m * k, k * n)
+    dd, gd, crt, tm = oz.plan2_fp8_device(a, b, m, n, k)
+    dd.encoding = encoding
+    nd, b_ = dd.mo.nd, crt.b
+    shift = b_ - 20 * (nd - 1)
+    Mg, Ng, Kg = -(-m // 16) * 16 + 16, -(-n // 16) * 16, -(-k // 64) * 64 + 64
+    P = gd.nplanes
+    bA, bB = dev.upload(a), dev.upload(b)
+    bdA, bdB, bfl = dev.alloc(4 * m), dev.alloc(4 * n), dev.alloc(8)
+    dev.fill_u32(bfl, 0, 2)
+    dev.scale(bA, m, k, k, 0, 1, shift, bdA, bfl, 0)
+    dev.scale(bB, k, n, n, 1, 1, shift, bdB, bfl, 1)
+    pA, pB, qA, qB = (dev.alloc(P * r * Kg) for r in (Mg, Ng, Mg, Ng))
+    dev.fill_u32(pA, 0x5A5A5A5A, P * Mg * Kg // 4)
+    dev.fill_u32(pB, 0x5A5A5A5A, P * Ng * Kg // 4)
+    dev.split_digits_pair(bA, m, k, k, bdA, bB, n, n, bdB, dd, pA, pB, Mg, Ng, Kg)
+    dev.split_digits(bA, m, k, k, 0, bdA, dd, qA, 2, Mg, Kg, Mg * Kg)
+    dev.split_digits(bB, k, n, n, 1, bdB, dd, qB, 3, Ng, Kg, Ng * Kg)
+    got = [dev.download(x, np.uint8, P * r * Kg) for x, r in ((pA, Mg), (pB, Ng), (qA, Mg), (qB, Ng))]
+    for x in (bA, bB, bdA, bdB, bfl, pA, pB, qA, qB):
+        x.free()
+    dev.bufs.clear()
+    np.testing.assert_array_equal(got[0], got[2])
+    np.testing.assert_array_equal(got[1], got[3])
+    assert got[0].any() and got[1].any()
+
+
 def test_fp8_stages_quick_case_reference_hash(dev, oracle):
     """quick.csv:11: II FP8 128^3, uniform seed 7, b = 54, 14 moduli requested, one pass."""
     n = 128
