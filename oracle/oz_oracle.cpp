@@ -1035,6 +1035,96 @@ void orc_oz1_slices(const double* X, int rows, int cols, int ld, int mode, const
         }
 }
 
+// tfMulR with each limb product and its error taken by one multiply and one FMA (TwoProduct), in the
+// FP32 model: the form the GPU's slicer and reconstruction use where it gives tf_mul_r's result.
+static void tf_mul_r_twoproduct(float& hi, float& mid, float& lo, float r) {
+    auto f_fma = [](float a, float b, float c) { return flush(std::fmaf(flush(a), flush(b), flush(c))); };
+    const float acc_lo = f_mul(lo, r);
+    const float p1 = f_mul(mid, r);
+    float tmp0 = f_fma(mid, r, -p1);
+    const float p0 = f_mul(hi, r);
+    const float f0 = f_fma(hi, r, -p0);
+    tmp0 = f_add(tmp0, acc_lo);
+    float sa, ea, sb, eb, r0, ec;
+    two_sum(p1, tmp0, sa, ea);
+    two_sum(f0, sa, sb, eb);
+    two_sum(p0, sb, r0, ec);
+    const float g = f_add(ea, eb);
+    hi = r0;
+    fast_two_sum(ec, g, mid, lo);
+}
+
+// Equivalence check of the two forms of tfMulR (tf_mul_r, Dekker's, and tf_mul_r_twoproduct) on n
+// pseudo-random chains. mode 0, the slicer: x*2^d of a random double, scaled near 1/2 or 50-100
+// binades below, then `planes` digits in radix r with bound dmax; a chain counts as covered when
+// the GPU takes the TwoProduct form for it (x's last significand bit weighs at least 2^-126, or x
+// is zero; and |hi| r <= dmax + 1/2, so that the state never grows), and as differing when any
+// digit differs. mode 1, the reconstruction: Horner chains of up to `planes` diagonal sums (int32,
+// added as the reference's high and low parts), all covered; differing when a triple differs.
+// Returns the number of covered chains that differ; *covered receives the covered count.
+int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
+                                 int64_t* covered) {
+    const float r = (float)radix, dm = (float)dmax;
+    int64_t bad = 0, cov = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad, cov)
+    for (int64_t it = 0; it < n; it++) {
+        std::mt19937_64 g(seed * 0x9E3779B97F4A7C15ull + (uint64_t)it);
+        bool same = true, covered_chain = true;
+        if (mode == 0) {
+            uint64_t u = g();
+            const int E = (int)(g() % 2047);
+            u = (u & 0x800FFFFFFFFFFFFFull) | ((uint64_t)E << 52);
+            double x;
+            std::memcpy(&x, &u, 8);
+            int k = (int)(g() % 9);
+            if (g() % 2 == 0) k = 50 + (int)(g() % 51);
+            const int32_t d = -2 - k - (E - 1023);
+            float h1, m1, l1;
+            load_triple(x, d, h1, m1, l1);
+            float h2 = h1, m2 = m1, l2 = l1;
+            covered_chain = (E == 0 || E - 1075 + d >= -126) && std::fabs(h1) * r <= dm + 0.5f;
+            for (int t = 0; t < planes; t++) {
+                tf_mul_r(h1, m1, l1, r);
+                tf_mul_r_twoproduct(h2, m2, l2, r);
+                float a = f_rnd(h1), b = f_rnd(h2);
+                a = a < -dm ? -dm : (a >= dm ? dm : a);
+                b = b < -dm ? -dm : (b >= dm ? dm : b);
+                same = same && a == b;
+                h1 = f_sub(h1, a);
+                h2 = f_sub(h2, b);
+            }
+        } else {
+            const int p = 1 + (int)(g() % (uint64_t)planes);
+            float h1 = 0, m1 = 0, l1 = 0, h2 = 0, m2 = 0, l2 = 0;
+            for (int dd = 0; dd < p; dd++) {
+                if (dd) {
+                    tf_mul_r(h1, m1, l1, r);
+                    tf_mul_r_twoproduct(h2, m2, l2, r);
+                }
+                int64_t v;
+                switch (g() % 4) {
+                case 0: v = (int64_t)(g() % 4294967295ull) - 2147483647; break;
+                case 1: v = (g() & 1) ? 2147483647 : -2147483647; break;
+                case 2: v = (int64_t)(g() % 200001) - 100000; break;
+                default: v = 0;
+                }
+                const float vh = (float)(int32_t)((uint32_t)v & 0xFFFFFF00u), vl = (float)(int32_t)((uint32_t)v & 0xFFu);
+                tf_add_s(h1, m1, l1, vh);
+                tf_add_s(h1, m1, l1, vl);
+                tf_add_s(h2, m2, l2, vh);
+                tf_add_s(h2, m2, l2, vl);
+            }
+            same = f_bits(h1) == f_bits(h2) && f_bits(m1) == f_bits(m2) && f_bits(l1) == f_bits(l2);
+        }
+        if (covered_chain) {
+            cov++;
+            if (!same) bad++;
+        }
+    }
+    *covered = cov;
+    return bad;
+}
+
 // Diagonal partial products P_d = sum_{i<=d} A_i B_{d-i} (ozaki1/gemm.hpp:315, stages.hpp:157), exact in
 // int64; A: p planes M x K, B: p planes K x N (row-major); P: ndiag planes M x N as int32. Returns the
 // largest |P| seen.

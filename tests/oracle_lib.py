@@ -27,6 +27,9 @@ class Oracle:
         lib.orc_modround.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_float]
         lib.orc_oz1_gemm_diag.restype = ctypes.c_int64
         lib.orc_oz1_int8_gemm.restype = ctypes.c_int64
+        lib.orc_check_tf_mul_r_forms.restype = ctypes.c_int64
+        lib.orc_check_tf_mul_r_forms.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int,
+                                                 ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
 
     def inputs(self, seed, phi, na, nb):
         a = np.empty(na)

@@ -401,3 +401,39 @@ def test_fp8_reference_hash_from_digit_products(orc):
         r = (k[s] * pow(int(crt.y[s]), -1, m)) % m
         C[s] = np.where(r > m // 2, r - m, r)
     assert orc.hash(orc.crt_ref(C, n, n, ms, b, nd, 0, dA, dB)) == 0x20046E5BB3816CBB
+
+
+@pytest.mark.parametrize("radix,dmax", [(254, 127), (14, 7)])
+def test_tf_mul_r_forms_agree_where_the_slicer_takes_twoproduct(orc, radix, dmax):
+    """The GPU's Scheme I slicer multiplies by a general radix with tfMulR in its TwoProduct form
+    (one multiply and one FMA per limb product) for waves whose elements meet its condition: every
+    limb a multiple of 2^e with e >= -126, and |hi| r <= dmax + 1/2. Under that condition the digits
+    equal those of Dekker's form (the reference's) over 24 planes, in the FP32 model with flush to
+    zero, for elements near their row maximum and elements 50-100 binades below it."""
+    import ctypes
+    cov = ctypes.c_int64()
+    n = 300000
+    bad = orc.lib.orc_check_tf_mul_r_forms(0, n, 7, radix, dmax, 24, ctypes.byref(cov))
+    assert bad == 0
+    assert cov.value > n // 2
+
+
+@pytest.mark.parametrize("radix,pmax", [(254, 11), (14, 23)])
+def test_tf_mul_r_forms_agree_in_the_reconstruction(orc, radix, pmax):
+    """The reconstruction's Horner values are integers, so no intermediate is subnormal; with p at
+    most the bound the GPU applies (2^31 r^(p-1) r/(r-1) 4097 < 2^127: 11 diagonals for radix 254,
+    23 for radix 14) the two forms of tfMulR give identical triples, int32 extremes included."""
+    import ctypes
+    cov = ctypes.c_int64()
+    n = 200000
+    bad = orc.lib.orc_check_tf_mul_r_forms(1, n, 9, radix, 0, pmax, ctypes.byref(cov))
+    assert bad == 0 and cov.value == n
+
+
+def test_tf_mul_r_forms_checker_sees_overflow_beyond_the_bound(orc):
+    """The check can fail: past the bound (radix 14 with up to 30 diagonals) Dekker's split
+    overflows where the TwoProduct form does not, and the checker counts those chains."""
+    import ctypes
+    cov = ctypes.c_int64()
+    bad = orc.lib.orc_check_tf_mul_r_forms(1, 100000, 9, 14, 0, 30, ctypes.byref(cov))
+    assert bad > 0
