@@ -975,13 +975,15 @@ void orc_gemm_quad_sample(const double* A, const double* B, int M, int N, int K,
 // One block of rows [ib, i1) of the Dot2 GEMM, every column, in the reference's loop order (row
 // blocks of 8, column blocks of 512, k outermost inside a block). The reference builds its
 // evaluator with -O3 -march=native (Makefile:16, :132); this library travels to hosts other than
-// the one it is built on, so the same vectorized code is compiled for the AVX-512 and AVX2+FMA
-// instruction sets and picked at load time by the CPU's features (GCC function multiversioning),
-// with a portable fallback. No flag here changes a result: contraction stays off and the only FMA
-// is the explicit one of TwoProduct.
-__attribute__((target_clones("arch=skylake-avx512", "arch=haswell", "default")))
-static void dot2_block(const double* __restrict A, const double* __restrict B, int N, int K, int ib, int i1,
-                       double* __restrict Chi, double* __restrict Clo) {
+// the one it is built on, so the same code is compiled three times, for AVX-512, for AVX2 with FMA
+// and for the baseline instruction set, and dot2_block picks by the CPU's features at run time
+// (__builtin_cpu_supports, which tests features and so holds on any vendor's CPU). No choice
+// changes a result: contraction stays off, the vectorized loop runs over independent columns, and
+// the only FMA is the explicit one of TwoProduct (a library call on the baseline path).
+__attribute__((always_inline)) static inline void dot2_block_body(const double* __restrict A,
+                                                                  const double* __restrict B, int N, int K, int ib,
+                                                                  int i1, double* __restrict Chi,
+                                                                  double* __restrict Clo) {
     const int JB = 512;
     for (int j0 = 0; j0 < N; j0 += JB) {
         const int j1 = std::min(j0 + JB, N);
@@ -1002,6 +1004,33 @@ static void dot2_block(const double* __restrict A, const double* __restrict B, i
             }
         }
     }
+}
+__attribute__((target("avx512f,avx512dq,avx512vl,avx2,fma"))) static void dot2_block_avx512(
+    const double* __restrict A, const double* __restrict B, int N, int K, int ib, int i1, double* __restrict Chi,
+    double* __restrict Clo) {
+    dot2_block_body(A, B, N, K, ib, i1, Chi, Clo);
+}
+__attribute__((target("avx2,fma"))) static void dot2_block_avx2(const double* __restrict A, const double* __restrict B,
+                                                                 int N, int K, int ib, int i1, double* __restrict Chi,
+                                                                 double* __restrict Clo) {
+    dot2_block_body(A, B, N, K, ib, i1, Chi, Clo);
+}
+static void dot2_block_base(const double* __restrict A, const double* __restrict B, int N, int K, int ib, int i1,
+                            double* __restrict Chi, double* __restrict Clo) {
+    dot2_block_body(A, B, N, K, ib, i1, Chi, Clo);
+}
+static void dot2_block(const double* A, const double* B, int N, int K, int ib, int i1, double* Chi, double* Clo) {
+    static const int level = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512dq") &&
+                                     __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("fma")
+                                 ? 2
+                             : __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") ? 1
+                                                                                              : 0;
+    if (level == 2)
+        dot2_block_avx512(A, B, N, K, ib, i1, Chi, Clo);
+    else if (level == 1)
+        dot2_block_avx2(A, B, N, K, ib, i1, Chi, Clo);
+    else
+        dot2_block_base(A, B, N, K, ib, i1, Chi, Clo);
 }
 
 void orc_dot2_gemm(const double* A, const double* B, int M, int N, int K, int r0, int r1, double* Chi, double* Clo) {
