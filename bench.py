@@ -181,11 +181,11 @@ def vendor_int8_gemm(m: int, n: int, k: int, reps: int = 5) -> dict:
 CONFIGS = {
     "C1": ("II", "INT8", 1024, 1024, 1024, 1, 0.5, dict(reconstruction="OnePass"), INT8_PEAK_TOPS, 1024, 64),
     "C2": ("I", "INT8", 4096, 4096, 4096, 2, 1.0, dict(), INT8_PEAK_TOPS, 4096, 64),
-    "C3": ("II", "INT8", 8192, 8192, 8192, 3, 0.5, dict(reconstruction="TwoPass"), INT8_PEAK_TOPS, 1536, 64),
+    "C3": ("II", "INT8", 8192, 8192, 8192, 3, 0.5, dict(reconstruction="TwoPass"), INT8_PEAK_TOPS, 8192, 64),
     # e4m3 digit products on the FP8 matrix cores (dense FP8 peak 5.0 PFLOP/s)
-    "C4": ("II", "FP8", 16384, 16384, 16384, 4, 2.0, dict(), FP8_PEAK_TFLOPS, 256, 32),
+    "C4": ("II", "FP8", 16384, 16384, 16384, 4, 2.0, dict(), FP8_PEAK_TFLOPS, 1024, 32),
     # BF16 digits (+-32) run on the INT8 matrix cores, so the product roofline is the INT8 peak
-    "C5": ("I", "BF16", 8192, 8192, 65536, 5, 4.0, dict(slices=8), INT8_PEAK_TOPS, 128, 32),
+    "C5": ("I", "BF16", 8192, 8192, 65536, 5, 4.0, dict(slices=8), INT8_PEAK_TOPS, 512, 32),
 }
 WORKLOADS = {
     "C1": "C1 Ozaki-II INT8 m=n=k=1024, auto moduli, one-pass reconstruction",

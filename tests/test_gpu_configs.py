@@ -142,6 +142,23 @@ def test_c4_inner_dimension_dense_fp8_route(dev, oracle):
     check_fp8_chain(oracle, r, a, b, n)
 
 
+def test_c4_inner_dimension_public_call_equals_int8(ctx):
+    """The public FP8 call on C4's inner dimension (dense-digit route, both operands split in one
+    launch, products on the FP8 matrix cores) gives C bit for bit equal to INT8 residues at the
+    same width, and its whole-pass replay is checked."""
+    m = n = 256
+    k = 16384
+    a, b = oz.eval_inputs(4, 2.0, m * k, k * n)
+    o8 = oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8)
+    c8, info8, ev8 = ctx.evaluate(a, b, m, n, k, o8, warmup=0, repeats=1)
+    assert ev8.whole_checked
+    oi = oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, max_moduli=24)
+    ci, infoi, _ = ctx.evaluate(a, b, m, n, k, oi, fixed_bits=info8.integer_bits)
+    assert infoi.integer_bits == info8.integer_bits
+    log(f"C4 K: FP8 {info8.moduli} moduli, INT8 {infoi.moduli} moduli, b={info8.integer_bits}")
+    np.testing.assert_array_equal(c8.view(np.uint64), ci.view(np.uint64))
+
+
 def test_fp8_products_exact_at_the_fp32_bound(dev):
     """Digit planes of +-16 (e4m3 0x58 / 0xD8), K = 16384, outputs of three concatenated products:
     all-positive digits give 3 K 256 = 12582912 < 2^24 exactly; random signs give every smaller sum.
