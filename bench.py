@@ -3,7 +3,9 @@
 
 `--config C1|C2|C4|C5` measures the other BASELINE configs the same way (C1: II-INT8 1024^3 one
 pass; C2: I-INT8 4096^3 automatic slices; C4: II-FP8 16384^3, phi 2; C5: I-BF16 8192 x 8192 x 65536,
-8 slices, 1% zero rows and columns); the default line is C3.
+8 slices, 1% zero rows and columns); the default line is C3. C4 runs the library's default for the
+FP8 format (the FP8 route's plan carried by INT8 residues at its width) and reports the FP8 route's
+e4m3 digit products on the FP8 matrix cores beside it (`fp8_matrix_cores`, the same C).
 
 Workload: row-major FP64 A, B with entries (U(0,1)-0.5)*exp(0.5*N(0,1)),
 the reference's evaluation generator with seed 3; Scheme II, INT8 residues, automatic moduli (<= 24),
@@ -182,8 +184,9 @@ CONFIGS = {
     "C1": ("II", "INT8", 1024, 1024, 1024, 1, 0.5, dict(reconstruction="OnePass"), INT8_PEAK_TOPS, 1024, 64),
     "C2": ("I", "INT8", 4096, 4096, 4096, 2, 1.0, dict(), INT8_PEAK_TOPS, 4096, 64),
     "C3": ("II", "INT8", 8192, 8192, 8192, 3, 0.5, dict(reconstruction="TwoPass"), INT8_PEAK_TOPS, 8192, 64),
-    # e4m3 digit products on the FP8 matrix cores (dense FP8 peak 5.0 PFLOP/s)
-    "C4": ("II", "FP8", 16384, 16384, 16384, 4, 2.0, dict(), FP8_PEAK_TFLOPS, 1024, 32),
+    # the FP8 plan carried by INT8 residues (the library's default for FP8; the FP8 route's digits on the FP8
+    # matrix cores, dense FP8 peak 5.0 PFLOP/s, are measured beside it)
+    "C4": ("II", "FP8", 16384, 16384, 16384, 4, 2.0, dict(), INT8_PEAK_TOPS, 1024, 32),
     # BF16 digits (+-32) run on the INT8 matrix cores, so the product roofline is the INT8 peak
     "C5": ("I", "BF16", 8192, 8192, 65536, 5, 4.0, dict(slices=8), INT8_PEAK_TOPS, 512, 32),
 }
@@ -303,8 +306,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        # the products' arithmetic: int8 (C5's BF16-format digits are int8 values) or e4m3 digits (C4)
-        "dtype": "fp8_e4m3" if fmt == "FP8" else "int8",
+        # the products' arithmetic: int8 (C5's BF16-format digits are int8 values, C4's FP8 plan is carried
+        # by INT8 residues)
+        "dtype": "int8",
         "data": f"synthetic: reference evaluation generator, seed {seed}, (U(0,1)-0.5)*exp({phi}*N(0,1))",
         "config": {"workload": WORKLOADS[args.config], "m": m, "n": n, "k": k, "scheme": scheme, "format": fmt,
                    "slices": info.slices, "moduli": info.moduli, "integer_bits": info.integer_bits,
@@ -319,30 +323,38 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": C3_GEMM_TRAFFIC_BYTES if (headline and info.moduli == 17) else None,
-                     "kernel": ("gemm_f8_groups_kernel<TERMS> (oz2_gemm_groups_f8)" if fmt == "FP8" else
-                                "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II"
-                                                    else "<DIAG> (oz1_gemm_diag_i8)")),
+                     "kernel": "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II"
+                                                   else "<DIAG> (oz1_gemm_diag_i8)"),
                      "launch_ms": round(gemm_ms, 4), "ops_per_launch": ev.product_ops},
     }
     if fmt == "FP8":
-        # the same exact C' at the same width carried by INT8 residues (one int8 product per modulus)
-        log("INT8 residues at the FP8 plan's width")
-        o8 = oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, max_moduli=24)
-        c8, i8, e8 = ctx.evaluate(a, b, m, n, k, o8, fixed_bits=info.integer_bits, warmup=1, repeats=3)
-        out["int8_same_width"] = {"ms_per_step": round(e8.whole_ms, 4), "moduli": i8.moduli,
-                                  "integer_bits": i8.integer_bits,
-                                  "value": round(2.0 * m * n * k / (e8.whole_ms * 1e-3) / 1e12, 3),
-                                  "identical_output": bool(np.array_equal(c8.view(np.uint64), c.view(np.uint64)))}
+        out["config"]["int8_moduli_computed"] = ev.partial_products
+        # the FP8 route's e4m3 digit products on the FP8 matrix cores: the same exact C' at the same width
+        log("FP8 route's digits on the FP8 matrix cores")
+        c8, i8, e8 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=3, fp8_matrix_cores=True)
+        if not e8.whole_checked:
+            raise SystemExit("FP8 matrix-core whole-pass replay output differs from its first pass")
+        f8_tflops = e8.product_ops / (e8.gemm_launch_ms * 1e-3) / 1e12
+        out["fp8_matrix_cores"] = {
+            "ms_per_step": round(e8.whole_ms, 4), "value": round(2.0 * m * n * k / (e8.whole_ms * 1e-3) / 1e12, 3),
+            "dtype": "fp8_e4m3", "digit_products": e8.partial_products,
+            "phases_ms": {key: round(e8.phase_ms[i], 4)
+                          for i, key in enumerate(["scale", "slice", "gemm", "compose", "recon"])},
+            "roofline": {"bound": "mfma", "achieved": round(f8_tflops, 2), "peak": FP8_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(f8_tflops / FP8_PEAK_TFLOPS, 4),
+                         "kernel": "gemm_f8_groups_kernel<TERMS> (oz2_gemm_groups_f8)",
+                         "launch_ms": round(e8.gemm_launch_ms, 4), "ops_per_launch": e8.product_ops},
+            "same_info": i8 == info,
+            "identical_output": bool(np.array_equal(c8.view(np.uint64), c.view(np.uint64)))}
         del c8
     log("native FP64 GEMM on the GPU (rocBLAS dgemm)")
     out["native_fp64_gemm"] = native_fp64_gemm(a, b, m, n, k)
-    if fmt != "FP8":
-        log("vendor int8 GEMM on one product's shape (hipBLASLt)")
-        v = vendor_int8_gemm(m, n, k)
-        if "tops" in v:
-            # the product kernel's rate per unit of int8 work next to the vendor's on the same shape
-            v["product_kernel_tops"] = round(achieved, 2)
-        out["vendor_int8_gemm"] = v
+    log("vendor int8 GEMM on one product's shape (hipBLASLt)")
+    v = vendor_int8_gemm(m, n, k)
+    if "tops" in v:
+        # the product kernel's rate per unit of int8 work next to the vendor's on the same shape
+        v["product_kernel_tops"] = round(achieved, 2)
+    out["vendor_int8_gemm"] = v
     if cpu_rows > 0:
         log(f"CPU baseline: Dot2 on {cpu_rows} rows")
         out["cpu_baseline"], hi, lo = cpu_baseline(a, b, m, n, k, cpu_rows)

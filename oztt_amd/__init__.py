@@ -83,7 +83,8 @@ class EvalStats(ctypes.Structure):
                 ("gemm_launch_ms", ctypes.c_double), ("gemm_launches", ctypes.c_int),
                 ("max_band_rows", ctypes.c_uint), ("plan_reused", ctypes.c_int), ("force_kc", ctypes.c_uint),
                 ("replay_drop_phase", ctypes.c_int), ("whole_sentinel", ctypes.c_int),
-                ("whole_steps", ctypes.c_uint * 5), ("expected_steps", ctypes.c_uint * 5)]
+                ("whole_steps", ctypes.c_uint * 5), ("expected_steps", ctypes.c_uint * 5),
+                ("fp8_matrix_cores", ctypes.c_int)]
 
     def __init__(self, *args, **kw):
         super().__init__(*args, **kw)
@@ -100,7 +101,7 @@ class Plan2(ctypes.Structure):
                 ("rS", ctypes.c_int), ("rsparse", ctypes.c_int), ("rfold_first", ctypes.c_int), ("rmaxg", ctypes.c_int),
                 ("rnprod", ctypes.c_int), ("rnplane", ctypes.c_int), ("rnout", ctypes.c_int),
                 ("rm", ctypes.c_int * 24), ("rmode", ctypes.c_int * 24), ("rmaxg_m", ctypes.c_int * 24),
-                ("rlog2M", ctypes.c_double)]
+                ("rlog2M", ctypes.c_double), ("fp8_digits", ctypes.c_int)]
 
 
 class Plan1(ctypes.Structure):
@@ -247,13 +248,15 @@ class Context:
         return c
 
     def evaluate(self, a, b, m: int, n: int, k: int, options: Options, fixed_bits: int = 0, warmup: int = 0,
-                 repeats: int = 0, max_band_rows: int = 0, force_kc: int = 0, replay_drop_phase: int = -1):
+                 repeats: int = 0, max_band_rows: int = 0, force_kc: int = 0, replay_drop_phase: int = -1,
+                 fp8_matrix_cores: bool = False):
         """GEMM under the evaluation hooks: returns (C, Info, EvalStats) with phase and whole-pass times.
         max_band_rows > 0 caps the rows of a band (row bands are otherwise used only when the problem
         does not fit in device memory); force_kc > 0 makes Scheme I with an FP32-product format
         reconstruct K block by K block with blocks of that length. replay_drop_phase >= 0 is the
         self-test of the whole-pass check: its checking replay leaves out that phase's steps, so
-        whole_checked must be 0, and nothing is timed."""
+        whole_checked must be 0, and nothing is timed. fp8_matrix_cores runs Scheme II FP8 as the FP8
+        route's e4m3 digit products on the FP8 matrix cores instead of INT8 residues at its width."""
         a, b = _f64(a), _f64(b)
         c = np.empty(m * n, dtype=np.float64)
         ev = EvalStats()
@@ -261,6 +264,7 @@ class Context:
         ev.max_band_rows = max_band_rows
         ev.force_kc = force_kc
         ev.replay_drop_phase = replay_drop_phase
+        ev.fp8_matrix_cores = int(bool(fp8_matrix_cores))
         info = self._call(a, b, c, m, n, k, options, ev)
         return c, info, ev
 
@@ -307,14 +311,15 @@ class Context:
 
 
 def plan2(a, b, M: int, N: int, K: int, fmt: Format = Format.INT8, max_moduli: int = 0,
-          reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0) -> Plan2:
-    """Scheme II planner on padded row-major A (M x K) and B (K x N): the execution set (m, S, b, ...)
-    and the route's plan of the format (rm, rS, rmode, ...)."""
+          reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0,
+          fp8_matrix_cores: bool = False) -> Plan2:
+    """Scheme II planner on padded row-major A (M x K) and B (K x N): the execution set (m, S, b, ...;
+    fp8_digits when it is the FP8 route's digit set) and the route's plan of the format (rm, rS, rmode, ...)."""
     a, b = _f64(a), _f64(b)
     out = Plan2()
     err = ctypes.create_string_buffer(2048)
     _raise(host().ozt_plan_scheme2(_ptr(a), _ptr(b), M, N, K, int(fmt), max_moduli, int(reconstruction), fixed_bits,
-                            ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
+                                   int(bool(fp8_matrix_cores)), ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
     return out
 
 

@@ -80,6 +80,7 @@ struct ozt_eval {
     int whole_sentinel;      // the checking replay rewrote the sentinel-filled output with the first pass's bits
     unsigned whole_steps[5];     // steps per phase issued by the checking replay
     unsigned expected_steps[5];  // steps per phase the plan calls for
+    int fp8_matrix_cores;        // input: Scheme II FP8 on the FP8 matrix cores (0: INT8 residues at its width)
 };
 
 struct ozt_plan2 {
@@ -92,6 +93,7 @@ struct ozt_plan2 {
     int rS, rsparse, rfold_first, rmaxg, rnprod, rnplane, rnout;
     int rm[24], rmode[24], rmaxg_m[24];
     double rlog2M;
+    int fp8_digits;  // the device computes the FP8 route's e4m3 digit products (else the residues of m[])
 };
 
 static void fill_route(const ozTTgemm::detail::ModuliSet& r, ozt_plan2* out) {
@@ -170,6 +172,19 @@ static void fill_eval(const ozTTgemm::evaluation::Settings& s, ozt_eval* evo);
 
 // C = A B for resident A and B: into the host array c (nc elements) when cm is null, else into the
 // Matrix cm. evo, when not null, runs the call under the evaluation hooks.
+// The evaluation settings a caller passed in (the inputs of ozt_eval).
+static ozTTgemm::evaluation::Settings settings_of(const ozt_eval* evo) {
+    ozTTgemm::evaluation::Settings s;
+    s.fixed_bits = evo->fixed_bits;
+    s.warmup = evo->warmup;
+    s.repeats = evo->repeats;
+    s.max_band_rows = evo->max_band_rows;
+    s.force_kc = evo->force_kc;
+    s.replay_drop_phase = evo->replay_drop_phase;
+    s.fp8_matrix_cores = evo->fp8_matrix_cores != 0;
+    return s;
+}
+
 int ozt_gemm_resident(void* ctx, void* a, void* b, double* c, std::size_t nc, void* cm, int scheme, int format,
                       unsigned slices, unsigned max_moduli, int recon, ozt_info* info, ozt_eval* evo, char* err,
                       std::size_t errlen) {
@@ -183,13 +198,7 @@ int ozt_gemm_resident(void* ctx, void* a, void* b, double* c, std::size_t nc, vo
         };
         ozTTgemm::Info i;
         if (evo) {
-            ozTTgemm::evaluation::Settings s;
-            s.fixed_bits = evo->fixed_bits;
-            s.warmup = evo->warmup;
-            s.repeats = evo->repeats;
-            s.max_band_rows = evo->max_band_rows;
-            s.force_kc = evo->force_kc;
-            s.replay_drop_phase = evo->replay_drop_phase;
+            ozTTgemm::evaluation::Settings s = settings_of(evo);
             {
                 ozTTgemm::evaluation::Scope scope(s);
                 i = run();
@@ -206,13 +215,7 @@ int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, s
                   std::size_t nc, std::size_t m, std::size_t n, std::size_t k, int scheme, int format, unsigned slices,
                   unsigned max_moduli, int recon, ozt_info* info, ozt_eval* evo, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
-        ozTTgemm::evaluation::Settings s;
-        s.fixed_bits = evo->fixed_bits;
-        s.warmup = evo->warmup;
-        s.repeats = evo->repeats;
-        s.max_band_rows = evo->max_band_rows;
-        s.force_kc = evo->force_kc;
-        s.replay_drop_phase = evo->replay_drop_phase;
+        ozTTgemm::evaluation::Settings s = settings_of(evo);
         auto* cx = static_cast<ozTTgemm::Context*>(ctx);
         ozTTgemm::Info i;
         {
@@ -243,15 +246,18 @@ static void fill_eval(const ozTTgemm::evaluation::Settings& s, ozt_eval* evo) {
 int ozt_is_available(int format) { return ozTTgemm::is_available(static_cast<ozTTgemm::Format>(format)) ? 1 : 0; }
 const char* ozt_format_name(int format) { return ozTTgemm::format_name(static_cast<ozTTgemm::Format>(format)); }
 
-// Scheme II planner on padded row-major A (M x K) and B (K x N) for `format` (INT8 or FP8).
+// Scheme II planner on padded row-major A (M x K) and B (K x N) for `format`; fp8_matrix_cores as in
+// the evaluation settings.
 int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, unsigned K, int format, unsigned max_moduli,
-              int recon, unsigned fixed_b, ozt_plan2* out, char* err, std::size_t errlen) {
+              int recon, unsigned fixed_b, int fp8_matrix_cores, ozt_plan2* out, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
         const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, static_cast<ozTTgemm::Format>(format), max_moduli,
-                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb);
+                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb,
+                                                        fp8_matrix_cores != 0);
         std::memset(out, 0, sizeof(*out));
+        out->fp8_digits = p.fp8_digits;
         out->ok = p.mo.ok;
         out->b = p.b;
         out->S = p.S;
@@ -273,7 +279,8 @@ int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, u
     });
 }
 
-// The device descriptors of a Scheme II FP8 plan (digit split, product outputs, CRT, term moduli).
+// The device descriptors of a Scheme II FP8 plan on the FP8 matrix cores (digit split, product outputs,
+// CRT, term moduli).
 int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned max_moduli,
                          int recon, unsigned fixed_b, oz2_digit_dev* dd, oz2_groups_dev* gd, oz2_crt_dev* crt,
                          unsigned char* term_modulus, char* err, std::size_t errlen) {
@@ -281,7 +288,7 @@ int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned 
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
         const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, ozTTgemm::Format::FP8, max_moduli,
-                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb);
+                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb, true);
         *crt = ozTTgemm::detail::crt_descriptor(p);
         *dd = ozTTgemm::detail::digit_descriptor(p);
         std::vector<unsigned char> tm;

@@ -397,9 +397,9 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
     if (!handle || A.device != handle || B.device != handle)
         throw std::invalid_argument("the Matrix belongs to another Context");
     // the plan of this pair and these options, if an earlier call made one (not when the
-    // evaluation hooks fix the width b)
+    // evaluation hooks fix the width b or the FP8 transport)
     evaluation::Settings* es = evaluation::active();
-    const bool cacheable = !es || es->fixed_bits == 0;
+    const bool cacheable = !es || (es->fixed_bits == 0 && !es->fp8_matrix_cores);
     std::shared_ptr<const void> plan;
     if (cacheable)
         for (std::size_t i = plans.size(); i-- > 0;) {

@@ -33,6 +33,8 @@ struct Settings {
     int replay_drop_phase = -1;  // self-test of the whole-pass check: its checking replay leaves out the
                                  // steps of this phase (so whole_checked must come out false), and
                                  // nothing is timed; -1 (the default) replays every step
+    bool fp8_matrix_cores = false;  // Scheme II FP8: the FP8 route's e4m3 digit products on the FP8 matrix
+                                    // cores instead of INT8 residues at the same width (same C)
     // outputs
     double phase_ms[PhaseCount] = {};  // device time of each phase: the average of up to 5 warm passes
                                        // after the replays (the first pass when there are none)

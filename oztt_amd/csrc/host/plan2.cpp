@@ -216,12 +216,16 @@ double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st) {
 }
 
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
-                   std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b) {
-    // FP8 plans on the reference's FP8 route (e4m3 digits). Every other format plans on the INT8 route:
-    // on MI355X their digits are int8 values (BFP8, BFP4, BFP2, TF32 have no matrix instructions of
-    // their own; BF16/FP16 run at half the INT8 rate and need about twice the products), and INT8
-    // residues are the cheapest exact int8 transport. The exact reconstruction makes the result a
-    // function of the width b alone, which the INT8 route sets the same way.
+                   std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b,
+                   bool fp8_matrix_cores) {
+    // FP8 plans on the reference's FP8 route (e4m3 digits): its moduli, width b and pass choice are the
+    // reference's. Every other format plans on the INT8 route: on MI355X their digits are int8 values
+    // (BFP8, BFP4, BFP2, TF32 have no matrix instructions of their own; BF16/FP16 run at half the INT8
+    // rate and need about twice the products), and INT8 residues are the cheapest exact int8
+    // transport. The exact reconstruction makes the result a function of the width b alone. For the
+    // same reason FP8 is computed with INT8 residues at the FP8 plan's width: the FP8 and INT8 matrix
+    // cores have the same peak, and the FP8 route needs two to three digit products per modulus
+    // where INT8 needs one per modulus of a set a few moduli larger.
     if ((int)format < 0 || (int)format > (int)Format::BFP2) throw std::invalid_argument("unknown format");
     const bool fp8 = format == Format::FP8;
     Plan2 p;
@@ -289,8 +293,18 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
                                  "raise Options::max_moduli or use a smaller K.");
     p.b = r.b;
     p.mo = r;
+    p.fp8_digits = fp8;
+    if (fp8 && !fp8_matrix_cores) {
+        // INT8 residues of the same A' and B' (the shift b - 20 (nd - 1) is the same): a set of up to
+        // 24 moduli whose window holds width b; the FP8 digits when none does (b beyond about 88 bits)
+        ModuliSet x = choose_moduli_int8(K, kMaxModuli, p.b);
+        if (x.ok && x.b == p.b) {
+            p.mo = std::move(x);
+            p.fp8_digits = false;
+        }
+    }
     p.S = (int)p.mo.m.size();
-    if (fp8 && (p.mo.nplane > OZ2_MAXPLANES || p.mo.nout > OZ2_MAXOUT))
+    if (p.fp8_digits && (p.mo.nplane > OZ2_MAXPLANES || p.mo.nout > OZ2_MAXOUT))
         throw std::runtime_error("Ozaki II: the FP8 plan needs more digit planes or outputs than the device tables hold");
     // passes (plan.hpp:245-252)
     p.recon1_log2 = p.stats.measured ? recon1_log2(r, p.b, p.stats) : -INFINITY;

@@ -66,15 +66,19 @@ struct ModuliSet {
     int maxg = 1, nprod = 0, nplane = 0, nout = 0;
 };
 
-// The plan of one Scheme II call: the moduli set of the requested format's route (`route`, which is
-// also the set the device computes with, `mo`), the width b, digits of A' and passes.
+// The plan of one Scheme II call: the moduli set of the requested format's route (`route`: what Info
+// reports and what the pass choice is made on), the set the device computes with (`mo`), the width b,
+// digits of A' and passes. `mo` is `route` except for FP8 carried by INT8 residues (fp8_digits false):
+// then `mo` is an INT8 set of the same width b, and C is the same (both sets reconstruct the exact
+// product A'B').
 struct Plan2 {
     std::uint32_t M = 0, N = 0, K = 0;  // padded dimensions
     std::uint32_t S_req = 0;
     Format format = Format::INT8;
     ModuliSet route;
     ModuliSet mo;
-    int b = 0, nd = 3, S = 0;
+    bool fp8_digits = false;  // the products are the FP8 route's e4m3 digit products (mo == route)
+    int b = 0, nd = 3, S = 0;  // S: moduli of mo
     bool two_pass = false;
     int shift() const { return b - kDigitBits * (nd - 1); }  // plan.hpp:81 oz2_shift
     OperandStats stats;
@@ -102,9 +106,12 @@ ModuliSet choose_moduli_fp8(std::uint32_t K, int num_moduli, int b_cap,
 double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st);
 
 // The whole plan (plan.hpp:258-306). fixed_b: width fixed by the caller (evaluator only).
+// fp8_matrix_cores: FP8 computes the FP8 route's e4m3 digit products on the FP8 matrix cores; otherwise
+// it is carried by INT8 residues at the FP8 plan's width whenever an INT8 set reaches that width.
 // Throws std::runtime_error when no exact configuration exists.
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
-                   std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b);
+                   std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b,
+                   bool fp8_matrix_cores = false);
 
 // Device descriptors of the plan.
 oz2_moduli_dev split_descriptor(const Plan2& p);

@@ -14,7 +14,9 @@ Columns as the reference writes them. The phase times are the library's per-phas
 the first pass; total_ms is the average uninterrupted whole pass (the paper's Total) replayed on the
 device with the inputs resident; effective_tflops = 2 n^3 / total_ms; gemm_tops uses the product
 phase; nominal_peak_percent is against the dense MI355X peak of the matrix instructions used
-(5.0 POP/s INT8, 5.0 PFLOP/s FP8). effective_bits / relative_fro compare with the Dot2 reference
+(5.0 POP/s INT8, 5.0 PFLOP/s FP8). partial_products counts the products the device ran: for Scheme II
+FP8 one per modulus of the INT8 set that carries it, or with --fp8-matrix-cores the FP8 route's digit
+products (the reference's count); moduli is the FP8 route's either way. effective_bits / relative_fro compare with the Dot2 reference
 (computed by the library's evaluator numerics), cpu_dgemm_bits the host's native FP64 GEMM (BLAS
 through numpy) the same way. Columns that describe Tenstorrent telemetry (bw: the Tensix GEMM block
 width; gemm_aiclk_mhz; start_temperature_c) are written as 0 / nan.
@@ -80,6 +82,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-reference", action="store_true", help="no Dot2 reference (and no CPU GEMM)")
     ap.add_argument("--no-cpu", action="store_true", help="no host FP64 GEMM for cpu_dgemm_bits")
     ap.add_argument("--quick", action="store_true", help="sizes 128, phi size 128, phis 0.5,2,8, 1 repeat, no warmup")
+    ap.add_argument("--fp8-matrix-cores", action="store_true",
+                    help="Scheme II FP8 as the FP8 route's e4m3 digit products on the FP8 matrix cores (by default "
+                         "INT8 residues at the FP8 plan's width carry it, with the same output)")
     args = ap.parse_args(argv)
     sizes = [int(s) for s in args.sizes.split(",")]
     phis = [float(s) for s in args.phis.split(",")]
@@ -121,7 +126,8 @@ def main(argv=None) -> int:
                 cache[key] = (a, b, hi, lo, cpu_bits)
             a, b, hi, lo, cpu_bits = cache[key]
             t0 = time.perf_counter()
-            c, info, ev = ctx.evaluate(a, b, n, n, n, o, fixed_bits=bits, warmup=warmup, repeats=max(repeats, 1))
+            c, info, ev = ctx.evaluate(a, b, n, n, n, o, fixed_bits=bits, warmup=warmup, repeats=max(repeats, 1),
+                                       fp8_matrix_cores=args.fp8_matrix_cores)
             call_ms = (time.perf_counter() - t0) * 1e3
             if not ev.whole_checked:
                 raise SystemExit("whole-pass replay output differs from the first pass")

@@ -23,19 +23,22 @@ def ctx():
 
 
 CASES = [
-    ("II-INT8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8)),
-    ("II-FP8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8)),
-    ("I-INT8", oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8)),
-    ("I-BF16", oz.Options(scheme=oz.Scheme.I, format=oz.Format.BF16, slices=6)),
+    ("II-INT8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8), False),
+    ("II-FP8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8), False),
+    ("II-FP8-cores", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8), True),
+    ("I-INT8", oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8), False),
+    ("I-BF16", oz.Options(scheme=oz.Scheme.I, format=oz.Format.BF16, slices=6), False),
 ]
 
 
-@pytest.mark.parametrize("name,opts", CASES, ids=[c[0] for c in CASES])
-def test_bands_bit_identical(ctx, name, opts):
+@pytest.mark.parametrize("name,opts,fp8_cores", CASES, ids=[c[0] for c in CASES])
+def test_bands_bit_identical(ctx, name, opts, fp8_cores):
+    """II-FP8-cores: the FP8 route's e4m3 digits on the FP8 matrix cores (A's digit planes per band)."""
     m, n, k = 1000, 384, 512
     a, b = oz.eval_inputs(11, 1.0, m * k, k * n)
-    c1, i1, e1 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=2)
-    c4, i4, e4 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=2, max_band_rows=256)
+    c1, i1, e1 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=2, fp8_matrix_cores=fp8_cores)
+    c4, i4, e4 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=2, max_band_rows=256,
+                              fp8_matrix_cores=fp8_cores)
     assert e1.gemm_launches == 1
     assert e4.gemm_launches == 4  # 1024 padded rows: 256 + 256 + 256 + 232
     assert e1.whole_checked and e4.whole_checked

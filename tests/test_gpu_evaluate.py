@@ -24,8 +24,10 @@ QUICK = {
 
 
 def test_quick_table_suite_matches_reference_records(tmp_path):
+    """With the FP8 route's digits on the FP8 matrix cores, as the reference runs them (its partial
+    product count)."""
     out = tmp_path / "results.csv"
-    assert evaluate.main(["--quick", "--suite", "table", "--output", str(out)]) == 0
+    assert evaluate.main(["--quick", "--suite", "table", "--fp8-matrix-cores", "--output", str(out)]) == 0
     rows = list(csv.DictReader(open(out)))
     assert [r["format"] for r in rows[::2]] == list(QUICK) and len(rows) == 16
     ii_bits = set()

@@ -117,10 +117,12 @@ def test_resident_checks(ctx):
     X.close()  # a Matrix may outlive its Context: it holds the GPU open until it is freed
 
 
-@pytest.mark.parametrize("name,opts", CASES[:2] + CASES[3:4], ids=["II-INT8", "II-FP8", "I-INT8"])
-def test_resident_row_bands(ctx, name, opts):
+@pytest.mark.parametrize("name,opts,fp8_cores", [c + (False,) for c in CASES[:2] + CASES[3:4]] +
+                         [("II-FP8-cores", CASES[1][1], True)], ids=["II-INT8", "II-FP8", "I-INT8", "II-FP8-cores"])
+def test_resident_row_bands(ctx, name, opts, fp8_cores):
     """Resident operands through row bands (forced by the evaluation hook max_band_rows): the band
-    loop reads A's rows from the resident copy and writes C's rows into the result."""
+    loop reads A's rows from the resident copy and writes C's rows into the result. II-FP8-cores:
+    the FP8 route's e4m3 digits on the FP8 matrix cores, against the default call's C."""
     m, n, k = 1000, 384, 512
     a, b = oz.eval_inputs(11, 1.0, m * k, k * n)
     want = np.empty(m * n)
@@ -128,6 +130,7 @@ def test_resident_row_bands(ctx, name, opts):
     A, B = ctx.upload(a, m, k), ctx.upload(b, k, n)
     ev = oz.EvalStats()
     ev.max_band_rows = 256
+    ev.fp8_matrix_cores = int(fp8_cores)
     got = np.empty(m * n)
     ctx.gemm_resident(A, B, got, opts, evaluation=ev)
     assert ev.gemm_launches == 4
@@ -135,6 +138,7 @@ def test_resident_row_bands(ctx, name, opts):
     C = oz.Matrix()
     ev2 = oz.EvalStats()
     ev2.max_band_rows = 256
+    ev2.fp8_matrix_cores = int(fp8_cores)
     ctx.gemm_resident(A, B, C, opts, evaluation=ev2)
     assert ev2.gemm_launches == 4
     np.testing.assert_array_equal(bits(ctx.download(C)), bits(want))

@@ -67,12 +67,19 @@ CASES = [("uniform", 64, 64, 64), ("nonnegative", 3, 5, 7), ("scaled", 65, 67, 9
          ("largest-maximum", 1, 1, 1), ("uniform", 5056, 64, 32)]
 
 
-@pytest.mark.parametrize("fmt", [oz.Format.INT8, oz.Format.FP8])
+@pytest.mark.parametrize("fmt,fp8_cores", [(oz.Format.INT8, False), (oz.Format.FP8, False), (oz.Format.FP8, True)],
+                         ids=["INT8", "FP8", "FP8-cores"])
 @pytest.mark.parametrize("mode,m,n,k", CASES)
-def test_reference_correctness_cases(ctx, mode, m, n, k, fmt):
+def test_reference_correctness_cases(ctx, mode, m, n, k, fmt, fp8_cores):
+    """FP8-cores: the FP8 route's e4m3 digits on the FP8 matrix cores (FP8 runs INT8 residues at its
+    plan's width otherwise)."""
     a, b = pattern(mode, m, n, k)
-    c = np.full(m * n, 123.0)
-    info = ctx.gemm(a, b, c, m, n, k, oz.Options(scheme=oz.Scheme.II, format=fmt))
+    o = oz.Options(scheme=oz.Scheme.II, format=fmt)
+    if fp8_cores:
+        c, info, _ = ctx.evaluate(a, b, m, n, k, o, fp8_matrix_cores=True)
+    else:
+        c = np.full(m * n, 123.0)
+        info = ctx.gemm(a, b, c, m, n, k, o)
     assert info.format == fmt
     assert np.all(np.isfinite(c))
     err = ref_error(a, b, c, m, n, k)

@@ -6,8 +6,10 @@ cores, composition in the product epilogue, exact CRT.
    digit products, every uint16 term is coef * P mod m; the reference's published FP8 output hash
    (quick.csv:11, 20046e5bb3816cbb) follows from the GPU terms through the oracle's restatement of
    the reference reconstruction.
-2. The public API: the FP8 output is bit-identical to the INT8 output at the same width b (both
-   reconstruct the exact C' = A'B'), Info reports the FP8 route, accuracy on the C4 generator.
+2. The public API: FP8 runs INT8 residues at the FP8 plan's width by default and the e4m3 digits on
+   the FP8 matrix cores when the evaluation settings ask for them. Both outputs are bit-identical to
+   the INT8 output at the same width b (all reconstruct the exact C' = A'B'), Info reports the FP8
+   route either way, accuracy on the C4 generator.
 """
 import numpy as np
 import pytest
@@ -37,22 +39,31 @@ def test_fp8_quick_case_matches_int8_bits(ctx):
     n = 128
     a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
     one = oz.Reconstruction.OnePass
-    c8, i8, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.FP8, max_moduli=14, reconstruction=one), fixed_bits=54)
+    o8 = opts(oz.Format.FP8, max_moduli=14, reconstruction=one)
+    c8, i8, _ = ctx.evaluate(a, b, n, n, n, o8, fixed_bits=54, fp8_matrix_cores=True)
+    cr, ir, _ = ctx.evaluate(a, b, n, n, n, o8, fixed_bits=54)
     ci, ii, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.INT8, max_moduli=16, reconstruction=one), fixed_bits=54)
     assert i8.format == oz.Format.FP8 and i8.moduli == 12 and i8.integer_bits == 54
+    assert ir == i8
     assert ii.moduli == 15 and ii.integer_bits == 54
     np.testing.assert_array_equal(c8.view(np.uint64), ci.view(np.uint64))
+    np.testing.assert_array_equal(cr.view(np.uint64), ci.view(np.uint64))
 
 
 @pytest.mark.parametrize("n", [1024, 2048])
 def test_fp8_wide_range_auto(ctx, oracle, n):
-    """C4 generator (seed 4, phi 2) at reduced size: automatic b, FP8 route moduli, accuracy."""
+    """C4 generator (seed 4, phi 2) at reduced size: automatic b, FP8 route moduli, accuracy; the e4m3
+    digits on the FP8 matrix cores and the default INT8 residues give the same bits."""
     a, b = oz.eval_inputs(4, 2.0, n * n, n * n)
     p = oz.plan2(a, b, n, n, n, oz.Format.FP8)
+    assert not p.fp8_digits
     c = np.empty(n * n)
     info = ctx.gemm(a, b, c, n, n, n, opts(oz.Format.FP8))
     assert info.format == oz.Format.FP8 and info.moduli == p.rS and info.integer_bits == p.b
     assert info.reconstruction_passes == (2 if p.two_pass else 1)
+    cf, inf, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.FP8), fp8_matrix_cores=True)
+    assert inf == info
+    np.testing.assert_array_equal(c.view(np.uint64), cf.view(np.uint64))
     ci = np.empty(n * n)
     ii = ctx.gemm(a, b, ci, n, n, n, opts(oz.Format.INT8))
     if ii.integer_bits == info.integer_bits:

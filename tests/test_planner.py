@@ -213,7 +213,7 @@ FP8_PHI = [(0.0, 53, 12), (1.0, 57, 12), (2.0, 59, 12), (4.0, 61, 13)]
 @pytest.mark.parametrize("phi,b,S", [FP8_PHI[i] for i in (0, 3)])
 def test_fp8_auto_precision_records(phi, b, S):
     """The FP8 plan's width b equals the record; its set with the research planner's measured window has the
-    recorded size; the execution set is the route's FP8 set."""
+    recorded size; on the FP8 matrix cores the execution set is the route's FP8 set."""
     n = 4096
     a, bb = oz.eval_inputs(7, phi, n * n, n * n)
     p = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass)
@@ -223,7 +223,47 @@ def test_fp8_auto_precision_records(phi, b, S):
     wlog2 = math.log2(p.wA * p.wB * max(f, 1.001))
     research = oz.choose_moduli_fp8(n, 24, b, wlog2)
     assert research.b == b and research.rS == S
+    assert not p.fp8_digits  # carried by INT8 residues by default
+    p = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass, fp8_matrix_cores=True)
+    assert p.fp8_digits and p.b == b
     assert p.S == p.rS and [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
+
+
+@pytest.mark.parametrize("K,b", [(16384, 60), (4096, 54), (1024, 70)])
+def test_fp8_carried_by_int8_residues(K, b):
+    """FP8 keeps the FP8 route's plan (moduli of Info, width b, passes) and computes with an INT8 set of the
+    same width: pairwise coprime moduli <= 255 whose window holds K 2^(2b) < M/2. Its int32 products are
+    exact (K floor(m/2)^2 <= 2^31 - 1)."""
+    M = N = 64
+    a, bb = oz.eval_inputs(4, 2.0, M * K, K * N)
+    kw = dict(fixed_bits=b, max_moduli=24, reconstruction=oz.Reconstruction.OnePass)
+    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, **kw)
+    f = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fp8_matrix_cores=True, **kw)
+    i8 = oz.plan2(a, bb, M, N, K, oz.Format.INT8, fixed_bits=b, max_moduli=24,
+                  reconstruction=oz.Reconstruction.OnePass)
+    assert f.fp8_digits and not p.fp8_digits and not i8.fp8_digits
+    # the route (what Info reports) is the FP8 route's either way
+    assert p.rS == f.rS and [p.rm[i] for i in range(p.rS)] == [f.rm[i] for i in range(f.rS)]
+    assert p.b == f.b == b and p.nd == f.nd and p.two_pass == f.two_pass
+    # the execution set is the INT8 route's set at that width
+    ms = [p.m[i] for i in range(p.S)]
+    assert ms == [i8.m[i] for i in range(i8.S)] and i8.b == b
+    assert max(ms) <= 255 and all(math.gcd(x, y) == 1 for i, x in enumerate(ms) for y in ms[i + 1:])
+    assert sum(math.log2(x) for x in ms) >= 2 * b + 1 + math.log2(K)
+    assert all(K * (x // 2) ** 2 <= 2**31 - 1 for x in ms)
+
+
+def test_fp8_beyond_the_int8_width_keeps_its_digits():
+    """At K = 4096, 24 moduli <= 255 hold a width of at most 85 bits and the FP8 route's up to 100; a wider
+    FP8 plan runs its own digits."""
+    M = N = 64
+    K = 4096
+    a, bb = oz.eval_inputs(4, 2.0, M * K, K * N)
+    assert oz.choose_moduli_int8(K, 24, 90).b == 85
+    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=90, max_moduli=24)
+    assert p.fp8_digits and p.b == 90 and p.S == p.rS
+    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=85, max_moduli=24)
+    assert not p.fp8_digits and p.b == 85
 
 
 def test_fp8_composition_coefficients_kat():
