@@ -630,6 +630,30 @@ void oz1_scale_w(int radix, int L, uint32_t& Whi, uint32_t& Wlo, int32_t& qw) {
     qw = e - 64;
 }
 
+// A8 for any modulus up to 4096: the residues of A' as values of type T, planes[s][r][c].
+template <class T>
+static void residue_planes(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
+                           const int* m, T* planes) {
+    std::vector<float> rinv(S), cw((size_t)S * 4);
+    for (int s = 0; s < S; s++) {
+        const __float128 q = (__float128)1 / (__float128)m[s];
+        rinv[s] = (float)(double)q;
+        for (int j = 0; j < 4; j++) cw[(size_t)s * 4 + j] = pow2mod(20 * (j + 1), m[s]);
+    }
+    const size_t plane = (size_t)rows * cols;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        float dig[5];
+        for (int c = 0; c < cols; c++) {
+            make_digits(X[(size_t)r * ld + c], delta_of(delta, mode, r, c), nd, dig);
+            for (int s = 0; s < S; s++) {
+                const float v = residue(dig, nd, (float)m[s], rinv[s], &cw[(size_t)s * 4]);
+                planes[(size_t)s * plane + (size_t)r * cols + c] = (T)(int)v;
+            }
+        }
+    }
+}
+
 extern "C" {
 
 uint64_t orc_hash_f64(const double* c, size_t n) {
@@ -728,24 +752,12 @@ void orc_oz2_digits(const double* X, int rows, int cols, int ld, int mode, const
 
 void orc_oz2_residues(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
                       const int* m, int8_t* planes) {
-    std::vector<float> rinv(S), cw((size_t)S * 4);
-    for (int s = 0; s < S; s++) {
-        const __float128 q = (__float128)1 / (__float128)m[s];
-        rinv[s] = (float)(double)q;
-        for (int j = 0; j < 4; j++) cw[(size_t)s * 4 + j] = pow2mod(20 * (j + 1), m[s]);
-    }
-    const size_t plane = (size_t)rows * cols;
-#pragma omp parallel for schedule(static)
-    for (int r = 0; r < rows; r++) {
-        float dig[5];
-        for (int c = 0; c < cols; c++) {
-            make_digits(X[(size_t)r * ld + c], delta_of(delta, mode, r, c), nd, dig);
-            for (int s = 0; s < S; s++) {
-                const float v = residue(dig, nd, (float)m[s], rinv[s], &cw[(size_t)s * 4]);
-                planes[(size_t)s * plane + (size_t)r * cols + c] = (int8_t)(int)v;
-            }
-        }
-    }
+    residue_planes(X, rows, cols, ld, mode, delta, nd, S, m, planes);
+}
+
+void orc_oz2_residues16(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
+                        const int* m, int16_t* planes) {
+    residue_planes(X, rows, cols, ld, mode, delta, nd, S, m, planes);
 }
 
 // modslice_digit.cpp:195-218 + sparse_fix.h:53-73: the digits of residue r (d[0] = l, d[1] = h,

@@ -48,6 +48,9 @@ void orc_oz2_digits(const double* X, int rows, int cols, int ld, int mode, const
 // A8: residues A' mod m_s for S moduli, planes[s][r][c] (digits.h:165-179, modslice_int8.cpp:60-95).
 void orc_oz2_residues(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
                       const int* m, int8_t* planes);
+// The same residues as int16 values, for the moduli of the digit routes (up to 4096).
+void orc_oz2_residues16(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
+                        const int* m, int16_t* planes);
 // A18: the residues split into digit planes (modslice_digit.cpp:195-218, sparse_fix.h:53-73):
 // per modulus s with digit radix q[s] and mode xmode[s] (0 rounded, 1 Karatsuba, 2 sparse square),
 // planes l, h (and s = h + l for Karatsuba) as int8 values, planes[p][r][c], moduli in order.

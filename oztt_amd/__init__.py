@@ -101,7 +101,7 @@ class Plan2(ctypes.Structure):
                 ("rS", ctypes.c_int), ("rsparse", ctypes.c_int), ("rfold_first", ctypes.c_int), ("rmaxg", ctypes.c_int),
                 ("rnprod", ctypes.c_int), ("rnplane", ctypes.c_int), ("rnout", ctypes.c_int),
                 ("rm", ctypes.c_int * 24), ("rmode", ctypes.c_int * 24), ("rmaxg_m", ctypes.c_int * 24),
-                ("rlog2M", ctypes.c_double), ("fp8_digits", ctypes.c_int)]
+                ("rlog2M", ctypes.c_double), ("fp8_digits", ctypes.c_int), ("rmodel_set", ctypes.c_int)]
 
 
 class Plan1(ctypes.Structure):
@@ -363,6 +363,16 @@ def plan1(a, b, M: int, N: int, K: int, slices: int = 0, fmt: Format = Format.IN
 def choose_moduli_int8(K: int, num_moduli: int, b_cap: int) -> Plan2:
     out = Plan2()
     host().ozt_choose_moduli_int8(K, num_moduli, b_cap, ctypes.byref(out))
+    return out
+
+
+def choose_moduli_route(fmt: Format, M: int, N: int, K: int, num_moduli: int, b_cap: int) -> Plan2:
+    """Moduli selection on the digit route of a format other than INT8 (route fields r*; rmodel_set when the
+    stage-time model chose the set). M and N feed only the model's memory estimate."""
+    out = Plan2()
+    err = ctypes.create_string_buffer(2048)
+    _raise(host().ozt_choose_moduli_route(int(fmt), M, N, K, num_moduli, b_cap, ctypes.c_double(0.0),
+                                          ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
     return out
 
 

@@ -47,7 +47,7 @@ HIP_SOURCES = {
 }
 HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
               "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{CSRC / 'host'}"]
-HOST_SOURCES = ["context.cpp", "dispatch.cpp", "norm.cpp", "pipeline.cpp", "plan1.cpp", "plan2.cpp", "route_fp8.cpp", "ozaki1.cpp",
+HOST_SOURCES = ["context.cpp", "dispatch.cpp", "norm.cpp", "pipeline.cpp", "plan1.cpp", "plan2.cpp", "route_digits.cpp", "ozaki1.cpp",
                 "ozaki2.cpp", "evaluation.cpp", "capi.cpp"]
 
 

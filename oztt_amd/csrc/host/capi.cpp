@@ -94,6 +94,7 @@ struct ozt_plan2 {
     int rm[24], rmode[24], rmaxg_m[24];
     double rlog2M;
     int fp8_digits;  // the device computes the FP8 route's e4m3 digit products (else the residues of m[])
+    int rmodel_set;  // the route's set was chosen by the stage-time model (not from the table)
 };
 
 static void fill_route(const ozTTgemm::detail::ModuliSet& r, ozt_plan2* out) {
@@ -110,6 +111,7 @@ static void fill_route(const ozTTgemm::detail::ModuliSet& r, ozt_plan2* out) {
         out->rmaxg_m[s] = s < (int)r.maxg_m.size() ? r.maxg_m[s] : 1;
     }
     out->rlog2M = r.log2M;
+    out->rmodel_set = r.model_set;
 }
 
 int ozt_context_new(int device_id, const char* kernel_dir, void** out, char* err, std::size_t errlen) {
@@ -297,10 +299,30 @@ int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned 
     });
 }
 
+// Moduli selection alone on the digit route of `format` (not INT8; no input statistics); M and N feed
+// the stage-time model's memory estimate; window_log2 <= 0 selects log2 K.
+int ozt_choose_moduli_route(int format, unsigned M, unsigned N, unsigned K, int num_moduli, int b_cap,
+                            double window_log2, ozt_plan2* out, char* err, std::size_t errlen) {
+    return guarded(err, errlen, [&] {
+        const auto mo = ozTTgemm::detail::choose_moduli_digits(
+            static_cast<ozTTgemm::Format>(format), M, N, K, num_moduli, b_cap,
+            window_log2 > 0 ? window_log2 : std::numeric_limits<double>::quiet_NaN());
+        std::memset(out, 0, sizeof(*out));
+        out->ok = mo.ok;
+        out->b = mo.b;
+        out->S = (int)mo.m.size();
+        out->m_cap = mo.m_cap;
+        for (int s = 0; s < out->S && s < 24; s++) out->m[s] = mo.m[s];
+        out->log2M = mo.log2M;
+        fill_route(mo, out);
+    });
+}
+
 // FP8-route moduli selection alone (no input statistics); window_log2 <= 0 selects log2 K.
 int ozt_choose_moduli_fp8(unsigned K, int num_moduli, int b_cap, double window_log2, ozt_plan2* out) {
-    const auto mo = ozTTgemm::detail::choose_moduli_fp8(
-        K, num_moduli, b_cap, window_log2 > 0 ? window_log2 : std::numeric_limits<double>::quiet_NaN());
+    const auto mo = ozTTgemm::detail::choose_moduli_digits(
+        ozTTgemm::Format::FP8, K, K, K, num_moduli, b_cap,
+        window_log2 > 0 ? window_log2 : std::numeric_limits<double>::quiet_NaN());
     std::memset(out, 0, sizeof(*out));
     out->ok = mo.ok;
     out->b = mo.b;

@@ -218,16 +218,16 @@ double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st) {
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
                    std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b,
                    bool fp8_matrix_cores) {
-    // FP8 plans on the reference's FP8 route (e4m3 digits): its moduli, width b and pass choice are the
-    // reference's. Every other format plans on the INT8 route: on MI355X their digits are int8 values
-    // (BFP8, BFP4, BFP2, TF32 have no matrix instructions of their own; BF16/FP16 run at half the INT8
-    // rate and need about twice the products), and INT8 residues are the cheapest exact int8
-    // transport. The exact reconstruction makes the result a function of the width b alone. For the
-    // same reason FP8 is computed with INT8 residues at the FP8 plan's width: the FP8 and INT8 matrix
-    // cores have the same peak, and the FP8 route needs two to three digit products per modulus
-    // where INT8 needs one per modulus of a set a few moduli larger.
+    // Every format plans on its own route as the reference does (INT8 residues, or the FP8, TF32, BF16,
+    // FP16, BFP8, BFP4 or BFP2 digit route): its moduli, width b and pass choice are the reference's
+    // and are what Info reports. The products then run on INT8 residues of the same A' and B' at that
+    // width b for every format: on MI355X the digits of the other formats are int8 values anyway
+    // (BFP8, BFP4, BFP2 and TF32 have no matrix instructions of their own; BF16/FP16 run at half the
+    // INT8 rate; FP8 runs at the INT8 rate) and the digit routes need two to four digit products per
+    // modulus where INT8 needs one per modulus of a set a few moduli larger. The exact reconstruction
+    // makes C a function of the width b alone, so the output is the same whichever set computes it.
     if ((int)format < 0 || (int)format > (int)Format::BFP2) throw std::invalid_argument("unknown format");
-    const bool fp8 = format == Format::FP8;
+    const bool int8 = format == Format::INT8, fp8 = format == Format::FP8;
     Plan2 p;
     p.M = M;
     p.N = N;
@@ -242,32 +242,11 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
         b_cap = precision_cap(p.stats);
     }
     // limit on the number of moduli (plan.hpp:281): the caller's, else the route's default with a fixed
-    // width (16 for INT8, 14 for FP8; split.hpp:73-76), else 24
-    // For the formats carried by INT8 residues, a moduli limit counts the moduli of the format's own route
-    // (residues of up to 12 bits there, 8 here; checked below): the INT8 set takes as many as the width
-    // needs (<= 24).
-    const bool transported = !fp8 && format != Format::INT8;
-    if (transported)
-        p.S_req = (std::uint32_t)kMaxModuli;
-    else
-        p.S_req = max_moduli ? max_moduli : (b_fixed ? (fp8 ? 14u : 16u) : (std::uint32_t)kMaxModuli);
-    if (transported && max_moduli) {
-        // The caller's limit applies to the format's own route in the reference, whose moduli are at
-        // most the route's cap (split.hpp:86-106: 4096 for TF32, BF16, FP16 and BFP8; 3375 for BFP4;
-        // 243 for BFP2). That route's selection (a stage-time model of another device) is not
-        // restated, but a limit under which even max_moduli moduli at the cap cannot hold the CRT
-        // window log2 M >= 2b + 1 + log2 K of the smallest admissible width (53 bits, or the fixed
-        // width) fails there for certain; it is rejected here with the reference's error.
-        const double cap = format == Format::BFP2 ? 243.0 : format == Format::BFP4 ? 3375.0 : 4096.0;
-        const int width = b_fixed ? b_cap : kTargetBits;
-        if (max_moduli * std::log2(cap) < 2.0 * width + 1.0 + std::log2((double)K))
-            throw std::runtime_error("Ozaki II: the available moduli do not cover the CRT window for the padded inner "
-                                     "dimension K=" +
-                                     std::to_string(K) + ". The limit of " + std::to_string(max_moduli) +
-                                     " moduli is too small; raise Options::max_moduli.");
-    }
+    // width (16 for INT8, 14 for FP8, 11 for TF32, 24 otherwise; split.hpp:73-98), else 24
+    p.S_req = max_moduli ? max_moduli : (b_fixed ? default_moduli(format) : (std::uint32_t)kMaxModuli);
     if (b_fixed && passes == Reconstruction::Automatic) p.stats = measure_stats(A, B, M, N, K);
-    p.route = fp8 ? choose_moduli_fp8(K, (int)p.S_req, b_cap) : choose_moduli_int8(K, (int)p.S_req, b_cap);
+    p.route = int8 ? choose_moduli_int8(K, (int)p.S_req, b_cap)
+                   : choose_moduli_digits(format, M, N, K, (int)p.S_req, b_cap);
     const ModuliSet& r = p.route;
     if (!r.ok) {
         if (!r.acc_ok)
@@ -294,13 +273,22 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
     p.b = r.b;
     p.mo = r;
     p.fp8_digits = fp8;
-    if (fp8 && !fp8_matrix_cores) {
+    if (!int8 && !(fp8 && fp8_matrix_cores)) {
         // INT8 residues of the same A' and B' (the shift b - 20 (nd - 1) is the same): a set of up to
-        // 24 moduli whose window holds width b; the FP8 digits when none does (b beyond about 88 bits)
+        // 24 moduli whose window holds width b
         ModuliSet x = choose_moduli_int8(K, kMaxModuli, p.b);
         if (x.ok && x.b == p.b) {
             p.mo = std::move(x);
             p.fp8_digits = false;
+        } else if (!fp8) {
+            // a width beyond what 24 INT8 moduli hold (about 85 bits), which only extreme inputs or a
+            // fixed width ask for: FP8 keeps its own digits; the other formats run the widest INT8 plan,
+            // and Info reports that plan
+            p.route = choose_moduli_int8(K, kMaxModuli, b_cap);
+            if (!p.route.ok) throw std::runtime_error("Ozaki II: no INT8 moduli set covers the CRT window for K=" +
+                                                      std::to_string(K));
+            p.mo = p.route;
+            p.b = p.route.b;
         }
     }
     p.S = (int)p.mo.m.size();
@@ -392,7 +380,7 @@ oz2_digit_dev digit_descriptor(const Plan2& p) {
         const int mode = p.mo.mode[s];
         // digit-making modes of the slicer (split.hpp:218-227 oz2_xmode): rounded digits for the square
         // and wide methods, Karatsuba, sparse square
-        d.xmode[s] = mode == kFp8SplitKar ? 1 : (mode == kFp8SplitSqs ? 2 : 0);
+        d.xmode[s] = mode == kSplitKar ? 1 : (mode == kSplitSqs ? 2 : 0);
         d.q[s] = (float)p.mo.q[s];
         d.qinv[s] = 1.0f / (float)p.mo.q[s];  // stages.hpp:223
     }

@@ -35,9 +35,10 @@ struct OperandStats {
     bool measured = false;
 };
 
-// Carrying methods of a modulus on the FP8 route (split.hpp:176-214 OZ2_SPLIT_*): square modulus with
-// balanced digits (3 products), radix-16 Karatsuba (3), wide two-digit (4), square with sparse digits (3).
-inline constexpr int kFp8SplitSq = 0, kFp8SplitKar = 1, kFp8SplitWide = 2, kFp8SplitSqs = 4;
+// Carrying methods of a modulus on the digit routes (split.hpp:176-214 OZ2_SPLIT_*): square modulus
+// with balanced digits (3 products), Karatsuba (3), wide two-digit (4), n balanced digits (n^2, or
+// n(n+1)/2 when m divides the digit cap), square with sparse digits (3), one digit (1).
+inline constexpr int kSplitSq = 0, kSplitKar = 1, kSplitWide = 2, kSplitBal = 3, kSplitSqs = 4, kSplitOne = 5;
 
 // One product output of the FP8 route (split.hpp:628-661 oz2_product_groups): the sum of npairs
 // digit products over K, A digit plane a[t] times B digit plane b[t] (global plane indices, the
@@ -58,11 +59,12 @@ struct ModuliSet {
     double log2M = 0;
     int m_cap = 0, ncand = 0;
     std::string acc_fail;  // first failed accumulation condition (empty when all hold)
-    // FP8 route only
-    bool fp8 = false, sparse = false, fold_first = false;
+    // digit routes only (every format but INT8)
+    bool digits = false, sparse = false, fold_first = false;
+    bool model_set = false;         // chosen by the stage-time model (awe.hpp), not from the table
     std::vector<int> mode, maxg_m;  // carrying method and concatenation bound per modulus
     std::vector<int> q;             // digit radix per modulus
-    std::vector<Fp8Output> outputs; // product outputs in the reference's order (modulus by modulus)
+    std::vector<Fp8Output> outputs; // FP8: product outputs in the reference's order (modulus by modulus)
     int maxg = 1, nprod = 0, nplane = 0, nout = 0;
 };
 
@@ -96,11 +98,16 @@ int precision_cap(const OperandStats& st);
 
 // Moduli selection for the INT8 path (moduli.hpp:719-769 with the INT8 route of split.hpp:73).
 ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap);
-// Moduli selection for the FP8 route (moduli.hpp:719-769 with OZ2_ROUTE_FP8, split.hpp:72-76). The CRT
-// window is log2 K (the library's rule); window_log2 replaces it (used to restate the research planner
-// that wrote the reference's accuracy logs, which measured the window from the input).
-ModuliSet choose_moduli_fp8(std::uint32_t K, int num_moduli, int b_cap,
-                            double window_log2 = std::numeric_limits<double>::quiet_NaN());
+// Moduli selection on the digit route of a format other than INT8 (moduli.hpp:719-769 with the format's
+// row of OZ2_ROUTES, split.hpp:66-146): the table selection for FP8 and TF32, the stage-time model's
+// set (awe.hpp) for BF16, FP16, BFP8, BFP4 and BFP2. M and N feed only the model's memory estimate.
+// The CRT window is log2 K (the library's rule); window_log2 replaces it (used to restate the research
+// planner that wrote the reference's accuracy logs, which measured the window from the input).
+ModuliSet choose_moduli_digits(Format format, std::uint32_t M, std::uint32_t N, std::uint32_t K, int num_moduli,
+                               int b_cap, double window_log2 = std::numeric_limits<double>::quiet_NaN());
+// The limit on the number of moduli of a format's route when the caller fixes the width b and gives
+// no max_moduli (Oz2Route::def_s: 16 for INT8, 14 for FP8, 11 for TF32, 24 otherwise).
+std::uint32_t default_moduli(Format format);
 
 // log2 of the expected relative error of one reconstruction pass (auto_precision.hpp:128-139).
 double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st);

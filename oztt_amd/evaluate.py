@@ -14,9 +14,10 @@ Columns as the reference writes them. The phase times are the library's per-phas
 the first pass; total_ms is the average uninterrupted whole pass (the paper's Total) replayed on the
 device with the inputs resident; effective_tflops = 2 n^3 / total_ms; gemm_tops uses the product
 phase; nominal_peak_percent is against the dense MI355X peak of the matrix instructions used
-(5.0 POP/s INT8, 5.0 PFLOP/s FP8). partial_products counts the products the device ran: for Scheme II
-FP8 one per modulus of the INT8 set that carries it, or with --fp8-matrix-cores the FP8 route's digit
-products (the reference's count); moduli is the FP8 route's either way. effective_bits / relative_fro compare with the Dot2 reference
+(5.0 POP/s INT8, 5.0 PFLOP/s FP8). partial_products counts the products the device ran: for the
+Scheme II formats other than INT8 one per modulus of the INT8 set that carries the format's width,
+or for FP8 with --fp8-matrix-cores the FP8 route's digit products (the reference's count); moduli is
+the format's own route's (the reference's) either way. effective_bits / relative_fro compare with the Dot2 reference
 (computed by the library's evaluator numerics), cpu_dgemm_bits the host's native FP64 GEMM (BLAS
 through numpy) the same way. Columns that describe Tenstorrent telemetry (bw: the Tensix GEMM block
 width; gemm_aiclk_mhz; start_temperature_c) are written as 0 / nan.

@@ -68,11 +68,14 @@ class Oracle:
         return out.reshape(rows, cols, nd)
 
     def residues(self, X, rows, cols, mode, delta, nd, moduli):
+        """Symmetric residues of A' for INT8 moduli (<= 255), int8, shape (S, rows, cols); moduli above 255
+        (the digit routes) come back as int16."""
         X = np.ascontiguousarray(X, dtype=np.float64)
         m = np.array(moduli, dtype=np.int32)
-        out = np.empty((len(moduli), rows, cols), dtype=np.int8)
-        self.lib.orc_oz2_residues(P(X), rows, cols, cols, mode, P(np.ascontiguousarray(delta, np.int32)), nd, len(moduli),
-                                  P(m), P(out))
+        wide = int(m.max()) > 255
+        out = np.empty((len(moduli), rows, cols), dtype=np.int16 if wide else np.int8)
+        fn = self.lib.orc_oz2_residues16 if wide else self.lib.orc_oz2_residues
+        fn(P(X), rows, cols, cols, mode, P(np.ascontiguousarray(delta, np.int32)), nd, len(moduli), P(m), P(out))
         return out
 
     def digit_planes(self, X, rows, cols, mode, delta, nd, moduli, q, xmode):

@@ -1,7 +1,8 @@
 """The evaluator (python -m oztt_amd.evaluate) against the reference's validated quick run
 (tools/validated/quick.csv:2-17, values copied into QUICK below): Scheme I outputs are the
-reference's bit for bit (hash, effective bits, relative error); Scheme II FP8 and INT8 plan the
-reference's moduli and partial products; every Scheme II output is the exact rounding at b = 54."""
+reference's bit for bit (hash, effective bits, relative error); every Scheme II format plans the
+reference's moduli (Info), FP8 on the FP8 matrix cores and INT8 run the reference's partial products
+and the others the 15 INT8 products of b = 54; every Scheme II output is the exact rounding at b = 54."""
 import csv
 
 import pytest
@@ -10,16 +11,17 @@ from oztt_amd import evaluate
 
 pytestmark = pytest.mark.gpu
 
-# format: (I hash, I effective bits, I relative Frobenius error, I partial products, II moduli, II products)
+# format: (I hash, I effective bits, I relative Frobenius error, I partial products, II moduli, II products); the
+# II products of the formats carried by INT8 residues are the 15 int8 products the device runs at b = 54
 QUICK = {
-    "BF16": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, None, None),
-    "FP16": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, None, None),
-    "TF32": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, None, None),
-    "BFP8": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, None, None),
+    "BF16": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, 12, 15),
+    "FP16": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, 11, 15),
+    "TF32": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, 11, 15),
+    "BFP8": ("be6558fa9f435fa0", "54.2420686589", "4.69364573273e-17", 55, 12, 15),
     "FP8": ("4d24add106258287", "54.2417946941", "4.69453713108e-17", 78, 12, 36),
     "INT8": ("6c9693442bfc11b0", "54.243846521", "4.68786522126e-17", 36, 15, 15),
-    "BFP4": ("f353dbd6b57f8b99", "54.2426979466", "4.69159886276e-17", 136, None, None),
-    "BFP2": ("13cd8e69edca2911", "54.2388822441", "4.70402383076e-17", 1770, None, None),
+    "BFP4": ("f353dbd6b57f8b99", "54.2426979466", "4.69159886276e-17", 136, 14, 15),
+    "BFP2": ("13cd8e69edca2911", "54.2388822441", "4.70402383076e-17", 1770, 18, 15),
 }
 
 

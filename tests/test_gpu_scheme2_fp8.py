@@ -220,17 +220,18 @@ def test_fp8_gemm_rejects_inexact_bound(dev):
 @pytest.mark.parametrize("fmt", [oz.Format.BFP8, oz.Format.BF16, oz.Format.FP16, oz.Format.TF32, oz.Format.BFP4,
                                  oz.Format.BFP2])
 def test_other_formats_run_int8_residues(ctx, fmt):
-    """Scheme II with the formats that have no e4m3 route here: INT8 residues at the same width, so the
-    output is bit-identical to Format::INT8; Info reports the requested format."""
+    """Scheme II with BF16, FP16, TF32, BFP8, BFP4, BFP2: the format's own route plans (Info reports its
+    moduli, width and passes, as the reference's), INT8 residues at that width compute, so the output
+    is bit-identical to Format::INT8 at the same width."""
     n = 256
     a, b = oz.eval_inputs(5, 1.0, n * n, n * n)
+    p = oz.plan2(a, b, n, n, n, fmt)
     c = np.empty(n * n)
     info = ctx.gemm(a, b, c, n, n, n, opts(fmt))
-    ci = np.empty(n * n)
-    ii = ctx.gemm(a, b, ci, n, n, n, opts(oz.Format.INT8))
     assert info.format == fmt and info.scheme == oz.Scheme.II
-    assert (info.moduli, info.integer_bits, info.reconstruction_passes) == (ii.moduli, ii.integer_bits,
-                                                                              ii.reconstruction_passes)
+    assert (info.moduli, info.integer_bits, info.reconstruction_passes) == (p.rS, p.b, 2 if p.two_pass else 1)
+    ci, ii, ev = ctx.evaluate(a, b, n, n, n, opts(oz.Format.INT8, max_moduli=24), fixed_bits=info.integer_bits)
+    assert ii.integer_bits == info.integer_bits and ev.partial_products == p.S
     np.testing.assert_array_equal(c.view(np.uint64), ci.view(np.uint64))
 
 

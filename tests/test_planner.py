@@ -303,26 +303,87 @@ def test_fp8_rejects_k_beyond_exact_fp32():
     assert p.ok and p.b == 54
 
 
-def test_moduli_limit_of_transported_formats():
-    """Formats carried by INT8 residues: Options.max_moduli bounds the format's own route. A limit under
-    which even that many moduli at the route's cap (4096 for BF16/FP16/TF32/BFP8, 3375 for BFP4, 243 for
-    BFP2; reference split.hpp:86-106) cannot hold the CRT window of 53 bits is rejected with the
-    reference's runtime error (tests/correctness.cpp:291-300 uses max_moduli = 2); a feasible limit runs
-    the INT8 set the width needs."""
+def test_moduli_limit_of_digit_routes():
+    """Options.max_moduli bounds the format's own route (plan.hpp:281), as in the reference: a limit too
+    small for the 53-bit window fails with runtime_error (tests/correctness.cpp:291-300 uses
+    max_moduli = 2); a feasible limit is kept by the route's set; the evaluator's fixed width 54 with
+    TF32's limit of 11 holds (evaluate.cpp:163-177)."""
     n = 128
     a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
     for fmt in (oz.Format.BF16, oz.Format.FP16, oz.Format.TF32, oz.Format.BFP8, oz.Format.BFP4, oz.Format.BFP2):
-        with pytest.raises(RuntimeError, match="limit of 2 moduli is too small"):
+        with pytest.raises(RuntimeError, match="max_moduli"):
             oz.plan2(a, b, n, n, n, fmt=fmt, max_moduli=2)
-    # window for b = 53 at K = 128: 2*53 + 1 + 7 = 114 bits; 9 moduli of 4096 hold 108, 10 hold 120
-    with pytest.raises(RuntimeError, match="too small"):
-        oz.plan2(a, b, n, n, n, fmt=oz.Format.BF16, max_moduli=9)
-    p10 = oz.plan2(a, b, n, n, n, fmt=oz.Format.BF16, max_moduli=10)
-    p0 = oz.plan2(a, b, n, n, n, fmt=oz.Format.BF16)
-    assert (p10.S, p10.b) == (p0.S, p0.b) and p0.b >= 53
-    # BFP2: 243 = 3^5 carries 7.92 bits; 14 moduli hold 110.9 < 114, 15 hold 118.8
-    with pytest.raises(RuntimeError, match="too small"):
-        oz.plan2(a, b, n, n, n, fmt=oz.Format.BFP2, max_moduli=14)
-    assert oz.plan2(a, b, n, n, n, fmt=oz.Format.BFP2, max_moduli=15).S == p0.S
-    # the evaluator's fixed width 54 with TF32's limit of 11 (evaluate.cpp:163-177): 11 * 12 = 132 >= 116
-    assert oz.plan2(a, b, n, n, n, fmt=oz.Format.TF32, max_moduli=11, fixed_bits=54).b == 54
+        p = oz.plan2(a, b, n, n, n, fmt=fmt, max_moduli=20)
+        assert p.rS <= 20 and p.b >= 53 and not p.fp8_digits
+    p = oz.plan2(a, b, n, n, n, fmt=oz.Format.TF32, max_moduli=11, fixed_bits=54)
+    assert p.b == 54 and p.rS == 11
+
+
+# Scheme II digit routes at b = 54 with the evaluator's moduli limits (evaluate.cpp:162: TF32 11, FP8 14,
+# the others 24): (n, format, moduli, partial products) of tools/validated/quick.csv:3-17 (n = 128) and
+# all.csv:3-49 (n = 3520, 7040, 14080; the table suite, m = n = k).
+ROUTE_RECORDS = [(n, f, mod, pp) for n, rows in {
+    128: [("BF16", 12, 30), ("FP16", 11, 31), ("TF32", 11, 33), ("BFP8", 12, 30), ("FP8", 12, 36), ("BFP4", 14, 65),
+          ("BFP2", 18, 317)],
+    3520: [("BF16", 11, 32), ("FP16", 11, 32), ("TF32", 11, 33), ("BFP8", 11, 32), ("FP8", 12, 36), ("BFP4", 15, 66),
+           ("BFP2", 18, 336)],
+    7040: [("BF16", 14, 30), ("FP16", 14, 30), ("TF32", 11, 33), ("BFP8", 14, 30), ("FP8", 12, 36), ("BFP4", 16, 62),
+           ("BFP2", 19, 331)],
+    14080: [("BF16", 14, 30), ("FP16", 14, 30), ("TF32", 11, 33), ("BFP8", 14, 30), ("FP8", 12, 37), ("BFP4", 17, 58),
+            ("BFP2", 20, 329)],
+}.items() for f, mod, pp in rows]
+EVAL_LIMIT = {"TF32": 11, "FP8": 14}
+
+
+@pytest.mark.parametrize("n,fmt,mod,pp", ROUTE_RECORDS)
+def test_digit_route_records(n, fmt, mod, pp):
+    """The route's set (the stage-time model's for BF16/FP16/BFP8/BFP4/BFP2, the table's for TF32 and FP8)
+    has the recorded number of moduli and digit products, covers the window of b = 54 and is pairwise
+    coprime."""
+    f = oz.Format[fmt]
+    r = oz.choose_moduli_route(f, n, n, n, EVAL_LIMIT.get(fmt, 24), 54)
+    ms = [r.rm[i] for i in range(r.rS)]
+    assert r.ok and r.b == 54 and (r.rS, r.rnprod) == (mod, pp), ms
+    assert bool(r.rmodel_set) == (fmt not in ("TF32", "FP8"))
+    assert all(math.gcd(x, y) == 1 for i, x in enumerate(ms) for y in ms[i + 1:])
+    assert sum(math.log2(x) for x in ms) >= 2 * 54 + 1 + math.log2(n)
+
+
+@pytest.mark.parametrize("b,mod,pp", [(56, 14, 32), (58, 14, 34), (60, 14, 35), (65, 14, 39), (76, 16, 46)])
+def test_digit_route_phi_records(b, mod, pp):
+    """BFP8 with automatic width at 14080^3, phi = 0.5, 1, 2, 4, 8 (all.csv:51-64): the stage-time model's
+    set for the recorded width b (at most 24 moduli) has the recorded moduli and digit products."""
+    r = oz.choose_moduli_route(oz.Format.BFP8, 14080, 14080, 14080, 24, b)
+    assert r.ok and r.b == b and (r.rS, r.rnprod) == (mod, pp)
+
+
+# quick.csv:3-17 Scheme II output hashes of the digit routes (128^3, uniform seed 7, b = 54, one pass)
+ROUTE_HASHES = {"BF16": 0x13ABE4AC7F292F42, "FP16": 0x1811CF560959E61D, "TF32": 0x9A8F2780D4B9976B,
+                "BFP8": 0x13ABE4AC7F292F42, "BFP4": 0x4AD3B42022EA6AD9, "BFP2": 0xC168D203062C72EF}
+
+
+@pytest.mark.parametrize("fmt", list(ROUTE_HASHES))
+def test_digit_route_reference_hashes(oracle, fmt):
+    """The reference's published output of each digit route at 128^3 follows from the planner's set: the
+    exact residues of A'B' modulo the route's moduli (oracle residues of A' and B', int64 products)
+    through the oracle's restatement of the reference reconstruction (recon_crt.cpp) hash to the record.
+    The hash depends on every modulus of the set, so it pins the stage-time model's choice; Info reports
+    this set while the device computes with INT8 residues at the same width."""
+    n = 128
+    a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
+    f = oz.Format[fmt]
+    p = oz.plan2(a, b, n, n, n, f, max_moduli=EVAL_LIMIT.get(fmt, 24), fixed_bits=54,
+                 reconstruction=oz.Reconstruction.OnePass)
+    assert p.b == 54 and not p.fp8_digits and p.two_pass == 0
+    ms = [p.rm[i] for i in range(p.rS)]
+    A, B = a.reshape(n, n), b.reshape(n, n)
+    shift = 54 - 40
+    dA, _ = oracle.scale(A, n, n, 0, 1, shift)
+    dB, _ = oracle.scale(B, n, n, 1, 1, shift)
+    ra = oracle.residues(A, n, n, 0, dA, 3, ms).astype(np.int64)
+    rb = oracle.residues(B, n, n, 1, dB, 3, ms).astype(np.int64)
+    C = np.empty((len(ms), n, n), dtype=np.int32)
+    for s, m in enumerate(ms):
+        r = (ra[s] @ rb[s]) % m
+        C[s] = np.where(r > m // 2, r - m, r)
+    assert oracle.hash(oracle.crt_ref(C, n, n, ms, 54, 3, 0, dA, dB)) == ROUTE_HASHES[fmt]
