@@ -450,6 +450,8 @@ int slice_ops(int m, const Shape& S) {
 struct Cand {
     int m;
     double bits;
+    int np = 0;
+    short pr[4] = {0, 0, 0, 0};  // distinct prime factors of m
 };
 struct Class {
     int nprod, nout, npl, ops;
@@ -458,6 +460,25 @@ struct Class {
     std::vector<Cand> v;
     std::vector<double> est;
 };
+
+// The distinct prime factors of m <= 4096 (at most four), from a smallest-factor table built once.
+int distinct_primes(int m, int* out) {
+    static const std::vector<short> spf = [] {
+        std::vector<short> t(4097, 0);
+        for (int i = 2; i <= 4096; ++i)
+            if (!t[i])
+                for (int j = i; j <= 4096; j += i)
+                    if (!t[j]) t[j] = (short)i;
+        return t;
+    }();
+    int n = 0;
+    while (m > 1) {
+        const int p = spf[m];
+        out[n++] = p;
+        while (m % p == 0) m /= p;
+    }
+    return n;
+}
 
 std::vector<Class> model_classes(std::uint32_t K, const Coef& C, int cap, const Shape& S) {
     std::vector<Class> ks;
@@ -485,7 +506,11 @@ std::vector<Class> model_classes(std::uint32_t K, const Coef& C, int cap, const 
             ks.push_back({np, no, pl, op, one, cost, {}, {}});
             it = ks.end() - 1;
         }
-        it->v.push_back({m, std::log2((double)m)});
+        Cand cand{m, std::log2((double)m)};
+        int pr[5];
+        cand.np = distinct_primes(m, pr);
+        for (int t = 0; t < cand.np; ++t) cand.pr[t] = (short)pr[t];
+        it->v.push_back(cand);
     }
     for (Class& k : ks) {
         std::vector<int> got;
@@ -557,15 +582,46 @@ void enumerate(const Model& s, double incumbent, bool check_dram, bool& dram_cut
 
 // Pairwise coprime moduli for one count vector with bits in [need, need + tol], the smallest excess
 // first; classes are filled in the order `ord`, the walk stops after kNodeMax nodes or at an excess
-// of at most 1e-4 bits.
+// of at most 1e-4 bits. A candidate is coprime to the picked moduli when none of its prime factors
+// divides one of them (`uses` counts the picked moduli per prime).
+// Sums of `left` consecutive candidates' bits of a class, v[j].bits + v[j+1].bits + ... added in that
+// order, for every start j; made once per class and count and kept across count vectors.
+struct RunSums {
+    const std::vector<Class>& ks;
+    std::vector<std::vector<std::vector<double>>> t = std::vector<std::vector<std::vector<double>>>(ks.size());
+    const std::vector<double>& of(int c, int left) {
+        auto& byleft = t[c];
+        if ((int)byleft.size() <= left) byleft.resize(left + 1);
+        std::vector<double>& r = byleft[left];
+        if (r.empty()) {
+            const std::vector<Cand>& v = ks[c].v;
+            r.assign(v.size(), 0.0);
+            for (int j = 0; j + left <= (int)v.size(); ++j) {
+                double u = 0;
+                for (int q = 0; q < left; ++q) u += v[j + q].bits;
+                r[j] = u;
+            }
+        }
+        return r;
+    }
+};
+
 struct Assign {
     const Model& s;
     const std::vector<int>& ord;
+    RunSums& runs;
     std::vector<int> cnt;
     std::vector<double> ubrest, lbrest;  // most / fewest bits the classes ord[i..] can add
     std::vector<int> pick, best;
     double bestex = 1e300;
     long nodes = 0;
+    std::vector<short> uses = std::vector<short>(4097, 0);
+
+    bool coprime(const Cand& c) const {
+        for (int t = 0; t < c.np; ++t)
+            if (uses[c.pr[t]]) return false;
+        return true;
+    }
 
     void walk(int i, int start, int left, double bits) {
         const int NC = (int)s.ks.size();
@@ -583,23 +639,38 @@ struct Assign {
             return;
         }
         const std::vector<Cand>& v = s.ks[ord[i]].v;
+        if (left == 1) {
+            // the candidates that overshoot the window even with the fewest bits of the later classes
+            // are skipped; they form a prefix (v descends, rounding is monotone), found by bisection,
+            // and none of them could end the loop (ubrest >= lbrest)
+            int lo = start, hi = (int)v.size();
+            while (lo < hi) {
+                const int mid = (lo + hi) / 2;
+                if (bits + v[mid].bits + lbrest[i + 1] > s.need + s.tol)
+                    lo = mid + 1;
+                else
+                    hi = mid;
+            }
+            start = lo;
+        }
+        const std::vector<double>& run = runs.of(ord[i], left);
         for (int j = start; j + left <= (int)v.size(); ++j) {
-            double ubc = 0;
-            for (int t = 0; t < left; ++t) ubc += v[j + t].bits;
-            if (bits + ubc + ubrest[i + 1] < s.need) return;
+            if (bits + run[j] + ubrest[i + 1] < s.need) return;
             if (bits + v[j].bits + lbrest[i + 1] > s.need + s.tol && left == 1) continue;
-            if (!std::all_of(pick.begin(), pick.end(), [&](int x) { return std::gcd(x, v[j].m) == 1; })) continue;
+            if (!coprime(v[j])) continue;
             pick.push_back(v[j].m);
+            for (int t = 0; t < v[j].np; ++t) ++uses[v[j].pr[t]];
             walk(i, j + 1, left - 1, bits + v[j].bits);
+            for (int t = 0; t < v[j].np; ++t) --uses[v[j].pr[t]];
             pick.pop_back();
             if (nodes > kNodeMax || bestex <= 1e-4) return;
         }
     }
 };
 
-std::vector<int> assign(const Model& s, const std::vector<int>& ord, const CountVec& vec, long& nodes) {
+std::vector<int> assign(const Model& s, const std::vector<int>& ord, RunSums& runs, const CountVec& vec, long& nodes) {
     const int NC = (int)s.ks.size();
-    Assign a{s, ord, std::vector<int>(NC), std::vector<double>(NC + 1, 0.0), std::vector<double>(NC + 1, 0.0)};
+    Assign a{s, ord, runs, std::vector<int>(NC), std::vector<double>(NC + 1, 0.0), std::vector<double>(NC + 1, 0.0)};
     for (int i = 0; i < NC; ++i) a.cnt[i] = vec.n[ord[i]];
     for (int i = NC - 1; i >= 0; --i) {
         const std::vector<Cand>& v = s.ks[ord[i]].v;
@@ -627,11 +698,12 @@ std::vector<int> model_search(const Model& s, double ub, bool check_dram, bool& 
     std::vector<int> ord(NC);
     std::iota(ord.begin(), ord.end(), 0);
     std::stable_sort(ord.begin(), ord.end(), [&](int a, int b) { return s.ks[a].v.size() < s.ks[b].v.size(); });
+    RunSums runs{s.ks};
     long spent = 0;
     for (const CountVec& vec : vecs) {
         if (budget > 0 && spent > budget) break;
         long nodes = 0;
-        std::vector<int> best = assign(s, ord, vec, nodes);
+        std::vector<int> best = assign(s, ord, runs, vec, nodes);
         spent += nodes;
         if (!best.empty()) {
             std::sort(best.begin(), best.end(), std::greater<int>());
