@@ -387,3 +387,16 @@ def test_digit_route_reference_hashes(oracle, fmt):
         r = (ra[s] @ rb[s]) % m
         C[s] = np.where(r > m // 2, r - m, r)
     assert oracle.hash(oracle.crt_ref(C, n, n, ms, 54, 3, 0, dA, dB)) == ROUTE_HASHES[fmt]
+
+
+def test_digit_route_beyond_the_int8_width_runs_the_widest_int8_plan():
+    """BFP8's route holds b = 90 at K = 4096 (17 moduli up to 4096), 24 INT8 moduli at most 85 bits: the call
+    runs the widest INT8 plan (b = 85, 24 moduli), and Info reports that plan."""
+    M = N = 64
+    K = 4096
+    a, b = oz.eval_inputs(4, 2.0, M * K, K * N)
+    r = oz.choose_moduli_route(oz.Format.BFP8, M, N, K, 24, 90)
+    assert r.ok and r.b == 90 and r.rS == 17
+    p = oz.plan2(a, b, M, N, K, oz.Format.BFP8, fixed_bits=90, max_moduli=24)
+    assert p.b == 85 and p.S == p.rS == 24 and not p.fp8_digits
+    assert [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
