@@ -400,3 +400,15 @@ def test_digit_route_beyond_the_int8_width_runs_the_widest_int8_plan():
     p = oz.plan2(a, b, M, N, K, oz.Format.BFP8, fixed_bits=90, max_moduli=24)
     assert p.b == 85 and p.S == p.rS == 24 and not p.fp8_digits
     assert [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
+
+
+def test_digit_route_accumulation_limit_is_the_references():
+    """The digit routes accumulate digit products in FP32 in the reference, which bounds K (moduli.hpp:472-500):
+    TF32's digits up to 32 give K 32^2 > 2^24 at K = 20000, and the plan fails with the reference's
+    runtime_error although this build's INT8 residues could carry that K (INT8 itself still runs)."""
+    M = N = 64
+    K = 20000
+    a, b = oz.eval_inputs(1, 0.5, M * K, K * N)
+    with pytest.raises(RuntimeError, match="too large for this format.*2\\^24"):
+        oz.plan2(a, b, M, N, K, oz.Format.TF32)
+    assert oz.plan2(a, b, M, N, K, oz.Format.INT8).ok
