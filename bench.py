@@ -328,6 +328,9 @@ def main() -> int:
                      "launch_ms": round(gemm_ms, 4), "ops_per_launch": ev.product_ops},
     }
     if fmt == "FP8":
+        # BASELINE's C4 names e4m3 residues on the FP8 matrix cores: that route is `fp8_matrix_cores` below;
+        # `value` is the library's default for the FP8 format, the same plan carried by INT8 residues
+        out["config"]["transport"] = "INT8 residues at the FP8 plan's width (the library's default for FP8)"
         out["config"]["int8_moduli_computed"] = ev.partial_products
         # the FP8 route's e4m3 digit products on the FP8 matrix cores: the same exact C' at the same width
         log("FP8 route's digits on the FP8 matrix cores")
