@@ -156,14 +156,15 @@ int oz2_crt_f64(oz_dev* dev, const int32_t* C, int M, int N, int ldc, long long 
 /* ---- A9 + A10 fused: products reduced to CRT digits (reference ozaki2.cpp:333-350 followed by
  * the residue step of recon_crt.cpp:293) -------------------------------------------------------
  * The products of oz_gemm_i8 for the S moduli of crt (batch = S), each reduced in the GEMM's
- * epilogue to its CRT digit k_s = (C_s mod m_s) * y_s mod m_s in [0, m_s), stored as uint8:
+ * epilogue to its CRT digit k_s = (C_s mod m_s) * y_s mod m_s, stored as uint8 in [0, m_s] (a digit
+ * 0 may read m_s, which the reconstruction takes as 0):
  * D[s] is M x N bytes, row stride ldd, plane stride strideD bytes (D, ldd and strideD 16-byte
  * aligned). Same operand rules as oz_gemm_i8. Writing one byte instead of four per product is what makes this the production path. */
 int oz2_gemm_digits(oz_dev* dev, const int8_t* A, const int8_t* Bt, uint8_t* D, int M, int N, int K, int S, int ldd,
                     long long strideA, long long strideB, long long strideD, const oz2_crt_dev* crt);
 
-/* CRT reconstruction from the digits of oz2_gemm_digits: same result as oz2_crt_f64 on the
- * products. ldd and strideD (bytes) multiples of 4, D 4-byte aligned. */
+/* CRT reconstruction from the digits of oz2_gemm_digits (each in [0, m_s]): same result as
+ * oz2_crt_f64 on the products. ldd and strideD (bytes) multiples of 4, D 4-byte aligned. */
 int oz2_crt_digits_f64(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long strideD,
                        const oz2_crt_dev* crt, const int32_t* dA, const int32_t* dB, double* out, int ldo);
 
@@ -236,7 +237,7 @@ int oz2_split_digits_pair(oz_dev* dev, const double* A, int M, int K, int lda, c
  * point checks):  P_o = sum_t A[a[t]] * Bt[b[t]]^T  (the reference's concatenation along K).
  * out_kind 0 stores P_o as int32 (M x N per output, element strides, out 16-byte aligned and ldo,
  * strideO multiples of 4); out_kind 1 stores the CRT
- * term w_o = (coef * P_o) mod m in [0, m) as uint16, where coef is the composition coefficient
+ * term w_o = (coef * P_o) mod m as uint16 in [0, m] (m standing for 0), where coef is the composition coefficient
  * times y_s (mod m): for modulus s, sum over its outputs of w_o == D_s * y_s (mod m_s), D_s the
  * composed residue. A and Bt are e4m3 digit planes of oz2_split_digits (layouts 2 and 3);
  * strideA/strideB are the byte distances between planes (multiples of 1024), strideO between

@@ -9,7 +9,8 @@
 // mode and serve both.
 //
 // Per element, with k_s = (C_s mod m_s) * y_s mod m_s and Q_s = M/m_s (host constants):
-//   V = sum_s k_s Q_s  (< S M),   t = the integer nearest V / M,   C' = V - t M,
+//   V = sum_s k_s Q_s  (<= S M),   t = the integer nearest V / M,   C' = V - t M,
+// (the digits written by the product kernels may hold m_s for 0: that adds M to V, which t removes),
 // with C' taken in (floor(M/2) - M, floor(M/2)].
 //
 // MI355X design: exact integer arithmetic in FP64 limbs. Q_s and M are given as L = nw limbs of
@@ -21,6 +22,9 @@
 // M. Carries are then propagated (floor by 2^32, exact), the magnitude is taken, and its 32-bit
 // words are rounded once to FP64. One thread computes 4 consecutive output elements of a row; the
 // constants are kernel arguments (uniform, read with scalar loads).
+#include <algorithm>
+#include <cmath>
+
 #include "oz2_modular.hpp"
 #include "oz_internal.hpp"
 
@@ -28,21 +32,12 @@ namespace {
 
 using oz2::mod_small;
 
-// V = sum_l x_l 2^(32 l) >= 0 from normalized limbs (every x_l in [0, 2^32)) -> V 2^e2 rounded to
-// nearest-even, negated if neg; 0 when V = 0, signed zero below 2^-1022 (f64_tf.h:45-47), infinity
-// above the FP64 range. The limbs are read as 64-bit words (with a zero limb below x_0 when L is
-// odd); the leading nonzero word and the one below it form a 128-bit window, everything under the
-// window only matters as the sticky bit. Selects only, no branches.
-template <int L>
-__device__ __forceinline__ double magnitude_to_double(const double* x, int e2, bool neg) {
-    constexpr int NU = (L + 1) / 2, OFF = (L & 1) ? 32 : 0;  // V = sum_k U_k 2^(64 k - OFF)
-    uint64_t U[NU];
-#pragma unroll
-    for (int k = 0; k < NU; k++) {
-        const int lo = 2 * k - (L & 1);
-        const uint64_t wl = lo >= 0 ? (uint64_t)(uint32_t)x[lo] : 0ull;
-        U[k] = ((uint64_t)(uint32_t)x[lo + 1] << 32) | wl;
-    }
+// V = sum_k U_k 2^(64 k - OFF) >= 0 (64-bit words) -> V 2^e2 rounded to nearest-even, negated if
+// neg; 0 when V = 0, signed zero below 2^-1022 (f64_tf.h:45-47), infinity above the FP64 range. The
+// leading nonzero word and the one below it form a 128-bit window, everything under the window only
+// matters as the sticky bit. Selects only, no branches.
+template <int NU, int OFF>
+__device__ __forceinline__ double words_to_double(const uint64_t* U, int e2, bool neg) {
     uint64_t first = U[0], second = 0, below = 0;
     int base = 0;
 #pragma unroll
@@ -71,10 +66,38 @@ __device__ __forceinline__ double magnitude_to_double(const double* x, int e2, b
     return first == 0 ? 0.0 : r;
 }
 
+// V = sum_l x_l 2^(32 l) >= 0 from normalized limbs (every x_l in [0, 2^32)) -> words_to_double; the
+// limbs are read as 64-bit words, with a zero limb below x_0 when L is odd.
+template <int L>
+__device__ __forceinline__ double magnitude_to_double(const double* x, int e2, bool neg) {
+    constexpr int NU = (L + 1) / 2, OFF = (L & 1) ? 32 : 0;  // V = sum_k U_k 2^(64 k - OFF)
+    uint64_t U[NU];
+#pragma unroll
+    for (int k = 0; k < NU; k++) {
+        const int lo = 2 * k - (L & 1);
+        const uint64_t wl = lo >= 0 ? (uint64_t)(uint32_t)x[lo] : 0ull;
+        U[k] = ((uint64_t)(uint32_t)x[lo + 1] << 32) | wl;
+    }
+    return words_to_double<NU, OFF>(U, e2, neg);
+}
+
+// Limb formats of the accumulator. Wide32: limbs of 32 bits holding their integers as they are
+// (digits and terms up to 2^12). Byte40: limbs of 40 bits holding their integers times 2^-90 (the
+// byte digits of the product kernels, which enter the FMAs as FP64 denormals, see crt_digits_kernel).
+// carry: multiplier that maps a limb to its carry count; limb: a carry count in the limb's own
+// scale; unit: a carry count in the next limb's scale.
+struct Wide32 {
+    static constexpr double carry = 0x1p-32, limb = 0x1p32, unit = 1.0;
+};
+struct Byte40 {
+    static constexpr double carry = 0x1p50, limb = 0x1p-50, unit = 0x1p-90;
+};
+
 // Kernel constants: limbs of Q_s, M, floor(M/2), M - floor(M/2) (32-bit limbs as exact doubles).
 struct CrtLimbs {
+    using Format = Wide32;
     int S, shift, b;
-    double two32;  // 2^32 (a kernel argument, so that it sits in a scalar register)
+    double radix;  // 2^32 (a kernel argument, so that it sits in a scalar register)
     double invM;   // 1/M rounded
     double delta;  // exact-path threshold: 2^-28 + 2/M
     double Q[OZ2_MAXS][8];
@@ -84,16 +107,28 @@ struct CrtLimbs {
     unsigned char tcount[OZ2_MAXS], tidx[OZ2_MAXS][4];
 };
 
-constexpr double kTwo32 = 4294967296.0, kInv32 = 1.0 / 4294967296.0;
+// The same for the byte digits: 40-bit limbs, at most 5 (S M < 24 * 2^192 < 2^200).
+constexpr int kMaxLimbs40 = 5;
+struct CrtLimbs40 {
+    using Format = Byte40;
+    int S, shift, b;
+    double radix;  // 2^40
+    double invM;   // 2^90 / M rounded (the limbs hold V 2^-90)
+    double delta;  // exact-path threshold: 2^-28 + 2/M
+    double Q[OZ2_MAXS][kMaxLimbs40];  // limbs of Q_s times 2^984: a digit k enters as k 2^-1074
+    double Mw[kMaxLimbs40], Mhalf[kMaxLimbs40], Mrest[kMaxLimbs40];  // limbs times 2^-90
+    double two90, two52;  // 2^90, 2^52 (kernel arguments: scalar registers, not literals)
+};
 
-// Carry propagation: limbs 0..L-2 into [0, 2^32), the top limb keeps the sign. Exact.
-template <int L>
+// Carry propagation: limbs 0..L-2 into [0, 2^W), the top limb keeps the sign. Exact: every value is
+// an integer (in the format's scale) below 2^53.
+template <int L, class F>
 __device__ __forceinline__ void normalize(double* x) {
 #pragma unroll
     for (int l = 0; l + 1 < L; l++) {
-        const double c = __builtin_floor(x[l] * kInv32);
-        x[l] = __builtin_fma(-c, kTwo32, x[l]);
-        x[l + 1] += c;
+        const double c = __builtin_floor(x[l] * F::carry);
+        x[l] = __builtin_fma(-c, F::limb, x[l]);
+        x[l + 1] = __builtin_fma(c, F::unit, x[l + 1]);
     }
 }
 // Sign of a normalized limb vector.
@@ -106,41 +141,71 @@ __device__ __forceinline__ int limb_sign(const double* x) {
     return nz ? 1 : 0;
 }
 
+// Byte40 limbs (normalized, each an integer in [0, 2^40) times 2^-90) -> words_to_double. A limb's
+// integer is read from the mantissa of y 2^90 + 2^52 (exact); the 40-bit limbs are packed into
+// 64-bit words by constant shifts.
+template <int L>
+__device__ __forceinline__ double magnitude40(const double* x, int e2, bool neg, const CrtLimbs40& a) {
+    constexpr int NU = (40 * L + 63) / 64;
+    uint64_t U[NU];
+#pragma unroll
+    for (int k = 0; k < NU; k++) U[k] = 0;
+#pragma unroll
+    for (int l = 0; l < L; l++) {
+        const double t = __builtin_fma(x[l], a.two90, a.two52);
+        const uint64_t y = (uint64_t)__double_as_longlong(t) & 0x000000FFFFFFFFFFull;
+        const int p = 40 * l, k = p / 64, r = p % 64;
+        U[k] |= y << r;
+        if (r > 24) U[k + 1] |= y >> (64 - r);
+    }
+    return words_to_double<NU, 0>(U, e2, neg);
+}
+
+template <int L>
+__device__ __forceinline__ double magnitude(const double* x, int e2, bool neg, const CrtLimbs& a) {
+    return magnitude_to_double<L>(x, e2, neg);
+}
+template <int L>
+__device__ __forceinline__ double magnitude(const double* x, int e2, bool neg, const CrtLimbs40& a) {
+    return magnitude40<L>(x, e2, neg, a);
+}
+
 // x = V (exact limbs, each below 2^53) -> C' * 2^e2 rounded to nearest-even (subnormal -> signed 0).
 // C' = V - t M with t the nearest integer to an FP64 estimate of V/M. Its sign is that of q - t
 // whenever |C'| is not tiny, so the limbs are multiplied by that sign before the carries are
-// propagated, which leaves the magnitude in nonnegative 32-bit limbs; a tiny C' of the other sign
-// shows as a negative top limb and is negated once more (rare). An estimate near a half-integer is
-// settled exactly against floor(M/2) (rare).
-template <int L>
-__device__ __forceinline__ double crt_finish(double* x, const CrtLimbs& a, int e2) {
+// propagated, which leaves the magnitude in nonnegative limbs; a tiny C' of the other sign shows as
+// a negative top limb and is negated once more (rare). An estimate near a half-integer is settled
+// exactly against floor(M/2) (rare).
+template <int L, class A>
+__device__ __forceinline__ double crt_finish(double* x, const A& a, int e2) {
+    using F = typename A::Format;
     double vd = x[L - 1];
 #pragma unroll
-    for (int l = L - 2; l >= 0; l--) vd = __builtin_fma(vd, a.two32, x[l]);  // (2^32 from a register)
+    for (int l = L - 2; l >= 0; l--) vd = __builtin_fma(vd, a.radix, x[l]);  // (the radix from a register)
     const double q = vd * a.invM;
     const double t = __builtin_rint(q);
 #pragma unroll
-    for (int l = 0; l < L; l++) x[l] = __builtin_fma(-t, a.Mw[l], x[l]);  // |t M_l| < 2^37: exact
+    for (int l = 0; l < L; l++) x[l] = __builtin_fma(-t, a.Mw[l], x[l]);  // |t M_l| <= 25 M_l: exact
     bool neg = q - t < 0.0;
     if (__builtin_fabs(q - t) > 0.5 - a.delta) {
         // the estimate may pick the wrong neighbour: compare C' with floor(M/2) exactly
-        normalize<L>(x);
+        normalize<L, F>(x);
         double y[L];
 #pragma unroll
         for (int l = 0; l < L; l++) y[l] = x[l] - a.Mhalf[l];
-        normalize<L>(y);
+        normalize<L, F>(y);
         if (limb_sign<L>(y) > 0) {  // C' > floor(M/2)
 #pragma unroll
             for (int l = 0; l < L; l++) x[l] -= a.Mw[l];
-            normalize<L>(x);
+            normalize<L, F>(x);
         } else {
 #pragma unroll
             for (int l = 0; l < L; l++) y[l] = x[l] + a.Mrest[l];
-            normalize<L>(y);
+            normalize<L, F>(y);
             if (limb_sign<L>(y) <= 0) {  // C' <= floor(M/2) - M
 #pragma unroll
                 for (int l = 0; l < L; l++) x[l] += a.Mw[l];
-                normalize<L>(x);
+                normalize<L, F>(x);
             }
         }
         neg = x[L - 1] < 0.0;
@@ -148,14 +213,14 @@ __device__ __forceinline__ double crt_finish(double* x, const CrtLimbs& a, int e
     const double sg = neg ? -1.0 : 1.0;
 #pragma unroll
     for (int l = 0; l < L; l++) x[l] *= sg;
-    normalize<L>(x);
+    normalize<L, F>(x);
     if (x[L - 1] < 0.0) {  // |C'| so small that the estimate's sign was wrong
 #pragma unroll
         for (int l = 0; l < L; l++) x[l] = -x[l];
-        normalize<L>(x);
+        normalize<L, F>(x);
         neg = !neg;
     }
-    return magnitude_to_double<L>(x, e2, neg);
+    return magnitude<L>(x, e2, neg, a);
 }
 
 // x += k * Q_s (k < 2^12)
@@ -184,11 +249,16 @@ __global__ void __launch_bounds__(256) crt_kernel(const int32_t* __restrict__ C,
     out[(long long)i * ldo + j] = crt_finish<L>(x, a, g - 2 * a.b);
 }
 
-// From the CRT digits k_s (uint8, written by the product kernel): one thread per 4 consecutive
-// output elements of a row, so that each plane read is one 32-bit word per thread.
+// From the CRT digits k_s (uint8, written by the product kernel, k_s <= m_s <= 255): one thread per 4
+// consecutive output elements of a row, so that each plane read is one 32-bit word per thread.
+// Limbs of 40 bits: every k_s Q_s,l < 2^48 and every sum over at most 24 moduli stays below 2^53, so
+// 4 limbs cover the C3 plan (S M < 2^139) where 32-bit limbs need 5. A digit enters its FMAs as the
+// FP64 denormal k 2^-1074 (its byte in the low word, zero above: one bit-field extract, no
+// conversion), against limbs of Q_s stored times 2^984, so the accumulators hold V 2^-90 exactly
+// (integers times 2^-90 below 2^-37: normal doubles).
 template <int L>
 __global__ void __launch_bounds__(256) crt_digits_kernel(const uint8_t* __restrict__ D, int M, int N, int ldd,
-                                                         long long sD, CrtLimbs a, const int32_t* __restrict__ dA,
+                                                         long long sD, CrtLimbs40 a, const int32_t* __restrict__ dA,
                                                          const int32_t* __restrict__ dB, double* __restrict__ out,
                                                          int ldo) {
     const int j0 = 4 * (blockIdx.x * 256 + threadIdx.x);
@@ -210,7 +280,11 @@ __global__ void __launch_bounds__(256) crt_digits_kernel(const uint8_t* __restri
     for (int s = 0; s < OZ2_MAXS; s++)
         if (s < a.S) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) limb_add<L>(x[e], (double)((v[s] >> (8 * e)) & 0xFFu), a.Q[s]);
+            for (int e = 0; e < 4; e++) {
+                const double k = __hiloint2double(0, (int)((v[s] >> (8 * e)) & 0xFFu));  // k 2^-1074
+#pragma unroll
+                for (int l = 0; l < L; l++) x[e][l] = __builtin_fma(k, a.Q[s][l], x[e][l]);
+            }
         }
     const int gi = 2 * a.shift - dA[i] - 2 * a.b;
     double r[4];
@@ -271,7 +345,7 @@ __global__ void __launch_bounds__(256) crt_terms_kernel(const uint16_t* __restri
 // Kernel constants of a CRT descriptor whose moduli are at most mmax.
 int crt_limbs(oz_dev* dev, const char* name, const oz2_crt_dev* crt, uint32_t mmax, CrtLimbs& a) {
     a = CrtLimbs{};
-    a.two32 = 4294967296.0;
+    a.radix = 4294967296.0;
     a.S = crt->S;
     a.shift = crt->shift;
     a.b = crt->b;
@@ -331,7 +405,7 @@ int crt_limbs(oz_dev* dev, const char* name, const oz2_crt_dev* crt, uint32_t mm
         }
     }
     double Md = 0.0;
-    for (int w = 7; w >= 0; w--) Md = Md * kTwo32 + (double)Mw[w];
+    for (int w = 7; w >= 0; w--) Md = Md * 4294967296.0 + (double)Mw[w];
     a.invM = 1.0 / Md;
     a.delta = 0x1p-28 + 2.0 / Md;
     return OZ_OK;
@@ -340,11 +414,6 @@ int crt_limbs(oz_dev* dev, const char* name, const oz2_crt_dev* crt, uint32_t mm
 template <int L>
 int launch_crt(oz_dev* dev, const void* C, int kind, int M, int N, int ldc, long long sC, const CrtLimbs& a,
                const int32_t* dA, const int32_t* dB, double* out, int ldo) {
-    if (kind == 1) {
-        hipLaunchKernelGGL(crt_digits_kernel<L>, dim3(oz::ceil_div(N, 1024), M), dim3(256), 0, dev->stream,
-                           static_cast<const uint8_t*>(C), M, N, ldc, sC, a, dA, dB, out, ldo);
-        return oz::launch_check(dev, "crt_digits_kernel");
-    }
     if (kind == 2) {
         hipLaunchKernelGGL(crt_terms_kernel<L>, dim3(oz::ceil_div(N, 1024), M), dim3(256), 0, dev->stream,
                            static_cast<const uint16_t*>(C), M, N, ldc, sC, a, dA, dB, out, ldo);
@@ -355,12 +424,80 @@ int launch_crt(oz_dev* dev, const void* C, int kind, int M, int N, int ldc, long
     return oz::launch_check(dev, "crt_kernel");
 }
 
+// Constants of the byte-digit kernel from those of the 32-bit limbs: the 40-bit limbs of Q_s, M,
+// floor(M/2) and M - floor(M/2), scaled as CrtLimbs40 states, and the number of limbs that S M needs.
+uint64_t limb40(const double* words, int l) {  // bits 40 l .. 40 l + 39 of 8 exact 32-bit words
+    uint64_t r = 0;
+    for (int b = 0; b < 40; b++) {
+        const int q = 40 * l + b;
+        if (q < 256 && (((uint64_t)words[q / 32] >> (q % 32)) & 1u)) r |= 1ull << b;
+    }
+    return r;
+}
+int crt_limbs40(const CrtLimbs& a, CrtLimbs40& b) {
+    b = CrtLimbs40{};
+    b.S = a.S;
+    b.shift = a.shift;
+    b.b = a.b;
+    b.radix = 0x1p40;
+    b.two90 = 0x1p90;
+    b.two52 = 0x1p52;
+    b.invM = std::ldexp(a.invM, 90);
+    b.delta = a.delta;
+    // bit length of S M (S M < 2^200): the limbs needed
+    uint32_t sm[9] = {};
+    uint64_t carry = 0;
+    for (int w = 0; w < 8; w++) {
+        const uint64_t p = (uint64_t)(uint32_t)a.Mw[w] * (uint64_t)a.S + carry;
+        sm[w] = (uint32_t)p;
+        carry = p >> 32;
+    }
+    sm[8] = (uint32_t)carry;
+    int bits = 0;
+    for (int w = 8; w >= 0 && !bits; w--)
+        if (sm[w]) bits = 32 * w + 32 - __builtin_clz(sm[w]);
+    const int L = std::max(2, (bits + 39) / 40);
+    for (int l = 0; l < kMaxLimbs40; l++) {
+        for (int s = 0; s < a.S; s++) b.Q[s][l] = std::ldexp((double)limb40(a.Q[s], l), 984);
+        b.Mw[l] = std::ldexp((double)limb40(a.Mw, l), -90);
+        b.Mhalf[l] = std::ldexp((double)limb40(a.Mhalf, l), -90);
+        b.Mrest[l] = std::ldexp((double)limb40(a.Mrest, l), -90);
+    }
+    return L;
+}
+
+template <int L>
+int launch_crt_digits(oz_dev* dev, const uint8_t* D, int M, int N, int ldd, long long sD, const CrtLimbs40& a,
+                      const int32_t* dA, const int32_t* dB, double* out, int ldo) {
+    hipLaunchKernelGGL(crt_digits_kernel<L>, dim3(oz::ceil_div(N, 1024), M), dim3(256), 0, dev->stream, D, M, N, ldd,
+                       sD, a, dA, dB, out, ldo);
+    return oz::launch_check(dev, "crt_digits_kernel");
+}
+
 // All entry points: C is int32 products (kind 0, element strides), uint8 digits (kind 1, byte
 // strides) or uint16 terms (kind 2, element strides); rows go on the grid's y (at most 65535 per
 // launch), so the launch is split in row chunks.
 int crt_launch(oz_dev* dev, const void* C, int kind, int M, int N, int ldc, long long strideC, int nw,
                const CrtLimbs& a, const int32_t* dA, const int32_t* dB, double* out, int ldo) {
     const size_t esz = kind == 1 ? 1 : kind == 2 ? 2 : 4;
+    if (kind == 1) {
+        CrtLimbs40 b;
+        const int L = crt_limbs40(a, b);
+        for (int i0 = 0; i0 < M; i0 += 65535) {
+            const int rows = std::min(65535, M - i0);
+            const uint8_t* Di = static_cast<const uint8_t*>(C) + (size_t)i0 * ldc;
+            double* oi = out + (long long)i0 * ldo;
+            int st;
+            switch (L) {
+            case 2: st = launch_crt_digits<2>(dev, Di, rows, N, ldc, strideC, b, dA + i0, dB, oi, ldo); break;
+            case 3: st = launch_crt_digits<3>(dev, Di, rows, N, ldc, strideC, b, dA + i0, dB, oi, ldo); break;
+            case 4: st = launch_crt_digits<4>(dev, Di, rows, N, ldc, strideC, b, dA + i0, dB, oi, ldo); break;
+            default: st = launch_crt_digits<5>(dev, Di, rows, N, ldc, strideC, b, dA + i0, dB, oi, ldo); break;
+            }
+            if (st) return st;
+        }
+        return OZ_OK;
+    }
     for (int i0 = 0; i0 < M; i0 += 65535) {
         const int rows = std::min(65535, M - i0);
         const void* Ci = static_cast<const char*>(C) + (size_t)i0 * ldc * esz;

@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(THREADS) gemm_f8_groups_kernel(const uint8_t* 
     float* tile = reinterpret_cast<float*>(lds) + wave * (64 * 128);
     const long long c0 = (long long)o * sO + (long long)(tm * BM + wm * 128) * ldo + tn * BN + wn * 128;
     const uint32_t mi = g.np_m & 0xFFFFu;
-    const double md = (double)mi, cf = (double)g.coef, rinv = 1.0 / md;
+    const double md = (double)mi, cfr = (double)g.coef / md;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
 #pragma unroll
@@ -230,13 +230,13 @@ __global__ void __launch_bounds__(THREADS) gemm_f8_groups_kernel(const uint8_t* 
             const v4f v0 = *reinterpret_cast<const v4f*>(src), v1 = *reinterpret_cast<const v4f*>(src + 4);
             const long long at = c0 + (long long)(64 * h + row) * ldo + 8 * cg;
             if constexpr (KIND == 1) {
-                // |P_o| < 2^24 and coef < m <= 2401: |P_o coef| < 2^36, within mod_mul_f64's range
+                // |P_o| < 2^24 and m <= 2401: |P_o| m < 2^36, within mod_mul_f64's range
                 const float s[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 uint32_t w[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++)
-                    w[k] = oz2::mod_mul_f64((double)s[2 * k], cf, md, rinv, mi) |
-                           oz2::mod_mul_f64((double)s[2 * k + 1], cf, md, rinv, mi) << 16;
+                    w[k] = oz2::mod_mul_f64((double)s[2 * k], cfr, md) |
+                           oz2::mod_mul_f64((double)s[2 * k + 1], cfr, md) << 16;
                 *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + at) = uint4{w[0], w[1], w[2], w[3]};
             } else {
                 int32_t* d = static_cast<int32_t*>(out) + at;

@@ -25,20 +25,17 @@ __device__ __forceinline__ uint32_t crt_digit(int32_t c, uint32_t m, uint32_t y,
     return mod_small(r * y, m, magic);
 }
 
-// (c * y) mod m in [0, m) for integers c, y with |c * y| < 2^40 and 2 <= m, in FP64 (one product,
-// one floor, one FMA: the FP64 pipes run these at full rate, where the 32-bit integer multiplies of
-// crt_digit run at a quarter). rinv = RN(1/m), mi = m as an integer. Exact: x = c*y is an integer
-// below 2^53, so x is exact; RN(x * rinv) differs from x/m by less than |x/m| 2^-52 < 2^-12 / m. If
-// x/m is not an integer it is at least 1/m away from one, so the floor is exact and the FMA (whose
-// exact value, x - q m, is a small integer) gives the remainder; if x/m is an integer the floor is
-// x/m or x/m - 1, giving 0 or m. So the FMA's result is an integer in [0, m]: it converts to uint32
-// exactly, and min(r, r - m) in unsigned arithmetic maps m to 0 and keeps r < m (r - m wraps above
-// it): two integer operations, with no compare, no condition register and no hazard wait. The same
-// residue as crt_digit(c, m, y, .) for |c| < 2^31, y < m <= 255.
-__device__ __forceinline__ uint32_t mod_mul_f64(double c, double y, double m, double rinv, uint32_t mi) {
-    const double x = c * y;
-    const uint32_t r = (uint32_t)__builtin_fma(-__builtin_floor(x * rinv), m, x);
-    return min(r, r - mi);
+// A representative of (c * y) mod m in [0, m] (m standing for 0) for integers c, y, m with
+// 0 <= y < m and |c| m < 2^50, in five FP64-pipe operations counting the conversion of c
+// (v_cvt_f64_i32, v_mul_f64, v_fract_f64, v_fma_f64, v_cvt_u32_f64); yr is y/m to within an ulp.
+// t = RN(c yr) lies within |c| 2^-51 of c y/m, so its fractional part f (exact: v_fract_f64 is
+// t - floor(t), clamped below 1) lies within delta = |c| 2^-51 of r/m modulo 1, r = (c y) mod m;
+// f m + 1/2 is then within delta m < 1/2 of r + 1/2, or of m + 1/2 when r = 0 and f fell just
+// below 1, and the truncating conversion of its rounded value gives r (or m). Every consumer of
+// these values reduces them modulo m (the CRT adds k Q_s, and m Q_s = M vanishes modulo M; the FP8
+// route's terms are summed modulo m), so m is as good as 0 and needs no fix-up.
+__device__ __forceinline__ uint32_t mod_mul_f64(double c, double yr, double m) {
+    return (uint32_t)__builtin_fma(__builtin_amdgcn_fract(c * yr), m, 0.5);
 }
 
 // Per-modulus constants of the digit epilogue (kernel argument).

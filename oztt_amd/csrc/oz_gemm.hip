@@ -37,7 +37,8 @@ namespace {
 using namespace ozg;
 
 // Output modes. PRODUCTS: C[b] = A[b] Bt[b]^T as int32. DIGITS: the same products reduced in the
-// epilogue to the CRT digit for modulus b ((C mod m_b) y_b mod m_b, from dc.m/y[b]), C as uint8. DIAG
+// epilogue to the CRT digit for modulus b ((C mod m_b) y_b mod m_b, from dc.m/y[b]; a digit 0 may be
+// stored as m_b, oz2::mod_mul_f64), C as uint8. DIAG
 // (scheme I): C[d] = sum_{i <= d} A[i] Bt[d-i]^T as int32 for the diagonals d < nbatch, the d+1
 // slice pairs concatenated along K in one accumulation.
 enum GemmMode { PRODUCTS = 0, DIGITS = 1, DIAG = 2 };
@@ -214,8 +215,8 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
                 y = dc.y[s];
             }
         uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
-        const double md = (double)m, yd = (double)y, rinv = 1.0 / md;
-        auto dg = [&](int32_t c) -> uint32_t { return oz2::mod_mul_f64((double)c, yd, md, rinv, m); };
+        const double md = (double)m, yr = (double)y / md;
+        auto dg = [&](int32_t c) -> uint32_t { return oz2::mod_mul_f64((double)c, yr, md); };
 #pragma unroll
         for (int h = 0; h < 2; h++) {
 #pragma unroll

@@ -14,6 +14,15 @@ ORACLE_SO = ROOT / "oracle" / "build" / "liboz_oracle.so"
 _lib = None
 
 
+def assert_residues(got, want, m, what: str = "") -> None:
+    """The product kernels store (c * y) mod m as a representative in [0, m], m standing for 0
+    (oz2::mod_mul_f64): `got` must lie in that range and agree with `want` modulo m."""
+    got = np.asarray(got).astype(np.int64)
+    m = np.asarray(m, dtype=np.int64)
+    assert np.all((got >= 0) & (got <= m)), f"{what}: a representative outside [0, m]"
+    np.testing.assert_array_equal(got % m, np.asarray(want).astype(np.int64) % m, err_msg=what)
+
+
 def P(a: np.ndarray) -> ctypes.c_void_p:
     return a.ctypes.data_as(ctypes.c_void_p)
 

@@ -26,6 +26,7 @@ import pytest
 
 import oztt_amd as oz
 from oztt_amd.device import E4M3, GroupsDesc, crt_desc, from_blocks, moduli_desc, to_blocks
+from tests.oracle_lib import assert_residues
 from tests.test_gpu_scheme2_fp8 import check_fp8_chain, run_fp8_stages
 
 pytestmark = pytest.mark.gpu
@@ -108,8 +109,7 @@ def test_c3_headline_plan_and_slab_parity(ctx, dev, oracle):
         # |C_s| <= 8192 * 127^2 < 2^27: the float64 product is the exact integer
         prod = want_A[s].astype(np.float64) @ want_B[s].astype(np.float64)
         Cs[s] = prod.astype(np.int64)
-        digit = ((prod.astype(np.int64) % m) * int(cd.y[s])) % m
-        np.testing.assert_array_equal(gD[s].astype(np.int64), digit)
+        assert_residues(gD[s], (prod.astype(np.int64) % m) * int(cd.y[s]), m, f"modulus {m}")
     ex = oracle.crt_exact(Cs, rows, n, moduli, bw, nd, wA[r0:r0 + rows], wB)
     np.testing.assert_array_equal(c.reshape(n, n)[r0:r0 + rows].ravel().view(np.uint64), ex.view(np.uint64))
 
@@ -169,7 +169,7 @@ def test_c4_inner_dimension_public_call_equals_int8(ctx):
 def test_fp8_products_exact_at_the_fp32_bound(dev):
     """Digit planes of +-16 (e4m3 0x58 / 0xD8), K = 16384, outputs of three concatenated products:
     all-positive digits give 3 K 256 = 12582912 < 2^24 exactly; random signs give every smaller sum.
-    Compared with int64 products, as int32 outputs and as uint16 terms coef * P mod m."""
+    Compared with int64 products, as int32 outputs and as uint16 terms coef * P mod m (representatives in [0, m])."""
     M = N = 256
     K = 16384
     code = {16: int(np.flatnonzero(E4M3 == 16.0)[0]), -16: int(np.flatnonzero(E4M3 == -16.0)[0])}
@@ -203,7 +203,7 @@ def test_fp8_products_exact_at_the_fp32_bound(dev):
     want = sum(sa[3 + t].astype(np.float64) @ sb[3 + t].astype(np.float64).T for t in range(3)).astype(np.int64)
     np.testing.assert_array_equal(P[1], want)
     for o in range(2):
-        np.testing.assert_array_equal(W[o], ((5 + o) * (P[o] % 1089)) % 1089)
+        assert_residues(W[o], (5 + o) * (P[o] % 1089), 1089, f"output {o}")
 
 
 @pytest.mark.parametrize("scheme,fmt,fp8_cores", [(oz.Scheme.II, oz.Format.INT8, False),

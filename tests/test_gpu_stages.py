@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 from oztt_amd.device import Device, crt_desc, from_blocks, moduli_desc, to_blocks
+from tests.oracle_lib import assert_residues
 
 pytestmark = pytest.mark.gpu
 
@@ -218,12 +219,16 @@ def test_crt_exact(dev, oracle, moduli, b, nd):
     np.testing.assert_array_equal(got.view(np.uint64), want.view(np.uint64))
     np.testing.assert_array_equal(got.view(np.uint64),
                                   oracle.crt_exact(C, M, N, moduli, b, nd, dA, dB).view(np.uint64))
-    # the same from CRT digits k_s = (C_s mod m_s) y_s mod m_s (uint8 planes, row stride a multiple of 4)
+    # the same from CRT digits k_s = (C_s mod m_s) y_s mod m_s (uint8 planes, row stride a multiple of 4);
+    # the product kernels may store a digit 0 as m_s: half of the zero digits are given that way
     desc = crt_desc(moduli, b, nd)
     ldd = (N + 3) // 4 * 4 + 4
     D = np.zeros((S, M, ldd), dtype=np.uint8)
     for s, m in enumerate(moduli):
-        D[s, :, :N] = (C[s].astype(np.int64) % m * int(desc.y[s]) % m).astype(np.uint8)
+        k = C[s].astype(np.int64) % m * int(desc.y[s]) % m
+        k = np.where((k == 0) & (rng.random(k.shape) < 0.5), m, k)
+        D[s, :, :N] = k.astype(np.uint8)
+    assert np.any(D == np.array(moduli, dtype=np.uint8)[:, None, None])
     bD = dev.upload(D)
     bo2 = dev.alloc(8 * n)
     dev.crt_digits(bD, M, N, ldd, M * ldd, desc, bdA, bdB, bo2, N)
@@ -249,7 +254,7 @@ def test_gemm_digits_exact(dev, M, N, K, S):
     for s, m in enumerate(moduli):
         prod = (A[s].astype(np.float64) @ Bt[s].astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
         want = (prod % m) * int(desc.y[s]) % m
-        np.testing.assert_array_equal(D[s].astype(np.int64), want)
+        assert_residues(D[s], want, m, f"modulus {m}")
 
 
 @pytest.mark.parametrize("M,N,K,S,digits", [(256, 256, 256, 300, False), (256, 512, 384, 150, False),
@@ -279,8 +284,10 @@ def test_gemm_tile_sequences(dev, M, N, K, S, digits):
     dev.bufs.clear()
     for t in range(S):
         prod = (A[t].astype(np.float64) @ Bt[t].astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
-        want = (prod % moduli[t]) * int(desc.y[t]) % moduli[t] if digits else prod
-        np.testing.assert_array_equal(got[t].astype(np.int64), want, err_msg=f"batch {t}")
+        if digits:
+            assert_residues(got[t], (prod % moduli[t]) * int(desc.y[t]), moduli[t], f"batch {t}")
+        else:
+            np.testing.assert_array_equal(got[t].astype(np.int64), prod, err_msg=f"batch {t}")
 
 
 def test_device_copy(dev):

@@ -2,27 +2,33 @@
 oztt_amd/csrc/oz2_modular.hpp), emulated with numpy's IEEE binary64 operations and checked against
 exact integer arithmetic.
 
-The device function computes r = x - floor(RN(x * RN(1/m))) * m for x = c * y, then maps r = m to 0.
-Its FMA rounds an exact small integer, so plain binary64 subtraction of the exact product q * m
-(an integer below 2^40) gives the same value here. The kernels use it for the CRT digit of an int32
-product (|c| < 2^31, y < m <= 255: reference recon_crt.cpp:293's residue step) and for the FP8
-route's terms (|P| < 2^24, coef < m <= 2401). CPU only.
+The device function computes t = RN(c * yr) with yr = RN(y / m), f = t - floor(t) clamped below 1
+(v_fract_f64), and the truncation of RN(f * m + 1/2) (v_fma_f64, v_cvt_u32_f64): a representative
+of (c * y) mod m in [0, m], m standing for 0. The emulation rounds f * m + 1/2 in 80-bit extended
+precision before binary64; f * m + 1/2 lies within 2^-13 of r + 1/2 for an integer r, so neither
+rounding can change its integer part. The kernels use it for the CRT digit of an int32 product
+(|c| < 2^31, y < m <= 255: reference recon_crt.cpp:293's residue step) and for the FP8 route's terms
+(|P| < 2^24, coef < m <= 2401). CPU only.
 """
 import numpy as np
 
 
 def mod_mul_f64(c: np.ndarray, y: np.ndarray, m: np.ndarray) -> np.ndarray:
-    x = c.astype(np.float64) * y.astype(np.float64)
     md = m.astype(np.float64)
-    rinv = 1.0 / md
-    r = x - np.floor(x * rinv) * md
-    return np.where(r >= md, r - md, r).astype(np.int64)
+    yr = y.astype(np.float64) / md
+    t = c.astype(np.float64) * yr
+    f = np.minimum(t - np.floor(t), np.nextafter(1.0, 0.0))
+    g = (f.astype(np.longdouble) * md.astype(np.longdouble) + np.longdouble(0.5)).astype(np.float64)
+    # the margin the truncation relies on: f m is within 1/4 of an integer
+    assert np.all(np.abs(g - 0.5 - np.rint(g - 0.5)) < 0.25)
+    return np.trunc(g).astype(np.int64)
 
 
 def _check(c, y, m):
     got = mod_mul_f64(c, y, m)
     want = np.array([(int(a) * int(b)) % int(q) for a, b, q in zip(c, y, m)], dtype=np.int64)
-    np.testing.assert_array_equal(got, want)
+    assert np.all((got >= 0) & (got <= m))
+    np.testing.assert_array_equal(got % m, want)
 
 
 def test_int8_digit_range_random():
