@@ -35,7 +35,7 @@ HIP_FLAGS = [
 HIP_SOURCES = {
     "oz_dev.hip": [],
     "oz_scale.hip": [],
-    "oz2_split.hip": ["-fgpu-flush-denormals-to-zero"],
+    "oz2_split.hip": ["-fgpu-flush-denormals-to-zero", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "oz_gemm.hip": [],
     "oz2_crt.hip": [],
     "oz1_slice.hip": ["-fgpu-flush-denormals-to-zero"],

@@ -26,6 +26,12 @@ struct SplitConsts {
     uint32_t magic[OZ2_MAXS];
     uint32_t badd[OZ2_MAXS];
     int mneg[OZ2_MAXS];  // 2^24 - m
+    // The plane lists of the blocked splitter (ResidueGen::run): the odd moduli from 17 up in pairs
+    // for the matrix-core dot products (planes pair[g][0], pair[g][1]; a last single modulus is paired
+    // with itself), and the odd moduli below 17 (small[0..nsmall)).
+    int npair, nsmall;
+    int pair[(OZ2_MAXS + 1) / 2][2];
+    int small[OZ2_MAXS];
 };
 
 // Step 2: nd digits, top first.
@@ -155,6 +161,17 @@ __device__ __forceinline__ void residues_odd_int(const uint32_t (*a)[W], const u
     // and it is that of u - q m
 #pragma unroll
     for (int e = 0; e < 16; e++) asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(x[e]) : "v"(q[e]), "s"(mneg), "v"(u[e]));
+}
+
+// The remainder step of residues_odd_int for one sum u in [0, 2^U) (the dot products computed
+// elsewhere, for example on the matrix cores).
+template <int W>
+__device__ __forceinline__ int reduce_odd_int(int u, uint32_t magic, int mneg) {
+    constexpr int sh = 24 - dot_bits<W>();
+    const uint32_t q = (uint32_t)(((unsigned long long)(((uint32_t)u << sh) & 0xFFFFFFu) * (magic & 0xFFFFFFu)) >> 32);
+    int x;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(x) : "v"(q), "s"(mneg), "v"(u));
+    return x;
 }
 
 // The symmetric residue of A' (balanced bytes a) modulo an odd m, as an FP32 integer.

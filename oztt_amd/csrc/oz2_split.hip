@@ -101,10 +101,27 @@ __global__ void __launch_bounds__(256) split_tran_kernel(const double* __restric
 
 // Layouts 2/3 (OZ_BLOCK tiles): split_block_kernel of oz_tf32.hpp with this generator: the state of
 // an element is A' in balanced base-256 bytes and its residue modulo the even modulus, if the set
-// has one (from the reference's sequence on the digits); plane s is the residue modulo m_s (odd
-// moduli: byte dot products and one FP32 reduction, oz2_residue.hpp).
+// has one (from the reference's sequence on the digits); plane s is the residue modulo m_s. The
+// generator runs the planes itself: the even modulus, the odd moduli below 17 (byte dot products and
+// one FP32 reduction, oz2_residue.hpp), then the odd moduli from 17 up four at a time, with their dot
+// products on the matrix cores and the integer remainder step on the VALU.
+//
+// Matrix-core dot products for nd = 3 (8 balanced bytes per element; v_mfma_i32_16x16x64_i8, operand
+// layout as in oz_gemm.hip: lane l holds row l%16 of the first operand and column l%16 of the second,
+// K bytes 16(l/16)..+15 of each; output register r of lane l is row 4(l/16) + r, column l%16). The
+// second operand of lane l is the bytes of two of its own elements, e in its low 8 bytes and e' in its
+// high 8. Row i = 4g + r of the first operand holds, in K chunk g only, the byte weights w_p of modulus
+// p = r%2 of a pair of moduli (symmetric residues of 256^j) over the half h = r/2 of the chunk, and zero
+// elsewhere. So D[4g + r][j] = dinit_p + w_p . (half h of the second operand of lane 16g + j), and
+// output register r of lane l is the dot product of lane l's element (e for r < 2, e' above) with
+// modulus p: every lane gets the four sums of its own two elements and two moduli, 8 MFMAs per pair of
+// moduli for its 16 elements in place of 2 v_dot4 per element and modulus. The sums are exact
+// integers, the same as the v_dot4 chain's. For nd = 4 and 5 (12 and 16 bytes) the v_dot4 chain stays.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
 template <int ND>
 struct ResidueGen {
+    static constexpr bool kDrivesPlanes = true;
     static constexpr int W = balanced_words<ND>();
     SplitConsts k;
     struct State {
@@ -117,31 +134,87 @@ struct ResidueGen {
         balanced_bytes<ND>(dig, st.a);
         st.even = k.even >= 0 ? residue<ND>(dig, k, k.even) : 0;
     }
-    // one branch per plane, on the plane index (uniform); each branch hands its own values to emit.
-    // Odd moduli from 17 up give x = r + (m-1)/2, four of which the fix turns into r: adding
-    // 128 - (m-1)/2 keeps every byte in [1, 255] (no carry into the next one), and xor 0x80 then
-    // subtracts 128 from each (two's complement bytes).
+    // x = r + (m-1)/2 in the low byte: adding 128 - (m-1)/2 keeps every byte in [1, 255] (no carry
+    // into the next one), and xor 0x80 then subtracts 128 from each (two's complement bytes)
     template <class EMIT>
-    __device__ __forceinline__ void planes(State* st, int s, EMIT&& emit) const {
-        int v[16];
-        if (s == k.even) {
+    __device__ __forceinline__ void emit_odd(EMIT& emit, int s, const uint32_t* pk) const {
+        const uint32_t badd = k.badd[s];
+        uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 16; e++) v[e] = st[e].even;
-            emit(v, NoFix{});
-        } else if (k.magic[s]) {
-            const uint32_t badd = k.badd[s];
-            uint32_t a[16][W];
+        for (int c = 0; c < 4; c++) w[c] = (pk[c] + badd) ^ 0x80808080u;
+        emit(s, w);
+    }
+    template <class EMIT>
+    __device__ __forceinline__ void run(State* st, EMIT&& emit) const {
+        uint32_t w[4];
+        if (k.even >= 0) {
 #pragma unroll
-            for (int e = 0; e < 16; e++)
+            for (int c = 0; c < 4; c++) w[c] = pack4(st[4 * c].even, st[4 * c + 1].even, st[4 * c + 2].even, st[4 * c + 3].even);
+            emit(k.even, w);
+        }
+        for (int i = 0; i < k.nsmall; i++) {
+            const int s = k.small[i];
+            int v[16];
 #pragma unroll
-                for (int i = 0; i < W; i++) a[e][i] = st[e].a[i];
-            residues_odd_int<W>(a, k.w[s], k.dinit[s], k.magic[s], k.mneg[s], v);
-            emit(v, [badd](uint32_t w) { return (w + badd) ^ 0x80808080u; });
+            for (int e = 0; e < 16; e++) v[e] = (int)residue_odd<W>(st[e].a, k.w[s], k.m[s], k.rinv[s]);
+#pragma unroll
+            for (int c = 0; c < 4; c++) w[c] = pack4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+            emit(s, w);
+        }
+        if constexpr (W == 2) {
+            const int lane = threadIdx.x & 63, r = lane & 3;
+            const bool on = (lane >> 4) == ((lane & 15) >> 2);
+            for (int g = 0; g < k.npair; g++) {
+                const int s0 = __builtin_amdgcn_readfirstlane(k.pair[g][0]);
+                const int s1 = __builtin_amdgcn_readfirstlane(k.pair[g][1]);
+                const uint32_t w00 = __builtin_amdgcn_readfirstlane(k.w[s0][0]), w01 = __builtin_amdgcn_readfirstlane(k.w[s0][1]);
+                const uint32_t w10 = __builtin_amdgcn_readfirstlane(k.w[s1][0]), w11 = __builtin_amdgcn_readfirstlane(k.w[s1][1]);
+                const uint32_t lo = (r & 1) ? w10 : w00, hi = (r & 1) ? w11 : w01;
+                const bool h = (r >> 1) != 0;
+                const v4i_t wa = {on && !h ? (int)lo : 0, on && !h ? (int)hi : 0, on && h ? (int)lo : 0, on && h ? (int)hi : 0};
+                const int d0 = k.dinit[s0], d1 = k.dinit[s1];
+                const v4i_t c0 = {d0, d1, d0, d1};
+                const uint32_t mg0 = k.magic[s0], mg1 = k.magic[s1];
+                const int mn0 = k.mneg[s0], mn1 = k.mneg[s1];
+                uint32_t pk0[4], pk1[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    int x0[4], x1[4];
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const State& ea = st[4 * c + 2 * t];
+                        const State& eb = st[4 * c + 2 * t + 1];
+                        const v4i_t b = {(int)ea.a[0], (int)ea.a[1], (int)eb.a[0], (int)eb.a[1]};
+                        const v4i_t u = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, b, c0, 0, 0, 0);
+                        x0[2 * t] = reduce_odd_int<W>(u[0], mg0, mn0);
+                        x1[2 * t] = reduce_odd_int<W>(u[1], mg1, mn1);
+                        x0[2 * t + 1] = reduce_odd_int<W>(u[2], mg0, mn0);
+                        x1[2 * t + 1] = reduce_odd_int<W>(u[3], mg1, mn1);
+                    }
+                    pk0[c] = pack4(x0[0], x0[1], x0[2], x0[3]);
+                    pk1[c] = pack4(x1[0], x1[1], x1[2], x1[3]);
+                }
+                emit_odd(emit, s0, pk0);
+                if (s1 != s0) emit_odd(emit, s1, pk1);
+            }
         } else {
-            const float m = k.m[s], rinv = k.rinv[s];
+            for (int g = 0; g < k.npair; g++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) v[e] = (int)residue_odd<W>(st[e].a, k.w[s], m, rinv);
-            emit(v, NoFix{});
+                for (int p = 0; p < 2; p++) {
+                    const int s = k.pair[g][p];
+                    if (p == 1 && s == k.pair[g][0]) break;
+                    uint32_t a[16][W];
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+#pragma unroll
+                        for (int i = 0; i < W; i++) a[e][i] = st[e].a[i];
+                    int v[16];
+                    residues_odd_int<W>(a, k.w[s], k.dinit[s], k.magic[s], k.mneg[s], v);
+                    uint32_t pk[4];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) pk[c] = pack4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+                    emit_odd(emit, s, pk);
+                }
         }
     }
 };
@@ -241,6 +314,13 @@ SplitConsts split_consts(const oz2_moduli_dev* mo, int* evens) {
         if (m % 2 == 0) {
             k.even = s;
             (*evens)++;
+        } else if (m < 17) {
+            k.small[k.nsmall++] = s;
+        } else if (k.npair && k.pair[k.npair - 1][1] < 0) {
+            k.pair[k.npair - 1][1] = s;
+        } else {
+            k.pair[k.npair][0] = s;
+            k.pair[k.npair++][1] = -1;
         }
         int p = 1;  // 256^j mod m
         for (int i = 0; i < 4; i++) {
@@ -253,6 +333,8 @@ SplitConsts split_consts(const oz2_moduli_dev* mo, int* evens) {
             k.w[s][i] = word;
         }
     }
+    if (k.npair && k.pair[k.npair - 1][1] < 0)  // a last single modulus is paired with itself (stored once)
+        k.pair[k.npair - 1][1] = k.pair[k.npair - 1][0];
     return k;
 }
 
