@@ -131,7 +131,8 @@ __device__ __forceinline__ int32_t key_delta(uint32_t key, int shift, uint32_t& 
 // A's rows and B's columns in one launch of 1024-thread workgroups, deltas written directly:
 //   workgroup j < ceil(N/16): columns 16j..16j+15 of B over all of its K rows, thread t taking
 //   column t % 16 and every 64th row from t / 16 (a wave reads four 128-byte row pieces per load);
-//   workgroup ceil(N/16) + r: row r of A, each thread a stride-1024 run of its K values.
+//   workgroup ceil(N/16) + r: rows rR..rR+R-1 of A (R = 1 for K > 4096, more for shorter rows), each
+//   thread a stride-(1024/R) run of its row's K values.
 // The column strips read 16 K doubles each workgroup, the rows K: the long strips are dispatched
 // first and the short rows fill in behind them, so no strip is left running alone at the end.
 // The 16 waves' maxima meet in LDS; flags[0] (A) and flags[1] (B) collect the flag bits with atomicOr.
@@ -139,38 +140,37 @@ template <int CEIL>
 __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restrict__ A, int M, int K, int lda,
                                                           const double* __restrict__ B, int N, int ldb, int shift,
                                                           int32_t* __restrict__ dA, int32_t* __restrict__ dB,
-                                                          uint32_t* __restrict__ flags) {
+                                                          uint32_t* __restrict__ flags, int rows_per_wg) {
     __shared__ uint32_t part[1024];
     const int t = threadIdx.x;
     const int strips = (N + 15) / 16;
     if ((int)blockIdx.x >= strips) {
-        const int i = (int)blockIdx.x - strips;
-        const double* row = A + (size_t)i * lda;
-        // up to 8 loads in flight per thread: a whole row of K <= 8192 in one round trip
+        // R rows per workgroup (rows_per_wg: R = 8192 / K rounded down to a power of two, 1..16), so
+        // that every thread has 8 loads in flight for K <= 8192: the 1024 / R threads of a row take a
+        // stride-(1024 / R) run of its K values each, and its 16 / R waves meet in LDS.
+        const int R = rows_per_wg, T = 1024 / R;
+        const int q = t / T, tt = t - q * T;
+        const int i = ((int)blockIdx.x - strips) * R + q;
         uint32_t k[4] = {0, 0, 0, 0};
-        int c = t;
-        for (; c + 7168 < K; c += 8192) {
-            double v[8];
+        if (i < M) {
+            const double* row = A + (size_t)i * lda;
+            int c = tt;
+            for (; c + 7 * T < K; c += 8 * T) {
+                double v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = row[c + 1024 * u];
+                for (int u = 0; u < 8; u++) v[u] = row[c + T * u];
 #pragma unroll
-            for (int u = 0; u < 8; u++) k[u & 3] = max(k[u & 3], bf16_key<CEIL>(v[u]));
+                for (int u = 0; u < 8; u++) k[u & 3] = max(k[u & 3], bf16_key<CEIL>(v[u]));
+            }
+            for (; c < K; c += T) k[0] = max(k[0], bf16_key<CEIL>(row[c]));
         }
-        for (; c + 3072 < K; c += 4096) {
-            double v[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) v[u] = row[c + 1024 * u];
-#pragma unroll
-            for (int u = 0; u < 4; u++) k[u] = max(k[u], bf16_key<CEIL>(v[u]));
-        }
-        for (; c < K; c += 1024) k[0] = max(k[0], bf16_key<CEIL>(row[c]));
         const uint32_t kk = wave_max(max(max(k[0], k[1]), max(k[2], k[3])));
         if ((t & 63) == 0) part[t >> 6] = kk;
         __syncthreads();
-        if (t == 0) {
+        if (tt == 0 && i < M) {
+            const int wpr = 16 / R;  // waves per row
             uint32_t m = 0;
-#pragma unroll
-            for (int w = 0; w < 16; w++) m = max(m, part[w]);
+            for (int w = 0; w < wpr; w++) m = max(m, part[q * wpr + w]);
             uint32_t bad;
             dA[i] = key_delta(m, shift, bad);
             if (bad) atomicOr(&flags[0], bad);
@@ -266,14 +266,16 @@ extern "C" int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int
         ceil_mode > 2 || ((uintptr_t)flags & 3))
         return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: invalid arguments (M=%d N=%d K=%d lda=%d ldb=%d ceil=%d)",
                         M, N, K, lda, ldb, ceil_mode);
-    const long long blocks = (long long)M + (N + 15) / 16;
+    int R = 1;  // rows of A per workgroup: 8 loads per thread for K <= 8192
+    while (R < 16 && (long long)K * R * 2 <= 8192) R *= 2;
+    const long long blocks = ((long long)M + R - 1) / R + (N + 15) / 16;
     if (blocks > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: grid too large");
     const dim3 grid((unsigned)blocks), block(1024);
     if (ceil_mode == 0)
-        hipLaunchKernelGGL(scale_pair_kernel<0>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags);
+        hipLaunchKernelGGL(scale_pair_kernel<0>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
     else if (ceil_mode == 1)
-        hipLaunchKernelGGL(scale_pair_kernel<1>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags);
+        hipLaunchKernelGGL(scale_pair_kernel<1>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
     else
-        hipLaunchKernelGGL(scale_pair_kernel<2>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags);
+        hipLaunchKernelGGL(scale_pair_kernel<2>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
     return oz::launch_check(dev, "scale_pair_kernel");
 }
