@@ -117,7 +117,7 @@ struct CrtLimbs40 {
     double delta;  // exact-path threshold: 2^-28 + 2/M
     double Q[OZ2_MAXS][kMaxLimbs40];  // limbs of Q_s times 2^984: a digit k enters as k 2^-1074
     double Mw[kMaxLimbs40], Mhalf[kMaxLimbs40], Mrest[kMaxLimbs40];  // limbs times 2^-90
-    double two90, two52;  // 2^90, 2^52 (kernel arguments: scalar registers, not literals)
+    double pow40[kMaxLimbs40];  // 2^(40 l): the weights of the limbs (scalar registers, not literals)
 };
 
 // Carry propagation: limbs 0..L-2 into [0, 2^W), the top limb keeps the sign. Exact: every value is
@@ -141,24 +141,46 @@ __device__ __forceinline__ int limb_sign(const double* x) {
     return nz ? 1 : 0;
 }
 
-// Byte40 limbs (normalized, each an integer in [0, 2^40) times 2^-90) -> words_to_double. A limb's
-// integer is read from the mantissa of y 2^90 + 2^52 (exact); the 40-bit limbs are packed into
-// 64-bit words by constant shifts.
+// Half an ulp of a positive normal double (2^(e - 53) for s in [2^e, 2^(e+1))), from its exponent bits.
+__device__ __forceinline__ double half_ulp(double s) {
+    return __hiloint2double((__double2hiint(s) & 0x7FF00000) - (53 << 20), 0);
+}
+
+// Byte40 limbs (normalized, each an integer in [0, 2^40) times 2^-90) -> V 2^e2 rounded to nearest-even,
+// negated if neg; 0 when V = 0, signed zero below 2^-1022 (f64_tf.h:45-47), infinity above the FP64
+// range. A cascade of exact FP64 additions from the top limb down, s_j = RN(s_(j-1) + T_j) with T_j the
+// j-th limb from the top at its weight, each stage's error from FastTwoSum (|s| >= |T_j| or s = 0). At
+// most one stage rounds: the terms below a rounding stage are worth less than half an ulp of it, so
+// the later sums return it unchanged. s is therefore RN(V), except when that stage's error was
+// exactly +ulp/2 (the tie went down to the even neighbour) and a nonzero term remains below it: V is
+// then above the midpoint and s moves one ulp up. tests/test_crt_round.py checks this sequence against
+// exact rational rounding.
 template <int L>
 __device__ __forceinline__ double magnitude40(const double* x, int e2, bool neg, const CrtLimbs40& a) {
-    constexpr int NU = (40 * L + 63) / 64;
-    uint64_t U[NU];
+    double T[L];
 #pragma unroll
-    for (int k = 0; k < NU; k++) U[k] = 0;
+    for (int j = 0; j < L; j++) T[j] = x[L - 1 - j] * a.pow40[L - 1 - j];  // exact: powers of two
+    double s = T[0], ek = 0.0, hk = 0.0;
+    bool have = false, lower = false;
 #pragma unroll
-    for (int l = 0; l < L; l++) {
-        const double t = __builtin_fma(x[l], a.two90, a.two52);
-        const uint64_t y = (uint64_t)__double_as_longlong(t) & 0x000000FFFFFFFFFFull;
-        const int p = 40 * l, k = p / 64, r = p % 64;
-        U[k] |= y << r;
-        if (r > 24) U[k + 1] |= y >> (64 - r);
+    for (int j = 1; j < L; j++) {
+        const double sn = s + T[j];
+        if (j < L - 1 || true) {
+            const double e = T[j] - (sn - s);
+            lower = lower || (have && T[j] != 0.0);
+            const bool first = !have && e != 0.0;
+            ek = first ? e : ek;
+            hk = first ? half_ulp(sn) : hk;
+            have = have || first;
+        }
+        s = sn;
     }
-    return words_to_double<NU, 0>(U, e2, neg);
+    const double r0 = have && lower && ek == hk ? __builtin_fma(2.0, hk, s) : s;
+    const int ex = ((__double2hiint(r0) >> 20) & 0x7FF) - 1023 + 90 + e2;  // exponent of the result
+    double r = __builtin_ldexp(r0, 90 + e2);
+    r = ex < -1022 ? 0.0 : r;
+    r = neg ? -r : r;
+    return r0 == 0.0 ? 0.0 : r;
 }
 
 template <int L>
@@ -440,8 +462,7 @@ int crt_limbs40(const CrtLimbs& a, CrtLimbs40& b) {
     b.shift = a.shift;
     b.b = a.b;
     b.radix = 0x1p40;
-    b.two90 = 0x1p90;
-    b.two52 = 0x1p52;
+    for (int l = 0; l < kMaxLimbs40; l++) b.pow40[l] = std::ldexp(1.0, 40 * l);
     b.invM = std::ldexp(a.invM, 90);
     b.delta = a.delta;
     // bit length of S M (S M < 2^200): the limbs needed
