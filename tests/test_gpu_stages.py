@@ -186,7 +186,11 @@ def exact_double(cprime: int, e: int) -> float:
 
 @pytest.mark.parametrize("moduli,b,nd", [(INT8_16, 54, 3), ([255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223,
                                                               217, 211, 199, 197, 193, 191, 181, 179], 70, 4),
-                                         ([251, 241, 239], 10, 3)])
+                                         ([251, 241, 239], 10, 3),
+                                         # S M of 99 and 190 bits: 3 and 5 limbs of 40 bits in the digits kernel
+                                         ([255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217], 40, 3),
+                                         ([255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199, 197,
+                                           193, 191, 181, 179, 173, 167, 163, 157, 151], 90, 5)])
 def test_crt_exact(dev, oracle, moduli, b, nd):
     rng = np.random.default_rng(len(moduli) * 31 + b)
     Mprod = 1
