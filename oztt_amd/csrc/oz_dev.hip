@@ -56,6 +56,12 @@ int oz_dev_open(int device_id, oz_dev** out) {
             return OZ_ERR_HIP;
         }
     }
+    if (hipDeviceGetAttribute(&d->cus, hipDeviceAttributeMultiprocessorCount, device_id) != hipSuccess ||
+        hipMalloc(&d->queue, 16 * sizeof(int)) != hipSuccess ||
+        hipMemsetAsync(d->queue, 0, 16 * sizeof(int), d->stream) != hipSuccess) {  // ordered before every launch
+        oz_dev_close(d);
+        return OZ_ERR_HIP;
+    }
     *out = d;
     return OZ_OK;
 }
@@ -66,6 +72,7 @@ void oz_dev_close(oz_dev* dev) {
     if (dev->stream) (void)hipStreamSynchronize(dev->stream);
     for (auto& e : dev->events)
         if (e) (void)hipEventDestroy(e);
+    if (dev->queue) (void)hipFree(dev->queue);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
 }

@@ -45,16 +45,56 @@ enum GemmMode { PRODUCTS = 0, DIGITS = 1, DIAG = 2 };
 
 constexpr int LOADS = LOADS_A + LOADS_B;  // global->LDS loads per wave per K step
 
+// The last tiles go to the XCDs that get there first. The hardware hands workgroups to the XCDs in
+// turn (workgroup w to XCD w % 8) and each XCD runs its share at its own pace; the CUs of one XCD
+// finish together, but the XCDs do not run at one speed (at C3 their last tiles ended up to 7% apart,
+// a different XCD lagging on different runs), so with a fixed tile per workgroup the slowest XCD sets
+// the launch time. So workgroup w < first runs item w of the lockstep tile sequence
+// (tile_of_lockstep) as before, and the remaining items, the last eighth of every XCD's share, form a
+// pool that the other workgroups take from in lockstep order, as they start; the grid holds 1/8 more
+// workgroups than tiles, and a workgroup that finds the pool empty ends at once. Only the pool's
+// workgroups pay for an atomic. Pool counters (per device handle, zero between launches): q[0] the
+// next item, q[1] the pool workgroups that have taken theirs; the last of them zeroes both.
+struct TilePool {
+    int* q;
+    int first, total;
+    __host__ __device__ static int first_of(int total) {
+        const int per = total / 8;
+        return 8 * (per - (per + 7) / 8);
+    }
+    // thread 0 of a workgroup w >= first, once. The second atomic is issued after the first has
+    // returned, so when the count reaches the number of pool workgroups every one of them is done with
+    // q[0]; no fence is needed (and an agent-scope release would write the XCD's L2 back).
+    __device__ int take() const {
+        const int p = atomicAdd(&q[0], 1);
+        if (atomicAdd(&q[1], 1) == (int)gridDim.x - first - 1) {
+            atomicExch(&q[0], 0);
+            atomicExch(&q[1], 0);
+        }
+        return first + p < total ? first + p : -1;
+    }
+};
+
 template <int MODE, bool EVEN>
 __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ Bt,
                                                           void* __restrict__ C, int K, int ldc, long long sA,
                                                           long long sB, long long sC, int tiles_m, int tiles_n,
-                                                          int nbatch, oz2::DigitConsts dc) {
+                                                          int nbatch, oz2::DigitConsts dc, int* __restrict__ queue) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int total = tiles_m * tiles_n * nbatch;
+    int w = blockIdx.x;
+    const TilePool pool{queue, TilePool::first_of(total), total};
+    if (w >= pool.first) {
+        __shared__ int item;
+        if (threadIdx.x == 0) item = pool.take();
+        __syncthreads();
+        w = __builtin_amdgcn_readfirstlane(item);
+        if (w < 0) return;
+    }
     int batch, tm, tn;
-    tile_of_lockstep(blockIdx.x, tiles_m, tiles_n, nbatch, batch, tm, tn);
+    tile_of_lockstep(w, tiles_m, tiles_n, nbatch, batch, tm, tn);
     // Scheme I: diagonal d has d+1 pairs; the heaviest are dispatched first.
     if constexpr (MODE == DIAG) batch = nbatch - 1 - batch;
     // The map divides with VALU code; its results are wave-uniform, so they are moved to SGPRs
@@ -260,7 +300,7 @@ const char* check_gemm(const int8_t* A, const int8_t* Bt, const void* C, int M, 
         ((uintptr_t)A & 15) || ((uintptr_t)Bt & 15) || strideA % 1024 || strideB % 1024 ||
         (batch > 1 && (strideA < (long long)M * K || strideB < (long long)N * K || strideC < (long long)M * ldc)))
         return "unsupported shape";
-    if ((long long)(M / BM) * (N / BN) * batch > 0x7FFFFFFFll) return "grid too large";
+    if ((long long)(M / BM) * (N / BN) * batch > (1ll << 30)) return "grid too large";
     return nullptr;
 }
 
@@ -268,14 +308,17 @@ template <int MODE>
 int launch_gemm(oz_dev* dev, const int8_t* A, const int8_t* Bt, void* C, int M, int N, int K, int batch, int ldc,
                 long long strideA, long long strideB, long long strideC, const oz2::DigitConsts& dc) {
     const int tiles_m = M / BM, tiles_n = N / BN;
-    const unsigned grid = (unsigned)((long long)tiles_m * tiles_n * batch);
+    const long long tiles = (long long)tiles_m * tiles_n * batch;
+    // 1/8 more workgroups than tiles (at least one more per XCD): the XCDs that run ahead take more of
+    // the pool's items, the others' spare workgroups find it empty (TilePool)
+    const unsigned grid = (unsigned)(tiles + std::max<long long>(tiles / 8, 8));
     // K/64 even: every tile has an even number of K steps (DIAG: (d+1) K/64), no tail step
     if ((K / BK) % 2 == 0)
         hipLaunchKernelGGL((gemm_i8_kernel<MODE, true>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
-                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc);
+                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue);
     else
         hipLaunchKernelGGL((gemm_i8_kernel<MODE, false>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
-                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc);
+                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue);
     return oz::launch_check(dev, "gemm_i8_kernel");
 }
 

@@ -76,7 +76,7 @@ def test_m0_only_feeds_the_lds_copies(gemm_asm):
         body = [l.strip() for l in lines if l.strip() and not l.strip().startswith(";")]
         for i, l in enumerate(body):
             if re.search(r"\bm0\b", l):
-                assert re.match(r"s_mov_b32 m0, s\d+$", l), (name, l)
+                assert re.match(r"s_mov_b32 m0, (s\d+|vcc_lo|vcc_hi)$", l), (name, l)  # an SGPR (VCC is one)
                 assert body[i + 1].startswith("global_load_lds_dwordx4"), (name, l, body[i + 1])
 
 
