@@ -14,8 +14,7 @@ struct oz_dev {
     hipStream_t stream = nullptr;
     hipEvent_t events[64] = {};
     std::string error;
-    int cus = 0;            // compute units of the device (the persistent product kernels' grid)
-    int* queue = nullptr;   // work queue of the product kernels (16 ints, zero between launches)
+    int* queue = nullptr;   // tile pool counters of the INT8 product kernel (16 ints, zero between launches)
 };
 
 namespace oz {
