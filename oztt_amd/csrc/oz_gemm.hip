@@ -256,7 +256,6 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
             }
         uint8_t* Cb = static_cast<uint8_t*>(C) + c0;
         const double md = (double)m, yr = (double)y / md;
-        auto dg = [&](int32_t c) -> uint32_t { return oz2::mod_mul_f64((double)c, yr, md); };
 #pragma unroll
         for (int h = 0; h < 2; h++) {
 #pragma unroll
@@ -272,12 +271,15 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
             for (int t = 0; t < 8; t++) {
                 const int e = 64 * t + lane, row = e >> 3, cg = e & 7;
                 const int* src = tile + row * 128 + ((16 * cg) ^ (16 * ((row >> 2) & 3)));
-                uint32_t w[4];
+                int32_t c[16];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const v4i v = *reinterpret_cast<const v4i*>(src + 4 * k);
-                    w[k] = dg(v[0]) | dg(v[1]) << 8 | dg(v[2]) << 16 | dg(v[3]) << 24;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) c[4 * k + q] = v[q];
                 }
+                uint32_t w[4];
+                oz2::mod_mul_f64_x16(c, yr, md, w);
                 *reinterpret_cast<uint4*>(Cb + (long long)(64 * h + row) * ldc + 16 * cg) = uint4{w[0], w[1], w[2], w[3]};
             }
         }

@@ -3,10 +3,10 @@ oztt_amd/csrc/oz2_modular.hpp), emulated with numpy's IEEE binary64 operations a
 exact integer arithmetic.
 
 The device function computes t = RN(c * yr) with yr = RN(y / m), f = t - floor(t) clamped below 1
-(v_fract_f64), and the truncation of RN(f * m + 1/2) (v_fma_f64, v_cvt_u32_f64): a representative
-of (c * y) mod m in [0, m], m standing for 0. The emulation rounds f * m + 1/2 in 80-bit extended
-precision before binary64; f * m + 1/2 lies within 2^-13 of r + 1/2 for an integer r, so neither
-rounding can change its integer part. The kernels use it for the CRT digit of an int32 product
+(v_fract_f64), and RN(f * m + 2^52) (v_fma_f64), whose low 32 bits are the result: a representative
+of (c * y) mod m in [0, m], m standing for 0. The emulation rounds f * m + 2^52 in 80-bit extended
+precision before binary64; f * m lies within 2^-13 of an integer r, so neither rounding can move the
+sum off 2^52 + r. The kernels use it for the CRT digit of an int32 product
 (|c| < 2^31, y < m <= 255: reference recon_crt.cpp:293's residue step) and for the FP8 route's terms
 (|P| < 2^24, coef < m <= 2401). CPU only.
 """
@@ -18,10 +18,12 @@ def mod_mul_f64(c: np.ndarray, y: np.ndarray, m: np.ndarray) -> np.ndarray:
     yr = y.astype(np.float64) / md
     t = c.astype(np.float64) * yr
     f = np.minimum(t - np.floor(t), np.nextafter(1.0, 0.0))
-    g = (f.astype(np.longdouble) * md.astype(np.longdouble) + np.longdouble(0.5)).astype(np.float64)
-    # the margin the truncation relies on: f m is within 1/4 of an integer
-    assert np.all(np.abs(g - 0.5 - np.rint(g - 0.5)) < 0.25)
-    return np.trunc(g).astype(np.int64)
+    p = f.astype(np.longdouble) * md.astype(np.longdouble)
+    # the margin the rounding relies on: f m is within 1/4 of an integer
+    assert np.all(np.abs(p - np.rint(p)) < 0.25)
+    g = (p + np.longdouble(2.0**52)).astype(np.float64)
+    assert np.all((g >= 2.0**52) & (g < 2.0**53))
+    return (g.view(np.uint64) & np.uint64(0xFFFFFFFF)).astype(np.int64)
 
 
 def _check(c, y, m):
