@@ -217,7 +217,7 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
     // roles). EVEN kernels (an even number of K steps in every tile: K/64 even) have no tail; the
     // others end an odd count with one more step.
     int kt = 0;
-    for (; kt + 1 < nst; kt += 2) {
+    auto trip = [&]() {
         wait_vmcnt_lgkm0<LOADS * (NS - 2)>();
         stage_barrier();
         substep(fa, fb, ga, gb, (kt + 1) % NS, kt % NS, min(kt + NS, nst - 1));
@@ -226,6 +226,25 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
         stage_barrier();
         substep(ga, gb, fa, fb, (kt + 2) % NS, (kt + 1) % NS, min(kt + 1 + NS, nst - 1));
         next_stage();
+        kt += 2;
+    };
+    // EVEN: K/64 is even and positive, so every tile has at least two steps; a loop that tests first
+    // makes the compiler keep a path around it and zero the 256 accumulators twice on the way in.
+    // (DIGITS only: in the other modes the bottom-tested loop moves accumulators inside the loop.)
+    if constexpr (EVEN && MODE == DIGITS) {
+        do trip();
+        while (kt < nst);
+    } else {
+        for (; kt + 1 < nst; kt += 2) {
+            wait_vmcnt_lgkm0<LOADS * (NS - 2)>();
+            stage_barrier();
+            substep(fa, fb, ga, gb, (kt + 1) % NS, kt % NS, min(kt + NS, nst - 1));
+            next_stage();
+            wait_vmcnt_lgkm0<LOADS * (NS - 2)>();
+            stage_barrier();
+            substep(ga, gb, fa, fb, (kt + 2) % NS, (kt + 1) % NS, min(kt + 1 + NS, nst - 1));
+            next_stage();
+        }
     }
     if constexpr (!EVEN) {
         if (kt < nst) {
