@@ -237,11 +237,15 @@ __device__ __forceinline__ void split_block(const double* __restrict__ X, int ro
 #pragma unroll
     for (int e = 0; e < 16; e++) gen.load(st[e], xv[e], dv[e]);
     if constexpr (drives_planes<GEN>::value) {
+        // The planes (17 x 2 x 64 MiB at C3) are read back only by the product kernel, long after
+        // the Infinity Cache has turned over: non-temporal stores (2-6% faster split).
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
         if constexpr (TRAN) {
             const int rr = lane >> 2;
             uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
             gen.run(st, [&](int p, const uint32_t* w) {
-                out[(long long)p * pstride_chunks] = make_uint4(w[0], w[1], w[2], w[3]);
+                __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]},
+                                            reinterpret_cast<u32x4*>(out + (long long)p * pstride_chunks));
             });
         } else {
             __shared__ __attribute__((aligned(16))) uint8_t image[4][1024];
@@ -252,7 +256,8 @@ __device__ __forceinline__ void split_block(const double* __restrict__ X, int ro
 #pragma unroll
                 for (int e = 0; e < 16; e++)
                     img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)(w[e >> 2] >> (8 * (e & 3)));
-                out[(long long)p * pstride_chunks] = *reinterpret_cast<const uint4*>(img + 16 * lane);
+                __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(img + 16 * lane),
+                                            reinterpret_cast<u32x4*>(out + (long long)p * pstride_chunks));
             });
         }
     } else if constexpr (TRAN) {
