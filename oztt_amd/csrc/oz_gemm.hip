@@ -299,7 +299,11 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
                 }
                 uint32_t w[4];
                 oz2::mod_mul_f64_x16(c, yr, md, w);
-                *reinterpret_cast<uint4*>(Cb + (long long)(64 * h + row) * ldc + 16 * cg) = uint4{w[0], w[1], w[2], w[3]};
+                // non-temporal: the digits (1.1 GB at C3) would only push the operand planes of the
+                // modulus in progress out of the Infinity Cache
+                typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]},
+                                            reinterpret_cast<u32x4*>(Cb + (long long)(64 * h + row) * ldc + 16 * cg));
             }
         }
     } else {
