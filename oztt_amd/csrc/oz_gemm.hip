@@ -307,6 +307,7 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
             }
         }
     } else {
+        // non-temporal, as the digits: the int32 sums (C2: 512 MB) need not displace the operand planes
         int32_t* Cb = static_cast<int32_t*>(C) + c0;
 #pragma unroll
         for (int i = 0; i < 8; i++)
@@ -314,7 +315,8 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
             for (int j = 0; j < 8; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++)
-                    Cb[(long long)(16 * i + 4 * (lane >> 4) + q) * ldc + 16 * j + (lane & 15)] = acc[i][j][q];
+                    __builtin_nontemporal_store(acc[i][j][q],
+                                                &Cb[(long long)(16 * i + 4 * (lane >> 4) + q) * ldc + 16 * j + (lane & 15)]);
     }
 }
 
