@@ -314,8 +314,10 @@ __global__ void __launch_bounds__(256) crt_digits_kernel(const uint8_t* __restri
     for (int e = 0; e < 4; e++) r[e] = j0 + e < N ? crt_finish<L>(x[e], a, gi - dB[j0 + e]) : 0.0;
     double* o = out + (long long)i * ldo + j0;
     if (j0 + 3 < N && !(reinterpret_cast<uintptr_t>(o) & 15)) {
-        reinterpret_cast<double2*>(o)[0] = make_double2(r[0], r[1]);
-        reinterpret_cast<double2*>(o)[1] = make_double2(r[2], r[3]);
+        // non-temporal: C (512 MB at C3) is not read again by the pass (0.418 against 0.431 ms)
+        typedef double f64x2 __attribute__((ext_vector_type(2)));
+        __builtin_nontemporal_store(f64x2{r[0], r[1]}, reinterpret_cast<f64x2*>(o));
+        __builtin_nontemporal_store(f64x2{r[2], r[3]}, reinterpret_cast<f64x2*>(o) + 1);
     } else {
 #pragma unroll
         for (int e = 0; e < 4; e++)
