@@ -141,7 +141,8 @@ __global__ void __launch_bounds__(256) recon_kernel(const int32_t* __restrict__ 
         }
     }
     const uint64_t u = assemble_tf_f64(hi, mid, lo, -(dA[i] + dB[j]), W, qw);
-    out[(long long)i * ldo + j] = __longlong_as_double((long long)u);
+    // non-temporal: C is not read again by the pass
+    __builtin_nontemporal_store(__longlong_as_double((long long)u), &out[(long long)i * ldo + j]);
 }
 
 // One K block of the reconstruction that runs block by block (reference recon_tf_f32in.cpp:54-89

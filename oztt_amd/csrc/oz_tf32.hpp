@@ -262,14 +262,17 @@ __device__ __forceinline__ void split_block(const double* __restrict__ X, int ro
         }
     } else if constexpr (TRAN) {
         // GEN::planes(st, s, emit) computes plane s's 16 values v and calls emit(v, fix) once, where
-        // fix(w) maps four packed values to the bytes stored; emit packs and stores them.
+        // fix(w) maps four packed values to the bytes stored; emit packs and stores them (non-temporal,
+        // as above).
         const int rr = lane >> 2;
         uint4* out = planes + blk * 64 + rr * 4 + ((lane & 3) ^ block_swizzle(rr));
         for (int s = 0; s < nplanes; s++) {
             gen.planes(st, s, [&](const int* v, auto fix) {
-                out[(long long)s * pstride_chunks] =
-                    make_uint4(fix(pack4(v[0], v[1], v[2], v[3])), fix(pack4(v[4], v[5], v[6], v[7])),
-                               fix(pack4(v[8], v[9], v[10], v[11])), fix(pack4(v[12], v[13], v[14], v[15])));
+                typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                __builtin_nontemporal_store(
+                    u32x4{fix(pack4(v[0], v[1], v[2], v[3])), fix(pack4(v[4], v[5], v[6], v[7])),
+                          fix(pack4(v[8], v[9], v[10], v[11])), fix(pack4(v[12], v[13], v[14], v[15]))},
+                    reinterpret_cast<u32x4*>(out + (long long)s * pstride_chunks));
             });
         }
     } else {
@@ -283,7 +286,9 @@ __device__ __forceinline__ void split_block(const double* __restrict__ X, int ro
 #pragma unroll
                 for (int e = 0; e < 16; e++) img[64 * e + (colpart ^ (16 * block_swizzle(e))) + colbyte] = (uint8_t)v[e];
                 const uint4 w = *reinterpret_cast<const uint4*>(img + 16 * lane);
-                out[(long long)s * pstride_chunks] = make_uint4(fix(w.x), fix(w.y), fix(w.z), fix(w.w));
+                typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                __builtin_nontemporal_store(u32x4{fix(w.x), fix(w.y), fix(w.z), fix(w.w)},
+                                            reinterpret_cast<u32x4*>(out + (long long)s * pstride_chunks));
             });
         }
     }
