@@ -10,6 +10,10 @@
  *     of the last failure of a device handle is oz_last_error().
  *   - All launches are ordered on the handle's own HIP stream (default priority); device pointers
  *     are plain addresses from oz_dev_malloc (or any HIP allocation on the same device).
+ *   - A handle holds 64 bytes of device counters through which its product kernels hand out their
+ *     last tiles (zero between launches; each launch leaves them zero). Launches through one handle
+ *     must therefore not overlap in time: use one handle per stream (or per thread), and do not
+ *     replay a graph captured from a handle's stream while that handle has other work in flight.
  *   - Matrices are row-major. "Planes" are the per-modulus (Scheme II) or per-slice (Scheme I)
  *     integer matrices; their layout is given with each function.
  *   - Sizes are checked against what the kernels assume before anything is launched; a mismatch
