@@ -261,6 +261,43 @@ def test_gemm_digits_exact(dev, M, N, K, S):
         assert_residues(D[s], want, m, f"modulus {m}")
 
 
+def test_gemm_tile_pool_counts(dev):
+    """The last eighth of every XCD's tiles is handed out through counters in the device handle, which
+    each launch must leave at zero: launches of 1, 7, 9, 63, 65 and 1031 tiles back to back on one
+    handle, int32 products (K/64 odd) and CRT digits (K/64 even), every output first filled with a
+    sentinel, so a tile that no workgroup ran (or a stale counter) shows."""
+    rng = np.random.default_rng(11)
+    moduli = INT8_16 + [193]
+    for M, N, batch in [(256, 256, 1), (256, 256, 7), (256, 768, 3), (768, 768, 7), (256, 1280, 13),
+                        (256, 256, 1031)]:
+        # digits: one batch per modulus, so at most the 17 moduli of the set (1031 tiles: int32 only)
+        for digits in (False, True) if batch <= len(moduli) else (False,):
+            K = 128 if digits else 192
+            A = rng.integers(-127, 128, (batch, M, K), dtype=np.int8)
+            Bt = rng.integers(-127, 128, (batch, N, K), dtype=np.int8)
+            bA, bB = dev.upload(to_blocks(A)), dev.upload(to_blocks(Bt))
+            esz = 1 if digits else 4
+            out = dev.alloc(esz * batch * M * N)
+            dev.fill_u32(out, 0xA5A5A5A5, esz * batch * M * N // 4)
+            if digits:
+                mods = moduli[:batch]
+                desc = crt_desc(mods, 54, 3)
+                dev.gemm_digits(bA, bB, out, M, N, K, batch, N, M * K, N * K, M * N, desc)
+                got = dev.download(out, np.uint8, batch * M * N).reshape(batch, M, N)
+            else:
+                dev.gemm_i8(bA, bB, out, M, N, K, batch, N, M * K, N * K, M * N)
+                got = dev.download(out, np.int32, batch * M * N).reshape(batch, M, N)
+            for x in (bA, bB, out):
+                x.free()
+            dev.bufs.clear()
+            prod = np.matmul(A.astype(np.float64), Bt.astype(np.float64).transpose(0, 2, 1)).astype(np.int64)
+            for t in range(batch):
+                if digits:
+                    assert_residues(got[t], (prod[t] % mods[t]) * int(desc.y[t]), mods[t], f"{batch} tiles, batch {t}")
+                else:
+                    np.testing.assert_array_equal(got[t].astype(np.int64), prod[t], err_msg=f"{batch} tiles, batch {t}")
+
+
 @pytest.mark.parametrize("M,N,K,S,digits", [(256, 256, 256, 300, False), (256, 512, 384, 150, False),
                                              (1024, 1024, 256, 20, True), (768, 1024, 384, 23, True)])
 def test_gemm_tile_sequences(dev, M, N, K, S, digits):
