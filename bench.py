@@ -47,7 +47,7 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, 5.0 PFLOP/s
 # HBM bytes per launch of the product kernel at n = 8192 (17 moduli), from the rocprofv3 FETCH_SIZE and
 # WRITE_SIZE passes over this script scaled by the counters' readings for a plain 1 GiB copy
 # (factors 2.000 and 1.000): profiles/scheme2_int8_c3_8192_traffic.md.
-C3_GEMM_TRAFFIC_BYTES = 17.70e9
+C3_GEMM_TRAFFIC_BYTES = 16.31e9
 
 
 def log(msg: str) -> None:

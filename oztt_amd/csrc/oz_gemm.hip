@@ -50,17 +50,18 @@ constexpr int LOADS = LOADS_A + LOADS_B;  // global->LDS loads per wave per K st
 // finish together, but the XCDs do not run at one speed (at C3 their last tiles ended up to 7% apart,
 // a different XCD lagging on different runs), so with a fixed tile per workgroup the slowest XCD sets
 // the launch time. So workgroup w < first runs item w of the lockstep tile sequence
-// (tile_of_lockstep) as before, and the remaining items, the last eighth of every XCD's share, form a
-// pool that the other workgroups take from in lockstep order, as they start; the grid holds 1/8 more
-// workgroups than tiles, and a workgroup that finds the pool empty ends at once. Only the pool's
-// workgroups pay for an atomic. Pool counters (per device handle, zero between launches): q[0] the
+// (tile_of_lockstep) as before, and the remaining items, the last sixteenth of every XCD's share
+// (room enough for the speed differences seen; a pool tile mostly runs where its bands are not in
+// L2, so a larger pool costs traffic), form a pool that the other workgroups take from in lockstep
+// order, as they start; the grid holds 1/8 more workgroups than tiles, and a workgroup that finds
+// the pool empty ends at once. Only the pool's workgroups pay for an atomic. Pool counters (per device handle, zero between launches): q[0] the
 // next item, q[1] the pool workgroups that have taken theirs; the last of them zeroes both.
 struct TilePool {
     int* q;
     int first, total;
     __host__ __device__ static int first_of(int total) {
         const int per = total / 8;
-        return 8 * (per - (per + 7) / 8);
+        return 8 * (per - (per + 15) / 16);
     }
     // thread 0 of a workgroup w >= first, once. The second atomic is issued after the first has
     // returned, so when the count reaches the number of pool workgroups every one of them is done with
