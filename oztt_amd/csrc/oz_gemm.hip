@@ -52,16 +52,17 @@ constexpr int LOADS = LOADS_A + LOADS_B;  // global->LDS loads per wave per K st
 // the launch time. So workgroup w < first runs item w of the lockstep tile sequence
 // (tile_of_lockstep) as before, and the remaining items, the last sixteenth of every XCD's share
 // (room enough for the speed differences seen; a pool tile mostly runs where its bands are not in
-// L2, so a larger pool costs traffic), form a pool that the other workgroups take from in lockstep
+// L2, so a larger pool costs traffic; an eighth for Scheme I's diagonals), form a pool that the other workgroups take from in lockstep
 // order, as they start; the grid holds 1/8 more workgroups than tiles, and a workgroup that finds
 // the pool empty ends at once. Only the pool's workgroups pay for an atomic. Pool counters (per device handle, zero between launches): q[0] the
 // next item, q[1] the pool workgroups that have taken theirs; the last of them zeroes both.
 struct TilePool {
     int* q;
     int first, total;
-    __host__ __device__ static int first_of(int total) {
+    // items of every XCD's share left to the pool: 1/frac of it
+    __host__ __device__ static int first_of(int total, int frac) {
         const int per = total / 8;
-        return 8 * (per - (per + 15) / 16);
+        return 8 * (per - (per + frac - 1) / frac);
     }
     // thread 0 of a workgroup w >= first, once. The second atomic is issued after the first has
     // returned, so when the count reaches the number of pool workgroups every one of them is done with
@@ -86,7 +87,9 @@ __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restri
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int total = tiles_m * tiles_n * nbatch;
     int w = blockIdx.x;
-    const TilePool pool{queue, TilePool::first_of(total), total};
+    // Scheme I's diagonals differ up to p-fold in length and leave the XCDs further apart: a larger
+    // pool (C2: 60.8 against 60.0 TFLOP/s with a sixteenth)
+    const TilePool pool{queue, TilePool::first_of(total, MODE == DIAG ? 8 : 16), total};
     if (w >= pool.first) {
         __shared__ int item;
         if (threadIdx.x == 0) item = pool.take();
