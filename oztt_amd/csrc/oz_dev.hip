@@ -56,7 +56,8 @@ int oz_dev_open(int device_id, oz_dev** out) {
             return OZ_ERR_HIP;
         }
     }
-    if (hipMalloc(&d->queue, 16 * sizeof(int)) != hipSuccess ||
+    if (hipDeviceGetAttribute(&d->cus, hipDeviceAttributeMultiprocessorCount, device_id) != hipSuccess ||
+        hipMalloc(&d->queue, 16 * sizeof(int)) != hipSuccess ||
         hipMemsetAsync(d->queue, 0, 16 * sizeof(int), d->stream) != hipSuccess) {  // ordered before every launch
         oz_dev_close(d);
         return OZ_ERR_HIP;

@@ -54,13 +54,14 @@ constexpr int LOADS = LOADS_A + LOADS_B;  // global->LDS loads per wave per K st
 // (room enough for the speed differences seen; a pool tile mostly runs where its bands are not in
 // L2, so a larger pool costs traffic; an eighth for Scheme I's diagonals), form a pool that the other workgroups take from in lockstep
 // order, as they start; the grid holds 1/8 more workgroups than tiles, and a workgroup that finds
-// the pool empty ends at once. Only the pool's workgroups pay for an atomic. Pool counters (per device handle, zero between launches): q[0] the
+// the pool empty ends at once. Only the pool's workgroups pay for an atomic. The host sets `first`
+// (launch_gemm; a launch of one wave has no pool). Pool counters (per device handle, zero between launches): q[0] the
 // next item, q[1] the pool workgroups that have taken theirs; the last of them zeroes both.
 struct TilePool {
     int* q;
     int first, total;
     // items of every XCD's share left to the pool: 1/frac of it
-    __host__ __device__ static int first_of(int total, int frac) {
+    __host__ static int first_of(int total, int frac) {
         const int per = total / 8;
         return 8 * (per - (per + frac - 1) / frac);
     }
@@ -81,15 +82,14 @@ template <int MODE, bool EVEN>
 __global__ void __launch_bounds__(THREADS) gemm_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ Bt,
                                                           void* __restrict__ C, int K, int ldc, long long sA,
                                                           long long sB, long long sC, int tiles_m, int tiles_n,
-                                                          int nbatch, oz2::DigitConsts dc, int* __restrict__ queue) {
+                                                          int nbatch, oz2::DigitConsts dc, int* __restrict__ queue,
+                                                          int first) {
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int total = tiles_m * tiles_n * nbatch;
     int w = blockIdx.x;
-    // Scheme I's diagonals differ up to p-fold in length and leave the XCDs further apart: a larger
-    // pool (C2: 60.8 against 60.0 TFLOP/s with a sixteenth)
-    const TilePool pool{queue, TilePool::first_of(total, MODE == DIAG ? 8 : 16), total};
+    const TilePool pool{queue, first, total};
     if (w >= pool.first) {
         __shared__ int item;
         if (threadIdx.x == 0) item = pool.take();
@@ -341,15 +341,21 @@ int launch_gemm(oz_dev* dev, const int8_t* A, const int8_t* Bt, void* C, int M, 
     const int tiles_m = M / BM, tiles_n = N / BN;
     const long long tiles = (long long)tiles_m * tiles_n * batch;
     // 1/8 more workgroups than tiles (at least one more per XCD): the XCDs that run ahead take more of
-    // the pool's items, the others' spare workgroups find it empty (TilePool)
-    const unsigned grid = (unsigned)(tiles + std::max<long long>(tiles / 8, 8));
+    // the pool's items, the others' spare workgroups find it empty (TilePool). The pool is the last
+    // sixteenth of every XCD's share; Scheme I's diagonals differ up to p-fold in length and leave
+    // the XCDs further apart, so theirs is an eighth (C2: 60.8 against 60.0 TFLOP/s). A launch of
+    // at most one tile per CU runs in one wave with nothing to even out: no pool, no spare
+    // workgroups (these would start only when the first tiles end, and lengthen the launch).
+    const bool one_wave = dev->cus > 0 && tiles <= dev->cus;
+    const int first = one_wave ? (int)tiles : TilePool::first_of((int)tiles, MODE == DIAG ? 8 : 16);
+    const unsigned grid = one_wave ? (unsigned)tiles : (unsigned)(tiles + std::max<long long>(tiles / 8, 8));
     // K/64 even: every tile has an even number of K steps (DIAG: (d+1) K/64), no tail step
     if ((K / BK) % 2 == 0)
         hipLaunchKernelGGL((gemm_i8_kernel<MODE, true>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
-                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue);
+                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue, first);
     else
         hipLaunchKernelGGL((gemm_i8_kernel<MODE, false>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
-                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue);
+                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue, first);
     return oz::launch_check(dev, "gemm_i8_kernel");
 }
 

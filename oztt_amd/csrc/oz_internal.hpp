@@ -15,6 +15,7 @@ struct oz_dev {
     hipEvent_t events[64] = {};
     std::string error;
     int* queue = nullptr;   // tile pool counters of the INT8 product kernel (16 ints, zero between launches)
+    int cus = 0;            // compute units: a product launch of at most this many tiles needs no pool
 };
 
 namespace oz {
