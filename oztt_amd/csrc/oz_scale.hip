@@ -129,11 +129,12 @@ __device__ __forceinline__ int32_t key_delta(uint32_t key, int shift, uint32_t& 
 }
 
 // A's rows and B's columns in one launch of 1024-thread workgroups, deltas written directly:
-//   workgroup j < ceil(N/16): columns 16j..16j+15 of B over all of its K rows, thread t taking
-//   column t % 16 and every 64th row from t / 16 (a wave reads four 128-byte row pieces per load);
-//   workgroup ceil(N/16) + r: rows rR..rR+R-1 of A (R = 1 for K > 4096, more for shorter rows), each
+//   workgroup j < ceil(N/32): columns 32j..32j+31 of B over all of its K rows, thread t taking
+//   column t % 32 and every 32nd row from t / 32 (a wave reads two 256-byte row pieces per load;
+//   with 16 columns, 128-byte pieces, the strips read at 4.9 instead of 5.7 TB/s at C3);
+//   workgroup ceil(N/32) + r: rows rR..rR+R-1 of A (R = 1 for K > 4096, more for shorter rows), each
 //   thread a stride-(1024/R) run of its row's K values.
-// The column strips read 16 K doubles each workgroup, the rows K: the long strips are dispatched
+// The column strips read 32 K doubles each workgroup, the rows K: the long strips are dispatched
 // first and the short rows fill in behind them, so no strip is left running alone at the end.
 // The 16 waves' maxima meet in LDS; flags[0] (A) and flags[1] (B) collect the flag bits with atomicOr.
 template <int CEIL>
@@ -143,7 +144,7 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
                                                           uint32_t* __restrict__ flags, int rows_per_wg) {
     __shared__ uint32_t part[1024];
     const int t = threadIdx.x;
-    const int strips = (N + 15) / 16;
+    const int strips = (N + 31) / 32;
     if ((int)blockIdx.x >= strips) {
         // R rows per workgroup (rows_per_wg: R = 8192 / K rounded down to a power of two, 1..16), so
         // that every thread has 8 loads in flight for K <= 8192: the 1024 / R threads of a row take a
@@ -176,47 +177,47 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
             if (bad) atomicOr(&flags[0], bad);
         }
     } else {
-        const int col = (int)blockIdx.x * 16 + (t & 15);
-        const int ph = t >> 4;
-        // 16 loads in flight per thread (1024 rows of the strip per round trip)
+        const int col = (int)blockIdx.x * 32 + (t & 31);
+        const int ph = t >> 5;
+        // 16 loads in flight per thread (512 rows of the strip per round trip)
         uint32_t k[4] = {0, 0, 0, 0};
         if (col < N) {
             const double* p = B + col;
             int r = ph;
-            for (; r + 960 < K; r += 1024) {
+            for (; r + 480 < K; r += 512) {
                 double v[16];
 #pragma unroll
-                for (int u = 0; u < 16; u++) v[u] = p[(size_t)(r + 64 * u) * ldb];
+                for (int u = 0; u < 16; u++) v[u] = p[(size_t)(r + 32 * u) * ldb];
 #pragma unroll
                 for (int u = 0; u < 16; u++) k[u & 3] = max(k[u & 3], bf16_key<CEIL>(v[u]));
             }
-            for (; r + 192 < K; r += 256) {
+            for (; r + 96 < K; r += 128) {
                 double v[4];
 #pragma unroll
-                for (int u = 0; u < 4; u++) v[u] = p[(size_t)(r + 64 * u) * ldb];
+                for (int u = 0; u < 4; u++) v[u] = p[(size_t)(r + 32 * u) * ldb];
 #pragma unroll
                 for (int u = 0; u < 4; u++) k[u] = max(k[u], bf16_key<CEIL>(v[u]));
             }
-            for (; r < K; r += 64) k[0] = max(k[0], bf16_key<CEIL>(p[(size_t)r * ldb]));
+            for (; r < K; r += 32) k[0] = max(k[0], bf16_key<CEIL>(p[(size_t)r * ldb]));
         }
-        part[t] = max(max(k[0], k[1]), max(k[2], k[3]));  // part[16 ph + c]
+        part[t] = max(max(k[0], k[1]), max(k[2], k[3]));  // part[32 ph + c]
         __syncthreads();
-        // 64 phases per column: 16 threads per column take 4 phases each, then one thread 16 of those
+        // 32 phases per column: 8 threads per column take 4 phases each, then one thread 8 of those
         uint32_t m4 = 0;
         if (t < 256) {
-            const int c = t & 15, q = t >> 4;
-            m4 = max(max(part[(4 * q) * 16 + c], part[(4 * q + 1) * 16 + c]),
-                     max(part[(4 * q + 2) * 16 + c], part[(4 * q + 3) * 16 + c]));
+            const int c = t & 31, q = t >> 5;
+            m4 = max(max(part[(4 * q) * 32 + c], part[(4 * q + 1) * 32 + c]),
+                     max(part[(4 * q + 2) * 32 + c], part[(4 * q + 3) * 32 + c]));
         }
         __syncthreads();
-        if (t < 256) part[t] = m4;  // part[16 q + c]
+        if (t < 256) part[t] = m4;  // part[32 q + c]
         __syncthreads();
-        if (t < 16 && (int)blockIdx.x * 16 + t < N) {
+        if (t < 32 && (int)blockIdx.x * 32 + t < N) {
             uint32_t m = 0;
 #pragma unroll
-            for (int q = 0; q < 16; q++) m = max(m, part[q * 16 + t]);
+            for (int q = 0; q < 8; q++) m = max(m, part[q * 32 + t]);
             uint32_t bad;
-            dB[(int)blockIdx.x * 16 + t] = key_delta(m, shift, bad);
+            dB[(int)blockIdx.x * 32 + t] = key_delta(m, shift, bad);
             if (bad) atomicOr(&flags[1], bad);
         }
     }
@@ -268,7 +269,7 @@ extern "C" int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int
                         M, N, K, lda, ldb, ceil_mode);
     int R = 1;  // rows of A per workgroup: 8 loads per thread for K <= 8192
     while (R < 16 && (long long)K * R * 2 <= 8192) R *= 2;
-    const long long blocks = ((long long)M + R - 1) / R + (N + 15) / 16;
+    const long long blocks = ((long long)M + R - 1) / R + (N + 31) / 32;
     if (blocks > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: grid too large");
     const dim3 grid((unsigned)blocks), block(1024);
     if (ceil_mode == 0)
