@@ -11,8 +11,7 @@
  *   - All launches are ordered on the handle's own HIP stream (default priority); device pointers
  *     are plain addresses from oz_dev_malloc (or any HIP allocation on the same device).
  *   - A handle holds 64 bytes of device counters through which its product kernels hand out their
- *     last tiles and oz_scale_pair_f64 gathers its flags (zero between launches; each launch leaves
- *     them zero). Launches through one handle
+ *     last tiles (zero between launches; each launch leaves them zero). Launches through one handle
  *     must therefore not overlap in time: use one handle per stream (or per thread), and do not
  *     replay a graph captured from a handle's stream while that handle has other work in flight.
  *   - Matrices are row-major. "Planes" are the per-modulus (Scheme II) or per-slice (Scheme I)
@@ -87,8 +86,8 @@ int oz_scale_f64(oz_dev* dev, const double* X, int rows, int cols, int ld, int m
 
 /* Both operands of a product in one launch: the row maxima of A (M x K, lda) into dA[M] and the
  * column maxima of B (K x N, ldb) into dB[N], each as oz_scale_f64 (mode 0 for A, mode 1 for B, the
- * same ceil_mode and shift), with the range flags of A written to flags[0] and those of B to
- * flags[1] (two device words, 4-byte aligned, overwritten: they need no zeroing beforehand). */
+ * same ceil_mode and shift), with the range flags of A ORed into flags[0] and those of B into
+ * flags[1] (two device words, 4-byte aligned). */
 int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int lda, const double* B, int N, int ldb,
                       int ceil_mode, int shift, int32_t* dA, int32_t* dB, uint32_t* flags);
 

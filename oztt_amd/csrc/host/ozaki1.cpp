@@ -107,6 +107,7 @@ Output ozaki1_run(Device& D, const Problem& p) {
 
     std::vector<Step> steps;
     steps.push_back({ev::Scale, [=] {
+                         device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
                          // BF16 of the maxima rounded as the format requires, target 2^nshift (format.hpp:76-101)
                          device_check(dev,
                                       oz_scale_pair_f64(dev, dAf, (int)M, (int)K, (int)K, dBf, (int)N, (int)N,

@@ -108,6 +108,7 @@ Output ozaki2_run(Device& D, const Problem& p) {
     const int shift = plan.shift();
     std::vector<Step> steps;
     steps.push_back({ev::Scale, [=] {
+                         device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
                          // Scheme II rounds the BF16 of the maxima up (ozaki2.cpp:143-146)
                          device_check(dev,
                                       oz_scale_pair_f64(dev, dAf, (int)M, (int)K, (int)K, dBf, (int)N, (int)N, 1, shift,

@@ -14,7 +14,7 @@ struct oz_dev {
     hipStream_t stream = nullptr;
     hipEvent_t events[64] = {};
     std::string error;
-    int* queue = nullptr;   // 16 ints, zero between launches: [0..1] the product kernel's tile pool, [12..14] the pair scale's flags
+    int* queue = nullptr;   // tile pool counters of the INT8 product kernel (16 ints, zero between launches)
     int cus = 0;            // compute units: a product launch of at most this many tiles needs no pool
 };
 

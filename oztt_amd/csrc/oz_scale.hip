@@ -136,18 +136,14 @@ __device__ __forceinline__ int32_t key_delta(uint32_t key, int shift, uint32_t& 
 //   thread a stride-(1024/R) run of its row's K values.
 // The column strips read 32 K doubles each workgroup, the rows K: the long strips are dispatched
 // first and the short rows fill in behind them, so no strip is left running alone at the end.
-// The 16 waves' maxima meet in LDS; flags[0] (A) and flags[1] (B) are written by the last workgroup
-// from counters in the device handle (no zeroing launch before the kernel).
+// The 16 waves' maxima meet in LDS; flags[0] (A) and flags[1] (B) collect the flag bits with atomicOr.
 template <int CEIL>
 __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restrict__ A, int M, int K, int lda,
                                                           const double* __restrict__ B, int N, int ldb, int shift,
                                                           int32_t* __restrict__ dA, int32_t* __restrict__ dB,
-                                                          uint32_t* __restrict__ flags, int rows_per_wg,
-                                                          uint32_t* __restrict__ acc) {
+                                                          uint32_t* __restrict__ flags, int rows_per_wg) {
     __shared__ uint32_t part[1024];
-    __shared__ uint32_t wbad;  // this workgroup's flag bits
     const int t = threadIdx.x;
-    if (t == 0) wbad = 0;  // read after the barriers below
     const int strips = (N + 31) / 32;
     if ((int)blockIdx.x >= strips) {
         // R rows per workgroup (rows_per_wg: R = 8192 / K rounded down to a power of two, 1..16), so
@@ -178,7 +174,7 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
             for (int w = 0; w < wpr; w++) m = max(m, part[q * wpr + w]);
             uint32_t bad;
             dA[i] = key_delta(m, shift, bad);
-            if (bad) atomicOr(&wbad, bad);
+            if (bad) atomicOr(&flags[0], bad);
         }
     } else {
         const int col = (int)blockIdx.x * 32 + (t & 31);
@@ -222,22 +218,7 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
             for (int q = 0; q < 8; q++) m = max(m, part[q * 32 + t]);
             uint32_t bad;
             dB[(int)blockIdx.x * 32 + t] = key_delta(m, shift, bad);
-            if (bad) atomicOr(&wbad, bad);
-        }
-    }
-    // The flags: every workgroup ORs its bits into acc[0] (A) or acc[1] (B) and counts itself in
-    // acc[2]; the last one writes them to flags and leaves acc zero for the next launch. Its count
-    // is issued after its OR has returned, so the last count sees every OR done (no fence needed).
-    __syncthreads();
-    if (t == 0) {
-        const uint32_t b = wbad;
-        uint32_t old = 0;
-        if (b) old = atomicOr(&acc[(int)blockIdx.x < strips ? 1 : 0], b);
-        asm volatile("" ::"v"(old));  // wait for the OR's return
-        if (atomicAdd(&acc[2], 1u) == gridDim.x - 1) {
-            flags[0] = atomicExch(&acc[0], 0u);
-            flags[1] = atomicExch(&acc[1], 0u);
-            atomicExch(&acc[2], 0u);
+            if (bad) atomicOr(&flags[1], bad);
         }
     }
 }
@@ -292,13 +273,10 @@ extern "C" int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int
     if (blocks > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: grid too large");
     const dim3 grid((unsigned)blocks), block(1024);
     if (ceil_mode == 0)
-        hipLaunchKernelGGL(scale_pair_kernel<0>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R,
-                           reinterpret_cast<uint32_t*>(dev->queue) + 12);
+        hipLaunchKernelGGL(scale_pair_kernel<0>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
     else if (ceil_mode == 1)
-        hipLaunchKernelGGL(scale_pair_kernel<1>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R,
-                           reinterpret_cast<uint32_t*>(dev->queue) + 12);
+        hipLaunchKernelGGL(scale_pair_kernel<1>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
     else
-        hipLaunchKernelGGL(scale_pair_kernel<2>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R,
-                           reinterpret_cast<uint32_t*>(dev->queue) + 12);
+        hipLaunchKernelGGL(scale_pair_kernel<2>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
     return oz::launch_check(dev, "scale_pair_kernel");
 }
