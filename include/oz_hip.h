@@ -194,7 +194,7 @@ int oz2_gemm_f64(oz_dev* dev, const double* A, int lda, const double* B, int ldb
  * It takes no workspace and allocates nothing: the intermediates live in a device array of
  * OZ2_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on until the process ends.
  * Shapes whose workspace (oz2_gemm_f64_workspace) exceeds it are refused with OZ_ERR_ARG; that
- * covers for example 2048 x 2048 x 2048 with up to 20 moduli. Every call on one GPU shares that
+ * covers for example 2048 x 2048 x 2048 with up to 21 moduli. Every call on one GPU shares that
  * GPU's array: calls that overlap on one GPU (several streams or host threads) race and must be
  * serialized by the caller. Otherwise as oz2_gemm_f64. */
 #define OZ2_NOALLOC_SCRATCH_BYTES (256u << 20)

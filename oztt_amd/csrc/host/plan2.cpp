@@ -282,13 +282,19 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
             p.fp8_digits = false;
         } else if (!fp8) {
             // a width beyond what 24 INT8 moduli hold (about 85 bits), which only extreme inputs or a
-            // fixed width ask for: FP8 keeps its own digits; the other formats run the widest INT8 plan,
-            // and Info reports that plan
-            p.route = choose_moduli_int8(K, kMaxModuli, b_cap);
-            if (!p.route.ok) throw std::runtime_error("Ozaki II: no INT8 moduli set covers the CRT window for K=" +
-                                                      std::to_string(K));
-            p.mo = p.route;
-            p.b = p.route.b;
+            // fixed width ask for: the FP8 route's e4m3 digits carry the same width b (moduli up to
+            // 2401, two or three digits each, at most 100 bits), so C is still the one of the format's
+            // own plan; a width that neither transport holds is refused, never lowered
+            ModuliSet f = choose_moduli_digits(Format::FP8, M, N, K, kMaxModuli, p.b);
+            if (!(f.ok && f.b == p.b))
+                throw std::runtime_error("Ozaki II: the " + std::string(format_name(format)) + " plan needs a width of " +
+                                         std::to_string(p.b) + " bits at the padded inner dimension K=" +
+                                         std::to_string(K) + ", beyond what this device's INT8 residues (" +
+                                         std::to_string(x.ok ? x.b : 0) + " bits) and FP8 digits (" +
+                                         std::to_string(f.ok ? f.b : 0) + " bits) carry exactly. Use a smaller "
+                                         "Options::max_moduli or a smaller K.");
+            p.mo = std::move(f);
+            p.fp8_digits = true;
         }
     }
     p.S = (int)p.mo.m.size();

@@ -65,12 +65,16 @@ struct TilePool {
         const int per = total / 8;
         return 8 * (per - (per + frac - 1) / frac);
     }
-    // thread 0 of a workgroup w >= first, once. The second atomic is issued after the first has
-    // returned, so when the count reaches the number of pool workgroups every one of them is done with
-    // q[0]; no fence is needed (and an agent-scope release would write the XCD's L2 back).
+    // thread 0 of a workgroup w >= first, once. The second atomic must not reach memory before the
+    // first has: then, when the count reaches the number of pool workgroups, every one of them is done
+    // with q[0], and the reset cannot be overtaken by a straggler's increment (which would leave q[0] = 1
+    // and make the next launch on the handle skip a tile). Its operand is computed from the first one's
+    // result (p >= 0, so the operand is 1), so it cannot be issued before that result has returned,
+    // whatever the compiler schedules; no fence is needed (and an agent-scope release would write the
+    // XCD's L2 back).
     __device__ int take() const {
         const int p = atomicAdd(&q[0], 1);
-        if (atomicAdd(&q[1], 1) == (int)gridDim.x - first - 1) {
+        if (atomicAdd(&q[1], 1 | (p >> 31)) == (int)gridDim.x - first - 1) {
             atomicExch(&q[0], 0);
             atomicExch(&q[1], 0);
         }

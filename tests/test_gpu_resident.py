@@ -6,12 +6,15 @@ The contract: gemm on resident a, b gives the same C bit for bit, and the same I
 their host copies, because the device copies use the same zero-padded layouts, and the planner
 reads the same padded host data or reuses the plan it made for the pair. The plan of a pair is
 kept: the second call reports plan_reused and gives the same C. A result kept on the GPU chains
-into later products, and a previous result's device memory is lent to the next one.
+into later products, and a previous result's device memory is lent to the next one. The resident C
+is also compared with the oracle's whole chain on the padded operands (tests/oracle_chains.py), so a
+mistake in the padded role copies or the kept plan that the host-span path shares is caught too.
 """
 import numpy as np
 import pytest
 
 import oztt_amd as oz
+from tests.test_gpu_bands import oracle_c
 
 pytestmark = pytest.mark.gpu
 
@@ -38,7 +41,7 @@ def bits(x):
 
 
 @pytest.mark.parametrize("name,opts", CASES, ids=[c[0] for c in CASES])
-def test_resident_matches_host_call(ctx, name, opts):
+def test_resident_matches_host_call(ctx, oracle, name, opts):
     m, n, k = 300, 200, 130  # every dimension padded
     a, b = oz.eval_inputs(21, 1.0, m * k, k * n)
     want = np.empty(m * n)
@@ -50,6 +53,7 @@ def test_resident_matches_host_call(ctx, name, opts):
     i1 = ctx.gemm_resident(A, B, got, opts, evaluation=ev1)
     np.testing.assert_array_equal(bits(got), bits(want))
     assert i1 == i0 and not ev1.plan_reused
+    np.testing.assert_array_equal(bits(got), bits(oracle_c(oracle, a, b, m, n, k, opts, False, i1)))
     # second call: the kept plan, the same C
     got2 = np.empty(m * n)
     ev2 = oz.EvalStats()
@@ -119,7 +123,7 @@ def test_resident_checks(ctx):
 
 @pytest.mark.parametrize("name,opts,fp8_cores", [c + (False,) for c in CASES[:2] + CASES[3:4]] +
                          [("II-FP8-cores", CASES[1][1], True)], ids=["II-INT8", "II-FP8", "I-INT8", "II-FP8-cores"])
-def test_resident_row_bands(ctx, name, opts, fp8_cores):
+def test_resident_row_bands(ctx, oracle, name, opts, fp8_cores):
     """Resident operands through row bands (forced by the evaluation hook max_band_rows): the band
     loop reads A's rows from the resident copy and writes C's rows into the result. II-FP8-cores:
     the FP8 route's e4m3 digits on the FP8 matrix cores, against the default call's C."""
@@ -132,9 +136,10 @@ def test_resident_row_bands(ctx, name, opts, fp8_cores):
     ev.max_band_rows = 256
     ev.fp8_matrix_cores = int(fp8_cores)
     got = np.empty(m * n)
-    ctx.gemm_resident(A, B, got, opts, evaluation=ev)
+    info = ctx.gemm_resident(A, B, got, opts, evaluation=ev)
     assert ev.gemm_launches == 4
     np.testing.assert_array_equal(bits(got), bits(want))
+    np.testing.assert_array_equal(bits(got), bits(oracle_c(oracle, a, b, m, n, k, opts, fp8_cores, info)))
     C = oz.Matrix()
     ev2 = oz.EvalStats()
     ev2.max_band_rows = 256

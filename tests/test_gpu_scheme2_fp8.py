@@ -16,6 +16,7 @@ import pytest
 
 import oztt_amd as oz
 from oztt_amd.device import E4M3, from_blocks
+from tests.oracle_chains import oz2_chain
 from tests.oracle_lib import assert_residues
 
 pytestmark = pytest.mark.gpu
@@ -219,11 +220,13 @@ def test_fp8_gemm_rejects_inexact_bound(dev):
 
 
 @pytest.mark.parametrize("fmt", [oz.Format.BFP8, oz.Format.BF16, oz.Format.FP16, oz.Format.TF32, oz.Format.BFP4,
-                                 oz.Format.BFP2])
-def test_other_formats_run_int8_residues(ctx, fmt):
-    """Scheme II with BF16, FP16, TF32, BFP8, BFP4, BFP2: the format's own route plans (Info reports its
-    moduli, width and passes, as the reference's), INT8 residues at that width compute, so the output
-    is bit-identical to Format::INT8 at the same width."""
+                                 oz.Format.BFP2, oz.Format.FP8])
+def test_other_formats_run_int8_residues(ctx, oracle, fmt):
+    """Scheme II with BF16, FP16, TF32, BFP8, BFP4, BFP2 and FP8: the format's own route plans (Info reports
+    its moduli, width and passes, as the reference's), INT8 residues at that width compute, so the output
+    is bit-identical to Format::INT8 at the same width, and to the oracle's whole chain at the route's
+    width b with the route's own moduli (up to 4096; residues, exact products and the exact CRT on the
+    CPU from the FP64 inputs)."""
     n = 256
     a, b = oz.eval_inputs(5, 1.0, n * n, n * n)
     p = oz.plan2(a, b, n, n, n, fmt)
@@ -234,6 +237,25 @@ def test_other_formats_run_int8_residues(ctx, fmt):
     ci, ii, ev = ctx.evaluate(a, b, n, n, n, opts(oz.Format.INT8, max_moduli=24), fixed_bits=info.integer_bits)
     assert ii.integer_bits == info.integer_bits and ev.partial_products == p.S
     np.testing.assert_array_equal(c.view(np.uint64), ci.view(np.uint64))
+    rm = [p.rm[i] for i in range(p.rS)]
+    want = oz2_chain(oracle, a.reshape(n, n), b.reshape(n, n), rm, p.b, p.nd).reshape(-1)
+    np.testing.assert_array_equal(c.view(np.uint64), want.view(np.uint64))
+
+
+def test_digit_route_beyond_the_int8_width_on_fp8_digits(ctx, oracle):
+    """BFP8 at a fixed width of 90 bits at K = 4096, beyond the 85 that 24 INT8 moduli hold: the call keeps
+    b = 90 (five digits of A') on the FP8 route's e4m3 digits, Info reports BFP8's route (17 moduli), and C
+    equals the oracle's chain at b = 90 with BFP8's own moduli."""
+    m = n = 64
+    k = 4096
+    a, b = oz.eval_inputs(4, 2.0, m * k, k * n)
+    p = oz.plan2(a, b, m, n, k, oz.Format.BFP8, fixed_bits=90, max_moduli=24)
+    assert p.fp8_digits and p.b == 90 and p.nd == 5
+    c, info, ev = ctx.evaluate(a, b, m, n, k, opts(oz.Format.BFP8, max_moduli=24), fixed_bits=90)
+    assert (info.moduli, info.integer_bits) == (17, 90)
+    rm = [p.rm[i] for i in range(p.rS)]
+    want = oz2_chain(oracle, a.reshape(m, k), b.reshape(k, n), rm, 90, 5).reshape(-1)
+    np.testing.assert_array_equal(c.view(np.uint64), want.view(np.uint64))
 
 
 def test_default_options_run(ctx):

@@ -389,17 +389,27 @@ def test_digit_route_reference_hashes(oracle, fmt):
     assert oracle.hash(oracle.crt_ref(C, n, n, ms, 54, 3, 0, dA, dB)) == ROUTE_HASHES[fmt]
 
 
-def test_digit_route_beyond_the_int8_width_runs_the_widest_int8_plan():
+def test_digit_route_beyond_the_int8_width_keeps_its_width_on_fp8_digits():
     """BFP8's route holds b = 90 at K = 4096 (17 moduli up to 4096), 24 INT8 moduli at most 85 bits: the call
-    runs the widest INT8 plan (b = 85, 24 moduli), and Info reports that plan."""
+    keeps b = 90 and carries it with the FP8 route's e4m3 digits at that width, and Info reports BFP8's
+    route. A width that neither transport holds is refused with runtime_error, never lowered."""
     M = N = 64
     K = 4096
     a, b = oz.eval_inputs(4, 2.0, M * K, K * N)
     r = oz.choose_moduli_route(oz.Format.BFP8, M, N, K, 24, 90)
     assert r.ok and r.b == 90 and r.rS == 17
     p = oz.plan2(a, b, M, N, K, oz.Format.BFP8, fixed_bits=90, max_moduli=24)
-    assert p.b == 85 and p.S == p.rS == 24 and not p.fp8_digits
-    assert [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
+    assert p.b == 90 and p.fp8_digits and p.rS == 17
+    f8 = oz.plan2(a, b, M, N, K, oz.Format.FP8, fixed_bits=90, max_moduli=24)
+    assert [p.m[i] for i in range(p.S)] == [f8.m[i] for i in range(f8.S)]
+    # at K = 16384 BFP4's route holds 100 bits, 24 INT8 moduli 84 and the FP8 route 83: refused
+    K = 16384
+    a, b = oz.eval_inputs(4, 2.0, M * K, K * N)
+    assert oz.choose_moduli_route(oz.Format.BFP4, M, N, K, 24, 100).b == 100
+    assert oz.choose_moduli_int8(K, 24, 100).b == 84
+    assert oz.choose_moduli_route(oz.Format.FP8, M, N, K, 24, 100).b == 83
+    with pytest.raises(RuntimeError, match="width of 100 bits.*beyond what this device"):
+        oz.plan2(a, b, M, N, K, oz.Format.BFP4, fixed_bits=100, max_moduli=24)
 
 
 def test_digit_route_accumulation_limit_is_the_references():
