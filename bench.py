@@ -3,9 +3,10 @@
 
 `--config C1|C2|C4|C5` measures the other BASELINE configs the same way (C1: II-INT8 1024^3 one
 pass; C2: I-INT8 4096^3 automatic slices; C4: II-FP8 16384^3, phi 2; C5: I-BF16 8192 x 8192 x 65536,
-8 slices, 1% zero rows and columns); the default line is C3. C4 runs the library's default for the
-FP8 format (the FP8 route's plan carried by INT8 residues at its width) and reports the FP8 route's
-e4m3 digit products on the FP8 matrix cores beside it (`fp8_matrix_cores`, the same C).
+8 slices, 1% zero rows and columns); the default line is C3. C4's value is the FP8 format as the
+config names it and the library runs it by default, the FP8 route's e4m3 digit products on the FP8
+matrix cores; the same plan carried by INT8 residues at its width (Transport.Int8Residues, the same C)
+is reported beside it (`int8_residues`).
 
 Workload: row-major FP64 A, B with entries (U(0,1)-0.5)*exp(0.5*N(0,1)),
 the reference's evaluation generator with seed 3; Scheme II, INT8 residues, automatic moduli (<= 24),
@@ -44,10 +45,18 @@ sys.path.insert(0, str(ROOT))
 METRIC = "effective FP64 TFLOP/s (2mnk/t) + max rel err vs binary128, Ozaki-II INT8 8192³"
 INT8_PEAK_TOPS = 5000.0  # MI355X dense INT8 MFMA, 5.0 POP/s
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, 5.0 PFLOP/s
-# HBM bytes per launch of the product kernel at n = 8192 (17 moduli), from the rocprofv3 FETCH_SIZE and
-# WRITE_SIZE passes over this script scaled by the counters' readings for a plain 1 GiB copy
-# (factors 2.000 and 1.000): profiles/scheme2_int8_c3_8192_traffic.md.
-C3_GEMM_TRAFFIC_BYTES = 16.31e9
+# Memory traffic per launch of each config's product kernel: 2.000 x FETCH_SIZE + 1.000 x WRITE_SIZE (KiB
+# per dispatch, from rocprofv3 --pmc passes over this script; the factors are what the same counters read
+# for a plain 1 GiB copy, whose FETCH_SIZE counts half of the bytes it reads), in bytes, with the committed
+# summary it comes from and the plan it was measured on (the figure is printed only for that plan).
+TRAFFIC = {
+    # config: (bytes per launch, profile, products per launch of the plan measured)
+    "C1": (None, "profiles/scheme2_int8_c1_1024_traffic.md", 16),
+    "C2": (None, "profiles/scheme1_int8_c2_4096_traffic.md", 36),
+    "C3": (16.31e9, "profiles/scheme2_int8_c3_8192_traffic.md", 17),
+    "C4": (None, "profiles/scheme2_fp8_c4_16384_traffic.md", 45),
+    "C5": (None, "profiles/scheme1_bf16_c5_8192x65536_traffic.md", 36),
+}
 
 
 def log(msg: str) -> None:
@@ -184,9 +193,9 @@ CONFIGS = {
     "C1": ("II", "INT8", 1024, 1024, 1024, 1, 0.5, dict(reconstruction="OnePass"), INT8_PEAK_TOPS, 1024, 64),
     "C2": ("I", "INT8", 4096, 4096, 4096, 2, 1.0, dict(), INT8_PEAK_TOPS, 4096, 64),
     "C3": ("II", "INT8", 8192, 8192, 8192, 3, 0.5, dict(reconstruction="TwoPass"), INT8_PEAK_TOPS, 8192, 64),
-    # the FP8 plan carried by INT8 residues (the library's default for FP8; the FP8 route's digits on the FP8
-    # matrix cores, dense FP8 peak 5.0 PFLOP/s, are measured beside it)
-    "C4": ("II", "FP8", 16384, 16384, 16384, 4, 2.0, dict(), INT8_PEAK_TOPS, 1024, 32),
+    # the FP8 route's e4m3 digit products on the FP8 matrix cores (dense FP8 peak 5.0 PFLOP/s); the same plan
+    # carried by INT8 residues is measured beside it
+    "C4": ("II", "FP8", 16384, 16384, 16384, 4, 2.0, dict(), FP8_PEAK_TFLOPS, 1024, 32),
     # BF16 digits (+-32) run on the INT8 matrix cores, so the product roofline is the INT8 peak
     "C5": ("I", "BF16", 8192, 8192, 65536, 5, 4.0, dict(slices=8), INT8_PEAK_TOPS, 512, 32),
 }
@@ -298,6 +307,12 @@ def main() -> int:
     gemm_ms = ev.gemm_launch_ms
     achieved = ev.product_ops / (gemm_ms * 1e-3) / 1e12
     headline = args.config == "C3"
+    traffic, traffic_profile, traffic_products = TRAFFIC[args.config]
+    if ev.partial_products != traffic_products:  # another plan than the one measured
+        traffic = None
+    fp8 = fmt == "FP8"
+    kernel = ("gemm_f8_groups_kernel<TERMS> (oz2_gemm_groups_f8)" if fp8 else
+              "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II" else "<DIAG> (oz1_gemm_diag_i8)"))
     out = {
         "metric": METRIC if headline else f"effective FP64 TFLOP/s (2mnk/t), {WORKLOADS[args.config]}",
         "value": round(value, 3),
@@ -309,9 +324,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        # the products' arithmetic: int8 (C5's BF16-format digits are int8 values, C4's FP8 plan is carried
-        # by INT8 residues)
-        "dtype": "int8",
+        # the products' arithmetic: int8 (C5's BF16-format digits are int8 values), e4m3 for C4
+        "dtype": "fp8_e4m3" if fp8 else "int8",
         "data": f"synthetic: reference evaluation generator, seed {seed}, (U(0,1)-0.5)*exp({phi}*N(0,1))",
         "config": {"workload": WORKLOADS[args.config], "m": m, "n": n, "k": k, "scheme": scheme, "format": fmt,
                    "slices": info.slices, "moduli": info.moduli, "integer_bits": info.integer_bits,
@@ -324,42 +338,39 @@ def main() -> int:
         "host_call_tflops": round(2.0 * m * n * k / (call_ms * 1e-3) / 1e12, 3),
         "resident": resident,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4),
-                     "traffic": C3_GEMM_TRAFFIC_BYTES if (headline and info.moduli == 17) else None,
-                     "kernel": "gemm_i8_kernel" + ("<DIGITS> (oz2_gemm_digits)" if scheme == "II"
-                                                   else "<DIAG> (oz1_gemm_diag_i8)"),
-                     "launch_ms": round(gemm_ms, 4), "ops_per_launch": ev.product_ops},
+                     "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_profile": traffic_profile,
+                     "kernel": kernel, "launch_ms": round(gemm_ms, 4), "ops_per_launch": ev.product_ops},
     }
-    if fmt == "FP8":
-        # BASELINE's C4 names e4m3 residues on the FP8 matrix cores: that route is `fp8_matrix_cores` below;
-        # `value` is the library's default for the FP8 format, the same plan carried by INT8 residues
-        out["config"]["transport"] = "INT8 residues at the FP8 plan's width (the library's default for FP8)"
-        out["config"]["int8_moduli_computed"] = ev.partial_products
-        # the FP8 route's e4m3 digit products on the FP8 matrix cores: the same exact C' at the same width
-        log("FP8 route's digits on the FP8 matrix cores")
-        c8, i8, e8 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=3, fp8_matrix_cores=True)
-        if not e8.whole_checked:
-            raise SystemExit("FP8 matrix-core whole-pass replay output differs from its first pass")
-        f8_tflops = e8.product_ops / (e8.gemm_launch_ms * 1e-3) / 1e12
-        out["fp8_matrix_cores"] = {
-            "ms_per_step": round(e8.whole_ms, 4), "value": round(2.0 * m * n * k / (e8.whole_ms * 1e-3) / 1e12, 3),
-            "dtype": "fp8_e4m3", "digit_products": e8.partial_products,
-            "phases_ms": {key: round(e8.phase_ms[i], 4)
+    if fp8:
+        out["config"]["transport"] = "the FP8 route's e4m3 digits on the FP8 matrix cores (the library's default)"
+        out["config"]["digit_products"] = ev.partial_products
+        # the same plan carried by INT8 residues at its width (Transport.Int8Residues): the same exact C'
+        log("the FP8 plan on INT8 residues (Transport.Int8Residues)")
+        oi = oz.Options(scheme=oz.Scheme[scheme], format=oz.Format[fmt], transport=oz.Transport.Int8Residues)
+        ci, ii, ei = ctx.evaluate(a, b, m, n, k, oi, warmup=1, repeats=3)
+        if not ei.whole_checked:
+            raise SystemExit("INT8-residue whole-pass replay output differs from its first pass")
+        i_tops = ei.product_ops / (ei.gemm_launch_ms * 1e-3) / 1e12
+        out["int8_residues"] = {
+            "ms_per_step": round(ei.whole_ms, 4), "value": round(2.0 * m * n * k / (ei.whole_ms * 1e-3) / 1e12, 3),
+            "dtype": "int8", "int8_moduli": ii.moduli,
+            "phases_ms": {key: round(ei.phase_ms[i], 4)
                           for i, key in enumerate(["scale", "slice", "gemm", "compose", "recon"])},
-            "roofline": {"bound": "mfma", "achieved": round(f8_tflops, 2), "peak": FP8_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(f8_tflops / FP8_PEAK_TFLOPS, 4),
-                         "kernel": "gemm_f8_groups_kernel<TERMS> (oz2_gemm_groups_f8)",
-                         "launch_ms": round(e8.gemm_launch_ms, 4), "ops_per_launch": e8.product_ops},
-            "same_info": i8 == info,
-            "identical_output": bool(np.array_equal(c8.view(np.uint64), c.view(np.uint64)))}
-        del c8
+            "roofline": {"bound": "mfma", "achieved": round(i_tops, 2), "peak": INT8_PEAK_TOPS,
+                         "unit": "TFLOP/s", "frac": round(i_tops / INT8_PEAK_TOPS, 4),
+                         "kernel": "gemm_i8_kernel<DIGITS> (oz2_gemm_digits)",
+                         "launch_ms": round(ei.gemm_launch_ms, 4), "ops_per_launch": ei.product_ops},
+            "same_width": (ii.integer_bits, ii.reconstruction_passes) == (info.integer_bits,
+                                                                         info.reconstruction_passes),
+            "identical_output": bool(np.array_equal(ci.view(np.uint64), c.view(np.uint64)))}
+        del ci
     log("native FP64 GEMM on the GPU (rocBLAS dgemm)")
     out["native_fp64_gemm"] = native_fp64_gemm(a, b, m, n, k)
     log("vendor int8 GEMM on one product's shape (hipBLASLt)")
     v = vendor_int8_gemm(m, n, k)
     if "tops" in v:
         # the product kernel's rate per unit of int8 work next to the vendor's on the same shape
-        v["product_kernel_tops"] = round(achieved, 2)
+        v["product_kernel_tops"] = out["int8_residues"]["roofline"]["achieved"] if fp8 else round(achieved, 2)
     out["vendor_int8_gemm"] = v
     if cpu_rows > 0:
         log(f"CPU baseline: Dot2 on {cpu_rows} rows")

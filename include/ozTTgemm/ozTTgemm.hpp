@@ -34,6 +34,19 @@ enum class Format { BF16, FP16, TF32, BFP8, FP8, INT8, BFP4, BFP2 };
 // statistics allows it, two otherwise.
 enum class Reconstruction { Automatic, OnePass, TwoPass };
 
+// Scheme II only, an extension of the reference's interface (which has no such option): how the
+// products of a format's plan run on the GPU. Both transports give the same C bit for bit (the
+// reconstruction is exact, so C depends on the plan's width b only) and the same plan.
+//   Automatic: the format's own digits on its own matrix instructions where this build has them
+//     (INT8 residues on the INT8 matrix cores; FP8: the reference's e4m3 digits on the FP8 matrix
+//     cores), and INT8 residues at the plan's width for the formats whose digits have no matrix
+//     instructions here (BF16, FP16, TF32, BFP8, BFP4, BFP2). Info is the reference's.
+//   Int8Residues: INT8 residues at the plan's width for every format. On MI355X this is the fastest
+//     transport: the FP8 and INT8 dense rates are equal, and the FP8 route needs two to three times
+//     the products of INT8 residues for one width. Info.moduli then counts the INT8 moduli that
+//     computed. A width beyond what INT8 residues hold (above about 84 bits) keeps the FP8 digits.
+enum class Transport { Automatic, Int8Residues };
+
 // Options of the scheme that is not selected must keep their defaults.
 struct Options {
     Scheme scheme = Scheme::II;
@@ -44,6 +57,8 @@ struct Options {
     std::uint32_t max_moduli = 0;
     // Scheme II only.
     Reconstruction reconstruction = Reconstruction::Automatic;
+    // Scheme II only (extension, see Transport).
+    Transport transport = Transport::Automatic;
 };
 
 struct DeviceOptions {

@@ -21,7 +21,7 @@ import numpy as np
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 
-__all__ = ["Scheme", "Format", "Reconstruction", "Options", "Info", "Context", "is_available", "format_name",
+__all__ = ["Scheme", "Format", "Reconstruction", "Transport", "Options", "Info", "Context", "is_available", "format_name",
            "hip", "host", "LIB_DIR"]
 
 
@@ -47,6 +47,14 @@ class Reconstruction(enum.IntEnum):
     TwoPass = 2
 
 
+class Transport(enum.IntEnum):
+    """Scheme II (extension of the reference's Options): Automatic runs INT8 and FP8 on their own matrix
+    instructions (FP8: the reference's e4m3 digits) and the other formats' plans on INT8 residues;
+    Int8Residues carries every format's plan by INT8 residues at its width (the same C)."""
+    Automatic = 0
+    Int8Residues = 1
+
+
 @dataclass
 class Options:
     scheme: Scheme = Scheme.II
@@ -54,6 +62,7 @@ class Options:
     slices: int = 0
     max_moduli: int = 0
     reconstruction: Reconstruction = Reconstruction.Automatic
+    transport: Transport = Transport.Automatic
 
 
 @dataclass
@@ -224,6 +233,7 @@ class Context:
         args = [self._ctx, _ptr(a), ctypes.c_size_t(a.size), _ptr(b), ctypes.c_size_t(b.size), _ptr(c),
                 ctypes.c_size_t(c.size), ctypes.c_size_t(m), ctypes.c_size_t(n), ctypes.c_size_t(k), int(o.scheme),
                 int(o.format), ctypes.c_uint(o.slices), ctypes.c_uint(o.max_moduli), int(o.reconstruction),
+                int(o.transport),
                 ctypes.byref(info)]
         if evaluation is None:
             code = host().ozt_gemm(*args, err, ctypes.c_size_t(4096))
@@ -256,7 +266,7 @@ class Context:
         reconstruct K block by K block with blocks of that length. replay_drop_phase >= 0 is the
         self-test of the whole-pass check: its checking replay leaves out that phase's steps, so
         whole_checked must be 0, and nothing is timed. fp8_matrix_cores runs Scheme II FP8 as the FP8
-        route's e4m3 digit products on the FP8 matrix cores instead of INT8 residues at its width."""
+        route's e4m3 digit products on the FP8 matrix cores also under Transport.Int8Residues."""
         a, b = _f64(a), _f64(b)
         c = np.empty(m * n, dtype=np.float64)
         ev = EvalStats()
@@ -303,7 +313,7 @@ class Context:
             cptr, nc, cm = _ptr(c), c.size, ctypes.c_void_p()
         _raise(host().ozt_gemm_resident(self._ctx, a._m, b._m, cptr, ctypes.c_size_t(nc), cm, int(o.scheme),
                                         int(o.format), ctypes.c_uint(o.slices), ctypes.c_uint(o.max_moduli),
-                                        int(o.reconstruction), ctypes.byref(info),
+                                        int(o.reconstruction), int(o.transport), ctypes.byref(info),
                                         ctypes.byref(evaluation) if evaluation is not None else None, err,
                                         ctypes.c_size_t(4096)), err)
         return Info(Scheme(info.scheme), Format(info.format), info.slices, info.moduli, info.integer_bits,
@@ -312,14 +322,16 @@ class Context:
 
 def plan2(a, b, M: int, N: int, K: int, fmt: Format = Format.INT8, max_moduli: int = 0,
           reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0,
-          fp8_matrix_cores: bool = False) -> Plan2:
+          transport: Transport = Transport.Automatic, fp8_matrix_cores: bool = False) -> Plan2:
     """Scheme II planner on padded row-major A (M x K) and B (K x N): the execution set (m, S, b, ...;
-    fp8_digits when it is the FP8 route's digit set) and the route's plan of the format (rm, rS, rmode, ...)."""
+    fp8_digits when it is the FP8 route's digit set) and the route's plan of the format (rm, rS, rmode, ...).
+    fp8_matrix_cores as the evaluation setting (FP8 keeps its digits also under Int8Residues)."""
     a, b = _f64(a), _f64(b)
     out = Plan2()
     err = ctypes.create_string_buffer(2048)
+    int8_transport = transport == Transport.Int8Residues and not fp8_matrix_cores
     _raise(host().ozt_plan_scheme2(_ptr(a), _ptr(b), M, N, K, int(fmt), max_moduli, int(reconstruction), fixed_bits,
-                                   int(bool(fp8_matrix_cores)), ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
+                                   int(int8_transport), ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
     return out
 
 

@@ -44,13 +44,14 @@ int guarded(char* err, std::size_t len, F&& f) {
     }
 }
 
-ozTTgemm::Options make_options(int scheme, int format, unsigned slices, unsigned max_moduli, int recon) {
+ozTTgemm::Options make_options(int scheme, int format, unsigned slices, unsigned max_moduli, int recon, int transport) {
     ozTTgemm::Options o;
     o.scheme = static_cast<ozTTgemm::Scheme>(scheme);
     o.format = static_cast<ozTTgemm::Format>(format);
     o.slices = slices;
     o.max_moduli = max_moduli;
     o.reconstruction = static_cast<ozTTgemm::Reconstruction>(recon);
+    o.transport = static_cast<ozTTgemm::Transport>(transport);
     return o;
 }
 }  // namespace
@@ -80,7 +81,7 @@ struct ozt_eval {
     int whole_sentinel;      // the checking replay rewrote the sentinel-filled output with the first pass's bits
     unsigned whole_steps[5];     // steps per phase issued by the checking replay
     unsigned expected_steps[5];  // steps per phase the plan calls for
-    int fp8_matrix_cores;        // input: Scheme II FP8 on the FP8 matrix cores (0: INT8 residues at its width)
+    int fp8_matrix_cores;        // input: Scheme II FP8 on the FP8 matrix cores also under Transport::Int8Residues
 };
 
 struct ozt_plan2 {
@@ -140,10 +141,10 @@ static void fill_info(const ozTTgemm::Info& i, ozt_info* o) {
 
 int ozt_gemm(void* ctx, const double* a, std::size_t na, const double* b, std::size_t nb, double* c, std::size_t nc,
              std::size_t m, std::size_t n, std::size_t k, int scheme, int format, unsigned slices, unsigned max_moduli,
-             int recon, ozt_info* info, char* err, std::size_t errlen) {
+             int recon, int transport, ozt_info* info, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
         auto* cx = static_cast<ozTTgemm::Context*>(ctx);
-        const auto i = cx->gemm({a, na}, {b, nb}, {c, nc}, m, n, k, make_options(scheme, format, slices, max_moduli, recon));
+        const auto i = cx->gemm({a, na}, {b, nb}, {c, nc}, m, n, k, make_options(scheme, format, slices, max_moduli, recon, transport));
         fill_info(i, info);
     });
 }
@@ -188,13 +189,13 @@ static ozTTgemm::evaluation::Settings settings_of(const ozt_eval* evo) {
 }
 
 int ozt_gemm_resident(void* ctx, void* a, void* b, double* c, std::size_t nc, void* cm, int scheme, int format,
-                      unsigned slices, unsigned max_moduli, int recon, ozt_info* info, ozt_eval* evo, char* err,
-                      std::size_t errlen) {
+                      unsigned slices, unsigned max_moduli, int recon, int transport, ozt_info* info, ozt_eval* evo,
+                      char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
         auto* cx = static_cast<ozTTgemm::Context*>(ctx);
         const auto& A = *static_cast<const ozTTgemm::Matrix*>(a);
         const auto& B = *static_cast<const ozTTgemm::Matrix*>(b);
-        const auto o = make_options(scheme, format, slices, max_moduli, recon);
+        const auto o = make_options(scheme, format, slices, max_moduli, recon, transport);
         auto run = [&] {
             return cm ? cx->gemm(A, B, *static_cast<ozTTgemm::Matrix*>(cm), o) : cx->gemm(A, B, {c, nc}, o);
         };
@@ -215,14 +216,15 @@ int ozt_gemm_resident(void* ctx, void* a, void* b, double* c, std::size_t nc, vo
 
 int ozt_eval_gemm(void* ctx, const double* a, std::size_t na, const double* b, std::size_t nb, double* c,
                   std::size_t nc, std::size_t m, std::size_t n, std::size_t k, int scheme, int format, unsigned slices,
-                  unsigned max_moduli, int recon, ozt_info* info, ozt_eval* evo, char* err, std::size_t errlen) {
+                  unsigned max_moduli, int recon, int transport, ozt_info* info, ozt_eval* evo, char* err,
+                  std::size_t errlen) {
     return guarded(err, errlen, [&] {
         ozTTgemm::evaluation::Settings s = settings_of(evo);
         auto* cx = static_cast<ozTTgemm::Context*>(ctx);
         ozTTgemm::Info i;
         {
             ozTTgemm::evaluation::Scope scope(s);
-            i = cx->gemm({a, na}, {b, nb}, {c, nc}, m, n, k, make_options(scheme, format, slices, max_moduli, recon));
+            i = cx->gemm({a, na}, {b, nb}, {c, nc}, m, n, k, make_options(scheme, format, slices, max_moduli, recon, transport));
         }
         fill_info(i, info);
         fill_eval(s, evo);
@@ -248,16 +250,16 @@ static void fill_eval(const ozTTgemm::evaluation::Settings& s, ozt_eval* evo) {
 int ozt_is_available(int format) { return ozTTgemm::is_available(static_cast<ozTTgemm::Format>(format)) ? 1 : 0; }
 const char* ozt_format_name(int format) { return ozTTgemm::format_name(static_cast<ozTTgemm::Format>(format)); }
 
-// Scheme II planner on padded row-major A (M x K) and B (K x N) for `format`; fp8_matrix_cores as in
-// the evaluation settings.
+// Scheme II planner on padded row-major A (M x K) and B (K x N) for `format`; int8_transport: the plan
+// of Transport::Int8Residues.
 int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, unsigned K, int format, unsigned max_moduli,
-              int recon, unsigned fixed_b, int fp8_matrix_cores, ozt_plan2* out, char* err, std::size_t errlen) {
+              int recon, unsigned fixed_b, int int8_transport, ozt_plan2* out, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
         const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, static_cast<ozTTgemm::Format>(format), max_moduli,
                                                         static_cast<ozTTgemm::Reconstruction>(recon), fb,
-                                                        fp8_matrix_cores != 0);
+                                                        int8_transport != 0);
         std::memset(out, 0, sizeof(*out));
         out->fp8_digits = p.fp8_digits;
         out->ok = p.mo.ok;
@@ -290,7 +292,7 @@ int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned 
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
         const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, ozTTgemm::Format::FP8, max_moduli,
-                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb, true);
+                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb, false);
         *crt = ozTTgemm::detail::crt_descriptor(p);
         *dd = ozTTgemm::detail::digit_descriptor(p);
         std::vector<unsigned char> tm;

@@ -47,12 +47,15 @@ constexpr OptionRule kOptionRules[] = {
                 o.reconstruction != Reconstruction::TwoPass;
      },
      "options.reconstruction is not a reconstruction mode"},
+    {[](const Options& o) { return o.transport != Transport::Automatic && o.transport != Transport::Int8Residues; },
+     "options.transport is not a transport"},
     {[](const Options& o) { return o.slices > 256; }, "options.slices must be 0 (automatic) or 1..256"},
     {[](const Options& o) { return o.max_moduli > 24; }, "options.max_moduli must be 0 (automatic) or 1..24"},
     {[](const Options& o) {
-         return o.scheme == Scheme::I && (o.max_moduli != 0 || o.reconstruction != Reconstruction::Automatic);
+         return o.scheme == Scheme::I && (o.max_moduli != 0 || o.reconstruction != Reconstruction::Automatic ||
+                                          o.transport != Transport::Automatic);
      },
-     "options.max_moduli and options.reconstruction are Ozaki II settings"},
+     "options.max_moduli, options.reconstruction and options.transport are Ozaki II settings"},
     {[](const Options& o) { return o.scheme == Scheme::II && o.slices != 0; }, "options.slices is an Ozaki I setting"},
     {[](const Options& o) { return !detail::scheme_available(o.format, o.scheme); },
      "this build has no such scheme for options.format"},
@@ -240,6 +243,7 @@ struct Context::Impl {
         Format format;
         std::uint32_t slices, max_moduli;
         Reconstruction reconstruction;
+        Transport transport;
         std::shared_ptr<const void> plan;
     };
     static constexpr std::size_t kPlanCacheSize = 16;
@@ -405,7 +409,8 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
         for (std::size_t i = plans.size(); i-- > 0;) {
             const CachedPlan& e = plans[i];
             if (e.a == A.id && e.b == B.id && e.scheme == opts.scheme && e.format == opts.format &&
-                e.slices == opts.slices && e.max_moduli == opts.max_moduli && e.reconstruction == opts.reconstruction) {
+                e.slices == opts.slices && e.max_moduli == opts.max_moduli && e.reconstruction == opts.reconstruction &&
+                e.transport == opts.transport) {
                 plan = e.plan;
                 std::rotate(plans.begin() + (std::ptrdiff_t)i, plans.begin() + (std::ptrdiff_t)i + 1, plans.end());
                 break;
@@ -453,7 +458,7 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
     if (!plan && cacheable) {
         if (plans.size() == kPlanCacheSize) plans.erase(plans.begin());
         plans.push_back({A.id, B.id, opts.scheme, opts.format, opts.slices, opts.max_moduli, opts.reconstruction,
-                         output.plan});
+                         opts.transport, output.plan});
     }
     if (c) {
         const double* vals = output.values;

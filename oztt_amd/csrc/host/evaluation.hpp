@@ -34,7 +34,7 @@ struct Settings {
                                  // steps of this phase (so whole_checked must come out false), and
                                  // nothing is timed; -1 (the default) replays every step
     bool fp8_matrix_cores = false;  // Scheme II FP8: the FP8 route's e4m3 digit products on the FP8 matrix
-                                    // cores instead of INT8 residues at the same width (same C)
+                                    // cores also under Transport::Int8Residues (same C)
     // outputs
     double phase_ms[PhaseCount] = {};  // device time of each phase: the average of up to 5 warm passes
                                        // after the replays (the first pass when there are none)

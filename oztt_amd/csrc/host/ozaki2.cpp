@@ -1,5 +1,6 @@
 // Ozaki scheme II driver (INT8 residues, or the FP8 route's e4m3 digits): one FP64 GEMM on the GPU.
-// Every format runs INT8 residues unless the plan keeps the FP8 route's digits (plan_scheme2).
+// Every format runs INT8 residues unless the plan keeps the FP8 route's digits (plan_scheme2: FP8
+// under Transport::Automatic, and widths beyond the INT8 residues').
 //
 // Pipeline of the reference's ozaki2.cpp:439-478: plan (moduli, width b, passes) -> upload the FP64
 // operands -> scale (row/column maxima, exponent deltas) -> slice -> products -> CRT reconstruction
@@ -65,7 +66,8 @@ Output ozaki2_run(Device& D, const Problem& p) {
         p.plan ? std::static_pointer_cast<const Plan2>(p.plan)
                : std::make_shared<const Plan2>(plan_scheme2(p.a, p.b, p.m, p.n, p.k, p.options.format,
                                                             p.options.max_moduli, p.options.reconstruction, fixed_b,
-                                                            es && es->fp8_matrix_cores));
+                                                            p.options.transport == Transport::Int8Residues &&
+                                                                !(es && es->fp8_matrix_cores)));
     const Plan2& plan = *planp;
     const bool fp8 = plan.fp8_digits;
     const std::uint32_t S = (std::uint32_t)plan.S;
@@ -216,7 +218,10 @@ Output ozaki2_run(Device& D, const Problem& p) {
     auto* host = p.c_dev ? nullptr : static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
     run_pipeline(dev, steps, shape, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * nprod, nprod);
     Info info{Scheme::II, p.options.format};
-    info.moduli = (std::uint32_t)plan.route.m.size();  // the format's route (FP8: the FP8 set also when INT8 carries it)
+    // the format's route under Transport::Automatic (the reference's Info: for BF16, FP16, TF32, BFP8,
+    // BFP4 and BFP2 also when INT8 residues carry it); the moduli that computed under Int8Residues
+    info.moduli = (std::uint32_t)(p.options.transport == Transport::Int8Residues ? plan.mo.m.size()
+                                                                                 : plan.route.m.size());
     info.integer_bits = (std::uint32_t)plan.b;
     info.reconstruction_passes = plan.two_pass ? 2 : 1;
     return {host, info, planp};

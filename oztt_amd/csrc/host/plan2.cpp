@@ -217,15 +217,16 @@ double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st) {
 
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
                    std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b,
-                   bool fp8_matrix_cores) {
+                   bool int8_transport) {
     // Every format plans on its own route as the reference does (INT8 residues, or the FP8, TF32, BF16,
-    // FP16, BFP8, BFP4 or BFP2 digit route): its moduli, width b and pass choice are the reference's
-    // and are what Info reports. The products then run on INT8 residues of the same A' and B' at that
-    // width b for every format: on MI355X the digits of the other formats are int8 values anyway
-    // (BFP8, BFP4, BFP2 and TF32 have no matrix instructions of their own; BF16/FP16 run at half the
-    // INT8 rate; FP8 runs at the INT8 rate) and the digit routes need two to four digit products per
-    // modulus where INT8 needs one per modulus of a set a few moduli larger. The exact reconstruction
-    // makes C a function of the width b alone, so the output is the same whichever set computes it.
+    // FP16, BFP8, BFP4 or BFP2 digit route): its moduli, width b and pass choice are the reference's.
+    // INT8 and FP8 then compute on their own matrix instructions (FP8: the route's e4m3 digits) unless
+    // the caller asks for INT8 residues; the other six formats run INT8 residues of the same A' and B'
+    // at that width b: on MI355X their digits are int8 values anyway (BFP8, BFP4, BFP2 and TF32 have no
+    // matrix instructions of their own; BF16/FP16 run at half the INT8 rate), and the digit routes need
+    // two to four digit products per modulus where INT8 needs one per modulus of a set a few moduli
+    // larger. The exact reconstruction makes C a function of the width b alone, so the output is the
+    // same whichever set computes it.
     if ((int)format < 0 || (int)format > (int)Format::BFP2) throw std::invalid_argument("unknown format");
     const bool int8 = format == Format::INT8, fp8 = format == Format::FP8;
     Plan2 p;
@@ -273,7 +274,7 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
     p.b = r.b;
     p.mo = r;
     p.fp8_digits = fp8;
-    if (!int8 && !(fp8 && fp8_matrix_cores)) {
+    if (!int8 && (!fp8 || int8_transport)) {
         // INT8 residues of the same A' and B' (the shift b - 20 (nd - 1) is the same): a set of up to
         // 24 moduli whose window holds width b
         ModuliSet x = choose_moduli_int8(K, kMaxModuli, p.b);

@@ -69,10 +69,10 @@ struct ModuliSet {
 };
 
 // The plan of one Scheme II call: the moduli set of the requested format's route (`route`: what Info
-// reports and what the pass choice is made on), the set the device computes with (`mo`), the width b,
-// digits of A' and passes. `mo` is `route` except for FP8 carried by INT8 residues (fp8_digits false):
-// then `mo` is an INT8 set of the same width b, and C is the same (both sets reconstruct the exact
-// product A'B').
+// reports under Transport::Automatic and what the pass choice is made on), the set the device computes
+// with (`mo`), the width b, digits of A' and passes. `mo` is `route` for INT8, and for FP8 on its own
+// digits (fp8_digits); otherwise an INT8 set of the same width b (or, beyond the INT8 width, the FP8
+// route's set), and C is the same (every set reconstructs the exact product A'B').
 struct Plan2 {
     std::uint32_t M = 0, N = 0, K = 0;  // padded dimensions
     std::uint32_t S_req = 0;
@@ -113,12 +113,13 @@ std::uint32_t default_moduli(Format format);
 double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st);
 
 // The whole plan (plan.hpp:258-306). fixed_b: width fixed by the caller (evaluator only).
-// fp8_matrix_cores: FP8 computes the FP8 route's e4m3 digit products on the FP8 matrix cores; otherwise
-// it is carried by INT8 residues at the FP8 plan's width whenever an INT8 set reaches that width.
+// int8_transport (Transport::Int8Residues): FP8 is carried by INT8 residues at the FP8 plan's width
+// whenever an INT8 set reaches that width; otherwise FP8 computes the FP8 route's e4m3 digit products
+// on the FP8 matrix cores. The other digit formats are carried by INT8 residues either way.
 // Throws std::runtime_error when no exact configuration exists.
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
                    std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b,
-                   bool fp8_matrix_cores = false);
+                   bool int8_transport = false);
 
 // Device descriptors of the plan.
 oz2_moduli_dev split_descriptor(const Plan2& p);

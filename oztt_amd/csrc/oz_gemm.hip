@@ -71,10 +71,12 @@ struct TilePool {
     // and make the next launch on the handle skip a tile). Its operand is computed from the first one's
     // result (p >= 0, so the operand is 1), so it cannot be issued before that result has returned,
     // whatever the compiler schedules; no fence is needed (and an agent-scope release would write the
-    // XCD's L2 back).
+    // XCD's L2 back). The operand is made wave-uniform, so the compiler's atomic combining stays a
+    // scalar multiply (a per-lane operand would make it loop over the lanes through M0).
     __device__ int take() const {
         const int p = atomicAdd(&q[0], 1);
-        if (atomicAdd(&q[1], 1 | (p >> 31)) == (int)gridDim.x - first - 1) {
+        const int one = __builtin_amdgcn_readfirstlane(1 | (p >> 31));
+        if (atomicAdd(&q[1], one) == (int)gridDim.x - first - 1) {
             atomicExch(&q[0], 0);
             atomicExch(&q[1], 0);
         }

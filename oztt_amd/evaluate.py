@@ -14,10 +14,11 @@ Columns as the reference writes them. The phase times are the library's per-phas
 the first pass; total_ms is the average uninterrupted whole pass (the paper's Total) replayed on the
 device with the inputs resident; effective_tflops = 2 n^3 / total_ms; gemm_tops uses the product
 phase; nominal_peak_percent is against the dense MI355X peak of the matrix instructions used
-(5.0 POP/s INT8, 5.0 PFLOP/s FP8). partial_products counts the products the device ran: for the
-Scheme II formats other than INT8 one per modulus of the INT8 set that carries the format's width,
-or for FP8 with --fp8-matrix-cores the FP8 route's digit products (the reference's count); moduli is
-the format's own route's (the reference's) either way. effective_bits / relative_fro compare with the Dot2 reference
+(5.0 POP/s INT8, 5.0 PFLOP/s FP8). partial_products counts the products the device ran: for FP8
+the FP8 route's digit products (the reference's count), for the other Scheme II formats but INT8 one
+per modulus of the INT8 set that carries the format's width; moduli is the format's own route's (the
+reference's). With --int8-residues (Transport.Int8Residues) FP8 is carried by INT8 residues too, and
+moduli counts the INT8 moduli that computed. effective_bits / relative_fro compare with the Dot2 reference
 (computed by the library's evaluator numerics), cpu_dgemm_bits the host's native FP64 GEMM (BLAS
 through numpy) the same way. Columns that describe Tenstorrent telemetry (bw: the Tensix GEMM block
 width; gemm_aiclk_mhz; start_temperature_c) are written as 0 / nan.
@@ -26,12 +27,13 @@ from __future__ import annotations
 
 import argparse
 import csv
+import dataclasses
 import sys
 import time
 
 import numpy as np
 
-from . import Context, Format, Options, Reconstruction, Scheme, eval_accuracy, eval_hash, eval_inputs, \
+from . import Context, Format, Options, Reconstruction, Scheme, Transport, eval_accuracy, eval_hash, eval_inputs, \
     eval_reference_gemm, format_name
 
 COLUMNS = ("suite,n,scheme,format,phi,timing,reference,slices,integer_bits,moduli,passes,partial_products,bw,"
@@ -83,9 +85,10 @@ def main(argv=None) -> int:
     ap.add_argument("--no-reference", action="store_true", help="no Dot2 reference (and no CPU GEMM)")
     ap.add_argument("--no-cpu", action="store_true", help="no host FP64 GEMM for cpu_dgemm_bits")
     ap.add_argument("--quick", action="store_true", help="sizes 128, phi size 128, phis 0.5,2,8, 1 repeat, no warmup")
-    ap.add_argument("--fp8-matrix-cores", action="store_true",
-                    help="Scheme II FP8 as the FP8 route's e4m3 digit products on the FP8 matrix cores (by default "
-                         "INT8 residues at the FP8 plan's width carry it, with the same output)")
+    ap.add_argument("--int8-residues", action="store_true",
+                    help="Scheme II with Transport.Int8Residues: every format's plan carried by INT8 residues at its "
+                         "width (FP8 runs the FP8 route's e4m3 digits on the FP8 matrix cores otherwise; the same "
+                         "output either way)")
     args = ap.parse_args(argv)
     sizes = [int(s) for s in args.sizes.split(",")]
     phis = [float(s) for s in args.phis.split(",")]
@@ -127,8 +130,9 @@ def main(argv=None) -> int:
                 cache[key] = (a, b, hi, lo, cpu_bits)
             a, b, hi, lo, cpu_bits = cache[key]
             t0 = time.perf_counter()
-            c, info, ev = ctx.evaluate(a, b, n, n, n, o, fixed_bits=bits, warmup=warmup, repeats=max(repeats, 1),
-                                       fp8_matrix_cores=args.fp8_matrix_cores)
+            if args.int8_residues and o.scheme == Scheme.II:
+                o = dataclasses.replace(o, transport=Transport.Int8Residues)
+            c, info, ev = ctx.evaluate(a, b, n, n, n, o, fixed_bits=bits, warmup=warmup, repeats=max(repeats, 1))
             call_ms = (time.perf_counter() - t0) * 1e3
             if not ev.whole_checked:
                 raise SystemExit("whole-pass replay output differs from the first pass")

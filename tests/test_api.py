@@ -56,6 +56,10 @@ def test_host_validation_leaves_c_untouched(ctx):
         lambda: ctx.gemm(a, b, c, 2, 2, 2, oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, max_moduli=25)),
         lambda: ctx.gemm(a, b, c, 2, 2, 2, oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8,
                                                       reconstruction=7)),
+        # the transport (an extension) is a Scheme II setting with two values
+        lambda: ctx.gemm(a, b, c, 2, 2, 2, oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8, transport=2)),
+        lambda: ctx.gemm(a, b, c, 2, 2, 2, oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8,
+                                                      transport=oz.Transport.Int8Residues)),
     ]
     for f in cases:
         with pytest.raises(ValueError):

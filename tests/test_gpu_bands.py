@@ -31,7 +31,10 @@ def ctx():
 CASES = [
     ("II-INT8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8), False),
     ("II-FP8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8), False),
-    ("II-FP8-cores", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8), True),
+    ("II-FP8-int8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8, transport=oz.Transport.Int8Residues),
+     False),
+    ("II-FP8-int8-cores", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8, transport=oz.Transport.Int8Residues),
+     True),
     ("I-INT8", oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8), False),
     ("I-BF16", oz.Options(scheme=oz.Scheme.I, format=oz.Format.BF16, slices=6), False),
 ]
@@ -42,11 +45,14 @@ def oracle_c(oracle, a, b, m, n, k, opts, fp8_cores, info):
     mp, np_, kp = pad_dims(m, n, k)
     A, B = padded(a.reshape(m, k), mp, kp), padded(b.reshape(k, n), kp, np_)
     if opts.scheme == oz.Scheme.II:
-        p = oz.plan2(A, B, mp, np_, kp, opts.format, fp8_matrix_cores=fp8_cores)
-        assert (p.rS, p.b) == (info.moduli, info.integer_bits)
-        ms = [p.m[i] for i in range(p.S)]  # the set the device computes with (FP8 cores: the route's)
-        if fp8_cores:
-            assert p.fp8_digits and ms == [p.rm[i] for i in range(p.rS)]
+        p = oz.plan2(A, B, mp, np_, kp, opts.format, transport=opts.transport, fp8_matrix_cores=fp8_cores)
+        int8_carried = opts.transport == oz.Transport.Int8Residues and not p.fp8_digits
+        assert (p.S if int8_carried else p.rS, p.b) == (info.moduli, info.integer_bits)
+        ms = [p.m[i] for i in range(p.S)]  # the set the device computes with (FP8 digits: the route's)
+        if opts.format == oz.Format.FP8:
+            assert p.fp8_digits == (fp8_cores or opts.transport == oz.Transport.Automatic)
+        if p.fp8_digits:
+            assert ms == [p.rm[i] for i in range(p.rS)]
         want = oz2_chain(oracle, A, B, ms, p.b, p.nd)
     else:
         pl = oz.plan1(A, B, mp, np_, kp, slices=opts.slices, fmt=opts.format)
@@ -57,7 +63,8 @@ def oracle_c(oracle, a, b, m, n, k, opts, fp8_cores, info):
 
 @pytest.mark.parametrize("name,opts,fp8_cores", CASES, ids=[c[0] for c in CASES])
 def test_bands_bit_identical(ctx, oracle, name, opts, fp8_cores):
-    """II-FP8-cores: the FP8 route's e4m3 digits on the FP8 matrix cores (A's digit planes per band)."""
+    """II-FP8 and II-FP8-int8-cores: the FP8 route's e4m3 digits on the FP8 matrix cores (A's digit planes
+    per band); II-FP8-int8: the FP8 plan on INT8 residues."""
     m, n, k = 1000, 384, 512
     a, b = oz.eval_inputs(11, 1.0, m * k, k * n)
     c1, i1, e1 = ctx.evaluate(a, b, m, n, k, opts, warmup=1, repeats=2, fp8_matrix_cores=fp8_cores)

@@ -143,23 +143,27 @@ def test_c4_inner_dimension_dense_fp8_route(dev, oracle):
 
 
 def test_c4_inner_dimension_public_call_equals_int8(ctx):
-    """The public FP8 call on C4's inner dimension, on the FP8 matrix cores (dense-digit route, both
-    operands split in one launch) and as by default with INT8 residues at the FP8 plan's width, gives
-    C bit for bit equal to the INT8 format at the same width, with the same Info both ways and
-    checked whole-pass replays."""
+    """The public FP8 call on C4's inner dimension, by default on the FP8 matrix cores (dense-digit route,
+    both operands split in one launch) and with Transport.Int8Residues (INT8 residues at the FP8 plan's
+    width), gives C bit for bit equal to the INT8 format at the same width, with the same plan both ways
+    (Info: the FP8 route's moduli by default, the INT8 moduli that computed otherwise) and checked
+    whole-pass replays."""
     m = n = 256
     k = 16384
     a, b = oz.eval_inputs(4, 2.0, m * k, k * n)
     o8 = oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8)
-    c8, info8, ev8 = ctx.evaluate(a, b, m, n, k, o8, warmup=0, repeats=1, fp8_matrix_cores=True)
+    c8, info8, ev8 = ctx.evaluate(a, b, m, n, k, o8, warmup=0, repeats=1)
     assert ev8.whole_checked
-    cd, infod, evd = ctx.evaluate(a, b, m, n, k, o8, warmup=0, repeats=1)
-    assert evd.whole_checked and infod == info8
+    od = oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8, transport=oz.Transport.Int8Residues)
+    cd, infod, evd = ctx.evaluate(a, b, m, n, k, od, warmup=0, repeats=1)
+    assert evd.whole_checked
+    assert (infod.integer_bits, infod.reconstruction_passes) == (info8.integer_bits, info8.reconstruction_passes)
     # products per pass: the FP8 route's digit products, or one per INT8 modulus
     oi = oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, max_moduli=24)
     ci, infoi, _ = ctx.evaluate(a, b, m, n, k, oi, fixed_bits=info8.integer_bits)
-    assert infoi.integer_bits == info8.integer_bits and evd.partial_products == infoi.moduli
-    assert ev8.partial_products == oz.plan2(a, b, m, n, k, oz.Format.FP8).rnprod
+    assert infoi.integer_bits == info8.integer_bits and evd.partial_products == infoi.moduli == infod.moduli
+    p = oz.plan2(a, b, m, n, k, oz.Format.FP8)
+    assert ev8.partial_products == p.rnprod and info8.moduli == p.rS
     log(f"C4 K: FP8 {info8.moduli} moduli ({ev8.partial_products} digit products), INT8 {infoi.moduli} moduli, "
         f"b={info8.integer_bits}")
     np.testing.assert_array_equal(c8.view(np.uint64), ci.view(np.uint64))
@@ -206,26 +210,29 @@ def test_fp8_products_exact_at_the_fp32_bound(dev):
         assert_residues(W[o], (5 + o) * (P[o] % 1089), 1089, f"output {o}")
 
 
-@pytest.mark.parametrize("scheme,fmt,fp8_cores", [(oz.Scheme.II, oz.Format.INT8, False),
-                                                  (oz.Scheme.II, oz.Format.FP8, False),
-                                                  (oz.Scheme.II, oz.Format.FP8, True),
-                                                  (oz.Scheme.I, oz.Format.INT8, False),
-                                                  (oz.Scheme.I, oz.Format.BF16, False)])
-def test_whole_pass_replay_is_checked(ctx, scheme, fmt, fp8_cores):
+AUTO, I8 = oz.Transport.Automatic, oz.Transport.Int8Residues
+
+
+@pytest.mark.parametrize("scheme,fmt,transport", [(oz.Scheme.II, oz.Format.INT8, AUTO),
+                                                  (oz.Scheme.II, oz.Format.FP8, AUTO),
+                                                  (oz.Scheme.II, oz.Format.FP8, I8),
+                                                  (oz.Scheme.I, oz.Format.INT8, AUTO),
+                                                  (oz.Scheme.I, oz.Format.BF16, AUTO)])
+def test_whole_pass_replay_is_checked(ctx, scheme, fmt, transport):
     """The whole-pass check (reference evaluation_hooks.hpp:175-211): the replays of a sound pass are
     checked; a replay that leaves out one phase's steps fails the check and is not timed, whichever
     phase it is, and the returned C stays the first pass's."""
     n = 512
     a, b = oz.eval_inputs(3, 0.5, n * n, n * n)
-    o = oz.Options(scheme=scheme, format=fmt)
+    o = oz.Options(scheme=scheme, format=fmt, transport=transport)
     c0 = ctx.multiply(a, b, n, n, n, o)
-    c, info, ev = ctx.evaluate(a, b, n, n, n, o, warmup=1, repeats=2, fp8_matrix_cores=fp8_cores)
+    c, info, ev = ctx.evaluate(a, b, n, n, n, o, warmup=1, repeats=2)
     assert ev.whole_checked == 1 and ev.whole_sentinel == 1 and ev.whole_ms > 0
     assert list(ev.whole_steps) == list(ev.expected_steps) and ev.expected_steps[2] >= 1
     np.testing.assert_array_equal(c.view(np.uint64), c0.view(np.uint64))
     phases = [1, 2, 4] + ([0] if scheme == oz.Scheme.II else [])
     for drop in phases:
-        c1, _, bad = ctx.evaluate(a, b, n, n, n, o, repeats=2, replay_drop_phase=drop, fp8_matrix_cores=fp8_cores)
+        c1, _, bad = ctx.evaluate(a, b, n, n, n, o, repeats=2, replay_drop_phase=drop)
         assert bad.whole_checked == 0 and bad.whole_ms == 0, drop
         assert bad.whole_steps[drop] == 0 and bad.expected_steps[drop] >= 1
         np.testing.assert_array_equal(c1.view(np.uint64), c0.view(np.uint64))

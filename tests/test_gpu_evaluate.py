@@ -1,8 +1,9 @@
 """The evaluator (python -m oztt_amd.evaluate) against the reference's validated quick run
 (tools/validated/quick.csv:2-17, values copied into QUICK below): Scheme I outputs are the
 reference's bit for bit (hash, effective bits, relative error); every Scheme II format plans the
-reference's moduli (Info), FP8 on the FP8 matrix cores and INT8 run the reference's partial products
-and the others the 15 INT8 products of b = 54; every Scheme II output is the exact rounding at b = 54."""
+reference's moduli (Info), FP8 (on the FP8 matrix cores, by default) and INT8 run the reference's partial
+products and the others the 15 INT8 products of b = 54; every Scheme II output is the exact rounding at
+b = 54."""
 import csv
 
 import pytest
@@ -26,10 +27,10 @@ QUICK = {
 
 
 def test_quick_table_suite_matches_reference_records(tmp_path):
-    """With the FP8 route's digits on the FP8 matrix cores, as the reference runs them (its partial
+    """FP8 runs the FP8 route's digits on the FP8 matrix cores, as the reference runs them (its partial
     product count)."""
     out = tmp_path / "results.csv"
-    assert evaluate.main(["--quick", "--suite", "table", "--fp8-matrix-cores", "--output", str(out)]) == 0
+    assert evaluate.main(["--quick", "--suite", "table", "--output", str(out)]) == 0
     rows = list(csv.DictReader(open(out)))
     assert [r["format"] for r in rows[::2]] == list(QUICK) and len(rows) == 16
     ii_bits = set()

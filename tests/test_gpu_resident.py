@@ -33,6 +33,7 @@ CASES = [
                                  reconstruction=oz.Reconstruction.TwoPass)),
     ("I-INT8", oz.Options(scheme=oz.Scheme.I, format=oz.Format.INT8)),
     ("I-BF16", oz.Options(scheme=oz.Scheme.I, format=oz.Format.BF16, slices=6)),
+    ("II-FP8-int8", oz.Options(scheme=oz.Scheme.II, format=oz.Format.FP8, transport=oz.Transport.Int8Residues)),
 ]
 
 
@@ -121,12 +122,14 @@ def test_resident_checks(ctx):
     X.close()  # a Matrix may outlive its Context: it holds the GPU open until it is freed
 
 
-@pytest.mark.parametrize("name,opts,fp8_cores", [c + (False,) for c in CASES[:2] + CASES[3:4]] +
-                         [("II-FP8-cores", CASES[1][1], True)], ids=["II-INT8", "II-FP8", "I-INT8", "II-FP8-cores"])
+@pytest.mark.parametrize("name,opts,fp8_cores", [c + (False,) for c in CASES[:2] + CASES[3:4] + CASES[5:6]] +
+                         [("II-FP8-int8-cores", CASES[5][1], True)],
+                         ids=["II-INT8", "II-FP8", "I-INT8", "II-FP8-int8", "II-FP8-int8-cores"])
 def test_resident_row_bands(ctx, oracle, name, opts, fp8_cores):
     """Resident operands through row bands (forced by the evaluation hook max_band_rows): the band
-    loop reads A's rows from the resident copy and writes C's rows into the result. II-FP8-cores:
-    the FP8 route's e4m3 digits on the FP8 matrix cores, against the default call's C."""
+    loop reads A's rows from the resident copy and writes C's rows into the result. II-FP8-int8-cores:
+    the FP8 route's e4m3 digits on the FP8 matrix cores under Transport.Int8Residues (the evaluation
+    setting), against the default call's C."""
     m, n, k = 1000, 384, 512
     a, b = oz.eval_inputs(11, 1.0, m * k, k * n)
     want = np.empty(m * n)

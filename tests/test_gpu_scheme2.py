@@ -67,19 +67,18 @@ CASES = [("uniform", 64, 64, 64), ("nonnegative", 3, 5, 7), ("scaled", 65, 67, 9
          ("largest-maximum", 1, 1, 1), ("uniform", 5056, 64, 32)]
 
 
-@pytest.mark.parametrize("fmt,fp8_cores", [(oz.Format.INT8, False), (oz.Format.FP8, False), (oz.Format.FP8, True)],
-                         ids=["INT8", "FP8", "FP8-cores"])
+@pytest.mark.parametrize("fmt,transport", [(oz.Format.INT8, oz.Transport.Automatic),
+                                           (oz.Format.FP8, oz.Transport.Automatic),
+                                           (oz.Format.FP8, oz.Transport.Int8Residues)],
+                         ids=["INT8", "FP8", "FP8-int8"])
 @pytest.mark.parametrize("mode,m,n,k", CASES)
-def test_reference_correctness_cases(ctx, mode, m, n, k, fmt, fp8_cores):
-    """FP8-cores: the FP8 route's e4m3 digits on the FP8 matrix cores (FP8 runs INT8 residues at its
-    plan's width otherwise)."""
+def test_reference_correctness_cases(ctx, mode, m, n, k, fmt, transport):
+    """FP8: the FP8 route's e4m3 digits on the FP8 matrix cores (the default); FP8-int8: the FP8 plan
+    carried by INT8 residues at its width (Transport.Int8Residues)."""
     a, b = pattern(mode, m, n, k)
-    o = oz.Options(scheme=oz.Scheme.II, format=fmt)
-    if fp8_cores:
-        c, info, _ = ctx.evaluate(a, b, m, n, k, o, fp8_matrix_cores=True)
-    else:
-        c = np.full(m * n, 123.0)
-        info = ctx.gemm(a, b, c, m, n, k, o)
+    o = oz.Options(scheme=oz.Scheme.II, format=fmt, transport=transport)
+    c = np.full(m * n, 123.0)
+    info = ctx.gemm(a, b, c, m, n, k, o)
     assert info.format == fmt
     assert np.all(np.isfinite(c))
     err = ref_error(a, b, c, m, n, k)

@@ -6,10 +6,10 @@ cores, composition in the product epilogue, exact CRT.
    digit products, every uint16 term is coef * P mod m (a representative in [0, m]); the reference's published FP8 output hash
    (quick.csv:11, 20046e5bb3816cbb) follows from the GPU terms through the oracle's restatement of
    the reference reconstruction.
-2. The public API: FP8 runs INT8 residues at the FP8 plan's width by default and the e4m3 digits on
-   the FP8 matrix cores when the evaluation settings ask for them. Both outputs are bit-identical to
-   the INT8 output at the same width b (all reconstruct the exact C' = A'B'), Info reports the FP8
-   route either way, accuracy on the C4 generator.
+2. The public API: FP8 runs the e4m3 digits on the FP8 matrix cores by default and INT8 residues at
+   the FP8 plan's width with Transport.Int8Residues. Both outputs are bit-identical to the INT8 output
+   at the same width b (all reconstruct the exact C' = A'B'); Info reports the FP8 route by default
+   and the INT8 moduli that computed otherwise; accuracy on the C4 generator.
 """
 import numpy as np
 import pytest
@@ -42,11 +42,12 @@ def test_fp8_quick_case_matches_int8_bits(ctx):
     a, b = oz.eval_inputs(7, -1.0, n * n, n * n)
     one = oz.Reconstruction.OnePass
     o8 = opts(oz.Format.FP8, max_moduli=14, reconstruction=one)
-    c8, i8, _ = ctx.evaluate(a, b, n, n, n, o8, fixed_bits=54, fp8_matrix_cores=True)
-    cr, ir, _ = ctx.evaluate(a, b, n, n, n, o8, fixed_bits=54)
+    c8, i8, _ = ctx.evaluate(a, b, n, n, n, o8, fixed_bits=54)
+    cr, ir, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.FP8, max_moduli=14, reconstruction=one,
+                                                  transport=oz.Transport.Int8Residues), fixed_bits=54)
     ci, ii, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.INT8, max_moduli=16, reconstruction=one), fixed_bits=54)
     assert i8.format == oz.Format.FP8 and i8.moduli == 12 and i8.integer_bits == 54
-    assert ir == i8
+    assert (ir.format, ir.integer_bits, ir.reconstruction_passes) == (oz.Format.FP8, 54, 1) and ir.moduli >= 15
     assert ii.moduli == 15 and ii.integer_bits == 54
     np.testing.assert_array_equal(c8.view(np.uint64), ci.view(np.uint64))
     np.testing.assert_array_equal(cr.view(np.uint64), ci.view(np.uint64))
@@ -55,16 +56,19 @@ def test_fp8_quick_case_matches_int8_bits(ctx):
 @pytest.mark.parametrize("n", [1024, 2048])
 def test_fp8_wide_range_auto(ctx, oracle, n):
     """C4 generator (seed 4, phi 2) at reduced size: automatic b, FP8 route moduli, accuracy; the e4m3
-    digits on the FP8 matrix cores and the default INT8 residues give the same bits."""
+    digits on the FP8 matrix cores (the default) and INT8 residues (Transport.Int8Residues) give the same
+    bits."""
     a, b = oz.eval_inputs(4, 2.0, n * n, n * n)
     p = oz.plan2(a, b, n, n, n, oz.Format.FP8)
-    assert not p.fp8_digits
+    assert p.fp8_digits
     c = np.empty(n * n)
     info = ctx.gemm(a, b, c, n, n, n, opts(oz.Format.FP8))
     assert info.format == oz.Format.FP8 and info.moduli == p.rS and info.integer_bits == p.b
     assert info.reconstruction_passes == (2 if p.two_pass else 1)
-    cf, inf, _ = ctx.evaluate(a, b, n, n, n, opts(oz.Format.FP8), fp8_matrix_cores=True)
-    assert inf == info
+    q = oz.plan2(a, b, n, n, n, oz.Format.FP8, transport=oz.Transport.Int8Residues)
+    cf = np.empty(n * n)
+    inf = ctx.gemm(a, b, cf, n, n, n, opts(oz.Format.FP8, transport=oz.Transport.Int8Residues))
+    assert not q.fp8_digits and inf.moduli == q.S and inf.integer_bits == info.integer_bits
     np.testing.assert_array_equal(c.view(np.uint64), cf.view(np.uint64))
     ci = np.empty(n * n)
     ii = ctx.gemm(a, b, ci, n, n, n, opts(oz.Format.INT8))
@@ -223,15 +227,15 @@ def test_fp8_gemm_rejects_inexact_bound(dev):
                                  oz.Format.BFP2, oz.Format.FP8])
 def test_other_formats_run_int8_residues(ctx, oracle, fmt):
     """Scheme II with BF16, FP16, TF32, BFP8, BFP4, BFP2 and FP8: the format's own route plans (Info reports
-    its moduli, width and passes, as the reference's), INT8 residues at that width compute, so the output
-    is bit-identical to Format::INT8 at the same width, and to the oracle's whole chain at the route's
-    width b with the route's own moduli (up to 4096; residues, exact products and the exact CRT on the
-    CPU from the FP64 inputs)."""
+    its moduli, width and passes, as the reference's), INT8 residues at that width compute (FP8: its own
+    e4m3 digits), so the output is bit-identical to Format::INT8 at the same width, and to the oracle's
+    whole chain at the route's width b with the route's own moduli (up to 4096; residues, exact products
+    and the exact CRT on the CPU from the FP64 inputs)."""
     n = 256
     a, b = oz.eval_inputs(5, 1.0, n * n, n * n)
-    p = oz.plan2(a, b, n, n, n, fmt)
+    p = oz.plan2(a, b, n, n, n, fmt, transport=oz.Transport.Int8Residues)
     c = np.empty(n * n)
-    info = ctx.gemm(a, b, c, n, n, n, opts(fmt))
+    info = ctx.gemm(a, b, c, n, n, n, opts(fmt))  # FP8: its own digits
     assert info.format == fmt and info.scheme == oz.Scheme.II
     assert (info.moduli, info.integer_bits, info.reconstruction_passes) == (p.rS, p.b, 2 if p.two_pass else 1)
     ci, ii, ev = ctx.evaluate(a, b, n, n, n, opts(oz.Format.INT8, max_moduli=24), fixed_bits=info.integer_bits)

@@ -223,22 +223,24 @@ def test_fp8_auto_precision_records(phi, b, S):
     wlog2 = math.log2(p.wA * p.wB * max(f, 1.001))
     research = oz.choose_moduli_fp8(n, 24, b, wlog2)
     assert research.b == b and research.rS == S
-    assert not p.fp8_digits  # carried by INT8 residues by default
-    p = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass, fp8_matrix_cores=True)
-    assert p.fp8_digits and p.b == b
-    assert p.S == p.rS and [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
+    # by default the execution set is the route's FP8 set (its e4m3 digits on the FP8 matrix cores)
+    assert p.fp8_digits and p.S == p.rS and [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
+    q = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass,
+                 transport=oz.Transport.Int8Residues)
+    assert not q.fp8_digits and q.b == b and max(q.m[i] for i in range(q.S)) <= 255
 
 
 @pytest.mark.parametrize("K,b", [(16384, 60), (4096, 54), (1024, 70)])
 def test_fp8_carried_by_int8_residues(K, b):
-    """FP8 keeps the FP8 route's plan (moduli of Info, width b, passes) and computes with an INT8 set of the
-    same width: pairwise coprime moduli <= 255 whose window holds K 2^(2b) < M/2. Its int32 products are
-    exact (K floor(m/2)^2 <= 2^31 - 1)."""
+    """Transport.Int8Residues: FP8 keeps the FP8 route's plan (width b, passes) and computes with an INT8 set
+    of the same width: pairwise coprime moduli <= 255 whose window holds K 2^(2b) < M/2. Its int32 products
+    are exact (K floor(m/2)^2 <= 2^31 - 1). The evaluation setting fp8_matrix_cores keeps the FP8 digits."""
     M = N = 64
     a, bb = oz.eval_inputs(4, 2.0, M * K, K * N)
     kw = dict(fixed_bits=b, max_moduli=24, reconstruction=oz.Reconstruction.OnePass)
-    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, **kw)
-    f = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fp8_matrix_cores=True, **kw)
+    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, transport=oz.Transport.Int8Residues, **kw)
+    f = oz.plan2(a, bb, M, N, K, oz.Format.FP8, transport=oz.Transport.Int8Residues, fp8_matrix_cores=True, **kw)
+    assert oz.plan2(a, bb, M, N, K, oz.Format.FP8, **kw).fp8_digits
     i8 = oz.plan2(a, bb, M, N, K, oz.Format.INT8, fixed_bits=b, max_moduli=24,
                   reconstruction=oz.Reconstruction.OnePass)
     assert f.fp8_digits and not p.fp8_digits and not i8.fp8_digits
@@ -254,15 +256,16 @@ def test_fp8_carried_by_int8_residues(K, b):
 
 
 def test_fp8_beyond_the_int8_width_keeps_its_digits():
-    """At K = 4096, 24 moduli <= 255 hold a width of at most 85 bits and the FP8 route's up to 100; a wider
-    FP8 plan runs its own digits."""
+    """At K = 4096, 24 moduli <= 255 hold a width of at most 85 bits and the FP8 route's up to 100; under
+    Transport.Int8Residues a wider FP8 plan runs its own digits."""
     M = N = 64
     K = 4096
     a, bb = oz.eval_inputs(4, 2.0, M * K, K * N)
     assert oz.choose_moduli_int8(K, 24, 90).b == 85
-    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=90, max_moduli=24)
+    i8 = oz.Transport.Int8Residues
+    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=90, max_moduli=24, transport=i8)
     assert p.fp8_digits and p.b == 90 and p.S == p.rS
-    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=85, max_moduli=24)
+    p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=85, max_moduli=24, transport=i8)
     assert not p.fp8_digits and p.b == 85
 
 
