@@ -87,9 +87,12 @@ int oz_scale_f64(oz_dev* dev, const double* X, int rows, int cols, int ld, int m
 /* Both operands of a product in one launch: the row maxima of A (M x K, lda) into dA[M] and the
  * column maxima of B (K x N, ldb) into dB[N], each as oz_scale_f64 (mode 0 for A, mode 1 for B, the
  * same ceil_mode and shift), with the range flags of A ORed into flags[0] and those of B into
- * flags[1] (two device words, 4-byte aligned). */
+ * flags[1] (two device words, 4-byte aligned). clear_flags, when not null, names two other device
+ * words (4-byte aligned, not overlapping flags) that the launch sets to zero: a caller that
+ * alternates between two flag slots, clearing the next pass's slot in this one, needs no launch
+ * to clear them. */
 int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int lda, const double* B, int N, int ldb,
-                      int ceil_mode, int shift, int32_t* dA, int32_t* dB, uint32_t* flags);
+                      int ceil_mode, int shift, int32_t* dA, int32_t* dB, uint32_t* flags, uint32_t* clear_flags);
 
 /* ---- A6-A8: Scheme II residues (reference modslice_int8.cpp:60, digits.h:80,165, f64_tf.h:141) -
  * For every element x of X (rows x cols, ld) with exponent delta d (delta[row] for mode 0,

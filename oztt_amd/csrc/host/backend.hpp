@@ -39,6 +39,20 @@ public:
     void release(int slot);
     void release_all();
 
+    // The range flags of the scaling stage (two device words per pass), kept in two slots so that
+    // no launch has to clear them: a pass ORs its flags into one slot while its scale launch zeroes
+    // the other, which the next pass then uses. flag_slots() gives this pass's slot (`use`) and the
+    // one to zero (`clear`); flags_issued() moves on once that scale launch has been issued (a pass
+    // whose scale launch failed uses the same slots again); last_flags() is the slot of the scale
+    // launch issued last. Both slots start at zero.
+    struct FlagSlots {
+        std::uint32_t* use;
+        std::uint32_t* clear;
+    };
+    FlagSlots flag_slots();
+    void flags_issued() { parity_ ^= 1u; }
+    const std::uint32_t* last_flags() const { return flags_ + 2 * (parity_ ^ 1u); }
+
 private:
     struct Buf {
         void* p = nullptr;
@@ -48,6 +62,8 @@ private:
     void free_host(Buf& b);
     oz_dev* dev_;
     std::vector<Buf> bufs_, host_;
+    std::uint32_t* flags_ = nullptr;  // 2 slots x 2 words
+    unsigned parity_ = 0;
 };
 
 // Host staging slots.

@@ -15,7 +15,21 @@ void device_check(oz_dev* dev, int status, const char* what) {
     throw std::runtime_error(std::string(what) + ": " + oz_last_error(dev));
 }
 
-Workspace::~Workspace() { release_all(); }
+Workspace::~Workspace() {
+    release_all();
+    if (flags_) (void)oz_dev_free(dev_, flags_);
+}
+
+Workspace::FlagSlots Workspace::flag_slots() {
+    if (!flags_) {
+        void* p = nullptr;
+        device_check(dev_, oz_dev_malloc(dev_, 4 * sizeof(std::uint32_t), &p), "device allocation");
+        flags_ = static_cast<std::uint32_t*>(p);
+        parity_ = 0;
+        device_check(dev_, oz_fill_u32(dev_, flags_, 0u, 4), "flags");  // stream-ordered before any use
+    }
+    return {flags_ + 2 * parity_, flags_ + 2 * (parity_ ^ 1u)};
+}
 
 void* Workspace::get(int slot, std::size_t bytes) {
     if (slot < 0) throw std::logic_error("workspace slot");

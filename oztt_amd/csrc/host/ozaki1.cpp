@@ -18,8 +18,8 @@
 // MI355X; its row bands (plan.hpp:386-444) remain for problems beyond the device memory (A's slices
 // and the partial sums are then per band, band_rows).
 //
-// Device layout: A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2]; slices of A: p planes of
-// Mbg x Kg int8 per band of rows, of B: p planes of Ng x Kg (B transposed), both in the GEMM's
+// Device layout: A (M x K f64), B (K x N f64), dA[M], dB[N] int32 (the range flags: Workspace::flag_slots);
+// slices of A: p planes of Mbg x Kg int8 per band of rows, of B: p planes of Ng x Kg (B transposed), both in the GEMM's
 // OZ_BLOCK tiles (Mbg, Ng multiples of 256, Kg of 64); partial sums (per band): p planes of Mbg x Ng
 // int32; output: M x N f64.
 #include <memory>
@@ -35,7 +35,7 @@ namespace {
 
 namespace ev = ::ozTTgemm::evaluation;
 
-enum Slot { kA = 0, kB, kDA, kDB, kFlags, kSlicesA, kSlicesB, kPartial, kOut, kLimbs };
+enum Slot { kA = 0, kB, kDA, kDB, kSlicesA, kSlicesB, kPartial, kOut, kLimbs };
 
 std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / q * q; }
 
@@ -96,7 +96,6 @@ Output ozaki1_run(Device& D, const Problem& p) {
 
     auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
     auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
-    auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
     const long long strideA = (long long)Mbg * Kbg, strideB = (long long)Ng * Kbg, strideP = (long long)Mbg * Ng;
     auto* slA = static_cast<std::int8_t*>(ws.get(kSlicesA, (std::size_t)P * strideA));
     auto* slB = static_cast<std::int8_t*>(ws.get(kSlicesB, (std::size_t)nkb * P * strideB));
@@ -105,14 +104,17 @@ Output ozaki1_run(Device& D, const Problem& p) {
     auto* limbs = by_block ? static_cast<float*>(ws.get(kLimbs, 3 * sizeof(float) * (std::size_t)M * N)) : nullptr;
     const long long limb_stride = (long long)M * N;
 
+    Workspace* wsp = &ws;
     std::vector<Step> steps;
     steps.push_back({ev::Scale, [=] {
-                         device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
+                         // the range flags: this pass's slot, and the next pass's cleared (Workspace::flag_slots)
+                         const Workspace::FlagSlots fs = wsp->flag_slots();
                          // BF16 of the maxima rounded as the format requires, target 2^nshift (format.hpp:76-101)
                          device_check(dev,
                                       oz_scale_pair_f64(dev, dAf, (int)M, (int)K, (int)K, dBf, (int)N, (int)N,
-                                                        (int)f.ceil, f.nshift, dltA, dltB, flags),
+                                                        (int)f.ceil, f.nshift, dltA, dltB, fs.use, fs.clear),
                                       "scale");
+                         wsp->flags_issued();
                      }});
     // B's slices once (per K block: rows kb Kc.. of B), then per band and K block: A's slices (columns
     // kb Kc.. of the band's rows), the diagonal products, the reconstruction. With one K block and one
@@ -186,8 +188,7 @@ Output ozaki1_run(Device& D, const Problem& p) {
     shape.steps[ev::Slice] = paired ? 1 : nkb + nbands * nkb;
     shape.steps[ev::Gemm] = nbands * nkb;
     shape.steps[ev::Recon] = nbands * nkb;
-    shape.written = {{flags, 2 * sizeof(std::uint32_t)},
-                     {dltA, sizeof(std::int32_t) * M},
+    shape.written = {{dltA, sizeof(std::int32_t) * M},
                      {dltB, sizeof(std::int32_t) * N},
                      {slA, (std::size_t)P * strideA},
                      {slB, (std::size_t)nkb * P * strideB},
@@ -195,7 +196,7 @@ Output ozaki1_run(Device& D, const Problem& p) {
                      {out, sizeof(double) * M * (std::size_t)N}};
     if (limbs) shape.written.push_back({limbs, 3 * sizeof(float) * (std::size_t)M * N});
     auto* host = p.c_dev ? nullptr : static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, shape, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * pairs, pairs);
+    run_pipeline(dev, steps, shape, out, host, (std::size_t)M * N, ws, 2.0 * M * (double)N * K * pairs, pairs);
     Info info{Scheme::I, p.options.format};
     info.slices = P;
     return {host, info, planp};

@@ -16,7 +16,7 @@
 //   the reference's composition launch; reconstruction from the output planes.
 //
 // Device layout (all row-major, zero-padded so that every kernel runs unguarded full tiles):
-//   A (M x K f64), B (K x N f64), dA[M], dB[N] int32, flags[2];
+//   A (M x K f64), B (K x N f64), dA[M], dB[N] int32 (range flags: Workspace::flag_slots);
 //   planes of A (per band of Mb rows): P x Mbg x Kg bytes, of B: P x Ng x Kg bytes (B transposed), both K-major in the
 //   GEMM's OZ_BLOCK tiles (1 KB blocks of 16 rows x 64 K-bytes), Mg, Ng multiples of 256 and Kg of
 //   64 (P = S residue planes, or the FP8 route's digit planes);
@@ -37,7 +37,7 @@ namespace {
 
 namespace ev = ::ozTTgemm::evaluation;
 
-enum Slot { kA = 0, kB, kDA, kDB, kFlags, kPlanesA, kPlanesB, kProducts, kOut };
+enum Slot { kA = 0, kB, kDA, kDB, kPlanesA, kPlanesB, kProducts, kOut };
 
 std::uint32_t round_up(std::uint32_t v, std::uint32_t q) { return (v + q - 1) / q * q; }
 
@@ -97,7 +97,6 @@ Output ozaki2_run(Device& D, const Problem& p) {
 
     auto* dltA = static_cast<std::int32_t*>(ws.get(kDA, sizeof(std::int32_t) * M));
     auto* dltB = static_cast<std::int32_t*>(ws.get(kDB, sizeof(std::int32_t) * N));
-    auto* flags = static_cast<std::uint32_t*>(ws.get(kFlags, 2 * sizeof(std::uint32_t)));
     const long long strideA = (long long)Mbg * Kg, strideB = (long long)Ng * Kg, strideC = (long long)Mbg * Ng;
     auto* planesA = static_cast<std::int8_t*>(ws.get(kPlanesA, (std::size_t)nplanes * strideA));
     auto* planesB = static_cast<std::int8_t*>(ws.get(kPlanesB, (std::size_t)nplanes * strideB));
@@ -108,14 +107,17 @@ Output ozaki2_run(Device& D, const Problem& p) {
     auto* terms = reinterpret_cast<std::uint16_t*>(prod);
 
     const int shift = plan.shift();
+    Workspace* wsp = &ws;
     std::vector<Step> steps;
     steps.push_back({ev::Scale, [=] {
-                         device_check(dev, oz_fill_u32(dev, flags, 0u, 2), "flags");
+                         // the range flags: this pass's slot, and the next pass's cleared (Workspace::flag_slots)
+                         const Workspace::FlagSlots fs = wsp->flag_slots();
                          // Scheme II rounds the BF16 of the maxima up (ozaki2.cpp:143-146)
                          device_check(dev,
                                       oz_scale_pair_f64(dev, dAf, (int)M, (int)K, (int)K, dBf, (int)N, (int)N, 1, shift,
-                                                        dltA, dltB, flags),
+                                                        dltA, dltB, fs.use, fs.clear),
                                       "scale");
+                         wsp->flags_issued();
                      }});
     // B's planes once, then per band: A's planes, the products, the reconstruction of the band's rows
     // (one band: A's and B's planes in one launch)
@@ -208,15 +210,14 @@ Output ozaki2_run(Device& D, const Problem& p) {
     shape.steps[ev::Slice] = nbands == 1 ? 1 : 1 + nbands;
     shape.steps[ev::Gemm] = nbands;
     shape.steps[ev::Recon] = nbands;
-    shape.written = {{flags, 2 * sizeof(std::uint32_t)},
-                     {dltA, sizeof(std::int32_t) * M},
+    shape.written = {{dltA, sizeof(std::int32_t) * M},
                      {dltB, sizeof(std::int32_t) * N},
                      {planesA, (std::size_t)nplanes * strideA},
                      {planesB, (std::size_t)nplanes * strideB},
                      {prod, (std::size_t)nterms * strideC * term_bytes},
                      {out, sizeof(double) * M * (std::size_t)N}};
     auto* host = p.c_dev ? nullptr : static_cast<double*>(ws.host(kHostC, sizeof(double) * M * (std::size_t)N));
-    run_pipeline(dev, steps, shape, out, host, (std::size_t)M * N, flags, 2.0 * M * (double)N * K * nprod, nprod);
+    run_pipeline(dev, steps, shape, out, host, (std::size_t)M * N, ws, 2.0 * M * (double)N * K * nprod, nprod);
     Info info{Scheme::II, p.options.format};
     // the format's route under Transport::Automatic (the reference's Info: for BF16, FP16, TF32, BFP8,
     // BFP4 and BFP2 also when INT8 residues carry it); the moduli that computed under Int8Residues

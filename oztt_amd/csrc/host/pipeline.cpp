@@ -37,7 +37,7 @@ bool whole_counts_match(const ev::Settings& s) {
 }  // namespace
 
 void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& shape, const double* out,
-                  double* host, std::size_t count, const std::uint32_t* flags, double product_ops,
+                  double* host, std::size_t count, const Workspace& ws, double product_ops,
                   unsigned partial_products) {
     ev::Settings* es = ev::active();
     // Per-phase device times: events around every step (slots 24 + 2i, 25 + 2i), summed by phase.
@@ -79,7 +79,7 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& 
     }
     if (host && count) device_check(dev, oz_memcpy_d2h(dev, host, out, sizeof(double) * count), "read C");
     std::uint32_t fl[2];
-    device_check(dev, oz_memcpy_d2h(dev, fl, flags, sizeof fl), "read flags");
+    device_check(dev, oz_memcpy_d2h(dev, fl, ws.last_flags(), sizeof fl), "read flags");
 
     // the first pass's result (when it is not in `host`), the reference of every replay
     std::vector<double> whole_ref;

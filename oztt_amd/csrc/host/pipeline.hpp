@@ -9,6 +9,7 @@
 #include <functional>
 #include <vector>
 
+#include "backend.hpp"
 #include "evaluation.hpp"
 #include "oz_hip.h"
 
@@ -35,16 +36,18 @@ struct PassShape {
 
 // Issues `steps` (timing each phase, then checking and replaying the whole pass under an active
 // evaluation Scope with repeats), reads back the `count` result values of `out` into `host` (none
-// when host is null: the result stays on the device) and the two range flags, and throws
-// std::runtime_error for a set flag (scale.hpp:187-208). `out` holds `count` values in any case.
+// when host is null: the result stays on the device) and the two range flags of the first pass (the
+// slot of `ws` its scale step used), and throws std::runtime_error for a set flag
+// (scale.hpp:187-208). `out` holds `count` values in any case.
 //
-// The whole-pass check (evaluation_hooks.hpp:175-211): every region of `shape.written` is filled
-// with a sentinel, which must then be read back from the output; one checking replay issues the
+// The whole-pass check (evaluation_hooks.hpp:175-211): every region of `shape.written` (every
+// intermediate and the output; the range flags are ORed into, not written, and have their own slots)
+// is filled with a sentinel, which must then be read back from the output; one checking replay issues the
 // steps, counted per phase against shape.steps; its output and the output after the timed replays
 // must both be bit-identical to the first pass. Only then is whole_checked set.
 // product_ops / partial_products describe the product phase for the evaluation record.
 void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& shape, const double* out,
-                  double* host, std::size_t count, const std::uint32_t* flags, double product_ops,
+                  double* host, std::size_t count, const Workspace& ws, double product_ops,
                   unsigned partial_products);
 
 }  // namespace ozTTgemm::detail

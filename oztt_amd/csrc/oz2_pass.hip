@@ -66,7 +66,7 @@ int run_pass(oz_dev* dev, const double* A, int lda, const double* B, int ldb, do
     const long long sA = (long long)L.Mg * L.Kg, sD = (long long)L.Mg * L.Ng;
     if (int st = oz_fill_u32(dev, flags, 0u, 2)) return st;
     // Scheme II rounds the BF16 of the maxima up (reference ozaki2.cpp:143-146)
-    if (int st = oz_scale_pair_f64(dev, A, M, K, lda, B, N, ldb, 1, crt->shift, dA, dB, flags)) return st;
+    if (int st = oz_scale_pair_f64(dev, A, M, K, lda, B, N, ldb, 1, crt->shift, dA, dB, flags, nullptr)) return st;
     if (int st = oz2_split_pair_int8(dev, A, M, K, lda, dA, B, N, ldb, dB, mo, pA, pB, L.Mg, L.Ng, L.Kg)) return st;
     if (int st = oz2_gemm_digits(dev, pA, pB, dg, L.Mg, L.Ng, L.Kg, S, L.Ng, sA, (long long)L.Ng * L.Kg, sD, crt))
         return st;

@@ -129,22 +129,31 @@ __device__ __forceinline__ int32_t key_delta(uint32_t key, int shift, uint32_t& 
 }
 
 // A's rows and B's columns in one launch of 1024-thread workgroups, deltas written directly:
-//   workgroup j < ceil(N/32): columns 32j..32j+31 of B over all of its K rows, thread t taking
-//   column t % 32 and every 32nd row from t / 32 (a wave reads two 256-byte row pieces per load;
-//   with 16 columns, 128-byte pieces, the strips read at 4.9 instead of 5.7 TB/s at C3);
-//   workgroup ceil(N/32) + r: rows rR..rR+R-1 of A (R = 1 for K > 4096, more for shorter rows), each
+//   workgroup j < ceil(N/W): columns Wj..Wj+W-1 of B over all of its K rows, thread t taking
+//   column t % W and every P-th row from t / W (P = 1024/W phases). W = 32 (a wave reads two
+//   256-byte row pieces per load; with 16 columns, 128-byte pieces, the strips read at 4.9 instead
+//   of 5.7 TB/s at C3); for K <= 1024, W = 16, so that every thread's rows are one round of 16 loads
+//   and there are twice as many strips (C1: 64 strips instead of 32 for 1024 columns);
+//   workgroup ceil(N/W) + r: rows rR..rR+R-1 of A (R = 1 for K > 4096, more for shorter rows), each
 //   thread a stride-(1024/R) run of its row's K values.
-// The column strips read 32 K doubles each workgroup, the rows K: the long strips are dispatched
+// The column strips read W K doubles each workgroup, the rows K: the long strips are dispatched
 // first and the short rows fill in behind them, so no strip is left running alone at the end.
 // The 16 waves' maxima meet in LDS; flags[0] (A) and flags[1] (B) collect the flag bits with atomicOr.
-template <int CEIL>
+// Thread 0 and 1 of workgroup 0 zero clear[0..1] (when given): the flag slot of the next pass, so
+// that a caller alternating between two slots needs no launch to clear them.
+template <int CEIL, int W>
 __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restrict__ A, int M, int K, int lda,
                                                           const double* __restrict__ B, int N, int ldb, int shift,
                                                           int32_t* __restrict__ dA, int32_t* __restrict__ dB,
-                                                          uint32_t* __restrict__ flags, int rows_per_wg) {
+                                                          uint32_t* __restrict__ flags, uint32_t* __restrict__ clear,
+                                                          int rows_per_wg) {
+    static_assert(W == 16 || W == 32, "strip width");
+    constexpr int P = 1024 / W;  // row phases of a strip
     __shared__ uint32_t part[1024];
     const int t = threadIdx.x;
-    const int strips = (N + 31) / 32;
+    // the other flag slot, which no workgroup of this launch touches otherwise
+    if (clear && blockIdx.x == 0 && t < 2) clear[t] = 0u;
+    const int strips = (N + W - 1) / W;
     if ((int)blockIdx.x >= strips) {
         // R rows per workgroup (rows_per_wg: R = 8192 / K rounded down to a power of two, 1..16), so
         // that every thread has 8 loads in flight for K <= 8192: the 1024 / R threads of a row take a
@@ -177,47 +186,47 @@ __global__ void __launch_bounds__(1024) scale_pair_kernel(const double* __restri
             if (bad) atomicOr(&flags[0], bad);
         }
     } else {
-        const int col = (int)blockIdx.x * 32 + (t & 31);
-        const int ph = t >> 5;
-        // 16 loads in flight per thread (512 rows of the strip per round trip)
+        const int col = (int)blockIdx.x * W + (t % W);
+        const int ph = t / W;
+        // 16 loads in flight per thread (16 P rows of the strip per round trip)
         uint32_t k[4] = {0, 0, 0, 0};
         if (col < N) {
             const double* p = B + col;
             int r = ph;
-            for (; r + 480 < K; r += 512) {
+            for (; r + 15 * P < K; r += 16 * P) {
                 double v[16];
 #pragma unroll
-                for (int u = 0; u < 16; u++) v[u] = p[(size_t)(r + 32 * u) * ldb];
+                for (int u = 0; u < 16; u++) v[u] = p[(size_t)(r + P * u) * ldb];
 #pragma unroll
                 for (int u = 0; u < 16; u++) k[u & 3] = max(k[u & 3], bf16_key<CEIL>(v[u]));
             }
-            for (; r + 96 < K; r += 128) {
+            for (; r + 3 * P < K; r += 4 * P) {
                 double v[4];
 #pragma unroll
-                for (int u = 0; u < 4; u++) v[u] = p[(size_t)(r + 32 * u) * ldb];
+                for (int u = 0; u < 4; u++) v[u] = p[(size_t)(r + P * u) * ldb];
 #pragma unroll
                 for (int u = 0; u < 4; u++) k[u] = max(k[u], bf16_key<CEIL>(v[u]));
             }
-            for (; r < K; r += 32) k[0] = max(k[0], bf16_key<CEIL>(p[(size_t)r * ldb]));
+            for (; r < K; r += P) k[0] = max(k[0], bf16_key<CEIL>(p[(size_t)r * ldb]));
         }
-        part[t] = max(max(k[0], k[1]), max(k[2], k[3]));  // part[32 ph + c]
+        part[t] = max(max(k[0], k[1]), max(k[2], k[3]));  // part[W ph + c]
         __syncthreads();
-        // 32 phases per column: 8 threads per column take 4 phases each, then one thread 8 of those
-        uint32_t m4 = 0;
-        if (t < 256) {
-            const int c = t & 31, q = t >> 5;
-            m4 = max(max(part[(4 * q) * 32 + c], part[(4 * q + 1) * 32 + c]),
-                     max(part[(4 * q + 2) * 32 + c], part[(4 * q + 3) * 32 + c]));
+        // P phases per column: 8 threads per column take P/8 phases each, then one thread 8 of those
+        uint32_t m8 = 0;
+        if (t < 8 * W) {
+            const int c = t % W, q = t / W;
+#pragma unroll
+            for (int u = 0; u < P / 8; u++) m8 = max(m8, part[((P / 8) * q + u) * W + c]);
         }
         __syncthreads();
-        if (t < 256) part[t] = m4;  // part[32 q + c]
+        if (t < 8 * W) part[t] = m8;  // part[W q + c]
         __syncthreads();
-        if (t < 32 && (int)blockIdx.x * 32 + t < N) {
+        if (t < W && (int)blockIdx.x * W + t < N) {
             uint32_t m = 0;
 #pragma unroll
-            for (int q = 0; q < 8; q++) m = max(m, part[q * 32 + t]);
+            for (int q = 0; q < 8; q++) m = max(m, part[q * W + t]);
             uint32_t bad;
-            dB[(int)blockIdx.x * 32 + t] = key_delta(m, shift, bad);
+            dB[(int)blockIdx.x * W + t] = key_delta(m, shift, bad);
             if (bad) atomicOr(&flags[1], bad);
         }
     }
@@ -261,22 +270,29 @@ extern "C" int oz_scale_f64(oz_dev* dev, const double* X, int rows, int cols, in
 }
 
 extern "C" int oz_scale_pair_f64(oz_dev* dev, const double* A, int M, int K, int lda, const double* B, int N, int ldb,
-                                 int ceil_mode, int shift, int32_t* dA, int32_t* dB, uint32_t* flags) {
+                                 int ceil_mode, int shift, int32_t* dA, int32_t* dB, uint32_t* flags,
+                                 uint32_t* clear_flags) {
     if (int st = oz::use(dev)) return st;
     if (!A || !B || !dA || !dB || !flags || M <= 0 || N <= 0 || K <= 0 || lda < K || ldb < N || ceil_mode < 0 ||
-        ceil_mode > 2 || ((uintptr_t)flags & 3))
+        ceil_mode > 2 || ((uintptr_t)flags & 3) || ((uintptr_t)clear_flags & 3) ||
+        (clear_flags && clear_flags + 2 > flags && flags + 2 > clear_flags))
         return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: invalid arguments (M=%d N=%d K=%d lda=%d ldb=%d ceil=%d)",
                         M, N, K, lda, ldb, ceil_mode);
     int R = 1;  // rows of A per workgroup: 8 loads per thread for K <= 8192
     while (R < 16 && (long long)K * R * 2 <= 8192) R *= 2;
-    const long long blocks = ((long long)M + R - 1) / R + (N + 31) / 32;
+    const int W = K <= 1024 ? 16 : 32;  // columns of B per workgroup
+    const long long blocks = ((long long)M + R - 1) / R + (N + W - 1) / W;
     if (blocks > 0x7FFFFFFFll) return oz::fail(dev, OZ_ERR_ARG, "oz_scale_pair_f64: grid too large");
     const dim3 grid((unsigned)blocks), block(1024);
-    if (ceil_mode == 0)
-        hipLaunchKernelGGL(scale_pair_kernel<0>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
-    else if (ceil_mode == 1)
-        hipLaunchKernelGGL(scale_pair_kernel<1>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags,
+                           clear_flags, R);
+    };
+    if (W == 16)
+        ceil_mode == 0 ? launch(scale_pair_kernel<0, 16>)
+                       : (ceil_mode == 1 ? launch(scale_pair_kernel<1, 16>) : launch(scale_pair_kernel<2, 16>));
     else
-        hipLaunchKernelGGL(scale_pair_kernel<2>, grid, block, 0, dev->stream, A, M, K, lda, B, N, ldb, shift, dA, dB, flags, R);
+        ceil_mode == 0 ? launch(scale_pair_kernel<0, 32>)
+                       : (ceil_mode == 1 ? launch(scale_pair_kernel<1, 32>) : launch(scale_pair_kernel<2, 32>));
     return oz::launch_check(dev, "scale_pair_kernel");
 }

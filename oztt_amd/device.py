@@ -168,9 +168,10 @@ class Device:
                                        flags.offset(4 * flag_index)), "oz_scale_f64")
 
     def scale_pair(self, A: Buffer, M, K, lda, B: Buffer, N, ldb, ceil_mode, shift, dA: Buffer, dB: Buffer,
-                   flags: Buffer):
+                   flags: Buffer, clear=None):
+        """clear: a pointer (ctypes.c_void_p, e.g. Buffer.offset) to two words the launch zeroes, or None."""
         self._check(hip().oz_scale_pair_f64(self.h, A.ptr, M, K, lda, B.ptr, N, ldb, ceil_mode, shift, dA.ptr, dB.ptr,
-                                            flags.ptr), "oz_scale_pair_f64")
+                                            flags.ptr, clear), "oz_scale_pair_f64")
 
     def split_pair_int8(self, A: Buffer, M, K, lda, dA: Buffer, B: Buffer, N, ldb, dB: Buffer, desc: ModuliDesc,
                         pA: Buffer, pB: Buffer, Mg, Ng, Kg):

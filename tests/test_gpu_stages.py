@@ -408,7 +408,8 @@ def test_scale_pair_matches_oracle(dev, oracle, ceil_mode, M, N, K):
 
 def test_scale_pair_flags(dev, oracle):
     """Range flags of the pair: Inf/NaN (4), a nonzero maximum below 2^-126 (2), above the largest BF16 (1),
-    A's into flags[0] and B's into flags[1], as oz_scale_f64 reports them."""
+    A's into flags[0] and B's into flags[1], as oz_scale_f64 reports them; the launch zeroes the other
+    flag slot it is given (the next pass's), and ORs into its own without clearing it first."""
     M, N, K = 64, 48, 96
     A = np.ones((M, K))
     B = np.ones((K, N))
@@ -417,7 +418,12 @@ def test_scale_pair_flags(dev, oracle):
     B[:, 9] = 2.0 ** 129
     B[11, 2] = np.nan
     bA, bB = dev.upload(A), dev.upload(B)
-    dA, dB, fl = dev.alloc(4 * M), dev.alloc(4 * N), dev.alloc(8)
+    dA, dB, fl = dev.alloc(4 * M), dev.alloc(4 * N), dev.alloc(16)
+    dev.fill_u32(fl, 0xFFFFFFFF, 4)
+    dev.fill_u32(fl, 8, 1)  # a bit already set in this pass's slot (the launch ORs into it)
+    dev.scale_pair(bA, M, K, K, bB, N, N, 1, 16, dA, dB, fl, fl.offset(8))
+    both = dev.download(fl, np.uint32, 4)
+    assert list(both[2:]) == [0, 0] and both[0] & 8 and both[1] == 0xFFFFFFFF
     dev.fill_u32(fl, 0, 2)
     dev.scale_pair(bA, M, K, K, bB, N, N, 1, 16, dA, dB, fl)
     flags = dev.download(fl, np.uint32, 2)
