@@ -1095,22 +1095,50 @@ static void tf_mul_r_twoproduct(float& hi, float& mid, float& lo, float r) {
     fast_two_sum(ec, g, mid, lo);
 }
 
-// Equivalence check of the two forms of tfMulR (tf_mul_r, Dekker's, and tf_mul_r_twoproduct) on n
-// pseudo-random chains. mode 0, the slicer: x*2^d of a random double, scaled near 1/2 or 50-100
-// binades below, then `planes` digits in radix r with bound dmax; a chain counts as covered when
-// the GPU takes the TwoProduct form for it (x's last significand bit weighs at least 2^-126, or x
-// is zero; and |hi| r <= dmax + 1/2, so that the state never grows), and as differing when any
-// digit differs. mode 1, the reconstruction: Horner chains of up to `planes` diagonal sums (int32,
-// added as the reference's high and low parts), all covered; differing when a triple differs.
-// Returns the number of covered chains that differ; *covered receives the covered count.
-int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
-                                 int64_t* covered) {
+// The TwoProduct form with two of its TwoSums taken as FastTwoSums, the form the GPU's slicer uses: FastTwoSum(a, b) gives TwoSum's (sum, error) exactly when |a| >= |b| (or a = 0)
+// and nothing overflows or is flushed. (p1, tmp0): tmp0 is the rounding error of mid*r plus lo*r, at
+// most about one unit in the last place of p1; (p0, sb): sb collects the lower limbs' products, below
+// one unit in the last place of p0. `violations` counts the calls where that order does not hold.
+static void tf_mul_r_fast(float& hi, float& mid, float& lo, float r, int64_t& violations) {
+    auto f_fma = [](float a, float b, float c) { return flush(std::fmaf(flush(a), flush(b), flush(c))); };
+    const float acc_lo = f_mul(lo, r);
+    const float p1 = f_mul(mid, r);
+    float tmp0 = f_fma(mid, r, -p1);
+    const float p0 = f_mul(hi, r);
+    const float f0 = f_fma(hi, r, -p0);
+    tmp0 = f_add(tmp0, acc_lo);
+    float sa, ea, sb, eb, r0, ec;
+    if (p1 != 0.0f && std::fabs(p1) < std::fabs(tmp0)) violations++;
+    fast_two_sum(p1, tmp0, sa, ea);
+    two_sum(f0, sa, sb, eb);
+    if (p0 != 0.0f && std::fabs(p0) < std::fabs(sb)) violations++;
+    fast_two_sum(p0, sb, r0, ec);
+    const float g = f_add(ea, eb);
+    hi = r0;
+    fast_two_sum(ec, g, mid, lo);
+}
+
+// Equivalence check of tfMulR forms against Dekker's (tf_mul_r, the reference's) on n pseudo-random
+// chains; form(hi, mid, lo, r, violations) is the other form. mode 0, the slicer: x*2^d of a random
+// double, scaled near 1/2 or 50-100 binades below, then `planes` digits in radix r with bound dmax; a
+// chain counts as covered when the GPU takes the TwoProduct form for it (x's last significand bit
+// weighs at least 2^-126, or x is zero; and |hi| r <= dmax + 1/2, so that the state never grows), and
+// as differing when any digit differs. mode 1, the reconstruction: Horner chains of up to `planes`
+// diagonal sums (int32, added as the reference's high and low parts), all covered; differing when a
+// triple differs. Returns the number of covered chains that differ; *covered receives the covered
+// count and *violations the form's precondition failures on covered chains.
+}  // extern "C"
+
+template <class FORM>
+static int64_t check_forms(FORM form, int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
+                           int64_t* covered, int64_t* violations) {
     const float r = (float)radix, dm = (float)dmax;
-    int64_t bad = 0, cov = 0;
-#pragma omp parallel for schedule(static) reduction(+ : bad, cov)
+    int64_t bad = 0, cov = 0, viol = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad, cov, viol)
     for (int64_t it = 0; it < n; it++) {
         std::mt19937_64 g(seed * 0x9E3779B97F4A7C15ull + (uint64_t)it);
         bool same = true, covered_chain = true;
+        int64_t v = 0;
         if (mode == 0) {
             uint64_t u = g();
             const int E = (int)(g() % 2047);
@@ -1126,7 +1154,7 @@ int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, 
             covered_chain = (E == 0 || E - 1075 + d >= -126) && std::fabs(h1) * r <= dm + 0.5f;
             for (int t = 0; t < planes; t++) {
                 tf_mul_r(h1, m1, l1, r);
-                tf_mul_r_twoproduct(h2, m2, l2, r);
+                form(h2, m2, l2, r, v);
                 float a = f_rnd(h1), b = f_rnd(h2);
                 a = a < -dm ? -dm : (a >= dm ? dm : a);
                 b = b < -dm ? -dm : (b >= dm ? dm : b);
@@ -1140,16 +1168,16 @@ int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, 
             for (int dd = 0; dd < p; dd++) {
                 if (dd) {
                     tf_mul_r(h1, m1, l1, r);
-                    tf_mul_r_twoproduct(h2, m2, l2, r);
+                    form(h2, m2, l2, r, v);
                 }
-                int64_t v;
+                int64_t w;
                 switch (g() % 4) {
-                case 0: v = (int64_t)(g() % 4294967295ull) - 2147483647; break;
-                case 1: v = (g() & 1) ? 2147483647 : -2147483647; break;
-                case 2: v = (int64_t)(g() % 200001) - 100000; break;
-                default: v = 0;
+                case 0: w = (int64_t)(g() % 4294967295ull) - 2147483647; break;
+                case 1: w = (g() & 1) ? 2147483647 : -2147483647; break;
+                case 2: w = (int64_t)(g() % 200001) - 100000; break;
+                default: w = 0;
                 }
-                const float vh = (float)(int32_t)((uint32_t)v & 0xFFFFFF00u), vl = (float)(int32_t)((uint32_t)v & 0xFFu);
+                const float vh = (float)(int32_t)((uint32_t)w & 0xFFFFFF00u), vl = (float)(int32_t)((uint32_t)w & 0xFFu);
                 tf_add_s(h1, m1, l1, vh);
                 tf_add_s(h1, m1, l1, vl);
                 tf_add_s(h2, m2, l2, vh);
@@ -1159,11 +1187,30 @@ int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, 
         }
         if (covered_chain) {
             cov++;
+            viol += v;
             if (!same) bad++;
         }
     }
     *covered = cov;
+    if (violations) *violations = viol;
     return bad;
+}
+
+extern "C" {
+
+// Dekker's form against the TwoProduct form (tf_mul_r_twoproduct).
+int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
+                                 int64_t* covered) {
+    auto form = [](float& h, float& m, float& l, float r, int64_t&) { tf_mul_r_twoproduct(h, m, l, r); };
+    return check_forms(form, mode, n, seed, radix, dmax, planes, covered, nullptr);
+}
+
+// Dekker's form against the TwoProduct form with FastTwoSums (tf_mul_r_fast); *violations counts its
+// precondition failures.
+int64_t orc_check_tf_mul_r_fast(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
+                                int64_t* covered, int64_t* violations) {
+    auto form = [](float& h, float& m, float& l, float r, int64_t& v) { tf_mul_r_fast(h, m, l, r, v); };
+    return check_forms(form, mode, n, seed, radix, dmax, planes, covered, violations);
 }
 
 // Diagonal partial products P_d = sum_{i<=d} A_i B_{d-i} (ozaki1/gemm.hpp:315, stages.hpp:157), exact in

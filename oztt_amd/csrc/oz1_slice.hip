@@ -40,7 +40,7 @@ struct SliceGen {
     }
     template <bool FMA>
     __device__ __forceinline__ int plane1(State& st) const {
-        tf_mul_radix<POW2, FMA>(st.hi, st.mid, st.lo, radix);
+        tf_mul_radix<POW2, FMA, true>(st.hi, st.mid, st.lo, radix);
         float v = __builtin_rintf(st.hi);  // Rnd: nearest, ties to even
         if (v < -dmax)
             v = -dmax;

@@ -135,12 +135,44 @@ __device__ __forceinline__ void tf_mul_r_fma(float& hi, float& mid, float& lo, f
     fast_two_sum(ec, G, mid, lo);
 }
 
+// The slicer's tfMulR: tf_mul_r_fma with two of its TwoSums taken as FastTwoSums (22 operations).
+//   FastTwoSum(a, b) gives TwoSum's sum and exact error whenever |a| >= |b| or a = 0 (and nothing
+// overflows or is flushed). (P1, tmp0): tmp0 is the FMA's error of mid r (at most half a unit in the
+// last place of P1) plus lo r, and |lo| is at most a unit in the last place of mid (the limbs of
+// load_triple and of every renormalization), so |tmp0| is a few units in the last place of P1 while
+// a nonzero P1 holds 2^23 of them; P1 = 0 (mid = 0) is exact either way. (P0, sb): sb sums F0 (at
+// most half a unit in the last place of P0) and about mid r, and |mid| <= |hi|/2: after a
+// renormalization mid is below half a unit in the last place of hi, and after a digit d is taken
+// (hi - d, a nonzero multiple of the unit in the last place of the renormalized hi, which bounds mid
+// by half of that unit) still at most half of |hi|. So |sb| < |P0| for hi != 0, and P0 = 0 is exact.
+// The oracle checks this form against Dekker's, and that both orders hold at every call, over slicer
+// chains (orc_check_tf_mul_r_fast). The reconstruction's states do not keep |mid| <= |hi|/2 (adding
+// a diagonal sum can cancel hi and leave mid), so it keeps tf_mul_r_fma.
+__device__ __forceinline__ void tf_mul_r_fast(float& hi, float& mid, float& lo, float r) {
+    const float acc_lo = lo * r;
+    const float P1 = mid * r;
+    float tmp0 = __builtin_fmaf(mid, r, -P1);  // F1
+    const float P0 = hi * r;
+    const float F0 = __builtin_fmaf(hi, r, -P0);
+    tmp0 = tmp0 + acc_lo;  // G1
+    float sa, ea, sb, eb, r0, ec;
+    fast_two_sum(P1, tmp0, sa, ea);
+    two_sum(F0, sa, sb, eb);
+    fast_two_sum(P0, sb, r0, ec);
+    const float G = ea + eb;
+    hi = r0;
+    fast_two_sum(ec, G, mid, lo);
+}
+
 // tfMulRadix (sfpu_tf.h:131-134): tfMulP2 for a power-of-two radix, tfMulR otherwise (FMA: its
-// TwoProduct form, for callers that meet the conditions of tf_mul_r_fma).
-template <bool POW2, bool FMA = false>
+// TwoProduct form, for callers that meet the conditions of tf_mul_r_fma; FAST: the slicer's form
+// tf_mul_r_fast, under the same conditions).
+template <bool POW2, bool FMA = false, bool FAST = false>
 __device__ __forceinline__ void tf_mul_radix(float& hi, float& mid, float& lo, float r) {
     if constexpr (POW2)
         tf_mul_pow2(hi, mid, lo, r);
+    else if constexpr (FMA && FAST)
+        tf_mul_r_fast(hi, mid, lo, r);
     else if constexpr (FMA)
         tf_mul_r_fma(hi, mid, lo, r);
     else

@@ -430,6 +430,24 @@ def test_tf_mul_r_forms_agree_in_the_reconstruction(orc, radix, pmax):
     assert bad == 0 and cov.value == n
 
 
+@pytest.mark.parametrize("radix,dmax", [(254, 127), (14, 7), (32, 16), (12, 6)])
+def test_tf_mul_r_fast_form_agrees_and_its_order_holds(orc, radix, dmax):
+    """The GPU's slicer also takes two of tfMulR's TwoSums as FastTwoSums (TwoProduct form): on the slicer
+    chains it covers its digits equal Dekker's form, and the FastTwoSum order (|a| >= |b| or a = 0) holds
+    at every call, so the substitution is exact there rather than merely lucky."""
+    mode, planes = 0, 24
+    import ctypes
+    f = orc.lib.orc_check_tf_mul_r_fast
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
+    cov, viol = ctypes.c_int64(), ctypes.c_int64()
+    n = 300000
+    bad = f(mode, n, 13, radix, dmax, planes, ctypes.byref(cov), ctypes.byref(viol))
+    assert bad == 0 and viol.value == 0
+    assert cov.value > n // 2
+
+
 def test_tf_mul_r_forms_checker_sees_overflow_beyond_the_bound(orc):
     """The check can fail: past the bound (radix 14 with up to 30 diagonals) Dekker's split
     overflows where the TwoProduct form does not, and the checker counts those chains."""
