@@ -119,27 +119,38 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& 
     if (es && es->repeats > 0 && es->replay_drop_phase < 0) {
         // 3. whole pass: warm up, then `repeats` replays between two events; the output must still
         //    be the first pass's
+        //    The product steps of the timed passes are bracketed by events too (slots 24.. while they
+        //    last: every pass whose product steps fit), which gives the products' time per pass as
+        //    they run inside the whole pass (an event marker costs no measurable time).
         for (int w = 0; w < es->warmup; w++)
             for (auto& s : steps) s.issue();
+        int slot = kFirstSlot, timed_passes = 0;
+        std::size_t gemm_steps = 0;
+        for (auto& s : steps) gemm_steps += s.phase == ev::Gemm;
         device_check(dev, oz_event_record(dev, 20), "event");
-        for (int r = 0; r < es->repeats; r++)
-            for (auto& s : steps) s.issue();
+        for (int r = 0; r < es->repeats; r++) {
+            const bool mark = slot + 2 * gemm_steps <= (std::size_t)kSlots;
+            for (auto& s : steps) {
+                if (mark && s.phase == ev::Gemm) device_check(dev, oz_event_record(dev, slot++), "event");
+                s.issue();
+                if (mark && s.phase == ev::Gemm) device_check(dev, oz_event_record(dev, slot++), "event");
+            }
+            timed_passes += mark;
+        }
         device_check(dev, oz_event_record(dev, 21), "event");
         float ms = 0;
         device_check(dev, oz_event_elapsed_ms(dev, 20, 21, &ms), "event time");
         es->whole_ms = ms / es->repeats;
+        double gemm_ms = 0;
+        for (int e = kFirstSlot; e < slot; e += 2) {
+            device_check(dev, oz_event_elapsed_ms(dev, e, e + 1, &ms), "event time");
+            gemm_ms += ms;
+        }
+        es->gemm_launch_ms = timed_passes ? gemm_ms / timed_passes : 0.0;
         const std::vector<double> last = read_back(dev, out, count);
         es->whole_checked = es->whole_sentinel && whole_counts_match(*es) &&
                             same_bits(last, host ? host : whole_ref.data(), count);
-        // 4. the product steps alone, for their average launch time
-        device_check(dev, oz_event_record(dev, 22), "event");
-        for (int r = 0; r < es->repeats; r++)
-            for (auto& s : steps)
-                if (s.phase == ev::Gemm) s.issue();
-        device_check(dev, oz_event_record(dev, 23), "event");
-        device_check(dev, oz_event_elapsed_ms(dev, 22, 23, &ms), "event time");
-        es->gemm_launch_ms = ms / es->repeats;
-        // warm phase times: the average of up to 5 more passes with events between the steps
+        // 4. warm phase times: the average of up to 5 more passes with events between the steps
         if (step_events) {
             const int passes = es->repeats < 5 ? es->repeats : 5;
             double acc[ev::PhaseCount] = {};
