@@ -1127,11 +1127,27 @@ static void tf_mul_r_fast(float& hi, float& mid, float& lo, float r, int64_t& vi
 // diagonal sums (int32, added as the reference's high and low parts), all covered; differing when a
 // triple differs. Returns the number of covered chains that differ; *covered receives the covered
 // count and *violations the form's precondition failures on covered chains.
+// tfMulP2 with both TwoSums taken as FastTwoSums, the form the GPU's slicer uses for a power-of-two
+// radix: (mid, lo) with |lo| at most a unit in the last place of mid, and (hi, fl(mid + lo)) with
+// |mid| <= |hi|/2 in every slicer state. `violations` counts the calls where that order does not hold.
+static void tf_mul_pow2_fast(float& hi, float& mid, float& lo, float r, int64_t& violations) {
+    hi = f_mul(hi, r);
+    mid = f_mul(mid, r);
+    lo = f_mul(lo, r);
+    float s3, e4, s5, e6;
+    if (mid != 0.0f && std::fabs(mid) < std::fabs(lo)) violations++;
+    fast_two_sum(mid, lo, s3, e4);
+    if (hi != 0.0f && std::fabs(hi) < std::fabs(s3)) violations++;
+    fast_two_sum(hi, s3, s5, e6);
+    hi = s5;
+    fast_two_sum(e6, e4, mid, lo);
+}
+
 }  // extern "C"
 
-template <class FORM>
-static int64_t check_forms(FORM form, int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
-                           int64_t* covered, int64_t* violations) {
+template <class FORM, class REF>
+static int64_t check_forms(FORM form, REF ref, int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
+                           int64_t* covered, int64_t* violations, bool all_chains = false) {
     const float r = (float)radix, dm = (float)dmax;
     int64_t bad = 0, cov = 0, viol = 0;
 #pragma omp parallel for schedule(static) reduction(+ : bad, cov, viol)
@@ -1151,9 +1167,9 @@ static int64_t check_forms(FORM form, int mode, int64_t n, uint64_t seed, int ra
             float h1, m1, l1;
             load_triple(x, d, h1, m1, l1);
             float h2 = h1, m2 = m1, l2 = l1;
-            covered_chain = (E == 0 || E - 1075 + d >= -126) && std::fabs(h1) * r <= dm + 0.5f;
+            covered_chain = all_chains || ((E == 0 || E - 1075 + d >= -126) && std::fabs(h1) * r <= dm + 0.5f);
             for (int t = 0; t < planes; t++) {
-                tf_mul_r(h1, m1, l1, r);
+                ref(h1, m1, l1, r);
                 form(h2, m2, l2, r, v);
                 float a = f_rnd(h1), b = f_rnd(h2);
                 a = a < -dm ? -dm : (a >= dm ? dm : a);
@@ -1167,7 +1183,7 @@ static int64_t check_forms(FORM form, int mode, int64_t n, uint64_t seed, int ra
             float h1 = 0, m1 = 0, l1 = 0, h2 = 0, m2 = 0, l2 = 0;
             for (int dd = 0; dd < p; dd++) {
                 if (dd) {
-                    tf_mul_r(h1, m1, l1, r);
+                    ref(h1, m1, l1, r);
                     form(h2, m2, l2, r, v);
                 }
                 int64_t w;
@@ -1202,7 +1218,8 @@ extern "C" {
 int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
                                  int64_t* covered) {
     auto form = [](float& h, float& m, float& l, float r, int64_t&) { tf_mul_r_twoproduct(h, m, l, r); };
-    return check_forms(form, mode, n, seed, radix, dmax, planes, covered, nullptr);
+    auto ref = [](float& h, float& m, float& l, float r) { tf_mul_r(h, m, l, r); };
+    return check_forms(form, ref, mode, n, seed, radix, dmax, planes, covered, nullptr);
 }
 
 // Dekker's form against the TwoProduct form with FastTwoSums (tf_mul_r_fast); *violations counts its
@@ -1210,7 +1227,18 @@ int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, 
 int64_t orc_check_tf_mul_r_fast(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
                                 int64_t* covered, int64_t* violations) {
     auto form = [](float& h, float& m, float& l, float r, int64_t& v) { tf_mul_r_fast(h, m, l, r, v); };
-    return check_forms(form, mode, n, seed, radix, dmax, planes, covered, violations);
+    auto ref = [](float& h, float& m, float& l, float r) { tf_mul_r(h, m, l, r); };
+    return check_forms(form, ref, mode, n, seed, radix, dmax, planes, covered, violations);
+}
+
+// tfMulP2 (the reference's, for a power-of-two radix) against tf_mul_pow2_fast on every chain of the
+// mode (*covered = n; mode 0: slicer chains, 1: reconstruction chains); *violations counts its
+// precondition failures.
+int64_t orc_check_tf_mul_pow2_fast(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
+                                   int64_t* covered, int64_t* violations) {
+    auto form = [](float& h, float& m, float& l, float r, int64_t& v) { tf_mul_pow2_fast(h, m, l, r, v); };
+    auto ref = [](float& h, float& m, float& l, float r) { tf_mul_pow2(h, m, l, r); };
+    return check_forms(form, ref, mode, n, seed, radix, dmax, planes, covered, violations, true);
 }
 
 // Diagonal partial products P_d = sum_{i<=d} A_i B_{d-i} (ozaki1/gemm.hpp:315, stages.hpp:157), exact in

@@ -18,7 +18,8 @@
 //                                 phi_sweep.log:116,122)
 //   orc_oz2_crt_exact             exact integer arithmetic; cross-checked against a binary128 GEMM
 //   orc_check_tf_mul_r_forms      checkers, not restatements: the GPU's forms of tfMulR against Dekker's
-//   orc_check_tf_mul_r_fast       in the FP32 model
+//   orc_check_tf_mul_r_fast,      in the FP32 model
+//   orc_check_tf_mul_pow2_fast
 //   orc_oz1_slices/gemm_diag/     reference output hashes of scheme I INT8 (tools/validated/quick.csv:12,
 //   recon/int8_gemm               phi_sweep.log chash of I-INT8 4096^3), the slice exactness
 //                                 invariant sum_i d_i radix^-(i+1) + residual == x*2^delta, brute force
@@ -108,6 +109,8 @@ int64_t orc_check_tf_mul_r_forms(int mode, int64_t n, uint64_t seed, int radix, 
                                  int64_t* covered);
 int64_t orc_check_tf_mul_r_fast(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
                                 int64_t* covered, int64_t* violations);
+int64_t orc_check_tf_mul_pow2_fast(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
+                                   int64_t* covered, int64_t* violations);
 // Diagonal partial products P_d = sum_{i<=d} A_i B_{d-i} (ozaki1/gemm.hpp:315), exact; returns max |P|.
 int64_t orc_oz1_gemm_diag(const int8_t* A, const int8_t* B, int32_t* P, int M, int N, int K, int p, int ndiag);
 // Horner reconstruction + FP64 assembly (recon_tf_i32in.cpp:116-157, recon_f64_writer.cpp:148-160).

@@ -75,6 +75,24 @@ __device__ __forceinline__ void tf_mul_pow2(float& hi, float& mid, float& lo, fl
     fast_two_sum(e6, e4, mid, lo);
 }
 
+// tfMulP2 on a slicer state, with both TwoSums taken as FastTwoSums; equal to tf_mul_pow2 bit for bit
+// on such states. FastTwoSum(a, b) returns TwoSum's pair when |a| >= |b| or a = 0, and r scales the
+// limbs exactly. Order of (mid, lo): a loaded triple has |lo| below one unit of mid's last chunk bit,
+// or mid = 0; later states take (mid, lo) from FastTwoSum(e6, e4), with |lo| <= ulp(mid)/2. Order of
+// (hi, s3): the slicer only subtracts an integer digit from hi, which leaves hi = 0 or a nonzero
+// multiple of ulp(old hi) >= 2|mid| > |fl(mid + lo)|. The oracle's orc_check_tf_mul_pow2_fast checks
+// the equality and counts order violations on slicer chains (radix 2 to 2^20, every exponent).
+__device__ __forceinline__ void tf_mul_pow2_fast(float& hi, float& mid, float& lo, float r) {
+    hi = hi * r;
+    mid = mid * r;
+    lo = lo * r;
+    float s3, e4, s5, e6;
+    fast_two_sum(mid, lo, s3, e4);
+    fast_two_sum(hi, s3, s5, e6);
+    hi = s5;
+    fast_two_sum(e6, e4, mid, lo);
+}
+
 // tfMulR: the triple times a general radix r <= 254, each limb split by Dekker's 4097 so that the
 // limb products are exact, then renormalized (sfpu_tf_proc.h:108-141; names of the procedure).
 __device__ __forceinline__ void tf_mul_r(float& hi, float& mid, float& lo, float r) {
@@ -165,11 +183,13 @@ __device__ __forceinline__ void tf_mul_r_fast(float& hi, float& mid, float& lo, 
 }
 
 // tfMulRadix (sfpu_tf.h:131-134): tfMulP2 for a power-of-two radix, tfMulR otherwise (FMA: its
-// TwoProduct form, for callers that meet the conditions of tf_mul_r_fma; FAST: the slicer's form
-// tf_mul_r_fast, under the same conditions).
+// TwoProduct form, for callers that meet the conditions of tf_mul_r_fma; FAST: the slicer's forms,
+// tf_mul_pow2_fast, and tf_mul_r_fast under the conditions of tf_mul_r_fma).
 template <bool POW2, bool FMA = false, bool FAST = false>
 __device__ __forceinline__ void tf_mul_radix(float& hi, float& mid, float& lo, float r) {
-    if constexpr (POW2)
+    if constexpr (POW2 && FAST)
+        tf_mul_pow2_fast(hi, mid, lo, r);
+    else if constexpr (POW2)
         tf_mul_pow2(hi, mid, lo, r);
     else if constexpr (FMA && FAST)
         tf_mul_r_fast(hi, mid, lo, r);

@@ -448,6 +448,37 @@ def test_tf_mul_r_fast_form_agrees_and_its_order_holds(orc, radix, dmax):
     assert cov.value > n // 2
 
 
+def _pow2_fast(orc):
+    import ctypes
+    f = orc.lib.orc_check_tf_mul_pow2_fast
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
+
+    def run(mode, n, seed, radix, dmax, planes):
+        cov, viol = ctypes.c_int64(), ctypes.c_int64()
+        bad = f(mode, n, seed, radix, dmax, planes, ctypes.byref(cov), ctypes.byref(viol))
+        return bad, cov.value, viol.value
+    return run
+
+
+@pytest.mark.parametrize("radix,dmax", [(64, 32), (2, 1), (1 << 20, 1 << 30)])
+def test_tf_mul_pow2_fast_form_agrees_and_its_order_holds(orc, radix, dmax):
+    """For a power-of-two radix the slicer takes both TwoSums of tfMulP2 as FastTwoSums: on the slicer
+    chains of every element, near its row maximum or 50-100 binades below it (subnormal limbs
+    included), the digits equal the reference form's and the FastTwoSum order holds at every call."""
+    bad, cov, viol = _pow2_fast(orc)(0, 300000, 17, radix, dmax, 24)
+    assert bad == 0 and viol == 0 and cov == 300000
+
+
+def test_tf_mul_pow2_fast_checker_counts_order_violations(orc):
+    """The order count can fire: on the reconstruction's Horner chains (integers added between the
+    multiplications) radix 64 leaves states where |mid| < |lo|, which is why only the slicer takes
+    the fast form."""
+    bad, cov, viol = _pow2_fast(orc)(1, 300000, 5, 64, 0, 12)
+    assert viol > 0
+
+
 def test_tf_mul_r_forms_checker_sees_overflow_beyond_the_bound(orc):
     """The check can fail: past the bound (radix 14 with up to 30 diagonals) Dekker's split
     overflows where the TwoProduct form does not, and the checker counts those chains."""
