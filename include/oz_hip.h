@@ -70,7 +70,8 @@ int oz_memcpy_d2d(oz_dev* dev, void* dst, const void* src, size_t bytes);
  * zero-padded shapes of the products. */
 int oz_pad_copy_f64(oz_dev* dev, double* dst, int drows, int dcols, const double* src, int srows, int scols, int sld);
 int oz_sync(oz_dev* dev);
-/* Stream-ordered timing (64 event slots per handle). */
+/* Stream-ordered timing (OZ_EVENT_SLOTS event slots per handle). */
+#define OZ_EVENT_SLOTS 256
 int oz_event_record(oz_dev* dev, int slot);
 int oz_event_elapsed_ms(oz_dev* dev, int slot_begin, int slot_end, float* ms);
 

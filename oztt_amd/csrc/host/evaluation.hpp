@@ -49,7 +49,8 @@ struct Settings {
     unsigned partial_products = 0;     // low-precision matrix products per call (S or slice pairs)
     double product_ops = 0;            // algorithmic operations of the product phase (2*M*N*K*products)
     double gemm_launch_ms = 0;         // device time of the product launches of one pass, bracketed by
-                                       // events inside the timed whole-pass replays (up to 20 passes)
+                                       // events in whole-pass replays right after the timed ones (up to
+                                       // `repeats` passes, 58 product launches in all)
     int gemm_launches = 0;             // product-kernel launches per pass (one per row band)
     bool plan_reused = false;          // resident operands: the call ran the plan kept from an earlier call
 };

@@ -40,32 +40,49 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& 
                   double* host, std::size_t count, const Workspace& ws, double product_ops,
                   unsigned partial_products) {
     ev::Settings* es = ev::active();
-    // Per-phase device times: events around every step (slots 24 + 2i, 25 + 2i), summed by phase.
-    // The events are read after the pass, so each step needs its own pair.
-    constexpr int kFirstSlot = 24, kSlots = 64;
-    const bool step_events = es && kFirstSlot + 2 * steps.size() <= kSlots;
-    auto timed_pass = [&](double* phase_ms) {
-        for (std::size_t i = 0; i < steps.size(); i++) {
-            device_check(dev, oz_event_record(dev, kFirstSlot + 2 * (int)i), "event");
-            steps[i].issue();
-            device_check(dev, oz_event_record(dev, kFirstSlot + 2 * (int)i + 1), "event");
-        }
-        for (std::size_t i = 0; i < steps.size(); i++) {
-            float ms = 0;
-            device_check(dev, oz_event_elapsed_ms(dev, kFirstSlot + 2 * (int)i, kFirstSlot + 2 * (int)i + 1, &ms),
-                         "event time");
-            phase_ms[steps[i].phase] += ms;
+    // Event slots: 20 and 21 bracket the timed replays; from 24 on, a pair of slots around each step
+    // that is timed on its own. Events are read only after every pass is issued, so no host wait
+    // leaves the device idle (and its clock falling) between the passes.
+    constexpr int kFirstSlot = 24, kSlots = OZ_EVENT_SLOTS;
+    struct Marked {
+        int phase, slot;
+    };
+    // one pass; each step that `mark` selects between its own pair of events (slots from `slot` on)
+    auto marked_pass = [&](auto&& mark, int& slot, std::vector<Marked>& marked) {
+        for (auto& s : steps) {
+            const bool m = mark(s);
+            if (m) {
+                device_check(dev, oz_event_record(dev, slot), "event");
+                marked.push_back({(int)s.phase, slot});
+            }
+            s.issue();
+            if (m) {
+                device_check(dev, oz_event_record(dev, slot + 1), "event");
+                slot += 2;
+            }
         }
     };
+    auto elapsed = [&](int a, int b) {
+        float ms = 0;
+        device_check(dev, oz_event_elapsed_ms(dev, a, b, &ms), "event time");
+        return (double)ms;
+    };
+    auto every = [](const Step&) { return true; };
+    auto product = [](const Step& s) { return s.phase == ev::Gemm; };
+    const bool step_events = es && kFirstSlot + 2 * steps.size() <= (std::size_t)kSlots;
     if (!es) {
         for (auto& s : steps) s.issue();
     } else {
         // first pass; its phase times stand unless replays follow (then the warm replays replace them)
         for (int ph = 0; ph < ev::PhaseCount; ph++) es->phase_ms[ph] = 0;
-        if (step_events)
-            timed_pass(es->phase_ms);
-        else
+        if (step_events) {
+            int slot = kFirstSlot;
+            std::vector<Marked> marked;
+            marked_pass(every, slot, marked);
+            for (const Marked& m : marked) es->phase_ms[m.phase] += elapsed(m.slot, m.slot + 1);
+        } else {
             for (auto& s : steps) s.issue();
+        }
         es->partial_products = partial_products;
         es->product_ops = product_ops;
         es->gemm_launches = 0;
@@ -119,44 +136,41 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& 
     if (es && es->repeats > 0 && es->replay_drop_phase < 0) {
         // 3. whole pass: warm up, then `repeats` replays between two events; the output must still
         //    be the first pass's
-        //    The product steps of the timed passes are bracketed by events too (slots 24.. while they
-        //    last: every pass whose product steps fit), which gives the products' time per pass as
-        //    they run inside the whole pass (an event marker costs no measurable time).
         for (int w = 0; w < es->warmup; w++)
             for (auto& s : steps) s.issue();
-        int slot = kFirstSlot, timed_passes = 0;
+        device_check(dev, oz_event_record(dev, 20), "event");
+        for (int r = 0; r < es->repeats; r++)
+            for (auto& s : steps) s.issue();
+        device_check(dev, oz_event_record(dev, 21), "event");
+        // 4. right after them, with no wait: up to `repeats` passes whose product steps are bracketed
+        //    by events (the products' time per pass as they run inside whole passes; the markers
+        //    stay out of the timed region, where each would cost a few microseconds on a pass of
+        //    tens), then up to 5 passes with events around every step (the warm phase times).
+        //    Slots [24, 140) take the products, [140, 256) the phases.
+        constexpr int kPhaseSlot = kFirstSlot + (kSlots - kFirstSlot) / 2;
         std::size_t gemm_steps = 0;
         for (auto& s : steps) gemm_steps += s.phase == ev::Gemm;
-        device_check(dev, oz_event_record(dev, 20), "event");
-        for (int r = 0; r < es->repeats; r++) {
-            const bool mark = slot + 2 * gemm_steps <= (std::size_t)kSlots;
-            for (auto& s : steps) {
-                if (mark && s.phase == ev::Gemm) device_check(dev, oz_event_record(dev, slot++), "event");
-                s.issue();
-                if (mark && s.phase == ev::Gemm) device_check(dev, oz_event_record(dev, slot++), "event");
-            }
-            timed_passes += mark;
-        }
-        device_check(dev, oz_event_record(dev, 21), "event");
-        float ms = 0;
-        device_check(dev, oz_event_elapsed_ms(dev, 20, 21, &ms), "event time");
-        es->whole_ms = ms / es->repeats;
+        int slot = kFirstSlot, gemm_passes = 0;
+        std::vector<Marked> gm;
+        for (int r = 0; r < es->repeats && slot + 2 * gemm_steps <= (std::size_t)kPhaseSlot; r++, gemm_passes++)
+            marked_pass(product, slot, gm);
+        int pslot = kPhaseSlot, phase_passes = 0;
+        std::vector<Marked> pm;
+        for (int r = 0; r < es->repeats && r < 5 && pslot + 2 * steps.size() <= (std::size_t)kSlots;
+             r++, phase_passes++)
+            marked_pass(every, pslot, pm);
+        es->whole_ms = elapsed(20, 21) / es->repeats;
         double gemm_ms = 0;
-        for (int e = kFirstSlot; e < slot; e += 2) {
-            device_check(dev, oz_event_elapsed_ms(dev, e, e + 1, &ms), "event time");
-            gemm_ms += ms;
+        for (const Marked& m : gm) gemm_ms += elapsed(m.slot, m.slot + 1);
+        es->gemm_launch_ms = gemm_passes ? gemm_ms / gemm_passes : 0.0;
+        if (phase_passes) {
+            double acc[ev::PhaseCount] = {};
+            for (const Marked& m : pm) acc[m.phase] += elapsed(m.slot, m.slot + 1);
+            for (int ph = 0; ph < ev::PhaseCount; ph++) es->phase_ms[ph] = acc[ph] / phase_passes;
         }
-        es->gemm_launch_ms = timed_passes ? gemm_ms / timed_passes : 0.0;
         const std::vector<double> last = read_back(dev, out, count);
         es->whole_checked = es->whole_sentinel && whole_counts_match(*es) &&
                             same_bits(last, host ? host : whole_ref.data(), count);
-        // 4. warm phase times: the average of up to 5 more passes with events between the steps
-        if (step_events) {
-            const int passes = es->repeats < 5 ? es->repeats : 5;
-            double acc[ev::PhaseCount] = {};
-            for (int r = 0; r < passes; r++) timed_pass(acc);
-            for (int ph = 0; ph < ev::PhaseCount; ph++) es->phase_ms[ph] = acc[ph] / passes;
-        }
     }
     // range flags of the scaling stage; the host validation rejects these inputs first, so they only
     // fire if the device disagrees with it

@@ -172,13 +172,13 @@ int oz_sync(oz_dev* dev) {
 
 int oz_event_record(oz_dev* dev, int slot) {
     if (int st = oz::use(dev)) return st;
-    if (slot < 0 || slot >= 64) return oz::fail(dev, OZ_ERR_ARG, "event slot %d out of range", slot);
+    if (slot < 0 || slot >= OZ_EVENT_SLOTS) return oz::fail(dev, OZ_ERR_ARG, "event slot %d out of range", slot);
     return oz::hip_check(dev, hipEventRecord(dev->events[slot], dev->stream), "hipEventRecord");
 }
 
 int oz_event_elapsed_ms(oz_dev* dev, int a, int b, float* ms) {
     if (int st = oz::use(dev)) return st;
-    if (a < 0 || a >= 64 || b < 0 || b >= 64 || !ms) return oz::fail(dev, OZ_ERR_ARG, "bad event slots");
+    if (a < 0 || a >= OZ_EVENT_SLOTS || b < 0 || b >= OZ_EVENT_SLOTS || !ms) return oz::fail(dev, OZ_ERR_ARG, "bad event slots");
     if (int st = oz::hip_check(dev, hipEventSynchronize(dev->events[b]), "hipEventSynchronize")) return st;
     return oz::hip_check(dev, hipEventElapsedTime(ms, dev->events[a], dev->events[b]), "hipEventElapsedTime");
 }

@@ -12,7 +12,7 @@
 struct oz_dev {
     int device = 0;
     hipStream_t stream = nullptr;
-    hipEvent_t events[64] = {};
+    hipEvent_t events[OZ_EVENT_SLOTS] = {};
     std::string error;
     int* queue = nullptr;   // tile pool counters of the INT8 product kernel (16 ints, zero between launches)
     int cus = 0;            // compute units: a product launch of at most this many tiles needs no pool
