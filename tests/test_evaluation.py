@@ -2,6 +2,8 @@
 GEMM and the accuracy measure, pinned by the effective bits and relative Frobenius errors that the
 reference's validated runs recorded (tools/validated/quick.csv:2, :12) for outputs this build
 reproduces bit for bit (their hashes are pinned in test_oracle.py)."""
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -54,3 +56,22 @@ def test_accuracy_edge_cases():
     z = np.zeros(4)
     assert oz.eval_accuracy(z, z, z) == (0.0, 99.0)
     assert oz.eval_accuracy(np.ones(4), z, z)[0] == np.inf
+
+
+def test_bench_traffic_figures_come_from_their_profiles():
+    """bench.py prints roofline.traffic for every configuration from its committed counter profile: the
+    figure (bytes per launch of the product kernel) is the one that profile's table derives from its
+    FETCH_SIZE and WRITE_SIZE counters, and the profile names the command that made it."""
+    import re
+    import bench
+    root = Path(__file__).resolve().parent.parent
+    for cfg, (traffic, prof, products) in bench.TRAFFIC.items():
+        assert traffic is not None and traffic > 0, cfg
+        text = (root / prof).read_text()
+        assert "rocprofv3 --pmc FETCH_SIZE" in text and "rocprofv3 --pmc WRITE_SIZE" in text, prof
+        kernel = "gemm_f8_groups_kernel" if cfg == "C4" else "gemm_i8_kernel"
+        rows = [ln for ln in text.splitlines() if ln.startswith(f"| `{kernel}") and "(GB)" not in ln]
+        gb = float(rows[0].split("|")[4])  # the traffic column of the per-kernel table
+        # the table prints GB to three decimals
+        assert abs(gb * 1e9 - traffic) <= max(0.5e6, 0.005 * traffic), (cfg, gb, traffic)
+        assert products > 0 and re.search(rf"--config {cfg}\b", text), cfg
