@@ -23,8 +23,8 @@ value = 2*m*n*k / (time of one whole pass)  [effective FP64 TFLOP/s]
 Also reported: accuracy against binary128 on a 64x64 sample of C at full K (and the same numbers
 for a native FP64 dot product), the per-phase device times, the roofline of the product kernel
 (algorithmic int8 operations per launch / its average launch time in whole-pass replays right
-after the timed ones, HIP events on the library stream around each product launch, kept out of the
-timed region; against 5.0 POP/s dense INT8, or FP8 for C4;
+after the timed ones, each product launch timed by its own dispatch on the library stream
+(oz_time_products_begin), kept out of the timed region; against 5.0 POP/s dense INT8, or FP8 for C4;
 `traffic` = the memory bytes per launch from the config's committed counter profile),
 the reference's host OpenMP Dot2 GEMM (the oracle's restatement) timed on this host on a row
 slab of the same problem, the GPU's own FP64 GEMM (rocBLAS dgemm) on the same operands, and the

@@ -74,6 +74,16 @@ int oz_sync(oz_dev* dev);
 #define OZ_EVENT_SLOTS 256
 int oz_event_record(oz_dev* dev, int slot);
 int oz_event_elapsed_ms(oz_dev* dev, int slot_begin, int slot_end, float* ms);
+/* Times product kernels by their own dispatches, with no marker in the stream. After
+ * oz_time_products_begin, the first product-kernel launch on the handle (oz_gemm_i8,
+ * oz2_gemm_digits, oz1_gemm_diag_i8, oz2_gemm_groups_f8 and the passes built on them) sets event
+ * slot_begin at the start of its dispatch, and each such launch sets slot_end at the end of its
+ * own, until oz_time_products_end, which reports in *launched whether any ran (0: the events were
+ * not touched). An event pair around a launch of tens of microseconds adds a few to it; these do
+ * not. No counterpart in the reference (its timing hooks, evaluation_hooks.hpp, bracket whole
+ * stages). */
+int oz_time_products_begin(oz_dev* dev, int slot_begin, int slot_end);
+int oz_time_products_end(oz_dev* dev, int* launched);
 
 /* ---- A5: normalization (reference scale_f64_reader.cpp:129, expdelta.cpp:44, scale_bits.h) --
  * Largest |x| of every row (mode 0, `rows` outputs) or column (mode 1, `cols` outputs) of X

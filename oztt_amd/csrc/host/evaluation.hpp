@@ -48,9 +48,9 @@ struct Settings {
     unsigned expected_steps[PhaseCount] = {};  // device steps per phase that the plan calls for
     unsigned partial_products = 0;     // low-precision matrix products per call (S or slice pairs)
     double product_ops = 0;            // algorithmic operations of the product phase (2*M*N*K*products)
-    double gemm_launch_ms = 0;         // device time of the product launches of one pass, bracketed by
-                                       // events in whole-pass replays right after the timed ones (up to
-                                       // `repeats` passes, 58 product launches in all)
+    double gemm_launch_ms = 0;         // device time of the product launches of one pass, from their own
+                                       // dispatches (oz_time_products_begin) in whole-pass replays right
+                                       // after the timed ones (up to `repeats` passes, 58 launches in all)
     int gemm_launches = 0;             // product-kernel launches per pass (one per row band)
     bool plan_reused = false;          // resident operands: the call ran the plan kept from an earlier call
 };

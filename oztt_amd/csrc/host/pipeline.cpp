@@ -68,7 +68,6 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& 
         return (double)ms;
     };
     auto every = [](const Step&) { return true; };
-    auto product = [](const Step& s) { return s.phase == ev::Gemm; };
     const bool step_events = es && kFirstSlot + 2 * steps.size() <= (std::size_t)kSlots;
     if (!es) {
         for (auto& s : steps) s.issue();
@@ -142,18 +141,32 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& 
         for (int r = 0; r < es->repeats; r++)
             for (auto& s : steps) s.issue();
         device_check(dev, oz_event_record(dev, 21), "event");
-        // 4. right after them, with no wait: up to `repeats` passes whose product steps are bracketed
-        //    by events (the products' time per pass as they run inside whole passes; the markers
-        //    stay out of the timed region, where each would cost a few microseconds on a pass of
-        //    tens), then up to 5 passes with events around every step (the warm phase times).
-        //    Slots [24, 140) take the products, [140, 256) the phases.
+        // 4. right after them, with no wait: up to `repeats` passes whose product launches are timed
+        //    (the products' time per pass as they run inside whole passes; kept out of the timed
+        //    region all the same), then up to 5 passes with events around every step (the warm phase
+        //    times). Slots [24, 140) take the products, [140, 256) the phases.
         constexpr int kPhaseSlot = kFirstSlot + (kSlots - kFirstSlot) / 2;
         std::size_t gemm_steps = 0;
         for (auto& s : steps) gemm_steps += s.phase == ev::Gemm;
+        //    A product step is timed by its kernels' own dispatches (oz_time_products_begin), not by
+        //    markers around it: those would add the dispatch latency they bracket, a fifth of a
+        //    20 µs launch. A step that launched no product kernel counts as zero.
         int slot = kFirstSlot, gemm_passes = 0;
         std::vector<Marked> gm;
         for (int r = 0; r < es->repeats && slot + 2 * gemm_steps <= (std::size_t)kPhaseSlot; r++, gemm_passes++)
-            marked_pass(product, slot, gm);
+            for (auto& s : steps) {
+                if (s.phase != ev::Gemm) {
+                    s.issue();
+                    continue;
+                }
+                device_check(dev, oz_time_products_begin(dev, slot, slot + 1), "product timing");
+                s.issue();
+                int launched = 0;
+                device_check(dev, oz_time_products_end(dev, &launched), "product timing");
+                if (launched)
+                    gm.push_back({(int)s.phase, slot});
+                slot += 2;
+            }
         int pslot = kPhaseSlot, phase_passes = 0;
         std::vector<Marked> pm;
         for (int r = 0; r < es->repeats && r < 5 && pslot + 2 * steps.size() <= (std::size_t)kSlots;

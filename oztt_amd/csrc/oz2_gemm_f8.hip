@@ -288,8 +288,8 @@ extern "C" int oz2_gemm_groups_f8(oz_dev* dev, const uint8_t* A, const uint8_t* 
     const unsigned grid = (unsigned)((long long)tiles_m * tiles_n * gd->nout);
     const int nout = gd->nout;
 #define OZ_F8_LAUNCH(KIND, EVEN)                                                                                      \
-    hipLaunchKernelGGL((gemm_f8_groups_kernel<KIND, EVEN>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, out, K, \
-                       ldo, strideA, strideB, strideO, tiles_m, tiles_n, nout, ga)
+    oz::launch_product(dev, gemm_f8_groups_kernel<KIND, EVEN>, dim3(grid), dim3(THREADS), A, Bt, out, K, ldo,     \
+                       strideA, strideB, strideO, tiles_m, tiles_n, nout, ga)
     const bool even = (K / BK) % 2 == 0;
     if (out_kind == 1) {
         if (even) OZ_F8_LAUNCH(1, true);

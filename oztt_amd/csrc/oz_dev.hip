@@ -176,6 +176,25 @@ int oz_event_record(oz_dev* dev, int slot) {
     return oz::hip_check(dev, hipEventRecord(dev->events[slot], dev->stream), "hipEventRecord");
 }
 
+int oz_time_products_begin(oz_dev* dev, int slot_begin, int slot_end) {
+    if (int st = oz::use(dev)) return st;
+    if (slot_begin < 0 || slot_begin >= OZ_EVENT_SLOTS || slot_end < 0 || slot_end >= OZ_EVENT_SLOTS ||
+        slot_begin == slot_end)
+        return oz::fail(dev, OZ_ERR_ARG, "oz_time_products_begin: bad event slots %d, %d", slot_begin, slot_end);
+    dev->time_begin = slot_begin;
+    dev->time_end = slot_end;
+    dev->time_launched = false;
+    return OZ_OK;
+}
+
+int oz_time_products_end(oz_dev* dev, int* launched) {
+    if (int st = oz::use(dev)) return st;
+    if (launched) *launched = dev->time_launched ? 1 : 0;
+    dev->time_begin = dev->time_end = -1;
+    dev->time_launched = false;
+    return OZ_OK;
+}
+
 int oz_event_elapsed_ms(oz_dev* dev, int a, int b, float* ms) {
     if (int st = oz::use(dev)) return st;
     if (a < 0 || a >= OZ_EVENT_SLOTS || b < 0 || b >= OZ_EVENT_SLOTS || !ms) return oz::fail(dev, OZ_ERR_ARG, "bad event slots");

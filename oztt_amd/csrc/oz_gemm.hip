@@ -366,11 +366,11 @@ int launch_gemm(oz_dev* dev, const int8_t* A, const int8_t* Bt, void* C, int M, 
     const unsigned grid = one_wave ? (unsigned)tiles : (unsigned)(tiles + std::max<long long>(tiles / 8, 8));
     // K/64 even: every tile has an even number of K steps (DIAG: (d+1) K/64), no tail step
     if ((K / BK) % 2 == 0)
-        hipLaunchKernelGGL((gemm_i8_kernel<MODE, true>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
-                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue, first);
+        oz::launch_product(dev, gemm_i8_kernel<MODE, true>, dim3(grid), dim3(THREADS), A, Bt, C, K, ldc, strideA,
+                           strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue, first);
     else
-        hipLaunchKernelGGL((gemm_i8_kernel<MODE, false>), dim3(grid), dim3(THREADS), 0, dev->stream, A, Bt, C, K, ldc,
-                           strideA, strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue, first);
+        oz::launch_product(dev, gemm_i8_kernel<MODE, false>, dim3(grid), dim3(THREADS), A, Bt, C, K, ldc, strideA,
+                           strideB, strideC, tiles_m, tiles_n, batch, dc, dev->queue, first);
     return oz::launch_check(dev, "gemm_i8_kernel");
 }
 

@@ -1,6 +1,7 @@
 // Internal helpers of the device layer (liboz_hip.so): the device handle, error reporting and
 // launch checks shared by the kernel sources.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -16,9 +17,28 @@ struct oz_dev {
     std::string error;
     int* queue = nullptr;   // tile pool counters of the INT8 product kernel (16 ints, zero between launches)
     int cus = 0;            // compute units: a product launch of at most this many tiles needs no pool
+    // oz_time_products_begin: event slots of the product launches to time (-1: none), and whether
+    // one has run under the request
+    int time_begin = -1, time_end = -1;
+    bool time_launched = false;
 };
 
 namespace oz {
+
+// Launches a product kernel on the handle's stream. Under oz_time_products_begin the launch carries
+// the requested events, which the runtime sets from the dispatch's own start and end
+// (hipExtLaunchKernel); the start event only on the first such launch.
+template <class F, class... Args>
+inline void launch_product(oz_dev* dev, F kernel, dim3 grid, dim3 block, Args... args) {
+    hipEvent_t start = nullptr, stop = nullptr;
+    if (dev->time_end >= 0) {
+        if (dev->time_begin >= 0) start = dev->events[dev->time_begin];
+        stop = dev->events[dev->time_end];
+        dev->time_begin = -1;
+        dev->time_launched = true;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, dev->stream, start, stop, 0, args...);
+}
 
 // Records a message on the handle and returns the status (printf-style).
 inline int fail(oz_dev* dev, int status, const char* fmt, ...) {

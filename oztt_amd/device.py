@@ -162,6 +162,24 @@ class Device:
     def sync(self):
         self._check(hip().oz_sync(self.h), "oz_sync")
 
+    # ---- timing --------------------------------------------------------------------------------
+    def event_record(self, slot: int):
+        self._check(hip().oz_event_record(self.h, slot), "oz_event_record")
+
+    def elapsed_ms(self, begin: int, end: int) -> float:
+        ms = ctypes.c_float()
+        self._check(hip().oz_event_elapsed_ms(self.h, begin, end, ctypes.byref(ms)), "oz_event_elapsed_ms")
+        return ms.value
+
+    def time_products_begin(self, begin: int, end: int):
+        self._check(hip().oz_time_products_begin(self.h, begin, end), "oz_time_products_begin")
+
+    def time_products_end(self) -> bool:
+        """Ends the request; True if a product kernel ran under it."""
+        launched = ctypes.c_int()
+        self._check(hip().oz_time_products_end(self.h, ctypes.byref(launched)), "oz_time_products_end")
+        return bool(launched.value)
+
     # ---- stages --------------------------------------------------------------------------------
     def scale(self, X: Buffer, rows, cols, ld, mode, ceil_mode, shift, delta: Buffer, flags: Buffer, flag_index=0):
         self._check(hip().oz_scale_f64(self.h, X.ptr, rows, cols, ld, mode, ceil_mode, shift, delta.ptr,

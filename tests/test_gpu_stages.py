@@ -261,6 +261,41 @@ def test_gemm_digits_exact(dev, M, N, K, S):
         assert_residues(D[s], want, m, f"modulus {m}")
 
 
+def test_product_dispatch_timing(dev):
+    """oz_time_products_begin/end: the product launches between them set the requested events from their
+    own dispatches (the first launch the start, every launch the end), other launches do not consume the
+    request, a request with no product launch reports so, and the timed products' results are those of
+    untimed launches."""
+    rng = np.random.default_rng(12)
+    M = N = 512
+    K, batch = 1024, 3
+    A = rng.integers(-127, 128, (batch, M, K), dtype=np.int8)
+    Bt = rng.integers(-127, 128, (batch, N, K), dtype=np.int8)
+    bA, bB = dev.upload(to_blocks(A)), dev.upload(to_blocks(Bt))
+    c1, c2 = dev.alloc(4 * batch * M * N), dev.alloc(4 * batch * M * N)
+    args = (M, N, K, batch, N, M * K, N * K, M * N)
+    dev.gemm_i8(bA, bB, c1, *args)
+    # a request with no product launch in it (a fill only)
+    dev.time_products_begin(30, 31)
+    dev.fill_u32(c2, 0, batch * M * N)
+    assert not dev.time_products_end()
+    # two product launches under one request, events around the pair as markers
+    dev.event_record(40)
+    dev.time_products_begin(30, 31)
+    dev.gemm_i8(bA, bB, c2, *args)
+    dev.fill_u32(c2, 0, batch * M * N)
+    dev.gemm_i8(bA, bB, c2, *args)
+    assert dev.time_products_end()
+    dev.event_record(41)
+    dev.sync()
+    t_products, t_markers = dev.elapsed_ms(30, 31), dev.elapsed_ms(40, 41)
+    assert 0.0 < t_products <= t_markers
+    np.testing.assert_array_equal(dev.download(c2, np.int32, batch * M * N), dev.download(c1, np.int32, batch * M * N))
+    for x in (bA, bB, c1, c2):
+        x.free()
+    dev.bufs.clear()
+
+
 def test_gemm_tile_pool_counts(dev):
     """The last eighth of every XCD's tiles is handed out through counters in the device handle, which
     each launch must leave at zero: launches of 1, 7, 9, 63, 65 and 1031 tiles back to back on one
