@@ -1178,6 +1178,31 @@ static int64_t check_forms(FORM form, REF ref, int mode, int64_t n, uint64_t see
                 h1 = f_sub(h1, a);
                 h2 = f_sub(h2, b);
             }
+        } else if (mode == 2) {
+            // Scheme II digit chains (make_digits): the scaled element below 2^sh, digit = Rnd(hi) with
+            // no clamp, then `planes` multiplications by the radix, each followed by a digit
+            uint64_t u = g();
+            const int E = (int)(g() % 2047);
+            u = (u & 0x800FFFFFFFFFFFFFull) | ((uint64_t)E << 52);
+            double x;
+            std::memcpy(&x, &u, 8);
+            const int sh = (int)(g() % 25);
+            int k = (int)(g() % 9);
+            if (g() % 2 == 0) k = 50 + (int)(g() % 51);
+            const int32_t d = sh - 1 - k - (E - 1023);
+            float h1, m1, l1;
+            load_triple(x, d, h1, m1, l1);
+            float h2 = h1, m2 = m1, l2 = l1;
+            for (int t = 0; t <= planes; t++) {
+                if (t > 0) {
+                    ref(h1, m1, l1, r);
+                    form(h2, m2, l2, r, v);
+                }
+                const float a = f_rnd(h1), b = f_rnd(h2);
+                same = same && a == b;
+                h1 = f_sub(h1, a);
+                h2 = f_sub(h2, b);
+            }
         } else {
             const int p = 1 + (int)(g() % (uint64_t)planes);
             float h1 = 0, m1 = 0, l1 = 0, h2 = 0, m2 = 0, l2 = 0;
@@ -1232,8 +1257,8 @@ int64_t orc_check_tf_mul_r_fast(int mode, int64_t n, uint64_t seed, int radix, i
 }
 
 // tfMulP2 (the reference's, for a power-of-two radix) against tf_mul_pow2_fast on every chain of the
-// mode (*covered = n; mode 0: slicer chains, 1: reconstruction chains); *violations counts its
-// precondition failures.
+// mode (*covered = n; mode 0: slicer chains, 1: reconstruction chains, 2: Scheme II digit chains,
+// digits.h:80-112); *violations counts its precondition failures.
 int64_t orc_check_tf_mul_pow2_fast(int mode, int64_t n, uint64_t seed, int radix, int dmax, int planes,
                                    int64_t* covered, int64_t* violations) {
     auto form = [](float& h, float& m, float& l, float r, int64_t& v) { tf_mul_pow2_fast(h, m, l, r, v); };

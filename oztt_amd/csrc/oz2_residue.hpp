@@ -41,7 +41,9 @@ __device__ __forceinline__ void make_digits(double x, int32_t d, float* dig) {
     load_triple(x, d, hi, mid, lo);
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
-        if (i > 0) tf_mul_pow2(hi, mid, lo, 1048576.0f);  // tfMulP2 by 2^20
+        // tfMulP2 by 2^20, its TwoSums taken as FastTwoSums: the order they need holds on these chains
+        // too (a digit leaves hi = 0 or a multiple of ulp(old hi) >= 2|mid|; see tf_mul_pow2_fast)
+        if (i > 0) tf_mul_pow2_fast(hi, mid, lo, 1048576.0f);
         const float t = __builtin_rintf(hi);
         hi = hi - t;
         dig[i] = t;

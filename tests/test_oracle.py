@@ -471,6 +471,16 @@ def test_tf_mul_pow2_fast_form_agrees_and_its_order_holds(orc, radix, dmax):
     assert bad == 0 and viol == 0 and cov == 300000
 
 
+@pytest.mark.parametrize("nd", [3, 4, 5])
+def test_tf_mul_pow2_fast_form_agrees_on_scheme2_digit_chains(orc, nd):
+    """Scheme II's digit extraction (digits.h:80-112: a digit Rnd(hi) without clamp, then tfMulP2 by 2^20
+    before each further digit) also takes the FastTwoSum form on the GPU: for elements up to 2^24 after
+    scaling and 50-100 binades below their row maximum, every exponent, the nd digits equal the
+    reference form's and the order holds at every call."""
+    bad, cov, viol = _pow2_fast(orc)(2, 300000, 19 + nd, 1 << 20, 0, nd - 1)
+    assert bad == 0 and viol == 0 and cov == 300000
+
+
 def test_tf_mul_pow2_fast_checker_counts_order_violations(orc):
     """The order count can fire: on the reconstruction's Horner chains (integers added between the
     multiplications) radix 64 leaves states where |mid| < |lo|, which is why only the slicer takes
