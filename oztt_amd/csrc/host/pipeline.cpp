@@ -160,6 +160,10 @@ void run_pipeline(oz_dev* dev, const std::vector<Step>& steps, const PassShape& 
                     continue;
                 }
                 device_check(dev, oz_time_products_begin(dev, slot, slot + 1), "product timing");
+                struct EndRequest {  // a step that throws leaves no request behind on the handle
+                    oz_dev* d;
+                    ~EndRequest() { oz_time_products_end(d, nullptr); }
+                } guard{dev};
                 s.issue();
                 int launched = 0;
                 device_check(dev, oz_time_products_end(dev, &launched), "product timing");
