@@ -148,34 +148,35 @@ __device__ __forceinline__ double half_ulp(double s) {
 
 // Byte40 limbs (normalized, each an integer in [0, 2^40) times 2^-90) -> V 2^e2 rounded to nearest-even,
 // negated if neg; 0 when V = 0, signed zero below 2^-1022 (f64_tf.h:45-47), infinity above the FP64
-// range. A cascade of exact FP64 additions from the top limb down, s_j = RN(s_(j-1) + T_j) with T_j the
-// j-th limb from the top at its weight, each stage's error from FastTwoSum (|s| >= |T_j| or s = 0). At
+// range. A cascade of FP64 additions from the top limb down, s_j = RN(s_(j-1) + T_j) with T_j the j-th
+// limb from the top at its weight, each stage's error e_j from FastTwoSum (|s| >= |T_j| or s = 0). At
 // most one stage rounds: the terms below a rounding stage are worth less than half an ulp of it, so
-// the later sums return it unchanged. s is therefore RN(V), except when that stage's error was
-// exactly +ulp/2 (the tie went down to the even neighbour) and a nonzero term remains below it: V is
-// then above the midpoint and s moves one ulp up. tests/test_crt_round.py checks this sequence against
-// exact rational rounding.
+// the later sums return it unchanged and their errors are their whole terms, each below the grid unit
+// of the rounding stage, which is at most h = ulp(s)/2. s is therefore RN(V), except when the rounding
+// stage's error was exactly +h (the tie went down to the even neighbour) and a nonzero term follows
+// it: V is then above the midpoint and s moves one ulp up. Only the rounding stage can have e_j == h,
+// so the fix is read off every stage's error against the final s's h. tests/test_crt_round.py checks
+// this sequence against exact rational rounding.
 template <int L>
 __device__ __forceinline__ double magnitude40(const double* x, int e2, bool neg, const CrtLimbs40& a) {
     double T[L];
 #pragma unroll
     for (int j = 0; j < L; j++) T[j] = x[L - 1 - j] * a.pow40[L - 1 - j];  // exact: powers of two
-    double s = T[0], ek = 0.0, hk = 0.0;
-    bool have = false, lower = false;
+    double s = T[0], e[L];
 #pragma unroll
     for (int j = 1; j < L; j++) {
         const double sn = s + T[j];
-        if (j < L - 1 || true) {
-            const double e = T[j] - (sn - s);
-            lower = lower || (have && T[j] != 0.0);
-            const bool first = !have && e != 0.0;
-            ek = first ? e : ek;
-            hk = first ? half_ulp(sn) : hk;
-            have = have || first;
-        }
+        e[j] = T[j] - (sn - s);
         s = sn;
     }
-    const double r0 = have && lower && ek == hk ? __builtin_fma(2.0, hk, s) : s;
+    const double h = half_ulp(s);
+    bool fix = false, below = false;  // (bitwise: lane masks, no branches or selects)
+#pragma unroll
+    for (int j = L - 1; j >= 1; j--) {
+        fix = fix | (below & (e[j] == h));
+        below = below | (T[j] != 0.0);
+    }
+    const double r0 = fix ? __builtin_fma(2.0, h, s) : s;
     const int ex = ((__double2hiint(r0) >> 20) & 0x7FF) - 1023 + 90 + e2;  // exponent of the result
     double r = __builtin_ldexp(r0, 90 + e2);
     r = ex < -1022 ? 0.0 : r;
@@ -232,9 +233,10 @@ __device__ __forceinline__ double crt_finish(double* x, const A& a, int e2) {
         }
         neg = x[L - 1] < 0.0;
     }
-    const double sg = neg ? -1.0 : 1.0;
+    // |C'| in nonnegative limbs: flip every limb's sign bit by one mask (an xor per limb)
+    const int sm = neg ? (int)0x80000000u : 0;
 #pragma unroll
-    for (int l = 0; l < L; l++) x[l] *= sg;
+    for (int l = 0; l < L; l++) x[l] = __hiloint2double(__double2hiint(x[l]) ^ sm, __double2loint(x[l]));
     normalize<L, F>(x);
     if (x[L - 1] < 0.0) {  // |C'| so small that the estimate's sign was wrong
 #pragma unroll

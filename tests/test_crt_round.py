@@ -1,5 +1,7 @@
 """The rounding step of the byte-digit CRT kernel (magnitude40 in oztt_amd/csrc/oz2_crt.hip), emulated
-with numpy's IEEE binary64 operations and checked against exact rational arithmetic.
+with numpy's IEEE binary64 operations and checked against exact rational arithmetic: the sequence as
+first written (round_limbs, which tracks the first stage that rounds) and the one the kernel runs now
+(round_limbs_direct, which reads the fix off every stage's error).
 
 The kernel rounds V = sum_l Y_l 2^(40 l) (normalized limbs: integers in [0, 2^40), at most 5) to the
 nearest FP64 value, ties to even, with a cascade of exact FP64 additions from the top limb down:
@@ -40,6 +42,30 @@ def round_limbs(y):
     return s
 
 
+def round_limbs_direct(y):
+    """The kernel's present sequence: the same cascade with every stage's FastTwoSum error kept, and the
+    fix read off directly. Only the first stage that rounds can leave an error of exactly h = ulp(s)/2
+    (a later stage's error is its whole term, below the grid unit of the rounding stage, which is at
+    most h), and the sum s no longer moves after it, so h is that of the final s: s moves one ulp up
+    exactly when some stage j has e_j == h and a nonzero term follows it."""
+    L = len(y)
+    T = [float(np.ldexp(y[L - 1 - j], 40 * (L - 1 - j))) for j in range(L)]
+    s = T[0]
+    e = [0.0] * L
+    for j in range(1, L):
+        sn = s + T[j]
+        e[j] = T[j] - (sn - s)
+        s = sn
+    if s == 0.0:
+        return s
+    h = half_ulp(s)
+    fix, below = False, False
+    for j in range(L - 1, 0, -1):
+        fix = fix or (below and e[j] == h)
+        below = below or T[j] != 0.0
+    return s + 2.0 * h if fix else s
+
+
 def exact_rn(Y) -> float:
     v = sum(Fraction(int(t)) * 2 ** (40 * l) for l, t in enumerate(Y)) * Fraction(1, 2 ** 90)
     return float(v)  # Python rounds a Fraction to the nearest double, ties to even
@@ -47,9 +73,11 @@ def exact_rn(Y) -> float:
 
 def check(Y):
     y = [float(t) * SCALE for t in Y]
-    got = round_limbs(y)
     want = exact_rn(Y)
+    got = round_limbs(y)
     assert got == want, (Y, got, want)
+    got = round_limbs_direct(y)
+    assert got == want, ("direct", Y, got, want)
 
 
 def test_random_limbs():
