@@ -239,6 +239,57 @@ def test_crt_exact(dev, oracle, moduli, b, nd):
     np.testing.assert_array_equal(dev.download(bo2, np.float64, n).view(np.uint64), want.view(np.uint64))
 
 
+@pytest.mark.parametrize("moduli,b,nd", [(INT8_16 + [193], 56, 3),
+                                         ([255, 254, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199, 197,
+                                           193, 191, 181, 179, 173, 167, 163, 157, 151], 90, 5)])
+def test_crt_rounding_ties(dev, moduli, b, nd):
+    """C' exactly at, one above and one below a midpoint of the FP64 grid, with the rounding position in
+    every 40-bit limb of the digits kernel (and the 32-bit limbs of the int32 kernel), both signs: the
+    outputs of both CRT kernels are the correctly rounded C' (ties to even), against exact integers."""
+    import random
+    Mprod = 1
+    for m in moduli:
+        Mprod *= m
+    half = (Mprod - 1) // 2
+    pyr = random.Random(b * 131 + len(moduli))
+    vals = []
+    while len(vals) < 1500:
+        n = pyr.randint(55, half.bit_length() - 1)
+        base = pyr.getrandbits(n) | (1 << (n - 1))
+        g = n - 53  # the rounding position
+        base = (base >> g) << g
+        mid = base + (1 << (g - 1))
+        for v in (mid, mid + 1, mid - 1, base + (2 << g) + (1 << (g - 1))):
+            if v <= half:
+                vals.append(v if pyr.random() < 0.5 else -v)
+    M, N = 3, len(vals) // 3
+    vals = vals[:M * N]
+    S = len(moduli)
+    desc = crt_desc(moduli, b, nd)
+    C = np.empty((S, M, N), dtype=np.int32)
+    ldd = (N + 3) // 4 * 4 + 4
+    D = np.zeros((S, M, ldd), dtype=np.uint8)
+    for idx, v in enumerate(vals):
+        i, j = divmod(idx, N)
+        for s, m in enumerate(moduli):
+            C[s, i, j] = v % m
+            D[s, i, j] = (v % m) * int(desc.y[s]) % m
+    shift = b - 20 * (nd - 1)
+    # the exponent 2 shift - dA - dB - 2b is zero: the outputs are C' itself, rounded
+    dA = np.full(M, shift - b, dtype=np.int32)
+    dB = np.full(N, shift - b, dtype=np.int32)
+    want = np.array([float(v) for v in vals])  # Python rounds an int to the nearest double, ties to even
+    bC, bD, bdA, bdB = dev.upload(C), dev.upload(D), dev.upload(dA), dev.upload(dB)
+    bo, bo2 = dev.alloc(8 * M * N), dev.alloc(8 * M * N)
+    dev.crt(bC, M, N, N, M * N, desc, bdA, bdB, bo, N)
+    dev.crt_digits(bD, M, N, ldd, M * ldd, desc, bdA, bdB, bo2, N)
+    np.testing.assert_array_equal(dev.download(bo, np.float64, M * N).view(np.uint64), want.view(np.uint64))
+    np.testing.assert_array_equal(dev.download(bo2, np.float64, M * N).view(np.uint64), want.view(np.uint64))
+    for x in (bC, bD, bdA, bdB, bo, bo2):
+        x.free()
+    dev.bufs.clear()
+
+
 @pytest.mark.parametrize("M,N,K,S", [(256, 512, 320, 17), (512, 256, 8192, 5)])
 def test_gemm_digits_exact(dev, M, N, K, S):
     """oz2_gemm_digits: the products of oz_gemm_i8 reduced to CRT digits in the epilogue, bit-exact;
