@@ -64,13 +64,16 @@ def test_slices_match_oracle(dev, oracle, layout, radix, dmax, ceil, p):
         assert not got[:, rows:, :].any() and not got[:, :, cols:].any()
 
 
-def test_slices_near_the_subnormal_range(dev, oracle):
+@pytest.mark.parametrize("radix,dmax", [(254, 127), (64, 32)])
+def test_slices_near_the_subnormal_range(dev, oracle, radix, dmax):
     """Digits of elements whose last significand bit sits just above and just below 2^-126 after
-    scaling (row maxima near 1/2, elements near 2^-73): deep planes reach them, and a wave takes the
-    TwoProduct form of tfMulR only when all its elements' limbs are normal, Dekker's otherwise; the
-    digits equal the oracle's either way."""
+    scaling (row maxima near 1/2, elements near 2^-73): deep planes reach them. For radix 254 a wave
+    takes the TwoProduct form of tfMulR only when all its elements' limbs are normal, Dekker's
+    otherwise; radix 64 takes tfMulP2 with FastTwoSums everywhere (limbs flushed to zero included);
+    the digits equal the oracle's either way."""
     rng = np.random.default_rng(21)
-    rows, cols, p = 64, 256, 16
+    rows, cols = 64, 256
+    p = 16 if radix == 254 else 20
     # |x| in [2^-k-1, 2^-k): the last bit weighs 2^(-k-53); rows 0-31 (two bands of blocks) keep
     # k <= 73, so every limb is normal there, rows 32-63 straddle the boundary
     k = np.where(np.arange(rows)[:, None] < 32, rng.integers(66, 74, (rows, cols)), rng.integers(70, 81, (rows, cols)))
@@ -79,12 +82,12 @@ def test_slices_near_the_subnormal_range(dev, oracle):
     X[40::3, 1] = 1e-300  # far below every normal limb
     delta, _ = oracle.scale(X, rows, cols, 0, 1, -1)
     assert not delta.any()
-    want = oracle.oz1_slices(X, rows, cols, 0, delta, p, 254, 127)
-    assert np.count_nonzero(want[8:, :32]) > 32 * cols  # the deep planes reach the small elements
+    want = oracle.oz1_slices(X, rows, cols, 0, delta, p, radix, dmax)
+    assert np.count_nonzero(want[p // 2:, :32]) > 32 * cols  # the deep planes reach the small elements
     prow, pld = rows, cols
     bx, bd = dev.upload(X), dev.upload(delta)
     bp = dev.alloc(p * prow * pld)
-    dev.oz1_split(bx, rows, cols, cols, 0, bd, p, 254, 127, bp, 2, prow, pld, prow * pld)
+    dev.oz1_split(bx, rows, cols, cols, 0, bd, p, radix, dmax, bp, 2, prow, pld, prow * pld)
     got = from_blocks(dev.download(bp, np.int8, p * prow * pld).reshape(p, -1), prow, pld)
     for x in (bx, bd, bp):
         x.free()
