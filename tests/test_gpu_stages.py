@@ -82,6 +82,9 @@ def split_inputs(rows, cols, rng, phi):
     X[2, :] = rng.uniform(-1, 1, cols) * 2.0 ** -70   # far below the row maximum
     X[2, 0] = 1.0
     X[3, :] = np.ldexp(rng.integers(-2 ** 52, 2 ** 52, cols).astype(np.float64), -52)  # full significands
+    # 90-120 binades below the row maximum: after scaling their low limbs fall below 2^-126 and flush
+    X[4, :] = rng.uniform(-1, 1, cols) * np.exp2(-rng.integers(90, 121, cols).astype(np.float64))
+    X[4, 0] = 1.0
     return X
 
 
