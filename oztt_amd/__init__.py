@@ -93,7 +93,7 @@ class EvalStats(ctypes.Structure):
                 ("max_band_rows", ctypes.c_uint), ("plan_reused", ctypes.c_int), ("force_kc", ctypes.c_uint),
                 ("replay_drop_phase", ctypes.c_int), ("whole_sentinel", ctypes.c_int),
                 ("whole_steps", ctypes.c_uint * 5), ("expected_steps", ctypes.c_uint * 5),
-                ("fp8_matrix_cores", ctypes.c_int)]
+                ("fp8_matrix_cores", ctypes.c_int), ("full_window", ctypes.c_int)]
 
     def __init__(self, *args, **kw):
         super().__init__(*args, **kw)
@@ -110,7 +110,8 @@ class Plan2(ctypes.Structure):
                 ("rS", ctypes.c_int), ("rsparse", ctypes.c_int), ("rfold_first", ctypes.c_int), ("rmaxg", ctypes.c_int),
                 ("rnprod", ctypes.c_int), ("rnplane", ctypes.c_int), ("rnout", ctypes.c_int),
                 ("rm", ctypes.c_int * 24), ("rmode", ctypes.c_int * 24), ("rmaxg_m", ctypes.c_int * 24),
-                ("rlog2M", ctypes.c_double), ("fp8_digits", ctypes.c_int), ("rmodel_set", ctypes.c_int)]
+                ("rlog2M", ctypes.c_double), ("fp8_digits", ctypes.c_int), ("rmodel_set", ctypes.c_int),
+                ("bound_log2", ctypes.c_double), ("S_window", ctypes.c_int), ("nprod", ctypes.c_int)]
 
 
 class Plan1(ctypes.Structure):
@@ -259,14 +260,16 @@ class Context:
 
     def evaluate(self, a, b, m: int, n: int, k: int, options: Options, fixed_bits: int = 0, warmup: int = 0,
                  repeats: int = 0, max_band_rows: int = 0, force_kc: int = 0, replay_drop_phase: int = -1,
-                 fp8_matrix_cores: bool = False):
+                 fp8_matrix_cores: bool = False, full_window: bool = False):
         """GEMM under the evaluation hooks: returns (C, Info, EvalStats) with phase and whole-pass times.
         max_band_rows > 0 caps the rows of a band (row bands are otherwise used only when the problem
         does not fit in device memory); force_kc > 0 makes Scheme I with an FP32-product format
         reconstruct K block by K block with blocks of that length. replay_drop_phase >= 0 is the
         self-test of the whole-pass check: its checking replay leaves out that phase's steps, so
         whole_checked must be 0, and nothing is timed. fp8_matrix_cores runs Scheme II FP8 as the FP8
-        route's e4m3 digit products on the FP8 matrix cores also under Transport.Int8Residues."""
+        route's e4m3 digit products on the FP8 matrix cores also under Transport.Int8Residues.
+        full_window makes Scheme II INT8 residues compute with the set for the window K 2^(2b) rather
+        than the smaller set the operands' own bound on |C'| allows (the same C)."""
         a, b = _f64(a), _f64(b)
         c = np.empty(m * n, dtype=np.float64)
         ev = EvalStats()
@@ -275,6 +278,7 @@ class Context:
         ev.force_kc = force_kc
         ev.replay_drop_phase = replay_drop_phase
         ev.fp8_matrix_cores = int(bool(fp8_matrix_cores))
+        ev.full_window = int(bool(full_window))
         info = self._call(a, b, c, m, n, k, options, ev)
         return c, info, ev
 
@@ -322,16 +326,21 @@ class Context:
 
 def plan2(a, b, M: int, N: int, K: int, fmt: Format = Format.INT8, max_moduli: int = 0,
           reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0,
-          transport: Transport = Transport.Automatic, fp8_matrix_cores: bool = False) -> Plan2:
+          transport: Transport = Transport.Automatic, fp8_matrix_cores: bool = False,
+          full_window: bool = False) -> Plan2:
     """Scheme II planner on padded row-major A (M x K) and B (K x N): the execution set (m, S, b, ...;
     fp8_digits when it is the FP8 route's digit set) and the route's plan of the format (rm, rS, rmode, ...).
-    fp8_matrix_cores as the evaluation setting (FP8 keeps its digits also under Int8Residues)."""
+    INT8 residues compute with the smallest set that covers the operands' bound on |C'| (bound_log2;
+    S_window > 0 is the size of the set for the window K 2^(2b) that it replaced); full_window keeps
+    that set, as the evaluation setting does. fp8_matrix_cores as the evaluation setting (FP8 keeps its
+    digits also under Int8Residues)."""
     a, b = _f64(a), _f64(b)
     out = Plan2()
     err = ctypes.create_string_buffer(2048)
     int8_transport = transport == Transport.Int8Residues and not fp8_matrix_cores
     _raise(host().ozt_plan_scheme2(_ptr(a), _ptr(b), M, N, K, int(fmt), max_moduli, int(reconstruction), fixed_bits,
-                                   int(int8_transport), ctypes.byref(out), err, ctypes.c_size_t(2048)), err)
+                                   int(int8_transport), int(bool(full_window)), ctypes.byref(out), err,
+                                   ctypes.c_size_t(2048)), err)
     return out
 
 

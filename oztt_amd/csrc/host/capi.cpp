@@ -82,6 +82,7 @@ struct ozt_eval {
     unsigned whole_steps[5];     // steps per phase issued by the checking replay
     unsigned expected_steps[5];  // steps per phase the plan calls for
     int fp8_matrix_cores;        // input: Scheme II FP8 on the FP8 matrix cores also under Transport::Int8Residues
+    int full_window;             // input: Scheme II INT8 residues with the set for the window K 2^(2b)
 };
 
 struct ozt_plan2 {
@@ -96,6 +97,9 @@ struct ozt_plan2 {
     double rlog2M;
     int fp8_digits;  // the device computes the FP8 route's e4m3 digit products (else the residues of m[])
     int rmodel_set;  // the route's set was chosen by the stage-time model (not from the table)
+    double bound_log2;  // log2 of the operands' bound on max |C'| (+inf when not measured)
+    int S_window;       // moduli of the set for the window K 2^(2b) that m[] replaced (0: none)
+    int nprod;          // products the device computes: S, or the FP8 route's digit products
 };
 
 static void fill_route(const ozTTgemm::detail::ModuliSet& r, ozt_plan2* out) {
@@ -185,6 +189,7 @@ static ozTTgemm::evaluation::Settings settings_of(const ozt_eval* evo) {
     s.force_kc = evo->force_kc;
     s.replay_drop_phase = evo->replay_drop_phase;
     s.fp8_matrix_cores = evo->fp8_matrix_cores != 0;
+    s.full_window = evo->full_window != 0;
     return s;
 }
 
@@ -253,13 +258,14 @@ const char* ozt_format_name(int format) { return ozTTgemm::format_name(static_ca
 // Scheme II planner on padded row-major A (M x K) and B (K x N) for `format`; int8_transport: the plan
 // of Transport::Int8Residues.
 int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, unsigned K, int format, unsigned max_moduli,
-              int recon, unsigned fixed_b, int int8_transport, ozt_plan2* out, char* err, std::size_t errlen) {
+              int recon, unsigned fixed_b, int int8_transport, int full_window, ozt_plan2* out, char* err,
+              std::size_t errlen) {
     return guarded(err, errlen, [&] {
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
         const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, static_cast<ozTTgemm::Format>(format), max_moduli,
                                                         static_cast<ozTTgemm::Reconstruction>(recon), fb,
-                                                        int8_transport != 0);
+                                                        int8_transport != 0, full_window == 0);
         std::memset(out, 0, sizeof(*out));
         out->fp8_digits = p.fp8_digits;
         out->ok = p.mo.ok;
@@ -279,12 +285,15 @@ int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, u
         out->wA = p.stats.wA;
         out->wB = p.stats.wB;
         out->b_cap = p.stats.measured ? ozTTgemm::detail::precision_cap(p.stats) : 0;
+        out->bound_log2 = p.bound_log2;
+        out->S_window = p.S_window;
+        out->nprod = p.fp8_digits ? p.mo.nprod : p.S;
         fill_route(p.route, out);
     });
 }
 
 // The device descriptors of a Scheme II FP8 plan on the FP8 matrix cores (digit split, product outputs,
-// CRT, term moduli).
+// CRT, term moduli), for the route's own set (the window K 2^(2b), as the reference plans it).
 int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned max_moduli,
                          int recon, unsigned fixed_b, oz2_digit_dev* dd, oz2_groups_dev* gd, oz2_crt_dev* crt,
                          unsigned char* term_modulus, char* err, std::size_t errlen) {
@@ -292,7 +301,8 @@ int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned 
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
         const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, ozTTgemm::Format::FP8, max_moduli,
-                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb, false);
+                                                        static_cast<ozTTgemm::Reconstruction>(recon), fb, false,
+                                                        false);
         *crt = ozTTgemm::detail::crt_descriptor(p);
         *dd = ozTTgemm::detail::digit_descriptor(p);
         std::vector<unsigned char> tm;

@@ -403,7 +403,7 @@ Info Context::Impl::resident(Matrix::State& A, Matrix::State& B, std::span<doubl
     // the plan of this pair and these options, if an earlier call made one (not when the
     // evaluation hooks fix the width b or the FP8 transport)
     evaluation::Settings* es = evaluation::active();
-    const bool cacheable = !es || (es->fixed_bits == 0 && !es->fp8_matrix_cores);
+    const bool cacheable = !es || (es->fixed_bits == 0 && !es->fp8_matrix_cores && !es->full_window);
     std::shared_ptr<const void> plan;
     if (cacheable)
         for (std::size_t i = plans.size(); i-- > 0;) {

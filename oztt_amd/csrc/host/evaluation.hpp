@@ -35,6 +35,8 @@ struct Settings {
                                  // nothing is timed; -1 (the default) replays every step
     bool fp8_matrix_cores = false;  // Scheme II FP8: the FP8 route's e4m3 digit products on the FP8 matrix
                                     // cores also under Transport::Int8Residues (same C)
+    bool full_window = false;       // Scheme II INT8 residues: compute with the set for the window
+                                    // K 2^(2b), not the smaller one the operands' bound allows (same C)
     // outputs
     double phase_ms[PhaseCount] = {};  // device time of each phase: the average of up to 5 warm passes
                                        // after the replays (the first pass when there are none)

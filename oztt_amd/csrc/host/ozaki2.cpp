@@ -67,7 +67,8 @@ Output ozaki2_run(Device& D, const Problem& p) {
                : std::make_shared<const Plan2>(plan_scheme2(p.a, p.b, p.m, p.n, p.k, p.options.format,
                                                             p.options.max_moduli, p.options.reconstruction, fixed_b,
                                                             p.options.transport == Transport::Int8Residues &&
-                                                                !(es && es->fp8_matrix_cores)));
+                                                                !(es && es->fp8_matrix_cores),
+                                                            !(es && es->full_window)));
     const Plan2& plan = *planp;
     const bool fp8 = plan.fp8_digits;
     const std::uint32_t S = (std::uint32_t)plan.S;

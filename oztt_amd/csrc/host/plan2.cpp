@@ -92,6 +92,23 @@ void reselect_tail(std::vector<int>& m, double& logM, double need, int m_cap) {
     logM = best;
 }
 
+// Upper bound on ||x||_2 / 2^ceil(log2 max|x_k|) for one row or column of n values x (each scaled by
+// the same power of two), from their maximum magnitude mx and the sum of squares s2 that
+// measure_stats computes. Recursive summation of n rounded squares errs by at most n 2^-53 of the
+// sum, and squares below 2^-1022 lose at most 2^-1074 each; the factors below cover both and the
+// bound's own rounding. A maximum below 2^-400 (where the lost squares could matter), or a sum that
+// is not finite, gives sqrt(n), which holds for any such vector since every |x_k| <= 2^ceil(log2 mx).
+double flatness_bound(double mx, double s2, std::uint32_t n) {
+    if (!(mx > 0)) return 0.0;
+    const double worst = std::sqrt((double)n) * (1.0 + 0x1p-50);
+    if (!(mx >= 0x1p-400) || !std::isfinite(s2)) return worst;
+    int e;
+    const double f = std::frexp(mx, &e);  // mx = f 2^e, 1/2 <= f < 1
+    const int te = f == 0.5 ? e - 1 : e;  // 2^te: the least power of two >= mx
+    const double s = s2 * (1.0 + (double)n * 0x1p-51) + (double)n * 0x1p-1022;
+    return std::min(std::ldexp(std::sqrt(s), -te) * (1.0 + 0x1p-50), worst);
+}
+
 }  // namespace
 
 OperandStats measure_stats(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K) {
@@ -100,7 +117,7 @@ OperandStats measure_stats(const double* A, const double* B, std::uint32_t M, st
     // Row statistics of A and column statistics of B (auto_precision.hpp:24-56). Per-row and per-column
     // values are computed in parallel with the reference's inner order; the sums over rows/columns
     // run sequentially in the reference's order.
-    std::vector<double> tA(M), sA(M), tB(N), sB(N), wA(M, 0.0), wB(N, 0.0);
+    std::vector<double> tA(M), sA(M), tB(N), sB(N), wA(M, 0.0), wB(N, 0.0), rA(M), rB(N);
 #pragma omp parallel for schedule(static)
     for (std::int64_t r = 0; r < (std::int64_t)M; r++) {
         double mx = 0, s2 = 0;
@@ -117,6 +134,7 @@ OperandStats measure_stats(const double* A, const double* B, std::uint32_t M, st
         }
         tA[r] = t2;
         sA[r] = s2;
+        rA[r] = flatness_bound(mx, s2, K);
     }
     constexpr std::uint32_t CB = 64;  // column block: row-major sweep, per-column order kept
 #pragma omp parallel for schedule(static)
@@ -138,17 +156,20 @@ OperandStats measure_stats(const double* A, const double* B, std::uint32_t M, st
             }
             tB[c] = t2;
             sB[c] = s2[c - c0];
+            rB[c] = flatness_bound(mx[c - c0], s2[c - c0], K);
         }
     }
     for (std::uint32_t r = 0; r < M; r++) {
         st.TA += tA[r];
         st.nA += sA[r];
         st.wA = std::max(st.wA, wA[r]);
+        st.rA = std::max(st.rA, rA[r]);
     }
     for (std::uint32_t c = 0; c < N; c++) {
         st.TB += tB[c];
         st.nB += sB[c];
         st.wB = std::max(st.wB, wB[c]);
+        st.rB = std::max(st.rB, rB[c]);
     }
     st.nC = estimate_product_norm(A, B, M, N, K, rgA, rgB);
     st.measured = true;
@@ -160,9 +181,9 @@ int precision_cap(const OperandStats& st) {
     return std::min(kMaxDigits * kDigitBits, kTargetBits + (int)std::ceil(std::log2(std::max(k2, 1.0))));
 }
 
-ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap) {
+ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap, double window_log2) {
     ModuliSet o;
-    const double W = std::log2((double)K);
+    const double W = std::isnan(window_log2) ? std::log2((double)K) : window_log2;
     const int m_cap = (int)std::min<long>(kInt8ModCap, 2 * int8_rmax(K) + 1);
     double logM = 0.0;
     for (int mm : kTableInt8) {
@@ -217,7 +238,7 @@ double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st) {
 
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
                    std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b,
-                   bool int8_transport) {
+                   bool int8_transport, bool operand_window) {
     // Every format plans on its own route as the reference does (INT8 residues, or the FP8, TF32, BF16,
     // FP16, BFP8, BFP4 or BFP2 digit route): its moduli, width b and pass choice are the reference's.
     // INT8 and FP8 then compute on their own matrix instructions (FP8: the route's e4m3 digits) unless
@@ -296,6 +317,36 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
                                          "Options::max_moduli or a smaller K.");
             p.mo = std::move(f);
             p.fp8_digits = true;
+        }
+    }
+    // The CRT window from the operands themselves. The reference sizes M for the worst case
+    // |C'_ij| <= K 2^(2b). With |A'_ik| <= 2^b |a_ik| / 2^ceil(log2 max_k |a_ik|) + 2 (the row's own
+    // power of two is at most the one its delta was taken from; the digits round by less than 2) and
+    // the same for the columns of B, Cauchy-Schwarz gives |C'_ij| <= ||A'_i||_2 ||B'_j||_2
+    // <= (2^b rA + 2 sqrt K)(2^b rB + 2 sqrt K), where rA, rB <= sqrt K, and far below it unless rows
+    // or columns are flat. Any set of moduli whose product exceeds twice that recovers the same exact
+    // C', so when a smaller set covers it, that set computes (C is bit for bit the same): fewer INT8
+    // moduli, or on the FP8 route a set of fewer digit products (chosen by the route's own rules for
+    // that window, as the reference's research planner did with windows measured from its inputs).
+    if (p.stats.measured) {
+        const double sk = std::ldexp(2.0 * std::sqrt((double)K) * (1.0 + 0x1p-50), -p.b);
+        const double w = std::log2(p.stats.rA + sk) + std::log2(p.stats.rB + sk) + 1e-12;
+        p.bound_log2 = 2.0 * p.b + w;
+        if (operand_window && w < std::log2((double)K)) {
+            if (!p.fp8_digits) {
+                ModuliSet t = choose_moduli_int8(K, kMaxModuli, p.b, w);
+                if (t.ok && t.b == p.b && t.m.size() < p.mo.m.size()) {
+                    p.S_window = (int)p.mo.m.size();
+                    p.mo = std::move(t);
+                }
+            } else {
+                ModuliSet t = choose_moduli_digits(Format::FP8, M, N, K, (int)p.S_req, p.b, w);
+                if (t.ok && t.b == p.b && t.nprod < p.mo.nprod && t.nplane <= OZ2_MAXPLANES &&
+                    t.nout <= OZ2_MAXOUT) {
+                    p.S_window = (int)p.mo.m.size();
+                    p.mo = std::move(t);
+                }
+            }
         }
     }
     p.S = (int)p.mo.m.size();

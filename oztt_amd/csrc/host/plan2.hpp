@@ -32,6 +32,9 @@ struct OperandStats {
     double nA = 0, nB = 0;  // ||A||_F^2, ||B||_F^2 (after the power-of-two normalization)
     double nC = 0;          // low-biased Hutchinson estimate of ||C||_F^2
     double wA = 0, wB = 0;  // largest normalized row norm of A / column norm of B (||a_i||_2 / tau_i)
+    // rigorous upper bounds on the largest ||a_i||_2 / 2^ceil(log2 max_k |a_ik|) over the rows of A and
+    // the same over the columns of B (between 0 and sqrt(K)); not part of the reference's statistics
+    double rA = 0, rB = 0;
     bool measured = false;
 };
 
@@ -72,19 +75,27 @@ struct ModuliSet {
 // reports under Transport::Automatic and what the pass choice is made on), the set the device computes
 // with (`mo`), the width b, digits of A' and passes. `mo` is `route` for INT8, and for FP8 on its own
 // digits (fp8_digits); otherwise an INT8 set of the same width b (or, beyond the INT8 width, the FP8
-// route's set), and C is the same (every set reconstructs the exact product A'B').
+// route's set); either is then replaced by a smaller set when the operands' own bound on |C'| allows
+// one (bound_log2). C is the same (every set reconstructs the exact product A'B').
 struct Plan2 {
     std::uint32_t M = 0, N = 0, K = 0;  // padded dimensions
     std::uint32_t S_req = 0;
     Format format = Format::INT8;
     ModuliSet route;
     ModuliSet mo;
-    bool fp8_digits = false;  // the products are the FP8 route's e4m3 digit products (mo == route)
+    bool fp8_digits = false;  // the products are the FP8 route's e4m3 digit products
     int b = 0, nd = 3, S = 0;  // S: moduli of mo
     bool two_pass = false;
     int shift() const { return b - kDigitBits * (nd - 1); }  // plan.hpp:81 oz2_shift
     OperandStats stats;
     double recon1_log2 = 0;  // one-pass error estimate (log2), -inf when not estimated
+    // The CRT window from the operands: log2 of an upper bound on max |C'_ij| (C' = A'B', the exact
+    // integer product), +inf when the operands were not measured. When it needs fewer products than
+    // the planned window K 2^(2b), `mo` is the set chosen for it (INT8 residues, or the FP8 route's
+    // digits) and S_window the number of moduli of the set it replaced (the exact CRT recovers the
+    // same C' from any set whose M exceeds 2 max |C'|).
+    double bound_log2 = std::numeric_limits<double>::infinity();
+    int S_window = 0;  // moduli of the set for the window K 2^(2b) (0: mo is that set)
 };
 
 // Statistics of padded row-major A (M x K) and B (K x N): tau sums and norms after the power-of-two
@@ -97,7 +108,9 @@ OperandStats measure_stats(const double* A, const double* B, std::uint32_t M, st
 int precision_cap(const OperandStats& st);
 
 // Moduli selection for the INT8 path (moduli.hpp:719-769 with the INT8 route of split.hpp:73).
-ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap);
+// window_log2 replaces the CRT window log2 K (|C'| <= 2^(2b + window_log2)); NaN keeps it.
+ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap,
+                             double window_log2 = std::numeric_limits<double>::quiet_NaN());
 // Moduli selection on the digit route of a format other than INT8 (moduli.hpp:719-769 with the format's
 // row of OZ2_ROUTES, split.hpp:66-146): the table selection for FP8 and TF32, the stage-time model's
 // set (awe.hpp) for BF16, FP16, BFP8, BFP4 and BFP2. M and N feed only the model's memory estimate.
@@ -116,10 +129,12 @@ double recon1_log2(const ModuliSet& mo, int b, const OperandStats& st);
 // int8_transport (Transport::Int8Residues): FP8 is carried by INT8 residues at the FP8 plan's width
 // whenever an INT8 set reaches that width; otherwise FP8 computes the FP8 route's e4m3 digit products
 // on the FP8 matrix cores. The other digit formats are carried by INT8 residues either way.
+// operand_window: INT8 residues compute with the smallest set that covers the operands' own bound
+// on |C'| (Plan2::bound_log2) when that needs fewer moduli than the window K 2^(2b).
 // Throws std::runtime_error when no exact configuration exists.
 Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint32_t N, std::uint32_t K, Format format,
                    std::uint32_t max_moduli, Reconstruction passes, std::optional<unsigned> fixed_b,
-                   bool int8_transport = false);
+                   bool int8_transport = false, bool operand_window = true);
 
 // Device descriptors of the plan.
 oz2_moduli_dev split_descriptor(const Plan2& p);

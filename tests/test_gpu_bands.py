@@ -46,14 +46,20 @@ def oracle_c(oracle, a, b, m, n, k, opts, fp8_cores, info):
     A, B = padded(a.reshape(m, k), mp, kp), padded(b.reshape(k, n), kp, np_)
     if opts.scheme == oz.Scheme.II:
         p = oz.plan2(A, B, mp, np_, kp, opts.format, transport=opts.transport, fp8_matrix_cores=fp8_cores)
-        int8_carried = opts.transport == oz.Transport.Int8Residues and not p.fp8_digits
-        assert (p.S if int8_carried else p.rS, p.b) == (info.moduli, info.integer_bits)
-        ms = [p.m[i] for i in range(p.S)]  # the set the device computes with (FP8 digits: the route's)
+        # Info: the route's moduli under Transport.Automatic, the moduli that computed under Int8Residues
+        computed = opts.transport == oz.Transport.Int8Residues
+        assert (p.S if computed else p.rS, p.b) == (info.moduli, info.integer_bits)
+        # the set the device computes with (FP8 digits: the route's, or the FP8 set for the operands' own
+        # window when that has fewer digit products)
+        ms = [p.m[i] for i in range(p.S)]
         if opts.format == oz.Format.FP8:
             assert p.fp8_digits == (fp8_cores or opts.transport == oz.Transport.Automatic)
         if p.fp8_digits:
-            assert ms == [p.rm[i] for i in range(p.rS)]
+            assert (p.S_window or p.S) == p.rS and p.nprod <= p.rnprod
         want = oz2_chain(oracle, A, B, ms, p.b, p.nd)
+        if p.S_window:  # the same C from the route's own set
+            full = oz2_chain(oracle, A, B, [p.rm[i] for i in range(p.rS)], p.b, p.nd)
+            np.testing.assert_array_equal(full.view(np.uint64), want.view(np.uint64))
     else:
         pl = oz.plan1(A, B, mp, np_, kp, slices=opts.slices, fmt=opts.format)
         assert pl.p == info.slices and pl.nkb == 1

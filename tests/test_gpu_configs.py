@@ -1,15 +1,16 @@
 """The BASELINE configurations whose own plans need their full shapes, on the GPU.
 
 C3 (the headline): Scheme II INT8, m = n = k = 8192, the evaluation generator with seed 3 and
-phi 0.5, automatic moduli, two passes forced. The planner's choice (17 moduli, b = 56, two passes)
-runs through the public API and, stage by stage, through the production kernels of the C ABI
-(scale, OZ_BLOCK residue split, products reduced to CRT digits in the GEMM epilogue, CRT from the
-digits). On a 64-row slab that crosses a tile boundary, every stage is checked against the oracle:
-the exponent deltas, the residue planes of A, all residue planes of B, the epilogue digits (the
-exact products mod m_s times y_s, from float64 products of the oracle's residues, which are exact
-below 2^53), and C (the oracle's exact CRT of the same products); the public call gives the same
-bits as the staged chain for the whole matrix; a binary128 sample lies within the FP64 bound
-k 2^-53 |A||B|. (Reference ozaki2.cpp:439-478; BASELINE.json configs[2].)
+phi 0.5, automatic moduli, two passes forced. The planner's choice (b = 56, two passes, 17 moduli
+for the reference's window K 2^(2b), of which the operands' own bound on |C'| needs 16) runs through
+the public API and, stage by stage, through the production kernels of the C ABI (scale, OZ_BLOCK
+residue split, products reduced to CRT digits in the GEMM epilogue, CRT from the digits). On a
+64-row slab that crosses a tile boundary, every stage is checked against the oracle: the exponent
+deltas, the residue planes of A, all residue planes of B, the epilogue digits (the exact products
+mod m_s times y_s, from float64 products of the oracle's residues, which are exact below 2^53), and
+C (the oracle's exact CRT of the same products, and its whole chain with the reference's 17 moduli);
+the public call gives the same bits as the staged chain for the whole matrix; a binary128 sample lies
+within the FP64 bound k 2^-53 |A||B|. (Reference ozaki2.cpp:439-478; BASELINE.json configs[2].)
 
 C4's K: Scheme II FP8 at k = 16384 (seed 4, phi 2) with m = n = 256. At this K the reference's
 planner cannot use its sparse e4m3 digits (K 32^2 + m > 2^24) and falls back to dense digits with
@@ -27,6 +28,7 @@ import pytest
 import oztt_amd as oz
 from oztt_amd.device import E4M3, GroupsDesc, crt_desc, from_blocks, moduli_desc, to_blocks
 from tests.oracle_lib import assert_residues
+from tests.oracle_chains import oz2_chain
 from tests.test_gpu_scheme2_fp8 import check_fp8_chain, run_fp8_stages
 
 pytestmark = pytest.mark.gpu
@@ -53,7 +55,8 @@ def test_c3_headline_plan_and_slab_parity(ctx, dev, oracle):
     p = oz.plan2(a, b, n, n, n, oz.Format.INT8, reconstruction=two)
     moduli = [p.m[i] for i in range(p.S)]
     S, bw, nd = p.S, p.b, p.nd
-    assert (S, bw, nd, p.two_pass) == (17, 56, 3, 1)
+    # the reference's plan: 17 moduli for the window K 2^(2b); the operands' own bound on |C'| needs 16
+    assert (p.rS, p.S_window, S, bw, nd, p.two_pass) == (17, 17, 16, 56, 3, 1)
     log("C3: public call")
     c = np.empty(n * n)
     info = ctx.gemm(a, b, c, n, n, n, oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, reconstruction=two))
@@ -112,6 +115,9 @@ def test_c3_headline_plan_and_slab_parity(ctx, dev, oracle):
         assert_residues(gD[s], (prod.astype(np.int64) % m) * int(cd.y[s]), m, f"modulus {m}")
     ex = oracle.crt_exact(Cs, rows, n, moduli, bw, nd, wA[r0:r0 + rows], wB)
     np.testing.assert_array_equal(c.reshape(n, n)[r0:r0 + rows].ravel().view(np.uint64), ex.view(np.uint64))
+    log("C3: oracle chain with the reference's 17 moduli")
+    full = oz2_chain(oracle, np.ascontiguousarray(A[r0:r0 + rows]), B, [p.rm[i] for i in range(p.rS)], bw, nd)
+    np.testing.assert_array_equal(c.reshape(n, n)[r0:r0 + rows].view(np.uint64), full.view(np.uint64))
 
     log("C3: binary128 sample")
     rng = np.random.default_rng(3)
@@ -160,10 +166,12 @@ def test_c4_inner_dimension_public_call_equals_int8(ctx):
     assert (infod.integer_bits, infod.reconstruction_passes) == (info8.integer_bits, info8.reconstruction_passes)
     # products per pass: the FP8 route's digit products, or one per INT8 modulus
     oi = oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8, max_moduli=24)
-    ci, infoi, _ = ctx.evaluate(a, b, m, n, k, oi, fixed_bits=info8.integer_bits)
-    assert infoi.integer_bits == info8.integer_bits and evd.partial_products == infoi.moduli == infod.moduli
+    ci, infoi, evi = ctx.evaluate(a, b, m, n, k, oi, fixed_bits=info8.integer_bits)
+    assert infoi.integer_bits == info8.integer_bits and evd.partial_products == evi.partial_products == infod.moduli
+    # the operands' own window: fewer FP8 digit products than the route's, fewer INT8 moduli than the window's
     p = oz.plan2(a, b, m, n, k, oz.Format.FP8)
-    assert ev8.partial_products == p.rnprod and info8.moduli == p.rS
+    assert ev8.partial_products == p.nprod < p.rnprod and info8.moduli == p.rS
+    assert infoi.moduli > infod.moduli
     log(f"C4 K: FP8 {info8.moduli} moduli ({ev8.partial_products} digit products), INT8 {infoi.moduli} moduli, "
         f"b={info8.integer_bits}")
     np.testing.assert_array_equal(c8.view(np.uint64), ci.view(np.uint64))

@@ -2,10 +2,10 @@
 
 The oracle cannot run these shapes whole, so each test checks what does not depend on the size:
 * C4 (Scheme II FP8, m = n = k = 16384, phi 2): the library's default, the FP8 route's e4m3 digits
-  on the FP8 matrix cores (45 digit products), and `Transport.Int8Residues` (the same plan on INT8
-  residues, other kernels, other moduli) give the same C bit for bit over the whole matrix: both are
-  the exact CRT of the same integer product A'B' (reference ozaki2.cpp:228-318 and :333-350,
-  BASELINE.json configs[3]);
+  on the FP8 matrix cores (42 digit products for the operands' own window, 45 for the reference's),
+  and `Transport.Int8Residues` (the same plan on INT8 residues, other kernels, other moduli) give the
+  same C bit for bit over the whole matrix: both are the exact CRT of the same integer product A'B'
+  (reference ozaki2.cpp:228-318 and :333-350, BASELINE.json configs[3]);
 * C5 (Scheme I BF16 format, 8 slices, m = n = 8192, k = 65536, phi 4, rows i % 100 == 0 of A and
   columns j % 100 == 0 of B zero): those rows and columns of C are zero (BASELINE.json configs[4]);
 * in both, a 16 x 16 block of C whose rows and columns cross 256-tile boundaries (and, for C5, hold a
@@ -70,10 +70,14 @@ def test_c4_full_size_transports_agree_and_block_parity(ctx, oracle):
     log("C4: oracle chain on a 16 x 16 block")
     A, B = a.reshape(n, n), b.reshape(n, n)
     r0, c0 = 8184, 4088  # rows 8184..8199 and columns 4088..4103 cross the tiles at 8192 and 4096
-    want = oz2_chain(oracle, np.ascontiguousarray(A[r0:r0 + 16]), np.ascontiguousarray(B[:, c0:c0 + 16]),
-                     [p.m[i] for i in range(p.S)], p.b, p.nd)
+    As, Bs = np.ascontiguousarray(A[r0:r0 + 16]), np.ascontiguousarray(B[:, c0:c0 + 16])
     got = np.ascontiguousarray(c8.reshape(n, n)[r0:r0 + 16, c0:c0 + 16])
-    np.testing.assert_array_equal(got.view(np.uint64), want.view(np.uint64))
+    # with the INT8 set that computed under Int8Residues and with the FP8 route's own set for the window
+    # K 2^(2b) (both calls computed with smaller sets, which the operands' bound on |C'| allows)
+    assert p.S_window > p.S and pr.S_window == pr.rS and pr.nprod < pr.rnprod
+    for ms in ([p.m[i] for i in range(p.S)], [pr.rm[i] for i in range(pr.rS)]):
+        want = oz2_chain(oracle, As, Bs, ms, p.b, p.nd)
+        np.testing.assert_array_equal(got.view(np.uint64), want.view(np.uint64))
 
 
 def test_c5_full_size_zero_lines_and_block_parity(ctx, oracle):

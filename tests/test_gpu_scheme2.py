@@ -182,7 +182,8 @@ def test_baseline_c1_bit_exact_chain(dev, oracle, ctx):
     c = np.empty(n * n)
     info = ctx.gemm(a, b, c, n, n, n, oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8,
                                                    reconstruction=oz.Reconstruction.OnePass))
-    assert info.moduli == len(moduli) and info.integer_bits == b_ and info.reconstruction_passes == 1
+    assert info.moduli == p.rS == (p.S_window or len(moduli)) and info.integer_bits == b_
+    assert info.reconstruction_passes == 1
     np.testing.assert_array_equal(c.view(np.uint64), r["out"].view(np.uint64))
     # accuracy against binary128 on a sample: within the FP64 bound |A||B| k 2^-53 and close to C
     rs = np.random.default_rng(0).integers(0, n, 256)

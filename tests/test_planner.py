@@ -95,9 +95,12 @@ def test_auto_precision_records(phi, b, S, pred):
     a, bb = oz.eval_inputs(7, phi, n * n, n * n)
     p = oz.plan2_int8(a, bb, n, n, n, reconstruction=oz.Reconstruction.TwoPass)
     assert p.b == b and p.two_pass == 1 and p.nd == (5 if b > 80 else 4 if b > 60 else 3)
-    # the library's window (log2 K) needs at least as many moduli as the research set
+    # the library's window (log2 K) needs at least as many moduli as the research set, and the route
+    # keeps it; the execution set covers the operands' own window (Cauchy-Schwarz on A', B'), which is
+    # the research planner's measured window made rigorous, and needs as many moduli as its set
     lib = oz.choose_moduli_int8(n, 24, b)
-    assert p.S == lib.S and p.S >= S
+    assert p.rS == lib.S and lib.S >= S
+    assert (p.S_window or p.S) == lib.S and p.S == S
     # the statistics behind b reproduce the research planner's one-pass estimate to 0.01 bit
     r = math.sqrt(n)
     f = (1 + r / math.ldexp(p.wA, b)) * (1 + r / math.ldexp(p.wB, b))
@@ -213,7 +216,8 @@ FP8_PHI = [(0.0, 53, 12), (1.0, 57, 12), (2.0, 59, 12), (4.0, 61, 13)]
 @pytest.mark.parametrize("phi,b,S", [FP8_PHI[i] for i in (0, 3)])
 def test_fp8_auto_precision_records(phi, b, S):
     """The FP8 plan's width b equals the record; its set with the research planner's measured window has the
-    recorded size; on the FP8 matrix cores the execution set is the route's FP8 set."""
+    recorded size; on the FP8 matrix cores the execution set is the route's FP8 set, or the FP8 set for the
+    operands' own window (the research planner's window made rigorous) when that has fewer products."""
     n = 4096
     a, bb = oz.eval_inputs(7, phi, n * n, n * n)
     p = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass)
@@ -223,8 +227,13 @@ def test_fp8_auto_precision_records(phi, b, S):
     wlog2 = math.log2(p.wA * p.wB * max(f, 1.001))
     research = oz.choose_moduli_fp8(n, 24, b, wlog2)
     assert research.b == b and research.rS == S
-    # by default the execution set is the route's FP8 set (its e4m3 digits on the FP8 matrix cores)
-    assert p.fp8_digits and p.S == p.rS and [p.m[i] for i in range(p.S)] == [p.rm[i] for i in range(p.rS)]
+    # by default the execution set is an FP8 set (its e4m3 digits on the FP8 matrix cores): the route's
+    # with the full window, else the set for the operands' window, of the research set's size
+    full = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass, full_window=True)
+    assert full.fp8_digits and full.S_window == 0
+    assert [full.m[i] for i in range(full.S)] == [p.rm[i] for i in range(p.rS)]
+    assert p.fp8_digits and p.S == S and (p.S_window or p.S) == p.rS and p.nprod <= p.rnprod
+    assert math.log2(p.wA * p.wB) <= p.bound_log2 - 2 * b <= math.log2(n)
     q = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass,
                  transport=oz.Transport.Int8Residues)
     assert not q.fp8_digits and q.b == b and max(q.m[i] for i in range(q.S)) <= 255
@@ -264,7 +273,7 @@ def test_fp8_beyond_the_int8_width_keeps_its_digits():
     assert oz.choose_moduli_int8(K, 24, 90).b == 85
     i8 = oz.Transport.Int8Residues
     p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=90, max_moduli=24, transport=i8)
-    assert p.fp8_digits and p.b == 90 and p.S == p.rS
+    assert p.fp8_digits and p.b == 90 and (p.S_window or p.S) == p.rS
     p = oz.plan2(a, bb, M, N, K, oz.Format.FP8, fixed_bits=85, max_moduli=24, transport=i8)
     assert not p.fp8_digits and p.b == 85
 
