@@ -111,7 +111,8 @@ class Plan2(ctypes.Structure):
                 ("rnprod", ctypes.c_int), ("rnplane", ctypes.c_int), ("rnout", ctypes.c_int),
                 ("rm", ctypes.c_int * 24), ("rmode", ctypes.c_int * 24), ("rmaxg_m", ctypes.c_int * 24),
                 ("rlog2M", ctypes.c_double), ("fp8_digits", ctypes.c_int), ("rmodel_set", ctypes.c_int),
-                ("bound_log2", ctypes.c_double), ("S_window", ctypes.c_int), ("nprod", ctypes.c_int)]
+                ("bound_log2", ctypes.c_double), ("S_window", ctypes.c_int), ("nprod", ctypes.c_int),
+                ("nplane", ctypes.c_int)]
 
 
 class Plan1(ctypes.Structure):

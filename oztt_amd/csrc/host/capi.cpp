@@ -100,6 +100,7 @@ struct ozt_plan2 {
     double bound_log2;  // log2 of the operands' bound on max |C'| (+inf when not measured)
     int S_window;       // moduli of the set for the window K 2^(2b) that m[] replaced (0: none)
     int nprod;          // products the device computes: S, or the FP8 route's digit products
+    int nplane;         // digit planes per operand on the FP8 route (0 for INT8 residues)
 };
 
 static void fill_route(const ozTTgemm::detail::ModuliSet& r, ozt_plan2* out) {
@@ -288,6 +289,7 @@ int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, u
         out->bound_log2 = p.bound_log2;
         out->S_window = p.S_window;
         out->nprod = p.fp8_digits ? p.mo.nprod : p.S;
+        out->nplane = p.fp8_digits ? p.mo.nplane : 0;
         fill_route(p.route, out);
     });
 }
