@@ -222,20 +222,21 @@ int oz2_gemm_f64_noalloc(oz_dev* dev, const double* A, int lda, const double* B,
 
 /* ---- A18 split (reference modslice_digit.cpp:142-243, sparse_fix.h:48-78, split.hpp:157-279) ---
  * As oz2_split_int8 (same residues r = A' mod m_s, m_s <= 2401), then r split into digits per
- * modulus, planes l, h (and s = h + l for xmode 1) in modulus order:
+ * modulus, planes l, h (and s = h + l for xmode 1; r alone for xmode 3) in modulus order:
  *   xmode 0 (rounded, square or wide modulus): h = Rnd(r*qinv), l = r - q*h;
  *   xmode 1 (Karatsuba): h = Rnd((r + sgn(r)*(q/2 - 1/2))*qinv), l = r - q*h, s = h + l;
- *   xmode 2 (sparse square, q odd): the rounded digits moved into {|x| <= 16} U {even, |x| <= 32}.
+ *   xmode 2 (sparse square, q odd): the rounded digits moved into {|x| <= 16} U {even, |x| <= 32};
+ *   xmode 3 (one digit, m <= 33): the residue r itself (|r| <= 16), one plane (q is not read).
  * Every operation is one binary32 operation as in the reference. encoding 1 stores e4m3 bytes
  * (gfx950 FP8, exact for these digits), 0 int8 values. Layouts 2 and 3 only (OZ_BLOCK tiles). */
 typedef struct oz2_digit_dev {
     oz2_moduli_dev mo;       /* moduli (m <= 2401), rinv, weights, nd */
-    int xmode[OZ2_MAXS];     /* 0 rounded, 1 Karatsuba, 2 sparse square */
+    int xmode[OZ2_MAXS];     /* 0 rounded, 1 Karatsuba, 2 sparse square, 3 one digit */
     float q[OZ2_MAXS];       /* digit radix */
     float qinv[OZ2_MAXS];    /* 1.0f / q (stages.hpp:223) */
     int encoding;            /* 1 e4m3, 0 int8 */
 } oz2_digit_dev;
-/* Number of digit planes of a descriptor (2 per modulus, 3 for Karatsuba), or -1. */
+/* Number of digit planes of a descriptor (2 per modulus, 3 for Karatsuba, 1 for one digit), or -1. */
 int oz2_digit_planes(const oz2_digit_dev* dd);
 int oz2_split_digits(oz_dev* dev, const double* X, int rows, int cols, int ld, int mode, const int32_t* delta,
                      const oz2_digit_dev* dd, uint8_t* planes, int layout, int prow, int pld, long long plane_stride);

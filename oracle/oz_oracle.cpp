@@ -763,6 +763,10 @@ void orc_oz2_residues16(const double* X, int rows, int cols, int ld, int mode, c
 // modslice_digit.cpp:195-218 + sparse_fix.h:53-73: the digits of residue r (d[0] = l, d[1] = h,
 // d[2] = s), in the FP32 operation model. xmode 0 rounded, 1 Karatsuba, 2 sparse square.
 static int split_residue(float r, int xmode, float q, float qinv, float* d) {
+    if (xmode == 3) {  // one digit: the residue itself (split.hpp:202-205, modslice_digit.cpp:76-79)
+        d[0] = r;
+        return 1;
+    }
     if (xmode == 1) {
         float sgn = std::signbit(r) ? 1.0f : 0.0f;          // Ltz
         sgn = f_add(f_mul(sgn, -2.0f), 1.0f);                // MulS -2, AddS 1
@@ -805,7 +809,7 @@ void orc_oz2_digit_planes(const double* X, int rows, int cols, int ld, int mode,
         rinv[s] = (float)(double)qq;
         for (int j = 0; j < 4; j++) cw[(size_t)s * 4 + j] = pow2mod(20 * (j + 1), m[s]);
         poff[s] = np;
-        np += xmode[s] == 1 ? 3 : 2;
+        np += xmode[s] == 1 ? 3 : (xmode[s] == 3 ? 1 : 2);
     }
     const size_t plane = (size_t)rows * cols;
 #pragma omp parallel for schedule(static)

@@ -54,7 +54,8 @@ void orc_oz2_residues(const double* X, int rows, int cols, int ld, int mode, con
 void orc_oz2_residues16(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
                         const int* m, int16_t* planes);
 // A18: the residues split into digit planes (modslice_digit.cpp:195-218, sparse_fix.h:53-73):
-// per modulus s with digit radix q[s] and mode xmode[s] (0 rounded, 1 Karatsuba, 2 sparse square),
+// per modulus s with digit radix q[s] and mode xmode[s] (0 rounded, 1 Karatsuba, 2 sparse square,
+// 3 one digit: the residue itself, one plane),
 // planes l, h (and s = h + l for Karatsuba) as int8 values, planes[p][r][c], moduli in order.
 void orc_oz2_digit_planes(const double* X, int rows, int cols, int ld, int mode, const int32_t* delta, int nd, int S,
                           const int* m, const int* q, const int* xmode, int8_t* planes);

@@ -346,16 +346,18 @@ def plan2(a, b, M: int, N: int, K: int, fmt: Format = Format.INT8, max_moduli: i
 
 
 def plan2_fp8_device(a, b, M: int, N: int, K: int, max_moduli: int = 0,
-                     reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0):
-    """Device descriptors of the Scheme II FP8 plan: (DigitDesc, GroupsDesc, CrtDesc, term moduli)."""
+                     reconstruction: Reconstruction = Reconstruction.Automatic, fixed_bits: int = 0,
+                     execution_set: bool = False):
+    """Device descriptors of the Scheme II FP8 plan: (DigitDesc, GroupsDesc, CrtDesc, term moduli), for the
+    route's own set, or with execution_set for the set the public call computes with."""
     from .device import CrtDesc, DigitDesc, GroupsDesc, OZ2_MAXOUT
     a, b = _f64(a), _f64(b)
     dd, gd, crt = DigitDesc(), GroupsDesc(), CrtDesc()
     tm = (ctypes.c_ubyte * OZ2_MAXOUT)()
     err = ctypes.create_string_buffer(2048)
     _raise(host().ozt_plan2_fp8_device(_ptr(a), _ptr(b), M, N, K, max_moduli, int(reconstruction), fixed_bits,
-                                       ctypes.byref(dd), ctypes.byref(gd), ctypes.byref(crt), tm, err,
-                                       ctypes.c_size_t(2048)), err)
+                                       int(bool(execution_set)), ctypes.byref(dd), ctypes.byref(gd), ctypes.byref(crt),
+                                       tm, err, ctypes.c_size_t(2048)), err)
     return dd, gd, crt, [tm[i] for i in range(gd.nout)]
 
 

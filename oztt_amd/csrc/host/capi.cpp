@@ -295,16 +295,18 @@ int ozt_plan_scheme2(const double* A, const double* B, unsigned M, unsigned N, u
 }
 
 // The device descriptors of a Scheme II FP8 plan on the FP8 matrix cores (digit split, product outputs,
-// CRT, term moduli), for the route's own set (the window K 2^(2b), as the reference plans it).
+// CRT, term moduli): for the route's own set (the window K 2^(2b), as the reference plans it), or with
+// execution_set for the set the public call computes with (the operands' window, fewest products).
 int ozt_plan2_fp8_device(const double* A, const double* B, unsigned M, unsigned N, unsigned K, unsigned max_moduli,
-                         int recon, unsigned fixed_b, oz2_digit_dev* dd, oz2_groups_dev* gd, oz2_crt_dev* crt,
-                         unsigned char* term_modulus, char* err, std::size_t errlen) {
+                         int recon, unsigned fixed_b, int execution_set, oz2_digit_dev* dd, oz2_groups_dev* gd,
+                         oz2_crt_dev* crt, unsigned char* term_modulus, char* err, std::size_t errlen) {
     return guarded(err, errlen, [&] {
         std::optional<unsigned> fb;
         if (fixed_b) fb = fixed_b;
         const auto p = ozTTgemm::detail::plan_scheme2(A, B, M, N, K, ozTTgemm::Format::FP8, max_moduli,
                                                         static_cast<ozTTgemm::Reconstruction>(recon), fb, false,
-                                                        false);
+                                                        execution_set != 0);
+        if (!p.fp8_digits) throw std::runtime_error("the FP8 plan does not run on FP8 digits");
         *crt = ozTTgemm::detail::crt_descriptor(p);
         *dd = ozTTgemm::detail::digit_descriptor(p);
         std::vector<unsigned char> tm;

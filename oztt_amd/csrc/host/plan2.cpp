@@ -326,27 +326,42 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
     // <= (2^b rA + 2 sqrt K)(2^b rB + 2 sqrt K), where rA, rB <= sqrt K, and far below it unless rows
     // or columns are flat. Any set of moduli whose product exceeds twice that recovers the same exact
     // C', so when a smaller set covers it, that set computes (C is bit for bit the same): fewer INT8
-    // moduli, or on the FP8 route a set of fewer digit products (chosen by the route's own rules for
-    // that window, as the reference's research planner did with windows measured from its inputs).
+    // moduli, or on the FP8 route a set of fewer digit products. On the FP8 route the set with the
+    // fewest digit products for the window is searched for too (choose_moduli_fp8_fewest: it also
+    // takes moduli of at most 33, whose residues are e4m3 digits themselves, one product each, which
+    // the reference's FP8 route leaves out), with the reference's window when the operands were not
+    // measured.
+    const double logK = std::log2((double)K);
+    double w = logK;
     if (p.stats.measured) {
         const double sk = std::ldexp(2.0 * std::sqrt((double)K) * (1.0 + 0x1p-50), -p.b);
-        const double w = std::log2(p.stats.rA + sk) + std::log2(p.stats.rB + sk) + 1e-12;
-        p.bound_log2 = 2.0 * p.b + w;
-        if (operand_window && w < std::log2((double)K)) {
-            if (!p.fp8_digits) {
-                ModuliSet t = choose_moduli_int8(K, kMaxModuli, p.b, w);
-                if (t.ok && t.b == p.b && t.m.size() < p.mo.m.size()) {
-                    p.S_window = (int)p.mo.m.size();
-                    p.mo = std::move(t);
-                }
-            } else {
-                ModuliSet t = choose_moduli_digits(Format::FP8, M, N, K, (int)p.S_req, p.b, w);
-                if (t.ok && t.b == p.b && t.nprod < p.mo.nprod && t.nplane <= OZ2_MAXPLANES &&
-                    t.nout <= OZ2_MAXOUT) {
-                    p.S_window = (int)p.mo.m.size();
-                    p.mo = std::move(t);
-                }
+        const double wb = std::log2(p.stats.rA + sk) + std::log2(p.stats.rB + sk) + 1e-12;
+        p.bound_log2 = 2.0 * p.b + wb;
+        w = std::min(wb, logK);
+    }
+    if (operand_window) {
+        auto take = [&](ModuliSet&& t, bool fewer) {
+            if (t.ok && t.b == p.b && fewer) {
+                if (!p.S_window) p.S_window = (int)p.mo.m.size();
+                p.mo = std::move(t);
             }
+        };
+        if (!p.fp8_digits) {
+            if (w < logK) {
+                ModuliSet t = choose_moduli_int8(K, kMaxModuli, p.b, w);
+                const bool fewer = t.m.size() < p.mo.m.size();
+                take(std::move(t), fewer);
+            }
+        } else {
+            auto fits = [](const ModuliSet& t) { return t.nplane <= OZ2_MAXPLANES && t.nout <= OZ2_MAXOUT; };
+            if (w < logK) {
+                ModuliSet t = choose_moduli_digits(Format::FP8, M, N, K, (int)p.S_req, p.b, w);
+                const bool fewer = t.nprod < p.mo.nprod && fits(t);
+                take(std::move(t), fewer);
+            }
+            ModuliSet t = choose_moduli_fp8_fewest(K, (int)p.S_req, p.b, w);
+            const bool fewer = t.nprod < p.mo.nprod && fits(t);
+            take(std::move(t), fewer);
         }
     }
     p.S = (int)p.mo.m.size();
@@ -437,8 +452,8 @@ oz2_digit_dev digit_descriptor(const Plan2& p) {
     for (int s = 0; s < p.S; s++) {
         const int mode = p.mo.mode[s];
         // digit-making modes of the slicer (split.hpp:218-227 oz2_xmode): rounded digits for the square
-        // and wide methods, Karatsuba, sparse square
-        d.xmode[s] = mode == kSplitKar ? 1 : (mode == kSplitSqs ? 2 : 0);
+        // and wide methods, Karatsuba, sparse square, and the residue itself for a one-digit modulus
+        d.xmode[s] = mode == kSplitKar ? 1 : (mode == kSplitSqs ? 2 : (mode == kSplitOne ? 3 : 0));
         d.q[s] = (float)p.mo.q[s];
         d.qinv[s] = 1.0f / (float)p.mo.q[s];  // stages.hpp:223
     }

@@ -118,6 +118,13 @@ ModuliSet choose_moduli_int8(std::uint32_t K, int num_moduli, int b_cap,
 // planner that wrote the reference's accuracy logs, which measured the window from the input).
 ModuliSet choose_moduli_digits(Format format, std::uint32_t M, std::uint32_t N, std::uint32_t K, int num_moduli,
                                int b_cap, double window_log2 = std::numeric_limits<double>::quiet_NaN());
+// The FP8 set of fewest e4m3 digit products (at most num_moduli moduli) whose M exceeds 2^(2b + 1 +
+// window_log2): every subset of one-digit moduli (residues of at most 16 in magnitude, the digit
+// itself, one product; the reference's FP8 route does not use them), filled with the route's squares,
+// Karatsuba and wide moduli in order of bits per product, then checked and laid out as
+// choose_moduli_digits lays out its sets (exact FP32 accumulation, outputs, planes). Not the
+// reference's selection: an execution set that gives the same C as the route's (the exact CRT).
+ModuliSet choose_moduli_fp8_fewest(std::uint32_t K, int num_moduli, int b, double window_log2);
 // The limit on the number of moduli of a format's route when the caller fixes the width b and gives
 // no max_moduli (Oz2Route::def_s: 16 for INT8, 14 for FP8, 11 for TF32, 24 otherwise).
 std::uint32_t default_moduli(Format format);

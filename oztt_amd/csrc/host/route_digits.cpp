@@ -831,69 +831,12 @@ void reselect_tail(std::vector<int>& m, double& logM, double need, std::uint32_t
 
 std::uint32_t default_moduli(Format format) { return format == Format::INT8 ? 16u : route_of(format).def_s; }
 
-ModuliSet choose_moduli_digits(Format format, std::uint32_t M, std::uint32_t N, std::uint32_t K, int num_moduli,
-                               int b_cap, double window_log2) {
-    const Route& rt = route_of(format);
-    ModuliSet o;
-    o.digits = true;
-    Shape S{rt.dmax, rt.nrdig, rt.smax, rt.one};
-    int cap = rt.mod_cap;
-    const double W = std::isnan(window_log2) ? std::log2((double)K) : window_log2;
-    // sparse digits only while K smax^2 + the cap stays within 2^24 (moduli.hpp:724-731)
-    if (S.smax && S.dmax && (double)K * S.smax * S.smax + cap > kExact24) {
-        S.smax = 0;
-        cap = std::min(cap, (2 * S.dmax + 1) * (2 * S.dmax + 1));
-    }
-    o.sparse = S.smax != 0;
-    // candidate table (moduli.hpp:246-261)
-    const int* tb;
-    int ntb;
-    if (S.n > 2) {
-        tb = kTableB2;
-        ntb = (int)std::size(kTableB2);
-    } else if (S.smax) {
-        tb = kTableF8S;
-        ntb = (int)std::size(kTableF8S);
-    } else if (S.dmax > 16) {
-        tb = kTableB8;
-        ntb = (int)std::size(kTableB8);
-    } else if (S.dmax < 16) {
-        tb = kTableB4;
-        ntb = (int)std::size(kTableB4);
-    } else {
-        tb = kTableF8;
-        ntb = (int)std::size(kTableF8);
-    }
-    // initial candidates: the model's set for the window of b_cap, else the table (moduli.hpp:267-300)
-    double logM = 0.0;
-    if (rt.model) {
-        const double need_model = 2.0 * std::min(b_cap, kMaxDigits * kDigitBits) + 1.0 + W + kWinEps;
-        o.m = model_choose(M, N, K, rt.model, cap, S, need_model, std::min(num_moduli, kMaxModuli));
-        o.model_set = !o.m.empty();
-        for (int mm : o.m) logM += std::log2((double)mm);
-    }
-    if (!o.model_set)
-        for (int t = 0; t < ntb && (int)o.m.size() < num_moduli; ++t) {
-            const int mm = tb[t];
-            if (mm > cap || !usable(mm, S)) continue;
-            o.m.push_back(mm);
-            logM += std::log2((double)mm);
-        }
-    o.m_cap = cap;
-    o.ncand = (int)o.m.size();
-    // width from the window |C'| <= K 2^(2b) < M/2 (moduli.hpp:314-318)
-    o.b = std::min(std::min((int)std::floor((logM - 1.0 - W - kWinEps) / 2.0), kMaxDigits * kDigitBits), b_cap);
-    const double need = 2.0 * o.b + 1.0 + W + kWinEps;
-    // a table set drops surplus moduli from the end and reselects its last two; a model set is kept
-    if (!o.model_set) {
-        while (o.m.size() > 2) {
-            const double l2 = std::log2((double)o.m.back());
-            if (logM - l2 < need) break;
-            o.m.pop_back();
-            logM -= l2;
-        }
-        reselect_tail(o.m, logM, need, K, cap, S);
-    }
+// The checks and the layout of a selected set (moduli.hpp:472-606): pairwise coprimality and the
+// window, the exact FP32 accumulation of the digit products, the concatenation bounds and the
+// composition conditions, then the carrying method, digit radix, planes and (FP8) product outputs of
+// every modulus. o.m and o.b are set; o.ok is false when a condition fails.
+static void finish_set(ModuliSet& o, Format format, std::uint32_t K, const Shape& S, int num_moduli, double logM,
+                       double need) {
     o.log2M = logM;
     const int s = (int)o.m.size();
     o.ok = (logM >= need) && s > 0 && s <= kMaxModuli && s <= num_moduli && o.b > 0;
@@ -992,7 +935,157 @@ ModuliSet choose_moduli_digits(Format format, std::uint32_t M, std::uint32_t N, 
         o.nplane += np;
         o.nout += ng;
     }
+}
+
+ModuliSet choose_moduli_digits(Format format, std::uint32_t M, std::uint32_t N, std::uint32_t K, int num_moduli,
+                               int b_cap, double window_log2) {
+    const Route& rt = route_of(format);
+    ModuliSet o;
+    o.digits = true;
+    Shape S{rt.dmax, rt.nrdig, rt.smax, rt.one};
+    int cap = rt.mod_cap;
+    const double W = std::isnan(window_log2) ? std::log2((double)K) : window_log2;
+    // sparse digits only while K smax^2 + the cap stays within 2^24 (moduli.hpp:724-731)
+    if (S.smax && S.dmax && (double)K * S.smax * S.smax + cap > kExact24) {
+        S.smax = 0;
+        cap = std::min(cap, (2 * S.dmax + 1) * (2 * S.dmax + 1));
+    }
+    o.sparse = S.smax != 0;
+    // candidate table (moduli.hpp:246-261)
+    const int* tb;
+    int ntb;
+    if (S.n > 2) {
+        tb = kTableB2;
+        ntb = (int)std::size(kTableB2);
+    } else if (S.smax) {
+        tb = kTableF8S;
+        ntb = (int)std::size(kTableF8S);
+    } else if (S.dmax > 16) {
+        tb = kTableB8;
+        ntb = (int)std::size(kTableB8);
+    } else if (S.dmax < 16) {
+        tb = kTableB4;
+        ntb = (int)std::size(kTableB4);
+    } else {
+        tb = kTableF8;
+        ntb = (int)std::size(kTableF8);
+    }
+    // initial candidates: the model's set for the window of b_cap, else the table (moduli.hpp:267-300)
+    double logM = 0.0;
+    if (rt.model) {
+        const double need_model = 2.0 * std::min(b_cap, kMaxDigits * kDigitBits) + 1.0 + W + kWinEps;
+        o.m = model_choose(M, N, K, rt.model, cap, S, need_model, std::min(num_moduli, kMaxModuli));
+        o.model_set = !o.m.empty();
+        for (int mm : o.m) logM += std::log2((double)mm);
+    }
+    if (!o.model_set)
+        for (int t = 0; t < ntb && (int)o.m.size() < num_moduli; ++t) {
+            const int mm = tb[t];
+            if (mm > cap || !usable(mm, S)) continue;
+            o.m.push_back(mm);
+            logM += std::log2((double)mm);
+        }
+    o.m_cap = cap;
+    o.ncand = (int)o.m.size();
+    // width from the window |C'| <= K 2^(2b) < M/2 (moduli.hpp:314-318)
+    o.b = std::min(std::min((int)std::floor((logM - 1.0 - W - kWinEps) / 2.0), kMaxDigits * kDigitBits), b_cap);
+    const double need = 2.0 * o.b + 1.0 + W + kWinEps;
+    // a table set drops surplus moduli from the end and reselects its last two; a model set is kept
+    if (!o.model_set) {
+        while (o.m.size() > 2) {
+            const double l2 = std::log2((double)o.m.back());
+            if (logM - l2 < need) break;
+            o.m.pop_back();
+            logM -= l2;
+        }
+        reselect_tail(o.m, logM, need, K, cap, S);
+    }
+    finish_set(o, format, K, S, num_moduli, logM, need);
     return o;
+}
+
+ModuliSet choose_moduli_fp8_fewest(std::uint32_t K, int num_moduli, int b, double window_log2) {
+    // The FP8 route's digit shape at this K (the dense fallback of choose_moduli_digits included), with
+    // moduli whose residues are e4m3 digits themselves (|r| <= 16: one plane, one product) allowed.
+    const Route& rt = kRouteFp8;
+    Shape S{rt.dmax, rt.nrdig, rt.smax, true};
+    int cap = rt.mod_cap;
+    if (S.smax && S.dmax && (double)K * S.smax * S.smax + cap > kExact24) {
+        S.smax = 0;
+        cap = std::min(cap, (2 * S.dmax + 1) * (2 * S.dmax + 1));
+    }
+    const double need = 2.0 * b + 1.0 + window_log2 + kWinEps;
+    struct Cand {
+        int m, prods;
+        double bits;
+    };
+    // one-digit moduli: the largest one-digit power of each small prime; the others by bits per product
+    std::vector<Cand> one, multi;
+    for (int m = cap; m >= 2; --m) {
+        if (!usable(m, S)) continue;
+        const Cand c{m, digit_prods(m, S), std::log2((double)m)};
+        if (split_mode(m, S, true) != kSplitOne) {
+            multi.push_back(c);
+            continue;
+        }
+        int pf[4];
+        if (distinct_primes(m, pf) != 1) continue;
+        bool largest = true;  // no larger one-digit power of the same prime
+        for (const Cand& x : one) largest = largest && std::gcd(x.m, m) == 1;
+        if (largest) one.push_back(c);
+    }
+    std::stable_sort(multi.begin(), multi.end(),
+                     [](const Cand& x, const Cand& y) { return x.bits / x.prods > y.bits / y.prods; });
+    // every subset of the one-digit moduli, filled up to the window with the others in that order;
+    // the sets in order of fewest products, then fewest moduli, then widest
+    struct Sol {
+        int prods;
+        double bits;
+        std::vector<int> m;
+    };
+    std::vector<Sol> sols;
+    const int n1 = (int)one.size();
+    for (unsigned mask = 0; mask < (1u << n1); ++mask) {
+        Sol x{0, 0.0, {}};
+        for (int i = 0; i < n1; ++i)
+            if (mask >> i & 1) {
+                x.m.push_back(one[i].m);
+                x.prods += one[i].prods;
+                x.bits += one[i].bits;
+            }
+        for (const Cand& c : multi) {
+            if (x.bits >= need || (int)x.m.size() >= std::min(num_moduli, kMaxModuli)) break;
+            bool cop = true;
+            for (int v : x.m) cop = cop && std::gcd(v, c.m) == 1;
+            if (!cop) continue;
+            x.m.push_back(c.m);
+            x.prods += c.prods;
+            x.bits += c.bits;
+        }
+        if (x.bits >= need) sols.push_back(std::move(x));
+    }
+    std::stable_sort(sols.begin(), sols.end(), [](const Sol& x, const Sol& y) {
+        if (x.prods != y.prods) return x.prods < y.prods;
+        if (x.m.size() != y.m.size()) return x.m.size() < y.m.size();
+        return x.bits > y.bits;
+    });
+    ModuliSet best;
+    for (std::size_t t = 0; t < sols.size() && t < 64; ++t) {
+        ModuliSet o;
+        o.digits = true;
+        o.sparse = S.smax != 0;
+        o.m = sols[t].m;
+        std::sort(o.m.begin(), o.m.end(), std::greater<int>());
+        o.m_cap = cap;
+        o.ncand = (int)(one.size() + multi.size());
+        o.b = b;
+        double logM = 0.0;
+        for (int mm : o.m) logM += std::log2((double)mm);
+        finish_set(o, Format::FP8, K, S, num_moduli, logM, need);
+        if (o.ok && o.nplane <= OZ2_MAXPLANES && o.nout <= OZ2_MAXOUT) return o;
+        if (t == 0) best = std::move(o);
+    }
+    return best;
 }
 
 }  // namespace ozTTgemm::detail

@@ -8,8 +8,10 @@
 //   sparse square (q odd): the rounded digits, then an odd digit with |.| >= 17 is moved by q
 //     (l -= sgn(l) q with h += sgn(l); then h -= sgn(h) q), so both are in {|x| <= 16} or even <= 32;
 //   Karatsuba (radix q = 16): h = Rnd((r + sgn(r)(q/2 - 1/2)) * qinv), l = r - q*h, s = h + l,
-//     sgn(r) read from the sign bit.
-// Planes per modulus in this order: l, h (and s for Karatsuba); the moduli follow each other.
+//     sgn(r) read from the sign bit;
+//   one digit (m <= 33, |r| <= 16; split.hpp:202-205, modslice_digit.cpp:76-79): the residue itself.
+// Planes per modulus in this order: l, h (and s for Karatsuba), or r alone; the moduli follow each
+// other.
 // Every step is one binary32 operation as in the reference (no contraction), so the digits equal
 // the reference's bit for bit; they are integers of magnitude <= 32.
 //
@@ -28,7 +30,9 @@
 
 namespace {
 
-constexpr int XM_ROUND = 0, XM_KAR = 1, XM_SPARSE = 2;
+constexpr int XM_ROUND = 0, XM_KAR = 1, XM_SPARSE = 2, XM_ONE = 3;
+
+__host__ __device__ constexpr int planes_of(int xm) { return xm == XM_KAR ? 3 : (xm == XM_ONE ? 1 : 2); }
 
 struct DigitConsts {
     SplitConsts k;
@@ -69,6 +73,17 @@ struct DigitGen {
             const int xm = k.xmode[s];
             const float q = k.q[s], qinv = k.qinv[s];
             float l[16], h[16], t[16];
+            if (xm == XM_ONE) {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 16; e++) l[e] = residue_f<ND>(st[e].dig, k.k, s);
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    w[c] = digit_bytes<E4M3>(l[4 * c], l[4 * c + 1], l[4 * c + 2], l[4 * c + 3]);
+                emit(p, w);
+                p += 1;
+                continue;
+            }
             if (xm == XM_KAR) {
                 const float half = q * 0.5f - 0.5f;
 #pragma unroll
@@ -162,7 +177,8 @@ const char* digit_consts(const oz2_digit_dev* dd, DigitConsts& k, int& np) {
     for (int s = 0; s < dd->mo.S; s++) {
         const float m = dd->mo.m[s], q = dd->q[s];
         const int xm = dd->xmode[s];
-        if (!(m >= 2.0f && m <= 2401.0f) || xm < XM_ROUND || xm > XM_SPARSE || !(q >= 2.0f && q <= 64.0f))
+        if (!(m >= 2.0f && m <= 2401.0f) || xm < XM_ROUND || xm > XM_ONE ||
+            (xm == XM_ONE ? !(m <= 33.0f) : !(q >= 2.0f && q <= 64.0f)))
             return "a modulus, radix or split mode is not supported";
         k.k.m[s] = m;
         k.k.rinv[s] = dd->mo.rinv[s];
@@ -170,7 +186,7 @@ const char* digit_consts(const oz2_digit_dev* dd, DigitConsts& k, int& np) {
         k.q[s] = q;
         k.qinv[s] = dd->qinv[s];
         k.xmode[s] = xm;
-        np += xm == XM_KAR ? 3 : 2;
+        np += planes_of(xm);
         if (np > OZ2_MAXPLANES) return "more digit planes than OZ2_MAXPLANES";
     }
     return nullptr;
@@ -197,7 +213,7 @@ int launch_digits_pair(oz_dev* dev, const double* A, int M, int K, int lda, cons
 extern "C" int oz2_digit_planes(const oz2_digit_dev* dd) {
     if (!dd || dd->mo.S < 1 || dd->mo.S > OZ2_MAXS) return -1;
     int n = 0;
-    for (int s = 0; s < dd->mo.S; s++) n += dd->xmode[s] == XM_KAR ? 3 : 2;
+    for (int s = 0; s < dd->mo.S; s++) n += planes_of(dd->xmode[s]);
     return n;
 }
 

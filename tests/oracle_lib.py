@@ -93,7 +93,7 @@ class Oracle:
         m = np.array(moduli, dtype=np.int32)
         qa = np.array(q, dtype=np.int32)
         xa = np.array(xmode, dtype=np.int32)
-        n = int(sum(3 if x == 1 else 2 for x in xmode))
+        n = int(sum(3 if x == 1 else (1 if x == 3 else 2) for x in xmode))
         out = np.empty((n, rows, cols), dtype=np.int8)
         self.lib.orc_oz2_digit_planes(P(X), rows, cols, cols, mode, P(np.ascontiguousarray(delta, np.int32)), nd,
                                       len(moduli), P(m), P(qa), P(xa), P(out))

@@ -19,7 +19,12 @@ from oztt_amd.device import E4M3, from_blocks
 from tests.oracle_chains import oz2_chain
 from tests.oracle_lib import assert_residues
 
+
 pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(f"[fp8] {msg}", flush=True)
 
 
 @pytest.fixture(scope="module")
@@ -82,14 +87,14 @@ def test_fp8_wide_range_auto(ctx, oracle, n):
     assert np.all(np.abs(got - q) <= absab * n * 2.0 ** -53)
 
 
-def run_fp8_stages(dev, a, b, n, max_moduli=0, fixed_bits=0, one_pass=True, m=None, k=None):
+def run_fp8_stages(dev, a, b, n, max_moduli=0, fixed_bits=0, one_pass=True, m=None, k=None, execution_set=False):
     """scale -> digit planes -> product outputs (int32 and uint16 terms) -> CRT on the GPU, for
     A (m x k) and B (k x n) (m = k = n unless given)."""
     m = n if m is None else m
     k = n if k is None else k
     rec = oz.Reconstruction.OnePass if one_pass else oz.Reconstruction.Automatic
     dd, gd, crt, tm = oz.plan2_fp8_device(a, b, m, n, k, max_moduli=max_moduli, reconstruction=rec,
-                                          fixed_bits=fixed_bits)
+                                          fixed_bits=fixed_bits, execution_set=execution_set)
     nd, b_ = dd.mo.nd, crt.b
     shift = b_ - 20 * (nd - 1)
     Mg, Ng = -(-m // 256) * 256, -(-n // 256) * 256
@@ -188,6 +193,26 @@ def test_split_digits_pair_equals_single_splits(dev, m, n, k, encoding):
     np.testing.assert_array_equal(got[0], got[2])
     np.testing.assert_array_equal(got[1], got[3])
     assert got[0].any() and got[1].any()
+
+
+@pytest.mark.parametrize("k,phi", [(16384, 2.0), (4096, 0.5)])
+def test_fp8_stages_fewest_products_set(dev, oracle, k, phi):
+    """The FP8 set the public call computes with (the operands' window, fewest digit products): moduli
+    of at most 33 carried as one digit (the residue itself, one plane and one product) next to the
+    route's squares, Karatsuba and (K = 4096) sparse squares; every stage equals the oracle, and C the
+    oracle's chain with the route's own set."""
+    m = n = 64
+    a, b = oz.eval_inputs(4, phi, m * k, k * n)
+    p = oz.plan2(a, b, m, n, k, oz.Format.FP8)
+    r = run_fp8_stages(dev, a, b, n, one_pass=False, m=m, k=k, execution_set=True)
+    S = r["dd"].mo.S
+    xm = [int(r["dd"].xmode[s]) for s in range(S)]
+    log(f"K {k}: {S} moduli, modes {xm}, {p.nprod} products against the route's {p.rnprod}")
+    assert S == p.S and 3 in xm and p.nprod < p.rnprod
+    assert all(int(r["crt"].m[s]) <= 33 for s in range(S) if xm[s] == 3)
+    check_fp8_chain(oracle, r, a, b, n)
+    want = oz2_chain(oracle, a.reshape(m, k), b.reshape(k, n), [p.rm[i] for i in range(p.rS)], p.b, p.nd)
+    np.testing.assert_array_equal(r["out"].reshape(m, n).view(np.uint64), want.view(np.uint64))
 
 
 def test_fp8_stages_quick_case_reference_hash(dev, oracle):

@@ -117,3 +117,23 @@ def test_window_bound_is_not_used_without_measured_operands():
     p = oz.plan2(a, b, M, N, K, oz.Format.INT8, fixed_bits=54, reconstruction=oz.Reconstruction.OnePass)
     assert math.isinf(p.bound_log2) and p.S_window == 0 and p.S == p.rS
 
+
+
+def test_fp8_fewest_products_set(oracle):
+    """On the FP8 route the execution set is the one of fewest e4m3 digit products for the window: at C4's
+    K = 16384 (phi 2) it mixes one-digit moduli (at most 33, residue = digit) with the route's squares and
+    Karatsuba moduli; it is pairwise coprime, covers twice the bound, and the oracle's chain gives the same
+    C from it as from the route's own set."""
+    M = N = 16
+    K = 16384
+    a, b = oz.eval_inputs(4, 2.0, M * K, K * N)
+    A, B = a.reshape(M, K), b.reshape(K, N)
+    p = oz.plan2(A, B, M, N, K, oz.Format.FP8)
+    ms = [p.m[i] for i in range(p.S)]
+    assert p.fp8_digits and p.S_window == p.rS and p.nprod < p.rnprod
+    assert all(math.gcd(x, y) == 1 for i, x in enumerate(ms) for y in ms[i + 1:])
+    assert any(x <= 33 for x in ms) and p.log2M > p.bound_log2 + 1.0
+    assert abs(sum(math.log2(x) for x in ms) - p.log2M) < 1e-9
+    c_small = oz2_chain(oracle, A, B, ms, p.b, p.nd)
+    c_full = oz2_chain(oracle, A, B, [p.rm[i] for i in range(p.rS)], p.b, p.nd)
+    np.testing.assert_array_equal(c_small.view(np.uint64), c_full.view(np.uint64))

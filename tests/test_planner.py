@@ -228,12 +228,15 @@ def test_fp8_auto_precision_records(phi, b, S):
     research = oz.choose_moduli_fp8(n, 24, b, wlog2)
     assert research.b == b and research.rS == S
     # by default the execution set is an FP8 set (its e4m3 digits on the FP8 matrix cores): the route's
-    # with the full window, else the set for the operands' window, of the research set's size
+    # with the full window; else the route's rules for the operands' window give a set of the research
+    # set's size, and the execution set has at most its digit products (one-digit moduli included)
     full = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass, full_window=True)
     assert full.fp8_digits and full.S_window == 0
     assert [full.m[i] for i in range(full.S)] == [p.rm[i] for i in range(p.rS)]
-    assert p.fp8_digits and p.S == S and (p.S_window or p.S) == p.rS and p.nprod <= p.rnprod
     assert math.log2(p.wA * p.wB) <= p.bound_log2 - 2 * b <= math.log2(n)
+    own = oz.choose_moduli_fp8(n, 24, b, p.bound_log2 - 2 * b)
+    assert own.b == b and own.rS == S
+    assert p.fp8_digits and (p.S_window or p.S) == p.rS and p.nprod <= own.rnprod <= p.rnprod
     q = oz.plan2(a, bb, n, n, n, oz.Format.FP8, reconstruction=oz.Reconstruction.TwoPass,
                  transport=oz.Transport.Int8Residues)
     assert not q.fp8_digits and q.b == b and max(q.m[i] for i in range(q.S)) <= 255
