@@ -252,8 +252,8 @@ int oz2_split_digits_pair(oz_dev* dev, const double* A, int M, int K, int lda, c
 /* ---- A18 products + composition (reference ozaki2.cpp:228-285 run_digit_modulus, compose.cpp,
  * split.hpp:541-661 product terms and groups) ------------------------------------------------
  * Output o sums npairs digit products over the full K on the FP8 matrix cores (e4m3 x e4m3,
- * FP32 accumulation; exact while the sum stays below 2^24, which `bound` states and the entry
- * point checks):  P_o = sum_t A[a[t]] * Bt[b[t]]^T  (the reference's concatenation along K).
+ * FP32 accumulation; exact while |sum| <= bound <= 2^24, which the entry point checks: every
+ * partial sum is then an integer that FP32 holds):  P_o = sum_t A[a[t]] * Bt[b[t]]^T  (the reference's concatenation along K).
  * out_kind 0 stores P_o as int32 (M x N per output, element strides, out 16-byte aligned and ldo,
  * strideO multiples of 4); out_kind 1 stores the CRT
  * term w_o = (coef * P_o) mod m as uint16 in [0, m] (m standing for 0), where coef is the composition coefficient

@@ -834,9 +834,12 @@ std::uint32_t default_moduli(Format format) { return format == Format::INT8 ? 16
 // The checks and the layout of a selected set (moduli.hpp:472-606): pairwise coprimality and the
 // window, the exact FP32 accumulation of the digit products, the concatenation bounds and the
 // composition conditions, then the carrying method, digit radix, planes and (FP8) product outputs of
-// every modulus. o.m and o.b are set; o.ok is false when a condition fails.
+// every modulus. o.m and o.b are set; o.ok is false when a condition fails. fp64_terms: the set runs
+// on this build's FP8 kernel, whose epilogue reduces every output exactly in FP64 (no FP32
+// composition stage): an output needs only |P_o| <= 2^24 (exact FP32 sums), without the reference's
+// margin of a modulus for its FP32 composition and without its composition-sum conditions.
 static void finish_set(ModuliSet& o, Format format, std::uint32_t K, const Shape& S, int num_moduli, double logM,
-                       double need) {
+                       double need, bool fp64_terms = false) {
     o.log2M = logM;
     const int s = (int)o.m.size();
     o.ok = (logM >= need) && s > 0 && s <= kMaxModuli && s <= num_moduli && o.b > 0;
@@ -860,7 +863,7 @@ static void finish_set(ModuliSet& o, Format format, std::uint32_t K, const Shape
         for (int mm : o.m)
             if (split_mode(mm, S, true) == kSplitOne) {
                 const double R = (double)resid_bound(mm);
-                if ((double)K * R * R + mm > kExact24)
+                if ((double)K * R * R + (fp64_terms ? 0 : mm) > kExact24)
                     fail("the one-digit products of modulus " + std::to_string(mm) +
                          " exceed the exact FP32 integers 2^24");
             }
@@ -869,7 +872,7 @@ static void finish_set(ModuliSet& o, Format format, std::uint32_t K, const Shape
     for (int mm : o.m) mmax = std::max(mmax, mm);
     o.maxg_m.assign(s, 1);
     for (int i = 0; i < s; ++i)
-        if (split_mode(o.m[i], S, true) != kSplitOne) o.maxg_m[i] = maxg_for(o.m[i], K, mmax, S);
+        if (split_mode(o.m[i], S, true) != kSplitOne) o.maxg_m[i] = maxg_for(o.m[i], K, fp64_terms ? 0 : mmax, S);
     auto sync = [&] { o.maxg = *std::max_element(o.maxg_m.begin(), o.maxg_m.end()); };
     if (s) sync();
     auto groups = [&](int i, Group* gr) { return product_groups(o.m[i], S, o.maxg_m[i], gr); };
@@ -891,7 +894,27 @@ static void finish_set(ModuliSet& o, Format format, std::uint32_t K, const Shape
         for (int j = 0; j < ng; ++j) g = std::max(g, group_bound(o.m[i], gr[j], (double)K, S));
         return g;
     };
-    for (int attempt = 0; attempt < 2 && s; ++attempt) {
+    if (fp64_terms) {
+        for (int attempt = 0; attempt < 2 && s; ++attempt) {
+            bool grouped_ok = true;
+            for (int i = 0; i < s; ++i) {
+                Group gr[kMaxProd];
+                if (groups(i, gr) == 0) grouped_ok = false;
+            }
+            if (o.maxg > 1 && !grouped_ok) {
+                o.maxg_m.assign(s, 1);
+                sync();
+                continue;
+            }
+            for (int i = 0; i < s; ++i) {
+                Group gr[kMaxProd];
+                if (groups(i, gr) == 0 || gbound(i) > kExact24)
+                    fail("an output of modulus " + std::to_string(o.m[i]) + " exceeds the exact FP32 integers 2^24");
+            }
+            break;
+        }
+    }
+    for (int attempt = 0; attempt < 2 && s && !fp64_terms; ++attempt) {
         bool can_fold = true, grouped_ok = true;
         for (int i = 0; i < s; ++i) {
             Group gr[kMaxProd];
@@ -1005,12 +1028,15 @@ ModuliSet choose_moduli_digits(Format format, std::uint32_t M, std::uint32_t N, 
 }
 
 ModuliSet choose_moduli_fp8_fewest(std::uint32_t K, int num_moduli, int b, double window_log2) {
-    // The FP8 route's digit shape at this K (the dense fallback of choose_moduli_digits included), with
-    // moduli whose residues are e4m3 digits themselves (|r| <= 16: one plane, one product) allowed.
+    // The FP8 route's digit shape at this K, with moduli whose residues are e4m3 digits themselves
+    // (|r| <= 16: one plane, one product) allowed.
     const Route& rt = kRouteFp8;
     Shape S{rt.dmax, rt.nrdig, rt.smax, true};
     int cap = rt.mod_cap;
-    if (S.smax && S.dmax && (double)K * S.smax * S.smax + cap > kExact24) {
+    // sparse digits while their products stay exact FP32 integers (the reference also keeps room for a
+    // modulus, for its FP32 composition, which this build's FP64 epilogue does not need: K = 16384 keeps
+    // them)
+    if (S.smax && S.dmax && (double)K * S.smax * S.smax > kExact24) {
         S.smax = 0;
         cap = std::min(cap, (2 * S.dmax + 1) * (2 * S.dmax + 1));
     }
@@ -1081,7 +1107,7 @@ ModuliSet choose_moduli_fp8_fewest(std::uint32_t K, int num_moduli, int b, doubl
         o.b = b;
         double logM = 0.0;
         for (int mm : o.m) logM += std::log2((double)mm);
-        finish_set(o, Format::FP8, K, S, num_moduli, logM, need);
+        finish_set(o, Format::FP8, K, S, num_moduli, logM, need, true);
         if (o.ok && o.nplane <= OZ2_MAXPLANES && o.nout <= OZ2_MAXOUT) return o;
         if (t == 0) best = std::move(o);
     }

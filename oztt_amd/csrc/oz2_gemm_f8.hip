@@ -3,8 +3,8 @@
 // Semantics (reference ozaki2.cpp:228-285 run_digit_modulus and issue_digit_chunk, compose.cpp:115-153,
 // split.hpp:541-661): output o of modulus s is the sum of npairs digit products over the full K,
 // P_o = sum_t A_{a[t]} B_{b[t]}^T, which the reference obtains by concatenating the planes along K;
-// every P_o is an exact integer below 2^24 (the planner's concatenation bound), so FP32 accumulation
-// is exact and the order of the sums does not matter. The reference then composes the residue
+// every P_o is an exact integer of at most 2^24 in magnitude (the planner's concatenation bound), so
+// FP32 accumulation is exact and the order of the sums does not matter. The reference then composes the residue
 // D_s == sum_o c_o P_o (mod m_s) in FP32 (ModRound first, or a 2^12 split of P_o). Here the epilogue
 // reduces P_o exactly: w_o = (c_o y_s mod m_s) * (P_o mod m_s) mod m_s, so that the terms of modulus
 // s add up to D_s * y_s (mod m_s), the CRT digit of D_s; the reconstruction sums w_o * Q_s
@@ -277,8 +277,10 @@ extern "C" int oz2_gemm_groups_f8(oz_dev* dev, const uint8_t* A, const uint8_t* 
             ga.g[o].a[t] = g.a[t];
             ga.g[o].b[t] = g.b[t];
         }
-        // FP32 accumulation is exact while |P_o| stays below 2^24 (the reference keeps bound + m <= 2^24)
-        if (!(g.bound >= 0.0f) || (double)g.bound + g.m > 16777216.0)
+        // FP32 accumulation is exact while every partial sum is an integer of at most 2^24 in magnitude,
+        // which |P_o| <= bound <= 2^24 ensures; the epilogue reduces P_o in FP64 (the reference keeps
+        // bound + m <= 2^24 for its FP32 composition, which this epilogue replaces)
+        if (!(g.bound >= 0.0f) || (double)g.bound > 16777216.0)
             return oz::fail(dev, OZ_ERR_RANGE, "oz2_gemm_groups_f8: output %d can reach %g, beyond exact FP32", o,
                             (double)g.bound);
         ga.g[o].np_m = ((uint32_t)g.npairs << 16) | g.m;

@@ -20,7 +20,8 @@ oracle.
 
 The FP8 product at its exactness bound: outputs that sum three products of K = 16384 digits +-16
 reach 3 K 16^2 = 12582912, just below 2^24, where FP32 accumulation is still exact
-(split.hpp:676-688; the reference's probe experiments/paper_logs/measure_logs/probe_gemm_exact.log).
+(split.hpp:676-688; the reference's probe experiments/paper_logs/measure_logs/probe_gemm_exact.log);
+and single products of sparse digits up to 32 reach 2^24 itself, which FP32 still holds.
 """
 import numpy as np
 import pytest
@@ -216,6 +217,47 @@ def test_fp8_products_exact_at_the_fp32_bound(dev):
     np.testing.assert_array_equal(P[1], want)
     for o in range(2):
         assert_residues(W[o], (5 + o) * (P[o] % 1089), 1089, f"output {o}")
+
+
+def test_fp8_products_exact_at_2_24(dev):
+    """Sparse e4m3 digits (|d| <= 16, and even up to 32) at K = 16384, one product per output: digits
+    of 32 (e4m3 0x60) reach K 32^2 = 2^24 exactly, the largest integer up to which FP32 holds every
+    integer; random sparse digits with random signs give every smaller sum. The FP8 set of fewest
+    products uses such outputs at C4's K, whose epilogue reduces them in FP64."""
+    M = N = 256
+    K = 16384
+    sparse = np.array([v for v in range(0, 33) if v <= 16 or v % 2 == 0], dtype=np.int64)
+    code = {int(v): int(np.flatnonzero(E4M3 == float(v))[0]) for v in np.concatenate([sparse, -sparse])}
+    rng = np.random.default_rng(12)
+    sa = np.empty((2, M, K), dtype=np.int64)
+    sb = np.empty((2, N, K), dtype=np.int64)
+    sa[0], sb[0] = 32, 32
+    sa[1] = rng.choice(sparse, size=(M, K)) * rng.choice([-1, 1], size=(M, K))
+    sb[1] = rng.choice(sparse, size=(N, K)) * rng.choice([-1, 1], size=(N, K))
+    enc = np.vectorize(lambda v: code[int(v)], otypes=[np.uint8])
+    bA = dev.upload(to_blocks(enc(sa)).ravel())
+    bB = dev.upload(to_blocks(enc(sb)).ravel())
+    gd = GroupsDesc()
+    gd.nout, gd.nplanes = 2, 2
+    for o in range(2):
+        g = gd.g[o]
+        g.npairs, g.modulus, g.m, g.coef = 1, o, 2401, 7 + o
+        g.a[0] = g.b[0] = o
+        g.bound = float(K * 32 * 32)
+    assert gd.g[0].bound == 2.0 ** 24
+    bP, bW = dev.alloc(4 * 2 * M * N), dev.alloc(2 * 2 * M * N)
+    dev.gemm_groups_f8(bA, bB, bP, M, N, K, gd, 0, N, M * K, N * K, M * N)
+    dev.gemm_groups_f8(bA, bB, bW, M, N, K, gd, 1, N, M * K, N * K, M * N)
+    P = dev.download(bP, np.int32, 2 * M * N).reshape(2, M, N).astype(np.int64)
+    W = dev.download(bW, np.uint16, 2 * M * N).reshape(2, M, N).astype(np.int64)
+    for buf in (bA, bB, bP, bW):
+        buf.free()
+    dev.bufs.clear()
+    assert np.all(P[0] == 2 ** 24)
+    want = (sa[1].astype(np.float64) @ sb[1].astype(np.float64).T).astype(np.int64)
+    np.testing.assert_array_equal(P[1], want)
+    for o in range(2):
+        assert_residues(W[o], (7 + o) * (P[o] % 2401), 2401, f"output {o}")
 
 
 AUTO, I8 = oz.Transport.Automatic, oz.Transport.Int8Residues

@@ -237,8 +237,10 @@ def test_fp8_stages_bit_exact(dev, oracle, n, seed, phi, fixed):
 
 
 def test_fp8_gemm_rejects_inexact_bound(dev):
+    """An output bound above 2^24 (the next float, 2^24 + 2) is refused before any launch; 2^24 itself
+    is exact (test_fp8_products_exact_at_2_24)."""
     _, gd, _, _ = oz.plan2_fp8_device(*oz.eval_inputs(7, -1.0, 64 * 64, 64 * 64), 64, 64, 64)
-    gd.g[0].bound = 2.0 ** 24
+    gd.g[0].bound = 2.0 ** 24 + 2.0
     A = dev.alloc(gd.nplanes * 256 * 64)
     P = dev.alloc(4 * gd.nout * 256 * 256)
     with pytest.raises(RuntimeError, match="exact FP32"):
