@@ -329,8 +329,8 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
     // moduli, or on the FP8 route a set of fewer digit products. On the FP8 route the set with the
     // fewest digit products for the window is searched for too (choose_moduli_fp8_fewest: it also
     // takes moduli of at most 33, whose residues are e4m3 digits themselves, one product each, which
-    // the reference's FP8 route leaves out), with the reference's window when the operands were not
-    // measured.
+    // the reference's FP8 route leaves out). Operands that were not measured (a fixed width and pass
+    // count: the evaluator's table) keep the planned set, as the reference computes it.
     const double logK = std::log2((double)K);
     double w = logK;
     if (p.stats.measured) {
@@ -339,7 +339,7 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
         p.bound_log2 = 2.0 * p.b + wb;
         w = std::min(wb, logK);
     }
-    if (operand_window) {
+    if (operand_window && p.stats.measured) {
         auto take = [&](ModuliSet&& t, bool fewer) {
             if (t.ok && t.b == p.b && fewer) {
                 if (!p.S_window) p.S_window = (int)p.mo.m.size();
