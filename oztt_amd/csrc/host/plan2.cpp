@@ -353,13 +353,12 @@ Plan2 plan_scheme2(const double* A, const double* B, std::uint32_t M, std::uint3
                 take(std::move(t), fewer);
             }
         } else {
+            // the fewest-products set, else (when it cannot be formed within the moduli limit) the
+            // route's own rules for the operands' window
             auto fits = [](const ModuliSet& t) { return t.nplane <= OZ2_MAXPLANES && t.nout <= OZ2_MAXOUT; };
-            if (w < logK) {
-                ModuliSet t = choose_moduli_digits(Format::FP8, M, N, K, (int)p.S_req, p.b, w);
-                const bool fewer = t.nprod < p.mo.nprod && fits(t);
-                take(std::move(t), fewer);
-            }
             ModuliSet t = choose_moduli_fp8_fewest(K, (int)p.S_req, p.b, w);
+            if (!(t.ok && t.b == p.b && fits(t)) && w < logK)
+                t = choose_moduli_digits(Format::FP8, M, N, K, (int)p.S_req, p.b, w);
             const bool fewer = t.nprod < p.mo.nprod && fits(t);
             take(std::move(t), fewer);
         }

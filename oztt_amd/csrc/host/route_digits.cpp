@@ -1044,24 +1044,38 @@ ModuliSet choose_moduli_fp8_fewest(std::uint32_t K, int num_moduli, int b, doubl
     struct Cand {
         int m, prods;
         double bits;
+        int np, pf[4];  // distinct prime factors
     };
-    // one-digit moduli: the largest one-digit power of each small prime; the others by bits per product
-    std::vector<Cand> one, multi;
-    for (int m = cap; m >= 2; --m) {
-        if (!usable(m, S)) continue;
-        const Cand c{m, digit_prods(m, S), std::log2((double)m)};
-        if (split_mode(m, S, true) != kSplitOne) {
-            multi.push_back(c);
-            continue;
+    struct Cands {
+        std::vector<Cand> one, multi;
+    };
+    // The candidates depend only on the digit shape, which is one of two (sparse digits or not): built
+    // once each. One-digit moduli: the largest one-digit power of each small prime; the others in
+    // order of bits per product.
+    auto build = [](const Shape& Sh, int cp) {
+        Cands c;
+        for (int m = cp; m >= 2; --m) {
+            if (!usable(m, Sh)) continue;
+            Cand x{m, digit_prods(m, Sh), std::log2((double)m), 0, {0, 0, 0, 0}};
+            x.np = distinct_primes(m, x.pf);
+            if (split_mode(m, Sh, true) != kSplitOne) {
+                c.multi.push_back(x);
+                continue;
+            }
+            if (x.np != 1) continue;
+            bool largest = true;  // no larger one-digit power of the same prime
+            for (const Cand& y : c.one) largest = largest && y.pf[0] != x.pf[0];
+            if (largest) c.one.push_back(x);
         }
-        int pf[4];
-        if (distinct_primes(m, pf) != 1) continue;
-        bool largest = true;  // no larger one-digit power of the same prime
-        for (const Cand& x : one) largest = largest && std::gcd(x.m, m) == 1;
-        if (largest) one.push_back(c);
-    }
-    std::stable_sort(multi.begin(), multi.end(),
-                     [](const Cand& x, const Cand& y) { return x.bits / x.prods > y.bits / y.prods; });
+        std::stable_sort(c.multi.begin(), c.multi.end(),
+                         [](const Cand& x, const Cand& y) { return x.bits / x.prods > y.bits / y.prods; });
+        return c;
+    };
+    static const Cands sparse_cands = build(Shape{rt.dmax, rt.nrdig, rt.smax, true}, rt.mod_cap);
+    static const Cands dense_cands =
+        build(Shape{rt.dmax, rt.nrdig, 0, true}, std::min(rt.mod_cap, (2 * rt.dmax + 1) * (2 * rt.dmax + 1)));
+    const Cands& cands = S.smax ? sparse_cands : dense_cands;
+    const std::vector<Cand>&one = cands.one, &multi = cands.multi;
     // every subset of the one-digit moduli, filled up to the window with the others in that order;
     // the sets in order of fewest products, then fewest moduli, then widest
     struct Sol {
@@ -1071,23 +1085,28 @@ ModuliSet choose_moduli_fp8_fewest(std::uint32_t K, int num_moduli, int b, doubl
     };
     std::vector<Sol> sols;
     const int n1 = (int)one.size();
+    std::vector<char> used(4097, 0);  // primes taken by the set being filled
     for (unsigned mask = 0; mask < (1u << n1); ++mask) {
         Sol x{0, 0.0, {}};
-        for (int i = 0; i < n1; ++i)
-            if (mask >> i & 1) {
-                x.m.push_back(one[i].m);
-                x.prods += one[i].prods;
-                x.bits += one[i].bits;
-            }
-        for (const Cand& c : multi) {
-            if (x.bits >= need || (int)x.m.size() >= std::min(num_moduli, kMaxModuli)) break;
-            bool cop = true;
-            for (int v : x.m) cop = cop && std::gcd(v, c.m) == 1;
-            if (!cop) continue;
+        std::vector<int> taken;
+        auto take = [&](const Cand& c) {
             x.m.push_back(c.m);
             x.prods += c.prods;
             x.bits += c.bits;
+            for (int t = 0; t < c.np; ++t) {
+                used[c.pf[t]] = 1;
+                taken.push_back(c.pf[t]);
+            }
+        };
+        for (int i = 0; i < n1; ++i)
+            if (mask >> i & 1) take(one[i]);
+        for (const Cand& c : multi) {
+            if (x.bits >= need || (int)x.m.size() >= std::min(num_moduli, kMaxModuli)) break;
+            bool cop = true;
+            for (int t = 0; t < c.np; ++t) cop = cop && !used[c.pf[t]];
+            if (cop) take(c);
         }
+        for (int q : taken) used[q] = 0;
         if (x.bits >= need) sols.push_back(std::move(x));
     }
     std::stable_sort(sols.begin(), sols.end(), [](const Sol& x, const Sol& y) {
