@@ -137,3 +137,31 @@ def test_fp8_fewest_products_set(oracle):
     c_small = oz2_chain(oracle, A, B, ms, p.b, p.nd)
     c_full = oz2_chain(oracle, A, B, [p.rm[i] for i in range(p.rS)], p.b, p.nd)
     np.testing.assert_array_equal(c_small.view(np.uint64), c_full.view(np.uint64))
+
+
+def parallel_operands(phi: float, n: int = 64, K: int = 8192, seed: int = 5):
+    """Rows of A and columns of B that are the same heavy-tailed vector v up to signs, A_i = s_i v and
+    B_j = s_j v: C'_ii = ||A'_i||^2 makes Cauchy-Schwarz tight, so max |C'| reaches the bound, while the
+    heavy tail keeps the bound bits below the window K 2^(2b)."""
+    rng = np.random.default_rng(seed)
+    v = (rng.random(K) - 0.5) * np.exp(phi * rng.standard_normal(K))
+    s = rng.choice([-1.0, 1.0], size=(n, K))
+    return s * v, (s * v).T.copy()
+
+
+def test_tight_bound_near_the_smaller_modulus(oracle):
+    """phi 0.5: max |C'| equals the bound to 1/100 bit and lies within 1/8 bit of M/2 of the smaller set
+    that computes (15 moduli where the window needs 16); the oracle's chain gives the same C from that set
+    as from the window's."""
+    A, B = parallel_operands(0.5)
+    n, K = A.shape
+    p = oz.plan2(A, B, n, n, K, oz.Format.INT8)
+    Ai, Bi = exact_operands(oracle, A, B, p.b, p.nd)
+    c = math.log2(max_abs_product(Ai, Bi))
+    assert p.S_window == p.rS > p.S
+    assert c < p.bound_log2 < c + 0.01
+    assert c < p.log2M - 1.0 < c + 0.125
+    ms = [p.m[i] for i in range(p.S)]
+    c_small = oz2_chain(oracle, A, B, ms, p.b, p.nd)
+    c_full = oz2_chain(oracle, A, B, [p.rm[i] for i in range(p.rS)], p.b, p.nd)
+    np.testing.assert_array_equal(c_small.view(np.uint64), c_full.view(np.uint64))
