@@ -96,23 +96,26 @@ def test_resident_calls_keep_the_operand_window(ctx):
         rb.close()
 
 
-@pytest.mark.parametrize("phi", [0.5, 2.0])
-def test_tight_bound_near_the_smaller_modulus(ctx, oracle, phi):
+@pytest.mark.parametrize("fmt,phi,k", [("INT8", 0.5, 8192), ("INT8", 2.0, 8192), ("FP8", 2.0, 16384)])
+def test_tight_bound_near_the_smaller_modulus(ctx, oracle, fmt, phi, k):
     """Rows of A and columns of B parallel up to signs (tests/test_operand_window.py parallel_operands):
-    max |C'| reaches the operands' bound, which at phi 0.5 lies within 1/8 bit of M/2 of the 15 moduli
-    that compute. The public call, the full-window call and the oracle's chain with the reference's 16
-    moduli agree bit for bit."""
+    max |C'| reaches the operands' bound, which for INT8 at phi 0.5 lies within 1/8 bit of M/2 of the 15
+    moduli that compute (16 for the window); on the FP8 route at K = 16384 the set of fewest products
+    (one-digit moduli, sparse digits) computes. The public call, the full-window call and the oracle's
+    chain with the reference's own set agree bit for bit."""
     from tests.test_operand_window import parallel_operands
-    A, B = parallel_operands(phi)
-    n, k = A.shape
-    log(f"parallel rows and columns, phi {phi}")
+    A, B = parallel_operands(phi, K=k)
+    n = A.shape[0]
+    log(f"parallel rows and columns, {fmt}, phi {phi}, K {k}")
     a, b = A.ravel(), B.ravel()
-    opts = oz.Options(scheme=oz.Scheme.II, format=oz.Format.INT8)
-    p = oz.plan2(a, b, n, n, k, oz.Format.INT8)
-    assert p.S_window == p.rS > p.S
+    opts = oz.Options(scheme=oz.Scheme.II, format=oz.Format[fmt])
+    p = oz.plan2(a, b, n, n, k, oz.Format[fmt])
+    full = oz.plan2(a, b, n, n, k, oz.Format[fmt], full_window=True)
+    assert p.S_window == p.rS and p.nprod < full.nprod
     c, info, ev = ctx.evaluate(a, b, n, n, k, opts, warmup=1, repeats=2)
     cf, _, evf = ctx.evaluate(a, b, n, n, k, opts, warmup=1, repeats=2, full_window=True)
-    assert ev.whole_checked and evf.whole_checked and (ev.partial_products, evf.partial_products) == (p.S, p.rS)
+    assert ev.whole_checked and evf.whole_checked
+    assert (ev.partial_products, evf.partial_products) == (p.nprod, full.nprod)
     np.testing.assert_array_equal(c.view(np.uint64), cf.view(np.uint64))
     want = oz2_chain(oracle, A, B, [p.rm[i] for i in range(p.rS)], p.b, p.nd)
     np.testing.assert_array_equal(c.reshape(n, n).view(np.uint64), want.view(np.uint64))
