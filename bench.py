@@ -60,10 +60,10 @@ FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, 5.0 PFLOP/s
 TRAFFIC = {
     # config: (bytes per launch, profile, products per launch of the plan measured)
     "C1": (0.0506e9, "profiles/scheme2_int8_c1_1024_traffic.md", 16),
-    "C2": (4.454e9, "profiles/scheme1_int8_c2_4096_traffic.md", 36),
+    "C2": (4.415e9, "profiles/scheme1_int8_c2_4096_traffic.md", 36),
     "C3": (15.319e9, "profiles/scheme2_int8_c3_8192_traffic.md", 16),
     "C4": (247.123e9, "profiles/scheme2_fp8_c4_16384_traffic.md", 34),
-    "C5": (246.8e9, "profiles/scheme1_bf16_c5_8192x65536_traffic.md", 36),
+    "C5": (248.19e9, "profiles/scheme1_bf16_c5_8192x65536_traffic.md", 36),
 }
 
 
