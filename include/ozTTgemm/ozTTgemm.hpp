@@ -45,6 +45,10 @@ enum class Reconstruction { Automatic, OnePass, TwoPass };
 //     transport: the FP8 and INT8 dense rates are equal, and the FP8 route needs two to three times
 //     the products of INT8 residues for one width. Info.moduli then counts the INT8 moduli that
 //     computed. A width beyond what INT8 residues hold (above about 84 bits) keeps the FP8 digits.
+// Either way the set that computes can be smaller than the plan's: when the operands' own bound on
+// the integer product A'B' (Cauchy-Schwarz on its rows and columns) needs fewer moduli, or on the
+// FP8 digits fewer digit products, than the plan's window K 2^(2b), that set computes; C is the
+// same bit for bit.
 enum class Transport { Automatic, Int8Residues };
 
 // Options of the scheme that is not selected must keep their defaults.
