@@ -11,8 +11,9 @@
 //   orc_oz2_digits/residues       digits.h:44 KAT, ModRound KATs (sfpu_tf_proc.h:271,303,312),
 //                                 residue-class invariants, and end to end by the output hashes
 //   orc_oz2_digit_planes          closed forms (h = round(r/q) or the Karatsuba ceiling, l + q h == r,
-//                                 the sparse-set moves checked against an integer restatement), and end
-//                                 to end by the FP8 output hash (tools/validated/quick.csv:11)
+//                                 the sparse-set moves checked against an integer restatement; a
+//                                 one-digit plane equals orc_oz2_residues), and end to end by the FP8
+//                                 output hash (tools/validated/quick.csv:11)
 //   orc_gemm_i8                   brute force int64 (its own definition)
 //   orc_oz2_crt_ref               reference output hashes (tools/validated/quick.csv:13,
 //                                 phi_sweep.log:116,122)

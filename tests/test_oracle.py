@@ -496,3 +496,26 @@ def test_tf_mul_r_forms_checker_sees_overflow_beyond_the_bound(orc):
     cov = ctypes.c_int64()
     bad = orc.lib.orc_check_tf_mul_r_forms(1, 100000, 9, 14, 0, 30, ctypes.byref(cov))
     assert bad > 0
+
+
+def test_one_digit_planes_are_the_residues(orc):
+    """Mode 3 (one digit, split.hpp:202-205): the single plane of a modulus of at most 33 is the symmetric
+    residue of A' itself, within 16 in magnitude (exact in e4m3), next to the planes of other modes."""
+    n, nd, b = 64, 3, 56
+    a, _ = orc.inputs(4, 2.0, n * n, n * n)
+    X = a.reshape(n, n)
+    shift = b - 20 * (nd - 1)
+    dl, _ = orc.scale(X, n, n, 0, 1, shift)
+    ms, qs, xm = [32, 31, 29, 27, 25, 509, 23], [1, 1, 1, 1, 1, 16, 1], [3, 3, 3, 3, 3, 1, 3]
+    pl = orc.digit_planes(X, n, n, 0, dl, nd, ms, qs, xm).astype(np.int64)
+    res = orc.residues(X, n, n, 0, dl, nd, ms).astype(np.int64)
+    assert pl.shape[0] == 6 + 3
+    p = 0
+    for s, (m, x) in enumerate(zip(ms, xm)):
+        if x == 3:
+            np.testing.assert_array_equal(pl[p], res[s])
+            assert np.abs(pl[p]).max() <= 16
+            p += 1
+        else:
+            np.testing.assert_array_equal((pl[p] + 16 * pl[p + 1] - res[s]) % m, 0)
+            p += 3
